@@ -1,0 +1,152 @@
+/*
+ * l3p.h — C-ABI of libl3p.so, the MI355X (gfx950) quantized forward path of
+ * llama3pure.
+ *
+ * Plain pointers and sizes only.  Device pointers ("_dev") are HIP device
+ * addresses on the context's device; all work is ordered on the context's
+ * single HIP stream.  Every call returns L3P_OK (0) or a negative L3P_E_*
+ * code, with a message in l3p_last_error(ctx).
+ *
+ * Each entry point names the reference interface it replaces
+ * (llama3pure-c-engine.c "c:LINE", llama3pure-js-engine.js "js:LINE").
+ */
+#ifndef L3P_H
+#define L3P_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define L3P_OK 0
+#define L3P_E_INVALID (-1)     /* bad argument or shape                       */
+#define L3P_E_UNSUPPORTED (-2) /* tensor type / shape not implemented          */
+#define L3P_E_HIP (-3)         /* HIP runtime error                            */
+#define L3P_E_NOMEM (-4)       /* device or host allocation failed             */
+#define L3P_E_FORMAT (-5)      /* malformed GGUF                               */
+#define L3P_E_STATE (-6)       /* call out of order (e.g. no model loaded)     */
+
+/* GGML tensor type ids, identical to the reference's enum ggml_type (c:95-113). */
+enum l3p_type {
+    L3P_F32 = 0, L3P_F16 = 1, L3P_Q4_0 = 2, L3P_Q4_1 = 3, L3P_Q5_0 = 6, L3P_Q5_1 = 7,
+    L3P_Q8_0 = 8, L3P_Q2_K = 10, L3P_Q3_K = 11, L3P_Q4_K = 12, L3P_Q5_K = 13,
+    L3P_Q6_K = 14, L3P_IQ4_NL = 20, L3P_BF16 = 29
+};
+
+typedef struct l3p_ctx l3p_ctx;
+
+/* ---- context ------------------------------------------------------------ */
+/* Opens the GPU `device` and creates the context's stream.  Replaces the
+ * process-global engine state of the reference (c:4736-4764, js:205-223). */
+int l3p_create(int device, l3p_ctx** out);
+void l3p_destroy(l3p_ctx* ctx);
+/* Message of the last failed call on ctx (or of l3p_create when ctx is NULL). */
+const char* l3p_last_error(const l3p_ctx* ctx);
+/* The context's hipStream_t, for callers that time or order work around it. */
+void* l3p_stream(l3p_ctx* ctx);
+int l3p_synchronize(l3p_ctx* ctx);
+
+/* ---- device memory, for hosts without a GPU runtime of their own -------- */
+int l3p_malloc(l3p_ctx* ctx, size_t bytes, void** out_dev);
+int l3p_free(l3p_ctx* ctx, void* dev);
+int l3p_upload(l3p_ctx* ctx, void* dst_dev, const void* src_host, size_t bytes);
+int l3p_download(l3p_ctx* ctx, void* dst_host, const void* src_dev, size_t bytes);
+
+/* ---- quantized ops on device buffers ------------------------------------ */
+/* Block bytes of one row of `cols` elements (get_row_size, c:2076-2080). */
+size_t l3p_row_bytes(int type, int cols);
+
+/* Dequantize n elements of blocks to fp32, bit-exact with the reference's
+ * dequantize_row (c:956-1046; per-type c:611-934).  Types: F32 F16 BF16 Q4_0
+ * Q4_1 Q5_0 Q5_1 Q8_0 Q4_K Q6_K IQ4_NL. */
+int l3p_dequant(l3p_ctx* ctx, int type, const void* src_dev, int64_t n, float* dst_dev);
+
+/* Quantize n fp32 values (n % 32 == 0) to Q8_0 blocks of 34 bytes, bit-exact
+ * with quantize_row_q8_0 (c:1508-1528) and quantize_to_q8_0_cache
+ * (c:1535-1570): truncating fp16 scale, roundf quants. */
+int l3p_quantize_q8_0(l3p_ctx* ctx, const float* x_dev, int64_t n, void* dst_dev);
+
+/* y[rows] = W[rows x cols] . x[cols] with W in its native block layout.
+ * Replaces matmul_quantized (c:2091-2133; js:3107-3142).  Semantics per type
+ * follow the reference: Q8_0/Q4_K/Q6_K use fp32 x (matmul_deq_4row,
+ * c:2136-2176); Q4_0 quantizes x to Q8_0 first and uses integer block dots
+ * (c:2105-2116, c:1625-1643).  Results match the reference within the
+ * summation-order tolerance documented in DESIGN.md. */
+int l3p_gemv(l3p_ctx* ctx, int type, const void* w_dev, int rows, int cols, const float* x_dev,
+             float* y_dev);
+
+/* Batched form for prefill: y[b*out_stride + r] = W[r,:] . x[b*in_stride + :]
+ * for b < batch.  Replaces matmul_quantized_batch (c:2291-2331; js:3159-3845).
+ * Q8_0 runs on an MFMA-tiled GEMM; other types loop the GEMV kernels. */
+int l3p_gemm(l3p_ctx* ctx, int type, const void* w_dev, int rows, int cols, const float* x_dev,
+             int batch, int in_stride, float* y_dev, int out_stride);
+
+/* ---- model -------------------------------------------------------------- */
+typedef struct {
+    int context_size;   /* <=0: the model's context_length (c:5174-5178; js:4335)   */
+    int reserved[7];
+} l3p_load_opts;
+
+typedef struct {
+    int dim, hidden_dim, n_layers, n_heads, n_kv_heads, vocab_size, seq_len, head_dim;
+    int is_gemma, swa_window, swa_pattern, weight_type;
+    float rope_theta, rope_theta_swa, rms_eps, final_softcap;
+    int64_t device_bytes;   /* HBM held by weights + KV cache + scratch */
+} l3p_model_info;
+
+/* Parse a GGUF image in host memory and copy every tensor, unchanged, into
+ * HBM; allocate the device KV cache for the context length.  Replaces
+ * parse_gguf_file + init_weights_from_gguf + malloc_run_state (c:2500-2688,
+ * c:2939-3082, c:346-468) and js loadModel/loadWeights/createRunState
+ * (js:4288-4584, js:4586-4660).  The host image may be freed after return. */
+int l3p_load_gguf(l3p_ctx* ctx, const void* gguf, size_t len, const l3p_load_opts* opts);
+int l3p_get_model_info(l3p_ctx* ctx, l3p_model_info* out);
+
+/* One decode position: transformer(token, pos, compute_logits) (c:3190-3435;
+ * js:6121-6128).  When compute_logits, logits stay on the device and, if
+ * logits_host is non-NULL, vocab_size floats are copied there. */
+int l3p_forward(l3p_ctx* ctx, int32_t token, int32_t pos, int compute_logits, float* logits_host);
+
+/* Prefill tokens[0..n) at positions start_pos.. into the KV cache without
+ * logits: transformer_prefill (c:3439-3680; js:6130-6136). */
+int l3p_prefill(l3p_ctx* ctx, const int32_t* tokens_host, int n, int32_t start_pos);
+
+/* Sampling settings (c:4736-4741; js:218-223).  temperature == 0 -> argmax. */
+typedef struct {
+    float temperature;
+    int top_k;
+    float top_p;
+    int reserved;
+} l3p_sampler;
+
+/* Forward at (token, pos) with logits, then sample on the device; only the
+ * token id comes back.  *rng is the xorshift64* state (c:4266-4276),
+ * advanced by one draw when temperature != 0.  Replaces generate_token's
+ * forward + sampler (c:4766-4907) and js transformer + sample (js:6121,
+ * js:6158-6267). */
+int l3p_decode(l3p_ctx* ctx, int32_t token, int32_t pos, const l3p_sampler* s, uint64_t* rng,
+               int32_t* out_token);
+
+/* Sample from vocab logits already on the device (the sampler alone). */
+int l3p_sample(l3p_ctx* ctx, const float* logits_dev, int n, const l3p_sampler* s, uint64_t* rng,
+               int32_t* out_token);
+
+/* Device pointer of the last forward's logits (vocab_size floats). */
+int l3p_logits_device(l3p_ctx* ctx, const float** out_dev);
+
+/* Copy one layer's K or V cache in the reference layout
+ * [kv_head][seq_len][head_dim/32 x 34 B] (c:365-372) to host memory. */
+int l3p_copy_kv(l3p_ctx* ctx, int layer, int which_v, void* dst_host, size_t cap);
+
+/* Row `pos` of the RoPE cos/sin tables (head_dim/2 floats each) that the
+ * model uses, computed on the host with the reference's expression
+ * cosf((float)pos * (1.0f / powf(theta, 2i/head_dim))) (c:381-422); swa
+ * selects the sliding-window theta of Gemma models (c:398-416). */
+int l3p_rope_row(l3p_ctx* ctx, int swa, int pos, float* cos_host, float* sin_host);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* L3P_H */

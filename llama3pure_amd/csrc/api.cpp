@@ -1,0 +1,207 @@
+// api.cpp — the C-ABI of libl3p (include/l3p.h): context, device memory and
+// the standalone quantized ops.  The model entry points live in model.cpp.
+#include <new>
+
+#include "internal.h"
+#include "model.h"
+
+static thread_local std::string g_create_error;
+
+template <class F>
+static int guard(l3p_ctx* c, F&& f) {
+    try {
+        f();
+        return L3P_OK;
+    } catch (const L3pError& e) {
+        if (c) c->err = e.msg;
+        else g_create_error = e.msg;
+        return e.code;
+    } catch (const std::bad_alloc&) {
+        if (c) c->err = "host allocation failed";
+        return L3P_E_NOMEM;
+    }
+}
+
+#define CHECK_CTX(c)                                 \
+    do {                                             \
+        if (!(c)) {                                  \
+            g_create_error = "null context";         \
+            return L3P_E_INVALID;                    \
+        }                                            \
+    } while (0)
+
+extern "C" {
+
+int l3p_create(int device, l3p_ctx** out) {
+    if (!out) {
+        g_create_error = "out is NULL";
+        return L3P_E_INVALID;
+    }
+    *out = nullptr;
+    return guard(nullptr, [&] {
+        int n = 0;
+        L3P_HIP(hipGetDeviceCount(&n));
+        L3P_REQUIRE(device >= 0 && device < n, L3P_E_INVALID, "device %d out of range (%d devices)", device, n);
+        L3P_HIP(hipSetDevice(device));
+        auto* c = new l3p_ctx();
+        c->device = device;
+        hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+        if (e != hipSuccess) {
+            delete c;
+            throw L3pError{L3P_E_HIP, std::string("hipStreamCreate: ") + hipGetErrorString(e)};
+        }
+        *out = c;
+    });
+}
+
+void l3p_destroy(l3p_ctx* c) {
+    if (!c) return;
+    hipSetDevice(c->device);
+    hipStreamSynchronize(c->stream);
+    delete c->model;
+    c->model = nullptr;
+    c->scratch.release();
+    hipStreamDestroy(c->stream);
+    delete c;
+}
+
+const char* l3p_last_error(const l3p_ctx* c) { return c ? c->err.c_str() : g_create_error.c_str(); }
+
+void* l3p_stream(l3p_ctx* c) { return c ? (void*)c->stream : nullptr; }
+
+int l3p_synchronize(l3p_ctx* c) {
+    CHECK_CTX(c);
+    return guard(c, [&] { L3P_HIP(hipStreamSynchronize(c->stream)); });
+}
+
+int l3p_malloc(l3p_ctx* c, size_t bytes, void** out) {
+    CHECK_CTX(c);
+    return guard(c, [&] {
+        L3P_REQUIRE(out, L3P_E_INVALID, "out is NULL");
+        L3P_HIP(hipSetDevice(c->device));
+        hipError_t e = hipMalloc(out, bytes ? bytes : 1);
+        if (e == hipErrorOutOfMemory) throw L3pError{L3P_E_NOMEM, "hipMalloc: out of device memory"};
+        L3P_HIP(e);
+    });
+}
+
+int l3p_free(l3p_ctx* c, void* p) {
+    CHECK_CTX(c);
+    return guard(c, [&] {
+        L3P_HIP(hipStreamSynchronize(c->stream));
+        L3P_HIP(hipFree(p));
+    });
+}
+
+int l3p_upload(l3p_ctx* c, void* dst, const void* src, size_t n) {
+    CHECK_CTX(c);
+    return guard(c, [&] {
+        L3P_HIP(hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, c->stream));
+        L3P_HIP(hipStreamSynchronize(c->stream));
+    });
+}
+
+int l3p_download(l3p_ctx* c, void* dst, const void* src, size_t n) {
+    CHECK_CTX(c);
+    return guard(c, [&] {
+        L3P_HIP(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, c->stream));
+        L3P_HIP(hipStreamSynchronize(c->stream));
+    });
+}
+
+size_t l3p_row_bytes(int type, int cols) { return type_row_bytes(type, cols); }
+
+int l3p_dequant(l3p_ctx* c, int type, const void* src, int64_t n, float* dst) {
+    CHECK_CTX(c);
+    return guard(c, [&] {
+        const int e = type_block_elems(type);
+        L3P_REQUIRE(e > 0 && type != L3P_Q2_K && type != L3P_Q3_K && type != L3P_Q5_K, L3P_E_UNSUPPORTED,
+                    "dequant: unsupported type %d", type);
+        L3P_REQUIRE(n >= 0 && n % e == 0, L3P_E_INVALID, "dequant: n=%lld not a multiple of %d", (long long)n, e);
+        L3P_REQUIRE(n == 0 || (src && dst), L3P_E_INVALID, "dequant: null pointer");
+        launch_dequant(type, (const uint8_t*)src, n, dst, c->stream);
+    });
+}
+
+int l3p_quantize_q8_0(l3p_ctx* c, const float* x, int64_t n, void* dst) {
+    CHECK_CTX(c);
+    return guard(c, [&] {
+        L3P_REQUIRE(n >= 0 && n % 32 == 0, L3P_E_INVALID, "quantize_q8_0: n=%lld not a multiple of 32", (long long)n);
+        L3P_REQUIRE(n == 0 || (x && dst), L3P_E_INVALID, "quantize_q8_0: null pointer");
+        launch_quantize_q8_0_blocks(x, n, (uint8_t*)dst, c->stream);
+    });
+}
+
+int l3p_gemv(l3p_ctx* c, int type, const void* w, int rows, int cols, const float* x, float* y) {
+    CHECK_CTX(c);
+    return guard(c, [&] {
+        L3P_REQUIRE(rows >= 0 && cols > 0, L3P_E_INVALID, "gemv: bad shape %d x %d", rows, cols);
+        L3P_REQUIRE(type_block_elems(type) > 0 && cols % type_block_elems(type) == 0, L3P_E_INVALID,
+                    "gemv: cols=%d not a multiple of the block size of type %d", cols, type);
+        L3P_REQUIRE(gemv_supported(type, cols), L3P_E_UNSUPPORTED,
+                    "gemv: type %d with %d columns not supported", type, cols);
+        if (rows == 0) return;
+        L3P_REQUIRE(w && x && y, L3P_E_INVALID, "gemv: null pointer");
+        L3P_HIP(hipSetDevice(c->device));
+        GemvBatch b{};
+        b.seg[0] = GemvSegment{(const uint8_t*)w, y, rows};
+        b.nseg = 1;
+        b.epilogue = EPI_STORE;
+        if (type == L3P_Q4_0) {
+            XQ8 xq = c->scratch.xq(cols);
+            launch_quantize_x(x, cols, xq, c->stream);
+            launch_gemv(type, b, cols, x, &xq, c->stream);
+        } else {
+            launch_gemv(type, b, cols, x, nullptr, c->stream);
+        }
+    });
+}
+
+int l3p_gemm(l3p_ctx* c, int type, const void* w, int rows, int cols, const float* x, int batch,
+             int in_stride, float* y, int out_stride) {
+    CHECK_CTX(c);
+    return guard(c, [&] {
+        L3P_REQUIRE(batch >= 0 && in_stride >= cols && out_stride >= rows, L3P_E_INVALID,
+                    "gemm: bad batch/strides");
+        L3P_REQUIRE(gemv_supported(type, cols), L3P_E_UNSUPPORTED,
+                    "gemm: type %d with %d columns not supported", type, cols);
+        if (rows == 0 || batch == 0) return;
+        L3P_REQUIRE(w && x && y, L3P_E_INVALID, "gemm: null pointer");
+        L3P_HIP(hipSetDevice(c->device));
+        run_gemm(c, type, (const uint8_t*)w, rows, cols, x, batch, in_stride, y, out_stride);
+    });
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// scratch
+// ---------------------------------------------------------------------------
+void DevBuf::ensure(size_t n) {
+    if (n <= cap) return;
+    release();
+    hipError_t e = hipMalloc(&p, n);
+    if (e == hipErrorOutOfMemory) throw L3pError{L3P_E_NOMEM, "scratch: out of device memory"};
+    L3P_HIP(e);
+    cap = n;
+}
+void DevBuf::release() {
+    if (p) hipFree(p);
+    p = nullptr;
+    cap = 0;
+}
+
+XQ8 Scratch::xq(int cols) {
+    const size_t nb = (size_t)cols / 32;
+    xq_buf.ensure(cols + nb * 8 + 64);
+    XQ8 q;
+    q.qs = (int8_t*)xq_buf.p;
+    q.d = (float*)((char*)xq_buf.p + (cols + 15) / 16 * 16);
+    q.sum = (int32_t*)((char*)q.d + nb * 4);
+    return q;
+}
+
+void Scratch::release() {
+    xq_buf.release();
+    gemm_buf.release();
+}

@@ -1,0 +1,115 @@
+// internal.h — shared declarations of libl3p (host and device).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include <string>
+#include <vector>
+
+#include "../../include/l3p.h"
+
+// ---------------------------------------------------------------------------
+// errors
+// ---------------------------------------------------------------------------
+struct L3pError {
+    int code;
+    std::string msg;
+};
+
+#define L3P_HIP(expr)                                                                        \
+    do {                                                                                     \
+        hipError_t e_ = (expr);                                                              \
+        if (e_ != hipSuccess)                                                                \
+            throw L3pError{L3P_E_HIP, std::string(#expr ": ") + hipGetErrorString(e_)};      \
+    } while (0)
+
+#define L3P_REQUIRE(cond, code, ...)                                                         \
+    do {                                                                                     \
+        if (!(cond)) {                                                                       \
+            char b_[512];                                                                    \
+            snprintf(b_, sizeof b_, __VA_ARGS__);                                            \
+            throw L3pError{code, b_};                                                        \
+        }                                                                                    \
+    } while (0)
+
+// ---------------------------------------------------------------------------
+// block formats (llama3pure-c-engine.c:127-195)
+// ---------------------------------------------------------------------------
+inline int type_block_elems(int t) {
+    switch (t) {
+    case L3P_Q4_0: case L3P_Q4_1: case L3P_Q5_0: case L3P_Q5_1: case L3P_Q8_0: case L3P_IQ4_NL:
+        return 32;
+    case L3P_Q2_K: case L3P_Q3_K: case L3P_Q4_K: case L3P_Q5_K: case L3P_Q6_K:
+        return 256;
+    case L3P_F32: case L3P_F16: case L3P_BF16:
+        return 1;
+    default:
+        return 0;
+    }
+}
+inline int type_block_bytes(int t) {
+    switch (t) {
+    case L3P_F32: return 4;
+    case L3P_F16: case L3P_BF16: return 2;
+    case L3P_Q4_0: return 18;
+    case L3P_Q4_1: return 20;
+    case L3P_Q5_0: return 22;
+    case L3P_Q5_1: return 24;
+    case L3P_Q8_0: return 34;
+    case L3P_Q2_K: return 84;
+    case L3P_Q3_K: return 110;
+    case L3P_Q4_K: return 144;
+    case L3P_Q5_K: return 176;
+    case L3P_Q6_K: return 210;
+    case L3P_IQ4_NL: return 18;
+    default: return 0;
+    }
+}
+inline size_t type_row_bytes(int t, int64_t cols) {
+    int e = type_block_elems(t);
+    return e ? (size_t)(cols / e) * (size_t)type_block_bytes(t) : 0;
+}
+
+// ---------------------------------------------------------------------------
+// GEMV launch descriptions
+// ---------------------------------------------------------------------------
+enum GemvEpilogue : int {
+    EPI_STORE = 0,   // y[r] = W.x
+    EPI_ADD = 1,     // y[r] += W.x          (residual add, c:3111-3115)
+    EPI_SWIGLU = 2,  // pair (gate, up): y[r] = silu(g) * u      (c:3400-3406)
+    EPI_GEGLU = 3,   // pair (gate, up): y[r] = gelu_tanh(g) * u  (c:3391-3398)
+};
+
+// Up to three matrices sharing one input vector, run in one launch
+// (q/k/v, or gate/up with a fused activation).
+struct GemvSegment {
+    const uint8_t* w;
+    float* y;
+    int rows;
+};
+struct GemvBatch {
+    GemvSegment seg[3];
+    int nseg;
+    int pair;      // 1: seg[0] and seg[1] are (gate, up) processed together
+    int epilogue;  // GemvEpilogue
+};
+
+// Activation in the Q8_0 form used by the integer-dot path (Q4_0 weights):
+// int8 quants, the fp32 value of the truncated fp16 scale, and the per-block
+// sum of quants.  Same numbers as the reference's block_q8_0, laid out for
+// aligned loads.
+struct XQ8 {
+    int8_t* qs;     // [cols]
+    float* d;       // [cols/32]
+    int32_t* sum;   // [cols/32]
+};
+
+// launchers (gemv.hip)
+void launch_gemv(int type, const GemvBatch& b, int cols, const float* x, const XQ8* xq,
+                 hipStream_t s);
+void launch_quantize_x(const float* x, int cols, const XQ8& xq, hipStream_t s);
+void launch_quantize_q8_0_blocks(const float* x, int64_t n, uint8_t* dst, hipStream_t s);
+void launch_dequant(int type, const uint8_t* src, int64_t n, float* dst, hipStream_t s);
+bool gemv_supported(int type, int cols);

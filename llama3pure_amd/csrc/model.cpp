@@ -1,0 +1,685 @@
+// model.cpp — GGUF upload, the decode/prefill orchestration and the model
+// entry points of the C-ABI (include/l3p.h).
+//
+// Layer order and per-step arithmetic follow transformer() and
+// transformer_prefill() of llama3pure-c-engine.c (c:3190-3680); each device
+// launch below names the reference lines it replaces.
+#include <math.h>
+#include <string.h>
+
+#include <algorithm>
+#include <memory>
+#include <new>
+#include <string>
+
+#include "model.h"
+
+// ---------------------------------------------------------------------------
+// Model memory
+// ---------------------------------------------------------------------------
+void* Model::dalloc(size_t bytes) {
+    void* p = nullptr;
+    hipError_t e = hipMalloc(&p, bytes ? bytes : 16);
+    if (e == hipErrorOutOfMemory) throw L3pError{L3P_E_NOMEM, "model: out of device memory"};
+    L3P_HIP(e);
+    allocs.push_back(p);
+    device_bytes += (int64_t)bytes;
+    return p;
+}
+
+Model::~Model() {
+    for (void* p : allocs) hipFree(p);
+    if (out_token_host) hipHostFree(out_token_host);
+}
+
+// ---------------------------------------------------------------------------
+// GGUF parsing (format as read by parse_gguf_file, c:2500-2688)
+// ---------------------------------------------------------------------------
+namespace {
+
+struct Reader {
+    const uint8_t* p;
+    const uint8_t* end;
+    uint64_t u(int n) {
+        L3P_REQUIRE(end - p >= n, L3P_E_FORMAT, "GGUF: truncated");
+        uint64_t v = 0;
+        for (int i = 0; i < n; ++i) v |= (uint64_t)p[i] << (8 * i);
+        p += n;
+        return v;
+    }
+    std::string str() {
+        uint64_t n = u(8);
+        L3P_REQUIRE((uint64_t)(end - p) >= n, L3P_E_FORMAT, "GGUF: truncated string");
+        std::string s((const char*)p, n);
+        p += n;
+        return s;
+    }
+    void skip(uint32_t type) {
+        static const int sz[13] = {1, 1, 2, 2, 4, 4, 4, 1, 0, 0, 8, 8, 8};
+        if (type == 8) { str(); return; }
+        if (type == 9) {
+            uint32_t at = (uint32_t)u(4);
+            uint64_t n = u(8);
+            if (at != 8 && at != 9 && at < 13) {
+                uint64_t bytes = n * (uint64_t)sz[at];
+                L3P_REQUIRE((uint64_t)(end - p) >= bytes, L3P_E_FORMAT, "GGUF: truncated array");
+                p += bytes;
+                return;
+            }
+            for (uint64_t i = 0; i < n; ++i) skip(at);
+            return;
+        }
+        L3P_REQUIRE(type < 13 && sz[type] > 0, L3P_E_FORMAT, "GGUF: unknown value type %u", type);
+        u(sz[type]);
+    }
+};
+
+struct KV {
+    std::string key;
+    uint32_t type;
+    const uint8_t* val;
+    uint64_t alen = 0;
+    uint32_t atype = 0;
+};
+struct TI {
+    std::string name;
+    uint32_t ndim;
+    uint64_t ne[4];
+    uint32_t type;
+    uint64_t off;
+};
+
+struct Gguf {
+    std::vector<KV> kv;
+    std::vector<TI> ti;
+    const uint8_t* data = nullptr;
+    size_t data_len = 0;
+
+    const KV* find(const std::string& k) const {
+        for (const auto& e : kv)
+            if (e.key == k) return &e;
+        return nullptr;
+    }
+    // get_gguf_int / get_gguf_float / get_gguf_string (c:2447-2497)
+    int64_t geti(const std::string& k, int64_t d) const {
+        const KV* e = find(k);
+        if (!e) return d;
+        const uint8_t* v = e->val;
+        switch (e->type) {
+        case 0: return v[0];
+        case 1: return (int8_t)v[0];
+        case 2: { uint16_t x; memcpy(&x, v, 2); return x; }
+        case 3: { int16_t x; memcpy(&x, v, 2); return x; }
+        case 4: { uint32_t x; memcpy(&x, v, 4); return x; }
+        case 5: { int32_t x; memcpy(&x, v, 4); return x; }
+        case 10: { uint64_t x; memcpy(&x, v, 8); return (int64_t)x; }
+        case 11: { int64_t x; memcpy(&x, v, 8); return x; }
+        default: return d;
+        }
+    }
+    float getf(const std::string& k, float d) const {
+        const KV* e = find(k);
+        if (!e) return d;
+        if (e->type == 6) { float x; memcpy(&x, e->val, 4); return x; }
+        if (e->type == 12) { double x; memcpy(&x, e->val, 8); return (float)x; }
+        return d;
+    }
+    std::string gets(const std::string& k) const {
+        const KV* e = find(k);
+        if (!e || e->type != 8) return "";
+        uint64_t n;
+        memcpy(&n, e->val, 8);
+        return std::string((const char*)e->val + 8, n);
+    }
+    const TI* tensor(const std::string& n) const {
+        for (const auto& t : ti)
+            if (t.name == n) return &t;
+        return nullptr;
+    }
+};
+
+Gguf parse(const void* bytes, size_t len) {
+    Gguf g;
+    Reader r{(const uint8_t*)bytes, (const uint8_t*)bytes + len};
+    L3P_REQUIRE(len >= 24, L3P_E_FORMAT, "GGUF: file too small");
+    uint32_t magic = (uint32_t)r.u(4);
+    L3P_REQUIRE(magic == 0x46554747u, L3P_E_FORMAT, "Invalid GGUF magic: expected 0x46554747, got 0x%X", magic);
+    uint32_t ver = (uint32_t)r.u(4);
+    L3P_REQUIRE(ver >= 2 && ver <= 3, L3P_E_FORMAT, "Unsupported GGUF version: %u", ver);
+    uint64_t nt = r.u(8), nkv = r.u(8);
+    L3P_REQUIRE(nt < (1u << 24) && nkv < (1u << 24), L3P_E_FORMAT, "GGUF: implausible counts");
+    g.kv.reserve(nkv);
+    for (uint64_t i = 0; i < nkv; ++i) {
+        KV e;
+        e.key = r.str();
+        e.type = (uint32_t)r.u(4);
+        e.val = r.p;
+        if (e.type == 9) {
+            Reader a = r;
+            e.atype = (uint32_t)a.u(4);
+            e.alen = a.u(8);
+        }
+        r.skip(e.type);
+        g.kv.push_back(std::move(e));
+    }
+    g.ti.reserve(nt);
+    for (uint64_t i = 0; i < nt; ++i) {
+        TI t;
+        t.name = r.str();
+        t.ndim = (uint32_t)r.u(4);
+        L3P_REQUIRE(t.ndim >= 1 && t.ndim <= 4, L3P_E_FORMAT, "GGUF: tensor %s has %u dims", t.name.c_str(), t.ndim);
+        for (int d = 0; d < 4; ++d) t.ne[d] = 1;
+        for (uint32_t d = 0; d < t.ndim; ++d) t.ne[d] = r.u(8);
+        t.type = (uint32_t)r.u(4);
+        t.off = r.u(8);
+        g.ti.push_back(std::move(t));
+    }
+    const uint64_t align = (uint64_t)g.geti("general.alignment", 32);   // c:2617-2621
+    L3P_REQUIRE(align > 0, L3P_E_FORMAT, "GGUF: zero alignment");
+    const uint64_t hdr = (uint64_t)(r.p - (const uint8_t*)bytes);
+    const uint64_t doff = (hdr + align - 1) / align * align;
+    L3P_REQUIRE(doff <= len, L3P_E_FORMAT, "GGUF: truncated before tensor data");
+    g.data = (const uint8_t*)bytes + doff;
+    g.data_len = len - doff;
+    for (const auto& t : g.ti) {
+        const int be = type_block_elems((int)t.type);
+        L3P_REQUIRE(be > 0, L3P_E_UNSUPPORTED, "Unsupported quantization type: %u (tensor %s)", t.type, t.name.c_str());
+        const uint64_t ne = t.ne[0] * t.ne[1] * t.ne[2] * t.ne[3];
+        const uint64_t bytes_t = ne / be * type_block_bytes((int)t.type);
+        L3P_REQUIRE(t.off <= g.data_len && bytes_t <= g.data_len - t.off, L3P_E_FORMAT,
+                    "GGUF: tensor %s data out of file", t.name.c_str());
+    }
+    return g;
+}
+
+uint64_t tensor_bytes(const TI& t) {
+    const uint64_t ne = t.ne[0] * t.ne[1] * t.ne[2] * t.ne[3];
+    return ne / type_block_elems((int)t.type) * type_block_bytes((int)t.type);
+}
+
+// RoPE tables exactly as malloc_run_state builds them (c:381-422), with the
+// host C library's powf / cosf / sinf.  Called through pointers so the
+// compiler cannot fuse or constant-fold them.
+float (*volatile p_powf)(float, float) = powf;
+float (*volatile p_cosf)(float) = cosf;
+float (*volatile p_sinf)(float) = sinf;
+
+void rope_tables(int seq, int hs, float theta, std::vector<float>& c, std::vector<float>& s) {
+    const int half = hs / 2;
+    std::vector<float> fr(half);
+    for (int i = 0; i < half; ++i) fr[i] = 1.0f / p_powf(theta, (float)(i * 2) / (float)hs);
+    c.resize((size_t)seq * half);
+    s.resize((size_t)seq * half);
+    for (int p = 0; p < seq; ++p)
+        for (int i = 0; i < half; ++i) {
+            volatile float val = p * fr[i];
+            c[(size_t)p * half + i] = p_cosf(val);
+            s[(size_t)p * half + i] = p_sinf(val);
+        }
+}
+
+bool q8_class(int t) { return t == L3P_Q4_0; }   // q8_func && !deq_func (c:3221)
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// load
+// ---------------------------------------------------------------------------
+static Model* load_model(l3p_ctx* c, const void* bytes, size_t len, const l3p_load_opts* opts) {
+    Gguf g = parse(bytes, len);
+    std::unique_ptr<Model> mp(new Model());
+    Model& m = *mp;
+
+    // config, as main() reads it (c:5049-5182)
+    const std::string arch = g.gets("general.architecture");
+    m.is_gemma = arch == "gemma3" || arch == "gemma2" || arch == "gemma";
+    std::string pre = "llama";
+    if (m.is_gemma) {
+        pre = "gemma3";
+        if (g.geti("gemma3.embedding_length", 0) == 0) {
+            if (g.geti("gemma2.embedding_length", 0) != 0) pre = "gemma2";
+            else if (g.geti("gemma.embedding_length", 0) != 0) pre = "gemma";
+        }
+    }
+    auto K = [&](const char* s) { return pre + "." + s; };
+    m.swa_window = (int)g.geti(K("attention.sliding_window"), 0);
+    m.theta_swa = g.getf(K("rope.freq_base_swa"), 10000.0f);
+    m.swa_pattern = 6;
+    m.dim = (int)g.geti(K("embedding_length"), 4096);
+    m.hidden = (int)g.geti(K("feed_forward_length"), 11008);
+    m.n_layers = (int)g.geti(K("block_count"), 32);
+    m.n_heads = (int)g.geti(K("attention.head_count"), 32);
+    m.n_kv = (int)g.geti(K("attention.head_count_kv"), m.n_heads);
+    m.vocab = (int)g.geti(K("vocab_size"), 32000);
+    m.seq_len = (int)g.geti(K("context_length"), 2048);
+    m.theta = g.getf(K("rope.freq_base"), m.is_gemma ? 1000000.0f : 500000.0f);
+    L3P_REQUIRE(m.n_heads > 0, L3P_E_FORMAT, "GGUF: head_count is 0");
+    m.hs = (int)g.geti(K("attention.key_length"), m.dim / m.n_heads);
+    m.eps = g.getf(K("attention.layer_norm_rms_epsilon"), 1e-6f);
+    m.softcap = g.getf(K("final_logit_softcapping"), 0.0f);
+    if (const KV* tk = g.find("tokenizer.ggml.tokens"))   // vocab from the token list (c:5152-5157)
+        if (tk->type == 9 && tk->atype == 8 && tk->alen > 0) m.vocab = (int)tk->alen;
+    if (opts && opts->context_size > 0 && opts->context_size < m.seq_len) m.seq_len = opts->context_size;
+
+    L3P_REQUIRE(m.dim > 0 && m.hidden > 0 && m.n_layers > 0 && m.vocab > 0 && m.seq_len > 0, L3P_E_FORMAT,
+                "GGUF: bad dimensions");
+    L3P_REQUIRE(m.n_kv > 0 && m.n_heads % m.n_kv == 0, L3P_E_UNSUPPORTED, "n_heads %d not a multiple of n_kv %d",
+                m.n_heads, m.n_kv);
+    L3P_REQUIRE(m.hs % 64 == 0 && m.hs <= 256, L3P_E_UNSUPPORTED, "head_dim %d unsupported (need 64..256, /64)", m.hs);
+    L3P_REQUIRE(m.n_heads / m.n_kv <= 16, L3P_E_UNSUPPORTED, "GQA group of %d heads unsupported", m.n_heads / m.n_kv);
+    m.kv_dim = m.n_kv * m.hs;
+    m.q_dim = m.n_heads * m.hs;
+    m.max_dim = std::max(m.dim, m.q_dim);
+    m.kv_mul = m.n_heads / m.n_kv;
+    m.hq8 = m.hs / 32 * 34;
+    m.head_seq = (size_t)m.seq_len * m.hq8;
+    m.layer_kv = (size_t)m.n_kv * m.head_seq;
+    m.attn_scale = 1.0f / sqrtf((float)m.hs);
+    m.embed_scale = sqrtf((float)m.dim);
+    m.inv_dim = 1.0f / (float)m.dim;
+    m.inv_hs = 1.0f / (float)m.hs;
+
+    hipStream_t s = c->stream;
+    auto upload_raw = [&](const TI& t) -> const uint8_t* {
+        const uint64_t n = tensor_bytes(t);
+        void* d = m.dalloc(n);
+        L3P_HIP(hipMemcpyAsync(d, g.data + t.off, n, hipMemcpyHostToDevice, s));
+        return (const uint8_t*)d;
+    };
+    auto mat = [&](const std::string& name, int rows, int cols, bool required = true) -> Mat {
+        const TI* t = g.tensor(name);
+        L3P_REQUIRE(t || !required, L3P_E_FORMAT, "tensor not found: %s", name.c_str());
+        Mat M;
+        if (!t) return M;
+        L3P_REQUIRE(t->ne[0] == (uint64_t)cols && t->ne[1] * t->ne[2] * t->ne[3] == (uint64_t)rows, L3P_E_FORMAT,
+                    "tensor %s: expected %d x %d", name.c_str(), rows, cols);
+        M.w = upload_raw(*t);
+        M.type = (int)t->type;
+        M.rows = rows;
+        M.cols = cols;
+        M.rb = type_row_bytes(M.type, cols);
+        return M;
+    };
+    // norms become fp32 on the device (load_tensor_float, c:2838-2869)
+    auto vec = [&](const std::string& name, int n) -> float* {
+        const TI* t = g.tensor(name);
+        L3P_REQUIRE(t, L3P_E_FORMAT, "tensor not found: %s", name.c_str());
+        L3P_REQUIRE(t->ne[0] * t->ne[1] * t->ne[2] * t->ne[3] == (uint64_t)n, L3P_E_FORMAT, "tensor %s: expected %d values",
+                    name.c_str(), n);
+        float* d = (float*)m.dalloc((size_t)n * 4);
+        if (t->type == L3P_F32) {
+            L3P_HIP(hipMemcpyAsync(d, g.data + t->off, (size_t)n * 4, hipMemcpyHostToDevice, s));
+        } else {
+            const uint8_t* raw = upload_raw(*t);
+            launch_dequant((int)t->type, raw, n, d, s);
+        }
+        return d;
+    };
+
+    const TI* te = g.tensor("token_embd.weight");
+    L3P_REQUIRE(te, L3P_E_FORMAT, "Failed to load token embeddings");
+    m.emb = mat("token_embd.weight", m.vocab, m.dim);
+    m.layers.resize(m.n_layers);
+    for (int l = 0; l < m.n_layers; ++l) {
+        Layer& L = m.layers[l];
+        const std::string p = "blk." + std::to_string(l) + ".";
+        L.att_norm = vec(p + "attn_norm.weight", m.dim);
+        L.ffn_norm = vec(p + "ffn_norm.weight", m.dim);
+        L.wq = mat(p + "attn_q.weight", m.q_dim, m.dim);
+        L.wk = mat(p + "attn_k.weight", m.kv_dim, m.dim);
+        L.wv = mat(p + "attn_v.weight", m.kv_dim, m.dim);
+        L.wo = mat(p + "attn_output.weight", m.dim, m.q_dim);
+        L.w1 = mat(p + "ffn_gate.weight", m.hidden, m.dim);
+        L.w2 = mat(p + "ffn_down.weight", m.dim, m.hidden);
+        L.w3 = mat(p + "ffn_up.weight", m.hidden, m.dim);
+        if (m.is_gemma) {
+            L.q_norm = vec(p + "attn_q_norm.weight", m.hs);
+            L.k_norm = vec(p + "attn_k_norm.weight", m.hs);
+            L.post_att = vec(p + "post_attention_norm.weight", m.dim);
+            L.post_ffn = vec(p + "post_ffw_norm.weight", m.dim);
+        }
+        const Mat* all[7] = {&L.wq, &L.wk, &L.wv, &L.wo, &L.w1, &L.w2, &L.w3};
+        for (const Mat* M : all)
+            L3P_REQUIRE(gemv_supported(M->type, M->cols), L3P_E_UNSUPPORTED,
+                        "layer %d: weight type %d with %d columns not supported", l, M->type, M->cols);
+        L3P_REQUIRE(q8_class(L.wq.type) == q8_class(L.wk.type) && q8_class(L.wq.type) == q8_class(L.wv.type) &&
+                        q8_class(L.w1.type) == q8_class(L.w3.type) && L.w1.type == L.w3.type,
+                    L3P_E_UNSUPPORTED, "layer %d: mixed activation-quantized and float-input weight types", l);
+    }
+    m.weight_type = m.layers[0].wq.type;
+    m.final_norm = vec("output_norm.weight", m.dim);
+    if (g.tensor("output.weight")) m.wcls = mat("output.weight", m.vocab, m.dim);
+    else m.wcls = m.emb;                                           // tied (c:3064-3079)
+    L3P_REQUIRE(gemv_supported(m.wcls.type, m.dim), L3P_E_UNSUPPORTED, "output weight type %d unsupported", m.wcls.type);
+    L3P_REQUIRE(type_block_elems(m.emb.type) > 0, L3P_E_UNSUPPORTED, "embedding type unsupported");
+
+    // KV cache, zeroed like calloc (c:365-372)
+    m.kc = (uint8_t*)m.dalloc((size_t)m.n_layers * m.layer_kv);
+    m.vc = (uint8_t*)m.dalloc((size_t)m.n_layers * m.layer_kv);
+    L3P_HIP(hipMemsetAsync(m.kc, 0, (size_t)m.n_layers * m.layer_kv, s));
+    L3P_HIP(hipMemsetAsync(m.vc, 0, (size_t)m.n_layers * m.layer_kv, s));
+
+    // RoPE tables
+    {
+        std::vector<float> cd, sd;
+        rope_tables(m.seq_len, m.hs, m.theta, cd, sd);
+        const size_t nbytes = cd.size() * 4;
+        m.cos_d = (float*)m.dalloc(nbytes);
+        m.sin_d = (float*)m.dalloc(nbytes);
+        L3P_HIP(hipMemcpy(m.cos_d, cd.data(), nbytes, hipMemcpyHostToDevice));
+        L3P_HIP(hipMemcpy(m.sin_d, sd.data(), nbytes, hipMemcpyHostToDevice));
+        if (m.is_gemma) {
+            rope_tables(m.seq_len, m.hs, m.theta_swa > 0 ? m.theta_swa : 10000.0f, cd, sd);
+            m.cos_s = (float*)m.dalloc(nbytes);
+            m.sin_s = (float*)m.dalloc(nbytes);
+            L3P_HIP(hipMemcpy(m.cos_s, cd.data(), nbytes, hipMemcpyHostToDevice));
+            L3P_HIP(hipMemcpy(m.sin_s, sd.data(), nbytes, hipMemcpyHostToDevice));
+        } else {
+            m.cos_s = m.cos_d;
+            m.sin_s = m.sin_d;
+        }
+    }
+
+    // run state
+    const int maxin = std::max(m.max_dim, m.hidden);
+    m.x = (float*)m.dalloc((size_t)m.dim * 4);
+    m.xb = (float*)m.dalloc((size_t)m.max_dim * 4);
+    m.xb2 = (float*)m.dalloc((size_t)m.dim * 4);
+    m.q = (float*)m.dalloc((size_t)m.q_dim * 4);
+    m.k = (float*)m.dalloc((size_t)m.kv_dim * 4);
+    m.v = (float*)m.dalloc((size_t)m.kv_dim * 4);
+    m.hb = (float*)m.dalloc((size_t)m.hidden * 4);
+    m.hb2 = (float*)m.dalloc((size_t)m.hidden * 4);
+    m.logits = (float*)m.dalloc((size_t)m.vocab * 4);
+    m.qq = (int8_t*)m.dalloc((size_t)m.q_dim);
+    m.qd = (float*)m.dalloc((size_t)m.q_dim / 32 * 4);
+    m.xq.qs = (int8_t*)m.dalloc((size_t)maxin);
+    m.xq.d = (float*)m.dalloc((size_t)maxin / 32 * 4);
+    m.xq.sum = (int32_t*)m.dalloc((size_t)maxin / 32 * 4);
+    m.att = (float*)m.dalloc((size_t)m.n_heads * m.seq_len * 4);
+    m.max_chunks = (m.seq_len + 63) / 64;
+    m.part_acc = (float*)m.dalloc((size_t)m.n_heads * m.max_chunks * m.hs * 4);
+    m.counters = (unsigned*)m.dalloc((size_t)m.n_kv * sizeof(unsigned));
+    L3P_HIP(hipMemsetAsync(m.counters, 0, (size_t)m.n_kv * sizeof(unsigned), s));
+    const int ncand = std::max(256, sample_num_blocks(m.vocab) * sample_candidates_per_block());
+    m.cand_val = (float*)m.dalloc((size_t)ncand * 4);
+    m.cand_idx = (int*)m.dalloc((size_t)ncand * 4);
+    m.out_token = (int*)m.dalloc(16);
+    L3P_HIP(hipHostMalloc((void**)&m.out_token_host, 16, hipHostMallocDefault));
+    L3P_HIP(hipStreamSynchronize(s));
+    return mp.release();
+}
+
+// ---------------------------------------------------------------------------
+// forward (transformer, c:3190-3435)
+// ---------------------------------------------------------------------------
+static void gemv_into(const Model& m, const Mat& W, const float* x, float* y, int epi, hipStream_t s) {
+    GemvBatch b{};
+    b.seg[0] = GemvSegment{W.w, y, W.rows};
+    b.nseg = 1;
+    b.epilogue = epi;
+    if (q8_class(W.type)) {
+        launch_quantize_x(x, W.cols, m.xq, s);
+        launch_gemv(W.type, b, W.cols, x, &m.xq, s);
+    } else {
+        launch_gemv(W.type, b, W.cols, x, nullptr, s);
+    }
+}
+
+static void forward_impl(l3p_ctx* c, int token, int pos, bool with_logits) {
+    Model& m = *c->model;
+    hipStream_t s = c->stream;
+    const float eps = m.eps > 0 ? m.eps : 1e-5f;                 // c:3198
+    launch_embed(m.emb, token, m.x, s);                          // c:3204-3207
+    for (int l = 0; l < m.n_layers; ++l) {
+        const Layer& L = m.layers[l];
+        const bool qkv_q8 = q8_class(L.wq.type);
+        // attention rmsnorm (c:3211-3217); Q4_0 weights take the Q8_0 x (c:3221-3225)
+        if (m.is_gemma && l == 0)
+            launch_rmsnorm(m.x, m.x, m.embed_scale, L.att_norm, m.dim, m.inv_dim, eps, m.xb, qkv_q8 ? &m.xq : nullptr, s);
+        else
+            launch_rmsnorm(m.x, nullptr, 0.0f, L.att_norm, m.dim, m.inv_dim, eps, m.xb, qkv_q8 ? &m.xq : nullptr, s);
+        // q, k, v in one launch when the three share a type (c:3221-3230)
+        if (L.wq.type == L.wk.type && L.wq.type == L.wv.type) {
+            GemvBatch b{};
+            b.seg[0] = GemvSegment{L.wq.w, m.q, L.wq.rows};
+            b.seg[1] = GemvSegment{L.wk.w, m.k, L.wk.rows};
+            b.seg[2] = GemvSegment{L.wv.w, m.v, L.wv.rows};
+            b.nseg = 3;
+            b.epilogue = EPI_STORE;
+            launch_gemv(L.wq.type, b, m.dim, m.xb, qkv_q8 ? &m.xq : nullptr, s);
+        } else {
+            const Mat* W3[3] = {&L.wq, &L.wk, &L.wv};
+            float* Y3[3] = {m.q, m.k, m.v};
+            for (int i = 0; i < 3; ++i) {
+                GemvBatch b{};
+                b.seg[0] = GemvSegment{W3[i]->w, Y3[i], W3[i]->rows};
+                b.nseg = 1;
+                b.epilogue = EPI_STORE;
+                launch_gemv(W3[i]->type, b, m.dim, m.xb, qkv_q8 ? &m.xq : nullptr, s);
+            }
+        }
+        // QK-norm, RoPE, KV write, Q quantization (c:3232-3312)
+        launch_rope_kv(m, l, pos, s);
+        // attention (c:3314-3359)
+        const bool swa = m.swa_pattern > 0 && (l % m.swa_pattern < m.swa_pattern - 1);
+        int t0 = 0;
+        if (m.is_gemma && swa && m.swa_window > 0) t0 = std::max(0, pos - m.swa_window + 1);
+        AttnArgs a;
+        a.qq = m.qq;
+        a.qd = m.qd;
+        a.kc = m.kc + (size_t)l * m.layer_kv;
+        a.vc = m.vc + (size_t)l * m.layer_kv;
+        a.att = m.att;
+        a.part_acc = m.part_acc;
+        a.counters = m.counters;
+        a.out = m.xb;
+        a.n_heads = m.n_heads;
+        a.kv_mul = m.kv_mul;
+        a.hs = m.hs;
+        a.hq8 = m.hq8;
+        a.seq = m.seq_len;
+        a.t0 = t0;
+        a.na = pos - t0 + 1;
+        a.n_chunks = (a.na + 63) / 64;
+        a.head_seq = m.head_seq;
+        launch_attention(a, s);
+        // output projection + residual (c:3362-3371)
+        if (m.is_gemma) {
+            gemv_into(m, L.wo, m.xb, m.xb2, EPI_STORE, s);
+            launch_rmsnorm_add(m.xb2, L.post_att, m.dim, m.inv_dim, eps, m.x, s);
+        } else {
+            gemv_into(m, L.wo, m.xb, m.x, EPI_ADD, s);
+        }
+        // FFN (c:3373-3417)
+        const bool ffn_q8 = q8_class(L.w1.type);
+        launch_rmsnorm(m.x, nullptr, 0.0f, L.ffn_norm, m.dim, m.inv_dim, eps, m.xb, ffn_q8 ? &m.xq : nullptr, s);
+        {
+            GemvBatch b{};
+            b.seg[0] = GemvSegment{L.w1.w, m.hb, L.w1.rows};
+            b.seg[1] = GemvSegment{L.w3.w, m.hb2, L.w3.rows};
+            b.nseg = 2;
+            b.pair = 1;
+            b.epilogue = m.is_gemma ? EPI_GEGLU : EPI_SWIGLU;
+            launch_gemv(L.w1.type, b, m.dim, m.xb, ffn_q8 ? &m.xq : nullptr, s);
+        }
+        if (m.is_gemma) {
+            gemv_into(m, L.w2, m.hb, m.xb, EPI_STORE, s);
+            launch_rmsnorm_add(m.xb, L.post_ffn, m.dim, m.inv_dim, eps, m.x, s);
+        } else {
+            gemv_into(m, L.w2, m.hb, m.x, EPI_ADD, s);
+        }
+    }
+    // final rmsnorm in place (c:3420), classifier (c:3423-3433)
+    launch_rmsnorm(m.x, nullptr, 0.0f, m.final_norm, m.dim, m.inv_dim, eps, m.x, nullptr, s);
+    if (with_logits) {
+        gemv_into(m, m.wcls, m.x, m.logits, EPI_STORE, s);
+        if (m.is_gemma && m.softcap > 0.0f) launch_softcap(m.logits, m.vocab, m.softcap, s);
+    }
+}
+
+// xorshift64* (c:4266-4276)
+static float rng_f32(uint64_t* st) {
+    *st ^= *st >> 12;
+    *st ^= *st << 25;
+    *st ^= *st >> 27;
+    const uint32_t u = (uint32_t)((*st * 0x2545F4914F6CDD1Dull) >> 32);
+    return (u >> 8) / 16777216.0f;
+}
+
+static void sample_impl(l3p_ctx* c, const float* logits, int n, const l3p_sampler* sp, uint64_t* rng, int32_t* out) {
+    Model& m = *c->model;
+    hipStream_t s = c->stream;
+    if (sp->temperature == 0.0f) {                               // c:4812-4813
+        launch_argmax(logits, n, m.out_token, s, m.cand_val, m.cand_idx);
+    } else {
+        L3P_REQUIRE(rng, L3P_E_INVALID, "sampler: rng state is NULL");
+        const int k = std::min(sp->top_k, n);
+        const float r = rng_f32(rng);
+        launch_sample_topk(logits, n, sp->temperature, k, sp->top_p, r, m.cand_val, m.cand_idx, m.out_token, s);
+    }
+    L3P_HIP(hipMemcpyAsync(m.out_token_host, m.out_token, 4, hipMemcpyDeviceToHost, s));
+    L3P_HIP(hipStreamSynchronize(s));
+    *out = m.out_token_host[0];
+}
+
+// ---------------------------------------------------------------------------
+// batched matmul (matmul_quantized_batch): one GEMV per batch element
+// ---------------------------------------------------------------------------
+void run_gemm(l3p_ctx* c, int type, const uint8_t* w, int rows, int cols, const float* x, int batch, int in_stride,
+              float* y, int out_stride) {
+    for (int b = 0; b < batch; ++b) {
+        GemvBatch gb{};
+        gb.seg[0] = GemvSegment{w, y + (size_t)b * out_stride, rows};
+        gb.nseg = 1;
+        gb.epilogue = EPI_STORE;
+        const float* xb = x + (size_t)b * in_stride;
+        if (q8_class(type)) {
+            XQ8 xq = c->scratch.xq(cols);
+            launch_quantize_x(xb, cols, xq, c->stream);
+            launch_gemv(type, gb, cols, xb, &xq, c->stream);
+        } else {
+            launch_gemv(type, gb, cols, xb, nullptr, c->stream);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// C-ABI
+// ---------------------------------------------------------------------------
+template <class F>
+static int mguard(l3p_ctx* c, bool need_model, F&& f) {
+    if (!c) return L3P_E_INVALID;
+    try {
+        if (need_model && !c->model) throw L3pError{L3P_E_STATE, "no model loaded"};
+        L3P_HIP(hipSetDevice(c->device));
+        f();
+        return L3P_OK;
+    } catch (const L3pError& e) {
+        c->err = e.msg;
+        return e.code;
+    } catch (const std::bad_alloc&) {
+        c->err = "host allocation failed";
+        return L3P_E_NOMEM;
+    }
+}
+
+extern "C" {
+
+int l3p_load_gguf(l3p_ctx* c, const void* bytes, size_t len, const l3p_load_opts* opts) {
+    return mguard(c, false, [&] {
+        L3P_REQUIRE(bytes, L3P_E_INVALID, "gguf pointer is NULL");
+        L3P_HIP(hipStreamSynchronize(c->stream));
+        delete c->model;
+        c->model = nullptr;
+        c->model = load_model(c, bytes, len, opts);
+    });
+}
+
+int l3p_get_model_info(l3p_ctx* c, l3p_model_info* o) {
+    return mguard(c, true, [&] {
+        L3P_REQUIRE(o, L3P_E_INVALID, "out is NULL");
+        const Model& m = *c->model;
+        memset(o, 0, sizeof *o);
+        o->dim = m.dim; o->hidden_dim = m.hidden; o->n_layers = m.n_layers; o->n_heads = m.n_heads;
+        o->n_kv_heads = m.n_kv; o->vocab_size = m.vocab; o->seq_len = m.seq_len; o->head_dim = m.hs;
+        o->is_gemma = m.is_gemma; o->swa_window = m.swa_window; o->swa_pattern = m.swa_pattern;
+        o->weight_type = m.weight_type; o->rope_theta = m.theta; o->rope_theta_swa = m.theta_swa;
+        o->rms_eps = m.eps; o->final_softcap = m.softcap; o->device_bytes = m.device_bytes;
+    });
+}
+
+int l3p_forward(l3p_ctx* c, int32_t token, int32_t pos, int compute_logits, float* logits_host) {
+    return mguard(c, true, [&] {
+        const Model& m = *c->model;
+        L3P_REQUIRE(token >= 0 && token < m.vocab, L3P_E_INVALID, "token %d out of range [0, %d)", token, m.vocab);
+        L3P_REQUIRE(pos >= 0 && pos < m.seq_len, L3P_E_INVALID, "pos %d out of range [0, %d)", pos, m.seq_len);
+        forward_impl(c, token, pos, compute_logits != 0);
+        if (compute_logits && logits_host)
+            L3P_HIP(hipMemcpyAsync(logits_host, m.logits, (size_t)m.vocab * 4, hipMemcpyDeviceToHost, c->stream));
+        L3P_HIP(hipStreamSynchronize(c->stream));
+    });
+}
+
+int l3p_prefill(l3p_ctx* c, const int32_t* tokens, int n, int32_t start) {
+    return mguard(c, true, [&] {
+        const Model& m = *c->model;
+        L3P_REQUIRE(n >= 0 && (n == 0 || tokens), L3P_E_INVALID, "prefill: bad token buffer");
+        L3P_REQUIRE(start >= 0 && start + n <= m.seq_len, L3P_E_INVALID, "prefill: positions [%d, %d) exceed %d", start,
+                    start + n, m.seq_len);
+        for (int i = 0; i < n; ++i)
+            L3P_REQUIRE(tokens[i] >= 0 && tokens[i] < m.vocab, L3P_E_INVALID, "prefill: token %d out of range",
+                        tokens[i]);
+        for (int i = 0; i < n; ++i) forward_impl(c, tokens[i], start + i, false);
+        L3P_HIP(hipStreamSynchronize(c->stream));
+    });
+}
+
+int l3p_decode(l3p_ctx* c, int32_t token, int32_t pos, const l3p_sampler* sp, uint64_t* rng, int32_t* out) {
+    return mguard(c, true, [&] {
+        const Model& m = *c->model;
+        L3P_REQUIRE(sp && out, L3P_E_INVALID, "decode: null sampler/out");
+        L3P_REQUIRE(token >= 0 && token < m.vocab, L3P_E_INVALID, "token %d out of range [0, %d)", token, m.vocab);
+        L3P_REQUIRE(pos >= 0 && pos < m.seq_len, L3P_E_INVALID, "pos %d out of range [0, %d)", pos, m.seq_len);
+        forward_impl(c, token, pos, true);
+        sample_impl(c, m.logits, m.vocab, sp, rng, out);
+    });
+}
+
+int l3p_sample(l3p_ctx* c, const float* logits, int n, const l3p_sampler* sp, uint64_t* rng, int32_t* out) {
+    return mguard(c, true, [&] {
+        L3P_REQUIRE(logits && sp && out && n > 0, L3P_E_INVALID, "sample: bad arguments");
+        L3P_REQUIRE(n <= c->model->vocab, L3P_E_INVALID, "sample: n=%d exceeds the model vocabulary", n);
+        sample_impl(c, logits, n, sp, rng, out);
+    });
+}
+
+int l3p_logits_device(l3p_ctx* c, const float** out) {
+    return mguard(c, true, [&] {
+        L3P_REQUIRE(out, L3P_E_INVALID, "out is NULL");
+        *out = c->model->logits;
+    });
+}
+
+int l3p_copy_kv(l3p_ctx* c, int layer, int which_v, void* dst, size_t cap) {
+    return mguard(c, true, [&] {
+        const Model& m = *c->model;
+        L3P_REQUIRE(layer >= 0 && layer < m.n_layers, L3P_E_INVALID, "layer %d out of range", layer);
+        L3P_REQUIRE(dst && cap >= m.layer_kv, L3P_E_INVALID, "copy_kv: need %zu bytes", m.layer_kv);
+        const uint8_t* src = (which_v ? m.vc : m.kc) + (size_t)layer * m.layer_kv;
+        L3P_HIP(hipMemcpyAsync(dst, src, m.layer_kv, hipMemcpyDeviceToHost, c->stream));
+        L3P_HIP(hipStreamSynchronize(c->stream));
+    });
+}
+
+int l3p_rope_row(l3p_ctx* c, int swa, int pos, float* cos_host, float* sin_host) {
+    return mguard(c, true, [&] {
+        const Model& m = *c->model;
+        L3P_REQUIRE(pos >= 0 && pos < m.seq_len && cos_host && sin_host, L3P_E_INVALID, "rope_row: bad arguments");
+        const size_t half = m.hs / 2;
+        L3P_HIP(hipMemcpy(cos_host, (swa ? m.cos_s : m.cos_d) + pos * half, half * 4, hipMemcpyDeviceToHost));
+        L3P_HIP(hipMemcpy(sin_host, (swa ? m.sin_s : m.sin_d) + pos * half, half * 4, hipMemcpyDeviceToHost));
+    });
+}
+
+}  // extern "C"

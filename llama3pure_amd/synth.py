@@ -1,0 +1,224 @@
+"""Seeded synthetic inputs and a minimal GGUF writer.
+
+Used by tests and by ``bench.py`` to build block-quantized weights and whole
+models without any download.  The block byte layouts are GGML's
+(llama3pure-c-engine.c:127-195); the value distributions are the benchmark
+configurations':
+
+* Q8_0: quants uniform in [-127, 127], fp16 scale |N(0, 0.02)| / 127;
+* Q4_0: nibbles uniform in [0, 15], fp16 scale |N(0, 0.02)| / 8;
+* Q4_K: every scale and quant byte uniform, d and dmin |N(0, 0.02)| / (15*63);
+* Q6_K: ql, qh uniform, int8 sub-scales uniform, d |N(0, 0.02)| / (32*127);
+* activations N(0, 1) fp32.
+
+Model weights are drawn N(0, std) in fp32 and block-quantized with the
+llama.cpp reference quantizers (round-to-nearest-even fp16 scales).
+"""
+from __future__ import annotations
+
+import struct
+
+import numpy as np
+
+F32, F16, Q4_0, Q8_0, Q4_K, Q6_K = 0, 1, 2, 8, 12, 14
+BLOCK = {F32: (1, 4), F16: (1, 2), Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210)}
+
+
+def row_bytes(qtype: int, cols: int) -> int:
+    e, b = BLOCK[qtype]
+    return cols // e * b
+
+
+def _f16_bytes(v: np.ndarray) -> np.ndarray:
+    return np.ascontiguousarray(v.astype(np.float16)).view(np.uint8).reshape(v.shape + (2,))
+
+
+def random_blocks(qtype: int, rows: int, cols: int, seed: int) -> np.ndarray:
+    """uint8 [rows, row_bytes] of random blocks with the configured distribution."""
+    rng = np.random.default_rng(seed)
+    e, bb = BLOCK[qtype]
+    nb = cols // e
+    out = np.empty((rows, nb, bb), np.uint8)
+    if qtype == Q8_0:
+        out[:, :, 0:2] = _f16_bytes(np.abs(rng.normal(0, 0.02, (rows, nb))) / 127)
+        out[:, :, 2:] = rng.integers(-127, 128, (rows, nb, 32), dtype=np.int8).view(np.uint8)
+    elif qtype == Q4_0:
+        out[:, :, 0:2] = _f16_bytes(np.abs(rng.normal(0, 0.02, (rows, nb))) / 8)
+        out[:, :, 2:] = rng.integers(0, 256, (rows, nb, 16), dtype=np.uint8)
+    elif qtype == Q4_K:
+        out[:, :, 0:2] = _f16_bytes(np.abs(rng.normal(0, 0.02, (rows, nb))) / (15 * 63))
+        out[:, :, 2:4] = _f16_bytes(np.abs(rng.normal(0, 0.02, (rows, nb))) / (15 * 63))
+        out[:, :, 4:] = rng.integers(0, 256, (rows, nb, 140), dtype=np.uint8)
+    elif qtype == Q6_K:
+        out[:, :, 0:208] = rng.integers(0, 256, (rows, nb, 208), dtype=np.uint8)
+        out[:, :, 208:210] = _f16_bytes(np.abs(rng.normal(0, 0.02, (rows, nb))) / (32 * 127))
+    else:
+        raise ValueError(f"no synthetic generator for type {qtype}")
+    return out.reshape(rows, nb * bb)
+
+
+def random_x(n: int, seed: int, batch: int | None = None) -> np.ndarray:
+    rng = np.random.default_rng(seed)
+    shape = (n,) if batch is None else (batch, n)
+    return rng.standard_normal(shape, dtype=np.float32)
+
+
+# ---------------------------------------------------------------------------
+# weight quantizers (llama.cpp reference semantics, RNE fp16 scales)
+# ---------------------------------------------------------------------------
+
+def quantize_q8_0(w: np.ndarray) -> np.ndarray:
+    """fp32 [rows, cols] -> Q8_0 bytes [rows, cols/32*34]."""
+    rows, cols = w.shape
+    b = w.reshape(rows, cols // 32, 32).astype(np.float32)
+    amax = np.abs(b).max(axis=2)
+    d = (amax / np.float32(127)).astype(np.float32)
+    with np.errstate(divide="ignore"):
+        inv = np.where(d > 0, np.float32(1) / d, np.float32(0)).astype(np.float32)
+    t = (b * inv[:, :, None]).astype(np.float64)
+    q = np.clip(np.trunc(t + np.copysign(0.5, t)), -127, 127)   # roundf: half away from zero
+    out = np.empty((rows, cols // 32, 34), np.uint8)
+    out[:, :, 0:2] = _f16_bytes(d)
+    out[:, :, 2:] = q.astype(np.int8).view(np.uint8)
+    return out.reshape(rows, -1)
+
+
+def quantize_q4_0(w: np.ndarray) -> np.ndarray:
+    """fp32 [rows, cols] -> Q4_0 bytes, llama.cpp quantize_row_q4_0_ref."""
+    rows, cols = w.shape
+    b = w.reshape(rows, cols // 32, 32).astype(np.float32)
+    idx = np.abs(b).argmax(axis=2)
+    mx = np.take_along_axis(b, idx[:, :, None], axis=2)[:, :, 0]
+    d = (mx / np.float32(-8)).astype(np.float32)
+    with np.errstate(divide="ignore"):
+        inv = np.where(d != 0, np.float32(1) / d, np.float32(0)).astype(np.float32)
+    q = np.minimum(15, (b * inv[:, :, None] + np.float32(8.5)).astype(np.int8)).astype(np.uint8)
+    out = np.empty((rows, cols // 32, 18), np.uint8)
+    out[:, :, 0:2] = _f16_bytes(d)
+    out[:, :, 2:] = q[:, :, :16] | (q[:, :, 16:] << 4)
+    return out.reshape(rows, -1)
+
+
+def quantize(w: np.ndarray, qtype: int) -> np.ndarray:
+    if qtype == Q8_0:
+        return quantize_q8_0(w)
+    if qtype == Q4_0:
+        return quantize_q4_0(w)
+    if qtype == F32:
+        return np.ascontiguousarray(w, np.float32).view(np.uint8).reshape(w.shape[0], -1)
+    raise ValueError(f"no weight quantizer for type {qtype}")
+
+
+# ---------------------------------------------------------------------------
+# GGUF writer (v3, little endian; layout per llama3pure-c-engine.c:2500-2688)
+# ---------------------------------------------------------------------------
+
+_GT_U32, _GT_I32, _GT_F32, _GT_STR, _GT_ARR = 4, 5, 6, 8, 9
+
+
+def _s(b: bytes) -> bytes:
+    return struct.pack("<Q", len(b)) + b
+
+
+def _kv(key: str, val) -> bytes:
+    k = _s(key.encode())
+    if isinstance(val, str):
+        return k + struct.pack("<I", _GT_STR) + _s(val.encode())
+    if isinstance(val, float):
+        return k + struct.pack("<If", _GT_F32, val)
+    if isinstance(val, int):
+        return k + struct.pack("<II", _GT_U32, val)
+    if isinstance(val, list):   # list of str
+        body = b"".join(_s(v.encode()) for v in val)
+        return k + struct.pack("<IIQ", _GT_ARR, _GT_STR, len(val)) + body
+    raise TypeError(type(val))
+
+
+def write_gguf(meta: dict, tensors: list, alignment: int = 32) -> bytes:
+    """tensors: list of (name, qtype, ne (cols, rows) or (n,), raw uint8 bytes)."""
+    head = bytearray(b"GGUF" + struct.pack("<IQQ", 3, len(tensors), len(meta)))
+    for k, v in meta.items():
+        head += _kv(k, v)
+    off = 0
+    offsets = []
+    for name, qtype, ne, raw in tensors:
+        off = (off + alignment - 1) // alignment * alignment
+        offsets.append(off)
+        head += _s(name.encode()) + struct.pack("<I", len(ne))
+        for n in ne:
+            head += struct.pack("<Q", n)
+        head += struct.pack("<IQ", qtype, off)
+        off += len(raw)
+    pad = (-len(head)) % alignment
+    out = bytearray(head) + bytes(pad)
+    base = len(out)
+    for (name, qtype, ne, raw), o in zip(tensors, offsets):
+        out += bytes(base + o - len(out))
+        out += bytes(raw)
+    return bytes(out)
+
+
+def synthetic_model(arch: str = "llama", dim: int = 256, hidden: int = 512, n_layers: int = 2,
+                    n_heads: int = 8, n_kv: int = 2, head_dim: int | None = None, vocab: int = 512,
+                    ctx: int = 256, qtype: int = Q8_0, std: float = 0.02, seed: int = 0,
+                    rope_theta: float = 500000.0, eps: float = 1e-5, tied: bool = False,
+                    softcap: float = 0.0, swa_window: int = 0, rope_theta_swa: float = 10000.0,
+                    norm_jitter: float = 0.0) -> bytes:
+    """A random-init model in GGUF form.  arch 'llama' (Llama-3 layout) or
+    'gemma3' (Gemma layout: QK-norm, post norms, NEOX RoPE, GeGLU)."""
+    rng = np.random.default_rng(seed)
+    hd = head_dim or dim // n_heads
+    qd, kvd = n_heads * hd, n_kv * hd
+    pre = "gemma3" if arch.startswith("gemma") else "llama"
+    meta = {
+        "general.architecture": arch,
+        f"{pre}.embedding_length": dim,
+        f"{pre}.feed_forward_length": hidden,
+        f"{pre}.block_count": n_layers,
+        f"{pre}.attention.head_count": n_heads,
+        f"{pre}.attention.head_count_kv": n_kv,
+        f"{pre}.vocab_size": vocab,
+        f"{pre}.context_length": ctx,
+        f"{pre}.rope.freq_base": float(rope_theta),
+        f"{pre}.attention.key_length": hd,
+        f"{pre}.attention.layer_norm_rms_epsilon": float(eps),
+    }
+    if pre == "gemma3":
+        meta[f"{pre}.final_logit_softcapping"] = float(softcap)
+        meta[f"{pre}.attention.sliding_window"] = swa_window
+        meta[f"{pre}.rope.freq_base_swa"] = float(rope_theta_swa)
+    meta["tokenizer.ggml.tokens"] = [f"<t{i}>" for i in range(vocab)]
+    meta["tokenizer.ggml.bos_token_id"] = 1
+    meta["tokenizer.ggml.eos_token_id"] = 2
+
+    def mat(rows, cols):
+        w = rng.normal(0, std, (rows, cols)).astype(np.float32)
+        return (qtype, (cols, rows), quantize(w, qtype).ravel())
+
+    def norm(n):
+        v = np.ones(n, np.float32)
+        if norm_jitter:
+            v += rng.normal(0, norm_jitter, n).astype(np.float32)
+        return (F32, (n,), v.view(np.uint8))
+
+    tensors = [("token_embd.weight",) + mat(vocab, dim)]
+    for l in range(n_layers):
+        p = f"blk.{l}."
+        tensors += [(p + "attn_norm.weight",) + norm(dim),
+                    (p + "attn_q.weight",) + mat(qd, dim),
+                    (p + "attn_k.weight",) + mat(kvd, dim),
+                    (p + "attn_v.weight",) + mat(kvd, dim),
+                    (p + "attn_output.weight",) + mat(dim, qd),
+                    (p + "ffn_norm.weight",) + norm(dim),
+                    (p + "ffn_gate.weight",) + mat(hidden, dim),
+                    (p + "ffn_down.weight",) + mat(dim, hidden),
+                    (p + "ffn_up.weight",) + mat(hidden, dim)]
+        if pre == "gemma3":
+            tensors += [(p + "attn_q_norm.weight",) + norm(hd),
+                        (p + "attn_k_norm.weight",) + norm(hd),
+                        (p + "post_attention_norm.weight",) + norm(dim),
+                        (p + "post_ffw_norm.weight",) + norm(dim)]
+    tensors.append(("output_norm.weight",) + norm(dim))
+    if not tied:
+        tensors.append(("output.weight",) + mat(vocab, dim))
+    return write_gguf(meta, tensors)

@@ -1,0 +1,199 @@
+"""GPU parity of the standalone ops, through the C-ABI (libl3p.so).
+
+Bit-exact: dequantization and the Q8_0 quantizer.  GEMV: within the stated
+fp32 summation tolerance of the float64 value of the reference arithmetic:
+
+    |y_gpu - y64| <= gamma_(K+4) * S,   gamma_n = n u / (1 - n u), u = 2^-24
+
+where S bounds the magnitudes summed by either side:
+    Q8_0:  S = sum_j |w_j x_j|
+    Q4_0:  S = sum_blocks |dw dx isum|           (integer block dots are exact)
+    Q4_K:  S = sum_j (|d1 q_j| + |m1|) |x_j|     (kernel factors d1, m1 out of a sub-block)
+    Q6_K:  S = sum_j |d sc| (|q_j| + 32) |x_j|   (kernel factors d sc, offset 32)
+and the oracle itself must satisfy the same bound.
+"""
+import numpy as np
+import pytest
+
+import llama3pure_amd as l3p
+import oracle
+from llama3pure_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+
+def gamma(n):
+    u = 2.0 ** -24
+    return n * u / (1 - n * u)
+
+
+def dev(torch, a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def empty_f32(torch, n):
+    return torch.empty(n, dtype=torch.float32, device="cuda")
+
+
+# --------------------------------------------------------------------------- dequant / quantize
+@pytest.mark.parametrize("qtype", [l3p.Q8_0, l3p.Q4_0, l3p.Q4_1, l3p.Q5_0, l3p.Q5_1, l3p.Q4_K, l3p.Q6_K,
+                                   l3p.IQ4_NL, l3p.F16, l3p.BF16, l3p.F32])
+def test_dequant_bit_exact(ctx, torch_gpu, cpuref, qtype):
+    e, bb = oracle.BLOCK[qtype]
+    n = 256 * 40
+    raw = np.random.default_rng(qtype + 100).integers(0, 256, n // e * bb, dtype=np.uint8)
+    if qtype in (l3p.Q8_0, l3p.Q4_0, l3p.Q4_K, l3p.Q6_K):
+        raw[: synth.row_bytes(qtype, 2048)] = synth.random_blocks(qtype, 1, 2048, seed=3)[0]
+    d = dev(torch_gpu, raw)
+    out = empty_f32(torch_gpu, n)
+    ctx.dequant(qtype, d, n, out)
+    ctx.synchronize()
+    want = cpuref.dequant(qtype, raw, n)
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32))
+
+
+def test_quantize_q8_0_bit_exact(ctx, torch_gpu, cpuref):
+    rng = np.random.default_rng(7)
+    n = 32 * 4096
+    x = (rng.standard_normal(n) * np.float32(10.0) ** rng.integers(-8, 5, n)).astype(np.float32)
+    x[:32] = 0.0
+    x[32:64] = np.array([127.0] + [k + 0.5 for k in range(-15, 16)], np.float32)   # exact .5 ties
+    x[64:96] = 1e-30                                                               # subnormal scale
+    x[96:128] = -np.float32(3.0e38)
+    out = torch_gpu.empty(n // 32 * 34, dtype=torch_gpu.uint8, device="cuda")
+    ctx.quantize_q8_0(dev(torch_gpu, x), n, out)
+    ctx.synchronize()
+    assert np.array_equal(out.cpu().numpy(), cpuref.quantize_q8_0(x))
+
+
+# --------------------------------------------------------------------------- GEMV
+def _bound_terms(cpuref, qtype, w, rows, cols, x):
+    """(y64, S) of the reference arithmetic in float64, per the module doc."""
+    x64 = x.astype(np.float64)
+    if qtype == l3p.Q4_0:
+        xq = cpuref.quantize_q8_0(x).reshape(-1, 34)
+        dx = xq[:, 0:2].copy().view(np.float16).astype(np.float64)[:, 0]
+        qx = xq[:, 2:].view(np.int8).astype(np.int64)
+        wb = w.reshape(rows, -1, 18)
+        dw = wb[:, :, 0:2].copy().view(np.float16).astype(np.float64)[:, :, 0]
+        nib = np.concatenate([(wb[:, :, 2:] & 15), (wb[:, :, 2:] >> 4)], axis=2).astype(np.int64) - 8
+        terms = dw * dx[None] * np.einsum("rbj,bj->rb", nib, qx)
+        return terms.sum(1), np.abs(terms).sum(1)
+    W = np.stack([cpuref.dequant(qtype, w[r], cols) for r in range(rows)]).astype(np.float64)
+    y64 = W @ x64
+    if qtype == l3p.Q8_0:
+        return y64, np.abs(W) @ np.abs(x64)
+    if qtype == l3p.Q4_K:
+        # |d1 q| + |m1| per element, from the block fields
+        wb = w.reshape(rows, -1, 144)
+        d = wb[:, :, 0:2].copy().view(np.float16).astype(np.float64)[:, :, 0]
+        dmin = wb[:, :, 2:4].copy().view(np.float16).astype(np.float64)[:, :, 0]
+        s = wb[:, :, 4:16].astype(np.int64)
+        A = np.empty((rows, cols))
+        for j in range(8):
+            if j < 4:
+                sc, m = s[:, :, j] & 63, s[:, :, j + 4] & 63
+            else:
+                sc = (s[:, :, j + 4] & 15) | ((s[:, :, j - 4] >> 6) << 4)
+                m = (s[:, :, j + 4] >> 4) | ((s[:, :, j] >> 6) << 4)
+            q = wb[:, :, 16 + 32 * (j // 2): 48 + 32 * (j // 2)].astype(np.int64)
+            q = (q >> 4) if j % 2 else (q & 15)
+            a = np.abs(d * sc)[:, :, None] * q + np.abs(dmin * m)[:, :, None]
+            A.reshape(rows, -1, 8, 32)[:, :, j, :] = a
+        return y64, A @ np.abs(x64)
+    if qtype == l3p.Q6_K:
+        wb = w.reshape(rows, -1, 210)
+        d = wb[:, :, 208:210].copy().view(np.float16).astype(np.float64)[:, :, 0]
+        sc = wb[:, :, 192:208].view(np.int8).astype(np.float64)
+        # |d sc| (|q| + 32) <= |d sc| * 95
+        A = np.repeat(np.abs(d[:, :, None] * sc), 16, axis=2).reshape(rows, cols) * 95.0
+        return y64, A @ np.abs(x64)
+    raise ValueError(qtype)
+
+
+def _check_gemv(ctx, torch, cpuref, qtype, rows, cols, seed=0, sample_rows=None):
+    w = synth.random_blocks(qtype, rows, cols, seed=seed)
+    x = synth.random_x(cols, seed=seed + 1)
+    y = empty_f32(torch, rows)
+    ctx.gemv(qtype, dev(torch, w), rows, cols, dev(torch, x), y)
+    ctx.synchronize()
+    got = y.cpu().numpy()
+    idx = np.arange(rows) if sample_rows is None else np.random.default_rng(seed).choice(rows, sample_rows, False)
+    wi = w[idx]
+    y64, S = _bound_terms(cpuref, qtype, wi, len(idx), cols, x)
+    tol = gamma(cols + 4) * S
+    ref = cpuref.matmul(qtype, wi, len(idx), cols, x)
+    assert np.all(np.abs(ref - y64) <= tol), "oracle outside its own bound"
+    err = np.abs(got[idx] - y64)
+    assert np.all(err <= tol), f"max err/tol {np.max(err / np.maximum(tol, 1e-30)):.3g}"
+    return got
+
+
+@pytest.mark.parametrize("qtype,rows,cols", [
+    (l3p.Q8_0, 4096, 4096),        # attention shape
+    (l3p.Q8_0, 1024, 14336),
+    (l3p.Q4_0, 14336, 4096),       # FFN gate/up
+    (l3p.Q4_0, 4096, 14336),       # FFN down
+    (l3p.Q4_K, 14336, 4096),
+    (l3p.Q6_K, 2048, 4096),
+    (l3p.Q8_0, 2304, 2304),        # Gemma-2-2B dims
+    (l3p.Q8_0, 2304, 9216),
+])
+def test_gemv_parity(ctx, torch_gpu, cpuref, qtype, rows, cols):
+    _check_gemv(ctx, torch_gpu, cpuref, qtype, rows, cols, seed=rows + cols, sample_rows=min(rows, 768))
+
+
+def test_gemv_q6_k_lm_head_shape(ctx, torch_gpu, cpuref):
+    """Q6_K at the 128256 x 4096 output-projection shape (rows sampled)."""
+    _check_gemv(ctx, torch_gpu, cpuref, l3p.Q6_K, 128256, 4096, seed=9, sample_rows=512)
+
+
+@pytest.mark.parametrize("qtype", [l3p.Q8_0, l3p.Q4_0, l3p.Q4_K, l3p.Q6_K])
+@pytest.mark.parametrize("rows", [1, 3, 5, 7, 9, 4097])
+def test_gemv_ragged_rows(ctx, torch_gpu, cpuref, qtype, rows):
+    cols = 2048 if qtype == l3p.Q6_K else 512
+    _check_gemv(ctx, torch_gpu, cpuref, qtype, rows, cols, seed=rows)
+
+
+def test_gemv_zero_rows_and_errors(ctx, torch_gpu):
+    x = empty_f32(torch_gpu, 512)
+    y = empty_f32(torch_gpu, 8)
+    ctx.gemv(l3p.Q8_0, 0, 0, 512, x, y)              # no rows: nothing to do
+    with pytest.raises(l3p.L3PError) as e:
+        ctx.gemv(l3p.Q8_0, 0, 8, 500, x, y)          # cols not a block multiple
+    assert e.value.code == l3p.E_INVALID
+    with pytest.raises(l3p.L3PError) as e:
+        ctx.gemv(l3p.Q4_1, 0, 8, 512, x, y)          # type without a GEMV kernel
+    assert e.value.code == l3p.E_UNSUPPORTED
+    with pytest.raises(l3p.L3PError) as e:
+        ctx.gemv(l3p.Q8_0, 0, 8, 512, x, y)          # null weight pointer
+    assert e.value.code == l3p.E_INVALID
+
+
+def test_gemv_deterministic(ctx, torch_gpu):
+    rows, cols = 4096, 4096
+    w = dev(torch_gpu, synth.random_blocks(l3p.Q8_0, rows, cols, seed=1))
+    x = dev(torch_gpu, synth.random_x(cols, seed=2))
+    y1, y2 = empty_f32(torch_gpu, rows), empty_f32(torch_gpu, rows)
+    ctx.gemv(l3p.Q8_0, w, rows, cols, x, y1)
+    ctx.gemv(l3p.Q8_0, w, rows, cols, x, y2)
+    ctx.synchronize()
+    assert torch_gpu.equal(y1, y2)
+
+
+@pytest.mark.parametrize("qtype", [l3p.Q8_0, l3p.Q4_0])
+def test_gemm_equals_gemv_rows(ctx, torch_gpu, qtype):
+    """The batched form gives, per batch element, exactly the GEMV result."""
+    rows, cols, batch = 1024, 2048, 7
+    w = dev(torch_gpu, synth.random_blocks(qtype, rows, cols, seed=5))
+    xb = synth.random_x(cols, seed=6, batch=batch)
+    xd = dev(torch_gpu, xb)
+    y = empty_f32(torch_gpu, batch * rows)
+    ctx.gemm(qtype, w, rows, cols, xd, batch, cols, y, rows)
+    ys = []
+    for b in range(batch):
+        yb = empty_f32(torch_gpu, rows)
+        ctx.gemv(qtype, w, rows, cols, xd[b], yb)
+        ys.append(yb)
+    ctx.synchronize()
+    assert torch_gpu.equal(y.view(batch, rows), torch_gpu.stack(ys))
