@@ -1,0 +1,277 @@
+"""Decode throughput of the quantized forward path on one MI355X.
+
+Workload (one "step" = one greedy decode token, forward + on-device sampling,
+only the token id returns to the host): a random-init Llama-3-8B-architecture
+model, every matrix Q8_0 (32 layers, dim 4096, 32 query / 8 KV heads, head_dim
+128, SwiGLU 14336, vocab 128256, RoPE theta 500000, RMSNorm eps 1e-5, weights
+N(0, 0.02) before quantization, norm weights 1.0), KV cache prefilled to
+position 1024 of a 2048 context with uniform random token ids.
+
+Printed as one JSON line:
+  value        decode tok/s over exactly --steps timed steps (weights, KV
+               cache and run state already resident in HBM);
+  roofline     the dominant GEMV launch class: algorithmic bytes per launch
+               over its average launch duration, from HIP events recorded by
+               the library on its stream around every GEMV launch, over a
+               second pass of --steps decode steps;
+  gemv         standalone GEMV launches at the Llama-3-8B shapes (Q8_0, Q4_0,
+               Q4_K, Q6_K), weight copies rotated through >= 1 GiB so the
+               256 MB last-level cache does not serve them;
+  cpu_baseline the reference C engine (oracle/_ref/libref_omp.so: its own
+               source built with its Makefile's -Ofast -fopenmp line) decoding
+               the same GGUF on the host cores for a bounded sample; the
+               oracle (single-threaded C restatement) when that is not built.
+
+usage: python bench.py [--gpus 1] [--steps 128] [--warmup 8]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import subprocess
+import sys
+import tempfile
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0   # MI355X HBM3E, 8 TB/s
+
+LLAMA3_8B = dict(arch="llama", dim=4096, hidden=14336, n_layers=32, n_heads=32, n_kv=8, vocab=128256, ctx=2048,
+                 rope_theta=500000.0, eps=1e-5, std=0.02, seed=1234)
+
+
+def gpu_q8_0_maker(ctx, torch, seed):
+    """make_mat for synth.synthetic_model: N(0, std) drawn on the GPU and
+    quantized to Q8_0 blocks by the library's quantizer."""
+    st = torch.cuda.ExternalStream(ctx.stream)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed)
+    import llama3pure_amd as l3p
+
+    def make(qtype, rows, cols, std, view):
+        assert qtype == l3p.Q8_0
+        rb = cols // 32 * 34
+        step = max(1, (1 << 26) // cols)
+        with torch.cuda.stream(st):
+            for r0 in range(0, rows, step):
+                n = min(step, rows - r0)
+                w = torch.randn(n * cols, device="cuda", generator=gen) * std
+                q = torch.empty(n * rb, dtype=torch.uint8, device="cuda")
+                ctx.quantize_q8_0(w, n * cols, q)
+                view[r0 * rb:(r0 + n) * rb] = q.cpu().numpy()
+        return view
+
+    return make
+
+
+def time_gemv_shapes(ctx, torch, l3p, synth):
+    """GB/s of single GEMV launches (library call: input preparation + GEMV)."""
+    st = torch.cuda.ExternalStream(ctx.stream)
+    shapes = [("q8_0", l3p.Q8_0, 4096, 4096), ("q4_0", l3p.Q4_0, 14336, 4096), ("q4_0", l3p.Q4_0, 4096, 14336),
+              ("q4_k", l3p.Q4_K, 14336, 4096), ("q6_k", l3p.Q6_K, 128256, 4096)]
+    out = []
+    for name, qt, rows, cols in shapes:
+        wbytes = rows * synth.row_bytes(qt, cols)
+        copies = max(2, -(-(1 << 30) // wbytes))
+        base = torch.from_numpy(synth.random_blocks(qt, rows, cols, seed=7)).cuda()
+        ws = [base.clone() for _ in range(copies)]
+        x = torch.from_numpy(synth.random_x(cols, seed=8)).cuda()
+        y = torch.empty(rows, device="cuda")
+        torch.cuda.synchronize()
+        for i in range(copies):
+            ctx.gemv(qt, ws[i], rows, cols, x, y)
+        ctx.synchronize()
+        n = max(40, 2 * copies)
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+        with torch.cuda.stream(st):
+            for i in range(n):
+                ev[i][0].record(st)
+                ctx.gemv(qt, ws[i % copies], rows, cols, x, y)
+                ev[i][1].record(st)
+        ctx.synchronize()
+        us = sorted(a.elapsed_time(b) * 1e3 for a, b in ev)
+        med = us[len(us) // 2]
+        alg = wbytes + 4 * cols + 4 * rows
+        out.append({"shape": f"{name} {rows}x{cols}", "us": round(med, 2), "GB/s": round(alg / med / 1e3, 1),
+                    "frac": round(alg / med / 1e3 / HBM_PEAK_GBS, 4)})
+        del ws, base
+        torch.cuda.empty_cache()
+    return out
+
+
+def cpu_leg(path: str, seconds: float, max_tokens: int, use_ref: bool) -> dict:
+    """Runs in a subprocess: the reference engine (or the oracle) decoding
+    greedily from position 0 on the GGUF at path."""
+    import ctypes
+
+    import numpy as np
+
+    import oracle
+
+    if use_ref:
+        ref = oracle.Ref(oracle.REF_OMP_SO)
+        t0 = time.perf_counter()
+        if ref.lib.ref_model_open(path.encode(), 0) != 0:
+            raise RuntimeError("reference failed to open the model")
+        load_s = time.perf_counter() - t0
+        tok, n, seed = 1, 0, ctypes.c_ulonglong(42)
+        t0 = time.perf_counter()
+        while n < max_tokens and (n == 0 or time.perf_counter() - t0 < seconds):
+            tok = int(ref.lib.ref_generate_token(tok, n, 0.0, 40, 0.9, ctypes.byref(seed)))
+            n += 1
+        dt = time.perf_counter() - t0
+    else:
+        cr = oracle.CpuRef()
+        img = np.fromfile(path, np.uint8)
+        t0 = time.perf_counter()
+        m = cr.open_model(img.tobytes())
+        load_s = time.perf_counter() - t0
+        tok, n = 1, 0
+        t0 = time.perf_counter()
+        while n < max_tokens and (n == 0 or time.perf_counter() - t0 < seconds):
+            tok = int(np.argmax(m.forward(tok, n)))
+            n += 1
+        dt = time.perf_counter() - t0
+    return {"tokens": n, "seconds": dt, "load_seconds": load_s}
+
+
+def cpu_baseline(img, seconds: float) -> dict | None:
+    import oracle
+
+    use_ref = oracle.have_ref() and os.path.exists(oracle.REF_OMP_SO)
+    cores = min(16, os.cpu_count() or 1) if use_ref else 1
+    d = "/dev/shm" if os.path.isdir("/dev/shm") else None
+    fd, path = tempfile.mkstemp(suffix=".gguf", dir=d)
+    try:
+        with os.fdopen(fd, "wb") as f:
+            img.tofile(f)
+        env = dict(os.environ, OMP_NUM_THREADS=str(cores))
+        r = subprocess.run([sys.executable, os.path.abspath(__file__), "--cpu-leg", path, "--cpu-seconds",
+                            str(seconds), "--cpu-ref", str(int(use_ref))], env=env, capture_output=True, text=True,
+                           timeout=600)
+        if r.returncode != 0:
+            print(r.stderr[-2000:], file=sys.stderr)
+            return None
+        # the reference prints each decoded token's text to stdout before the result line
+        res = json.loads(r.stdout[r.stdout.rfind('{"tokens"'):].splitlines()[0])
+    finally:
+        os.unlink(path)
+    what = ("reference C engine built -Ofast -fopenmp (its Makefile OpenMP line)" if use_ref
+            else "oracle (C restatement of the reference, -O2, one thread)")
+    return {"value": round(res["tokens"] / res["seconds"], 4), "unit": "tok/s", "cores": cores,
+            "kind": "reference" if use_ref else "port",
+            "sample": f"{what}: {res['tokens']} greedy decode tokens from position 0 of the same GGUF "
+                      f"({res['seconds']:.1f} s); per-token cost is the 8.0 GB weight stream, attention "
+                      f"over <= {res['tokens']} positions instead of 1024"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=128)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--prefill", type=int, default=1024)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-gemv", action="store_true", help="skip the standalone GEMV shapes")
+    ap.add_argument("--cpu-leg", help=argparse.SUPPRESS)
+    ap.add_argument("--cpu-ref", type=int, default=1, help=argparse.SUPPRESS)
+    a = ap.parse_args()
+
+    if a.cpu_leg:
+        print(json.dumps(cpu_leg(a.cpu_leg, a.cpu_seconds, 64, bool(a.cpu_ref))))
+        return
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: the decode path runs on a single MI355X and has no multi-GPU "
+              "mode (--gpus must be 1)", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    import llama3pure_amd as l3p
+    from llama3pure_amd import synth
+
+    ctx = l3p.Context(0)
+    t0 = time.perf_counter()
+    img = synth.synthetic_model(qtype=synth.Q8_0, make_mat=gpu_q8_0_maker(ctx, torch, 99), **LLAMA3_8B)
+    t_gen = time.perf_counter() - t0
+    mi = ctx.load_gguf(img)
+    print(f"[bench] model {img.nbytes / 1e9:.2f} GB generated in {t_gen:.1f} s, "
+          f"{mi.device_bytes / 1e9:.2f} GB on device", file=sys.stderr, flush=True)
+
+    rng = np.random.default_rng(5)
+    prompt = rng.integers(0, mi.vocab_size, a.prefill + 1).astype(np.int32)
+    t0 = time.perf_counter()
+    ctx.prefill(prompt[:-1], 0)
+    print(f"[bench] prefill {a.prefill} positions in {time.perf_counter() - t0:.1f} s", file=sys.stderr, flush=True)
+
+    def run(n, tok, pos):
+        for _ in range(n):
+            tok, _ = ctx.decode(tok, pos, temperature=0.0)
+            pos += 1
+        return tok, pos
+
+    assert a.prefill + a.warmup + 2 * a.steps <= mi.seq_len, "steps exceed the 2048-position context"
+    tok, pos = run(a.warmup, int(prompt[-1]), a.prefill)
+    ctx.synchronize()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    tok, pos = run(a.steps, tok, pos)
+    ctx.synchronize()
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    tps = a.steps / dt
+    print(f"[bench] {a.steps} decode steps in {dt * 1e3:.1f} ms: {tps:.1f} tok/s", file=sys.stderr, flush=True)
+
+    # second pass with per-launch events: the roofline of the dominant GEMV class
+    ctx.profile(True)
+    tok, pos = run(a.steps, tok, pos)
+    stats = ctx.profile_read()
+    ctx.profile(False)
+    name, (launches, ms, bpl) = max(stats.items(), key=lambda kv: kv[1][1])
+    avg_us = ms * 1e3 / launches
+    achieved = bpl / (avg_us * 1e-6) / 1e9
+    kernels = {k: {"launches": v[0], "avg_us": round(v[1] * 1e3 / v[0], 2),
+                   "GB/s": round(v[2] / (v[1] * 1e-3 / v[0]) / 1e9, 1)} for k, v in stats.items()}
+    print(f"[bench] GEMV classes: {json.dumps(kernels)}", file=sys.stderr, flush=True)
+
+    gemv = None if a.no_gemv else time_gemv_shapes(ctx, torch, l3p, synth)
+    if gemv:
+        print(f"[bench] standalone GEMV: {json.dumps(gemv)}", file=sys.stderr, flush=True)
+
+    base = None if a.no_cpu else cpu_baseline(img, a.cpu_seconds)
+    del img
+
+    line = {
+        "metric": "quant GEMV HBM GB/s (% of peak); decode tok/s Llama-3-8B-arch Q8_0, 1 GPU",
+        "value": round(tps, 3),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(dt * 1e3 / a.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q8_0 weights, int8-digit dot, fp32 accumulate",
+        "data": "synthetic: random-init weights N(0,0.02) quantized to Q8_0, uniform random token ids",
+        "config": {"workload": "greedy decode, Llama-3-8B architecture, all matrices Q8_0, KV prefilled to "
+                               f"{a.prefill} of 2048", "layers": 32, "dim": 4096, "heads": 32, "kv_heads": 8,
+                   "ffn": 14336, "vocab": 128256, "start_pos": a.prefill, "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "kernel": name, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "bytes_per_launch": int(bpl), "avg_launch_us": round(avg_us, 2), "launches": launches},
+        "gemv_classes": kernels,
+        "gemv": gemv,
+        "cpu_baseline": base,
+    }
+    print(json.dumps(line), flush=True)
+    ctx.close()
+
+
+if __name__ == "__main__":
+    main()

@@ -146,6 +146,21 @@ int l3p_copy_kv(l3p_ctx* ctx, int layer, int which_v, void* dst_host, size_t cap
  * selects the sliding-window theta of Gemma models (c:398-416). */
 int l3p_rope_row(l3p_ctx* ctx, int swa, int pos, float* cos_host, float* sin_host);
 
+/* GEMV launch timing.  No counterpart in the reference, which only prints
+ * whole-token rates (c:5312-5314; tests.js:167-180).  l3p_profile(ctx, 1)
+ * clears the statistics and records HIP events on the context stream around
+ * every GEMV launch of l3p_forward/l3p_prefill/l3p_decode; l3p_profile(ctx, 0)
+ * stops.  l3p_profile_read fills up to cap entries, one per launch class
+ * ("<type> gemv <what> <rows>x<cols>"), and sets *n to the number of classes. */
+typedef struct {
+    char name[64];
+    int64_t launches;
+    double total_ms;          /* summed event-to-event time of the launches */
+    double bytes_per_launch;  /* weight blocks + 4*cols + 4*output rows */
+} l3p_kernel_stat;
+int l3p_profile(l3p_ctx* ctx, int on);
+int l3p_profile_read(l3p_ctx* ctx, l3p_kernel_stat* out, int cap, int* n);
+
 #ifdef __cplusplus
 }
 #endif

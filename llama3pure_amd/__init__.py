@@ -27,6 +27,7 @@ EXPORTS = [
     "l3p_dequant", "l3p_quantize_q8_0", "l3p_gemv", "l3p_gemm",
     "l3p_load_gguf", "l3p_get_model_info", "l3p_forward", "l3p_prefill", "l3p_decode",
     "l3p_sample", "l3p_logits_device", "l3p_copy_kv", "l3p_rope_row",
+    "l3p_profile", "l3p_profile_read",
 ]
 
 
@@ -46,6 +47,11 @@ class ModelInfo(C.Structure):
                                        "swa_pattern", "weight_type")] + \
                [(n, C.c_float) for n in ("rope_theta", "rope_theta_swa", "rms_eps", "final_softcap")] + \
                [("device_bytes", C.c_int64)]
+
+
+class KernelStat(C.Structure):
+    _fields_ = [("name", C.c_char * 64), ("launches", C.c_int64), ("total_ms", C.c_double),
+                ("bytes_per_launch", C.c_double)]
 
 
 class Sampler(C.Structure):
@@ -89,6 +95,8 @@ def lib() -> C.CDLL:
         "l3p_logits_device": (I, [P, C.POINTER(P)]),
         "l3p_copy_kv": (I, [P, I, I, P, SZ]),
         "l3p_rope_row": (I, [P, I, I, P, P]),
+        "l3p_profile": (I, [P, I]),
+        "l3p_profile_read": (I, [P, C.POINTER(KernelStat), I, C.POINTER(I)]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)
@@ -217,6 +225,19 @@ class Context:
         out = np.empty(n, np.uint8)
         self._check(self.L.l3p_copy_kv(self.h, layer, int(which_v), out.ctypes.data, n))
         return out
+
+    def profile(self, on: bool):
+        """Start (clearing earlier figures) or stop GEMV launch timing."""
+        self._check(self.L.l3p_profile(self.h, int(on)))
+
+    def profile_read(self):
+        """{label: (launches, total_ms, algorithmic bytes per launch)} of the timed GEMV launches."""
+        n = C.c_int(0)
+        self._check(self.L.l3p_profile_read(self.h, None, 0, C.byref(n)))
+        arr = (KernelStat * max(1, n.value))()
+        self._check(self.L.l3p_profile_read(self.h, arr, n.value, C.byref(n)))
+        return {arr[i].name.decode(): (arr[i].launches, arr[i].total_ms, arr[i].bytes_per_launch)
+                for i in range(n.value)}
 
     def rope_row(self, swa: bool, pos: int):
         import numpy as np

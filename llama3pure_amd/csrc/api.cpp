@@ -61,6 +61,7 @@ void l3p_destroy(l3p_ctx* c) {
     delete c->model;
     c->model = nullptr;
     c->scratch.release();
+    c->prof.release();
     hipStreamDestroy(c->stream);
     delete c;
 }
@@ -147,13 +148,12 @@ int l3p_gemv(l3p_ctx* c, int type, const void* w, int rows, int cols, const floa
         b.seg[0] = GemvSegment{(const uint8_t*)w, y, rows};
         b.nseg = 1;
         b.epilogue = EPI_STORE;
-        if (type == L3P_Q4_0) {
-            XQ8 xq = c->scratch.xq(cols);
-            launch_quantize_x(x, cols, xq, c->stream);
-            launch_gemv(type, b, cols, x, &xq, c->stream);
-        } else {
-            launch_gemv(type, b, cols, x, nullptr, c->stream);
-        }
+        XPrep xp;
+        xp.x = x;
+        xp.q8 = c->scratch.xq(cols);
+        xp.dig = c->scratch.xdig(cols);
+        prepare_x_form(type, cols, x, xp, c->stream);
+        launch_gemv(type, b, cols, xp, c->stream);
     });
 }
 
@@ -201,7 +201,17 @@ XQ8 Scratch::xq(int cols) {
     return q;
 }
 
+XDig Scratch::xdig(int cols) {
+    const size_t nb = (size_t)cols / 32;
+    xd_buf.ensure(nb * 128 + nb * 4 + 64);
+    XDig d;
+    d.dg = (int8_t*)xd_buf.p;
+    d.s = (float*)((char*)xd_buf.p + nb * 128);
+    return d;
+}
+
 void Scratch::release() {
+    xd_buf.release();
     xq_buf.release();
     gemm_buf.release();
 }

@@ -1,0 +1,120 @@
+// device_common.h — device helpers shared by the kernels of libl3p.
+#pragma once
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace l3pd {
+
+// fp16 -> fp32 (IEEE, exact).
+__device__ __forceinline__ float h2f(uint32_t h) {
+    return __half2float(__ushort_as_half((unsigned short)(h & 0xffffu)));
+}
+
+// fp16 -> fp32 exactly as the reference's table (c:547-582): NaN payloads are
+// kept without forcing the quiet bit.
+__device__ __forceinline__ float h2f_exact(uint32_t h) {
+    h &= 0xffffu;
+    if (((h >> 10) & 31u) == 31u)
+        return __uint_as_float(((h & 0x8000u) << 16) | 0x7f800000u | ((h & 0x3ffu) << 13));
+    return h2f(h);
+}
+
+// Truncating fp32 -> fp16 (c:585-599).
+__device__ __forceinline__ uint32_t f2h_trunc(float f) {
+    const uint32_t b = __float_as_uint(f);
+    const uint32_t sign = (b >> 16) & 0x8000u;
+    const int e = (int)((b >> 23) & 0xffu) - 112;
+    const uint32_t m = (b >> 13) & 0x3ffu;
+    if (e <= 0) {
+        if (e < -10) return sign;
+        return sign | ((m | 0x400u) >> (1 - e));
+    }
+    if (e >= 31) return sign | 0x7c00u;
+    return sign | ((uint32_t)e << 10) | m;
+}
+
+__device__ __forceinline__ uint32_t shr64(uint32_t lo, uint32_t hi, uint32_t sh) {
+    return (uint32_t)((((uint64_t)hi << 32) | lo) >> sh);
+}
+
+// fast_expf / fast_tanhf (c:3089-3106); the library is built with
+// -ffp-contract=off so these round exactly like the reference's C.
+__device__ __forceinline__ float ref_fast_expf(float x) {
+    if (x > 10.0f) return 22026.47f;
+    if (x < -10.0f) return 0.0f;
+    const float x2 = x * x;
+    const float x3 = x2 * x;
+    const float num = 120.0f + 60.0f * x + 12.0f * x2 + x3;
+    const float den = 120.0f - 60.0f * x + 12.0f * x2 - x3;
+    return num / den;
+}
+__device__ __forceinline__ float ref_fast_tanhf(float x) {
+    if (x < -4.0f) return -1.0f;
+    if (x > 4.0f) return 1.0f;
+    const float x2 = x * x;
+    return (x * (135135.0f + x2 * (17325.0f + x2 * (378.0f + x2)))) /
+           (135135.0f + x2 * (62370.0f + x2 * (3150.0f + 28.0f * x2)));
+}
+// SwiGLU (c:3400-3406) and GeGLU (c:3391-3398) of one gate/up pair.
+__device__ __forceinline__ float ref_swiglu(float g, float u) {
+    const float v = g * (1.0f / (1.0f + ref_fast_expf(-g)));
+    return v * u;
+}
+__device__ __forceinline__ float ref_geglu(float g, float u) {
+    const float x = 0.5f * g * (1.0f + ref_fast_tanhf(g * (0.7978845608f + 0.035677408137f * g * g)));
+    return x * u;
+}
+
+// Q8_0 quantization of 32 values (quantize_row_q8_0, c:1508-1528).
+struct QBlock {
+    uint32_t dh;   // truncated fp16 scale
+    int8_t q[32];
+    int sum;       // sum of quants
+};
+__device__ __forceinline__ void quantize32(const float* v, QBlock& o) {
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+        const float a = v[j] < 0 ? -v[j] : v[j];
+        if (a > amax) amax = a;
+    }
+    const float d = amax / 127.0f;
+    const float id = d > 0.0f ? 127.0f / amax : 0.0f;
+    o.dh = f2h_trunc(d);
+    int s = 0;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+        int qi = (int)roundf(v[j] * id);
+        qi = qi > 127 ? 127 : (qi < -128 ? -128 : qi);
+        o.q[j] = (int8_t)qi;
+        s += qi;
+    }
+    o.sum = s;
+}
+
+// Four int8 digits of 32 values against a power-of-two scale:
+// v = s * (d0 + d1/2^7 + d2/2^14 + d3/2^21) + r with |r| <= 2^-27 * max|v|,
+// where s = 2^(e-6) and max|v| < 2^e.  Every step is exact in fp32.
+__device__ __forceinline__ float digits32(const float* v, int8_t (*dg)[32]) {
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(v[j]));
+    int e = 0;
+    if (amax > 0.0f) frexpf(amax, &e);
+    const float up = amax > 0.0f ? ldexpf(1.0f, 6 - e) : 0.0f;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+        float r = v[j] * up;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float d = rintf(r);
+            dg[k][j] = (int8_t)(int)d;
+            r = (r - d) * 128.0f;
+        }
+    }
+    return amax > 0.0f ? ldexpf(1.0f, e - 6) : 0.0f;
+}
+
+}  // namespace l3pd

@@ -19,63 +19,14 @@
 // exactly and multiplied with fp32 x (matmul_deq_4row, c:2136-2176); Q4_0
 // takes x quantized to Q8_0 and exact integer block dots (c:1625-1643).
 // Only the fp32 summation order differs from the reference's sequential loop.
+#include "device_common.h"
 #include "internal.h"
-
-#include <hip/hip_fp16.h>
 
 namespace {
 
 constexpr int kMaxThreads = 1024;
 
-__device__ __forceinline__ float h2f(uint32_t h) {
-    return __half2float(__ushort_as_half((unsigned short)(h & 0xffffu)));
-}
-
-// fp16 -> fp32 exactly as the reference's table (c:547-582), NaN payload kept.
-__device__ __forceinline__ float h2f_exact(uint32_t h) {
-    h &= 0xffffu;
-    if (((h >> 10) & 31u) == 31u)
-        return __uint_as_float(((h & 0x8000u) << 16) | 0x7f800000u | ((h & 0x3ffu) << 13));
-    return h2f(h);
-}
-
-// Truncating fp32 -> fp16 (c:585-599).
-__device__ __forceinline__ uint32_t f2h_trunc(float f) {
-    uint32_t b = __float_as_uint(f);
-    uint32_t sign = (b >> 16) & 0x8000u;
-    int e = (int)((b >> 23) & 0xffu) - 112;
-    uint32_t m = (b >> 13) & 0x3ffu;
-    if (e <= 0) {
-        if (e < -10) return sign;
-        return sign | ((m | 0x400u) >> (1 - e));
-    }
-    if (e >= 31) return sign | 0x7c00u;
-    return sign | ((uint32_t)e << 10) | m;
-}
-
-__device__ __forceinline__ uint32_t shr64(uint32_t lo, uint32_t hi, uint32_t sh) {
-    return (uint32_t)((((uint64_t)hi << 32) | lo) >> sh);
-}
-
-// fast_expf / fast_tanhf of the reference (c:3089-3106).  The library is
-// built with -ffp-contract=off, so these evaluate with the reference's
-// roundings.
-__device__ __forceinline__ float ref_fast_expf(float x) {
-    if (x > 10.0f) return 22026.47f;
-    if (x < -10.0f) return 0.0f;
-    float x2 = x * x;
-    float x3 = x2 * x;
-    float num = 120.0f + 60.0f * x + 12.0f * x2 + x3;
-    float den = 120.0f - 60.0f * x + 12.0f * x2 - x3;
-    return num / den;
-}
-__device__ __forceinline__ float ref_fast_tanhf(float x) {
-    if (x < -4.0f) return -1.0f;
-    if (x > 4.0f) return 1.0f;
-    float x2 = x * x;
-    return (x * (135135.0f + x2 * (17325.0f + x2 * (378.0f + x2)))) /
-           (135135.0f + x2 * (62370.0f + x2 * (3150.0f + 28.0f * x2)));
-}
+using namespace l3pd;
 
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
@@ -149,15 +100,7 @@ __device__ __forceinline__ void finish(const GemvBatch& B, const TileLoc& L, flo
         }
         const int r = L.r0 + t;
         if (PAIR) {
-            float out;
-            if (B.epilogue == EPI_GEGLU) {
-                float g = 0.5f * a * (1.0f + ref_fast_tanhf(a * (0.7978845608f + 0.035677408137f * a * a)));
-                out = g * b;
-            } else {
-                float v = a * (1.0f / (1.0f + ref_fast_expf(-a)));
-                out = v * b;
-            }
-            B.seg[0].y[r] = out;
+            B.seg[0].y[r] = B.epilogue == EPI_GEGLU ? ref_geglu(a, b) : ref_swiglu(a, b);
         } else {
             float* y = B.seg[L.seg].y;
             if (B.epilogue == EPI_ADD) y[r] += a;
@@ -460,57 +403,35 @@ __global__ void __launch_bounds__(kMaxThreads) gemv_q6_k_kernel(GemvBatch B, int
 // ---------------------------------------------------------------------------
 // Activation quantization (quantize_row_q8_0, c:1508-1528), bit-exact.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ void quant_block(const float* __restrict__ xb, int8_t* q, uint32_t* dh,
-                                            int* qsum) {
-    float amax = 0.0f;
-    float v[32];
-#pragma unroll
-    for (int j = 0; j < 32; ++j) {
-        v[j] = xb[j];
-        float a = v[j] < 0 ? -v[j] : v[j];
-        if (a > amax) amax = a;
-    }
-    const float d = amax / 127.0f;
-    const float id = d > 0.0f ? 127.0f / amax : 0.0f;
-    *dh = f2h_trunc(d);
-    int s = 0;
-#pragma unroll
-    for (int j = 0; j < 32; ++j) {
-        int qi = (int)roundf(v[j] * id);
-        qi = qi > 127 ? 127 : (qi < -128 ? -128 : qi);
-        q[j] = (int8_t)qi;
-        s += qi;
-    }
-    *qsum = s;
-}
-
 __global__ void quantize_x_kernel(const float* __restrict__ x, int nb, XQ8 out) {
     const int b = blockIdx.x * blockDim.x + threadIdx.x;
     if (b >= nb) return;
-    int8_t q[32];
-    uint32_t dh;
-    int s;
-    quant_block(x + 32 * b, q, &dh, &s);
+    float v[32];
+#pragma unroll
+    for (int j = 0; j < 32; ++j) v[j] = x[32 * b + j];
+    QBlock qb;
+    quantize32(v, qb);
     int4* dst = reinterpret_cast<int4*>(out.qs + 32 * b);
-    const int* qi = reinterpret_cast<const int*>(q);
+    const int* qi = reinterpret_cast<const int*>(qb.q);
     dst[0] = make_int4(qi[0], qi[1], qi[2], qi[3]);
     dst[1] = make_int4(qi[4], qi[5], qi[6], qi[7]);
-    out.d[b] = h2f_exact(dh);
-    out.sum[b] = s;
+    out.d[b] = h2f_exact(qb.dh);
+    out.sum[b] = qb.sum;
 }
 
 __global__ void quantize_blocks_kernel(const float* __restrict__ x, int64_t nb, uint8_t* __restrict__ dst) {
     const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (b >= nb) return;
-    int8_t q[32];
-    uint32_t dh;
-    int s;
-    quant_block(x + 32 * b, q, &dh, &s);
-    uint8_t* o = dst + 34 * b;
-    o[0] = (uint8_t)(dh & 0xff);
-    o[1] = (uint8_t)(dh >> 8);
+    float v[32];
 #pragma unroll
-    for (int j = 0; j < 32; ++j) o[2 + j] = (uint8_t)q[j];
+    for (int j = 0; j < 32; ++j) v[j] = x[32 * b + j];
+    QBlock qb;
+    quantize32(v, qb);
+    uint8_t* o = dst + 34 * b;
+    o[0] = (uint8_t)(qb.dh & 0xff);
+    o[1] = (uint8_t)(qb.dh >> 8);
+#pragma unroll
+    for (int j = 0; j < 32; ++j) o[2 + j] = (uint8_t)qb.q[j];
 }
 
 // ---------------------------------------------------------------------------
@@ -623,7 +544,9 @@ Shape shape_of(int type, int cols) {
 }
 
 template <int R, bool PAIR>
-void launch_typed(int type, const GemvBatch& b, int cols, const float* x, const XQ8* xq, hipStream_t st) {
+void launch_typed(int type, const GemvBatch& b, int cols, const XPrep& xp, hipStream_t st) {
+    const float* x = xp.x;
+    const XQ8* xq = &xp.q8;
     const Shape sh = shape_of(type, cols);
     const int nrr = PAIR ? 2 * R : R;
     const size_t lds = ((size_t)(PAIR ? 2 : 1) * R * sh.rb + 15) / 16 * 16 + (size_t)(sh.threads / 64) * nrr * 4;
@@ -669,20 +592,38 @@ bool gemv_supported(int type, int cols) {
     }
 }
 
-void launch_gemv(int type, const GemvBatch& b, int cols, const float* x, const XQ8* xq, hipStream_t st) {
+int gemv_input_form(int type, int cols) {
+    if (type == L3P_Q4_0) return 1;
+    if (type == L3P_Q8_0 && gemv2_supported(type, cols)) return 2;
+    return 0;
+}
+
+void launch_gemv(int type, const GemvBatch& b, int cols, const XPrep& xp, hipStream_t st) {
     L3P_REQUIRE(gemv_supported(type, cols), L3P_E_UNSUPPORTED, "gemv: type %d with %d columns not supported",
                 type, cols);
-    L3P_REQUIRE(type != L3P_Q4_0 || xq, L3P_E_INVALID, "gemv: Q4_0 needs the quantized activation");
+    if (gemv2_supported(type, cols)) {
+        launch_gemv2(type, b, cols, xp, st);
+        return;
+    }
+    L3P_REQUIRE(type != L3P_Q4_0 || xp.q8.qs, L3P_E_INVALID, "gemv: Q4_0 needs the quantized activation");
     const size_t rb = type_row_bytes(type, cols);
     const bool pair = b.pair != 0;
     // Rows per tile: keep the LDS tile within 64 KB.
     const size_t tile_rows_budget = 65536 / ((pair ? 2 : 1) * rb);
     if (tile_rows_budget >= 4) {
-        pair ? launch_typed<4, true>(type, b, cols, x, xq, st) : launch_typed<4, false>(type, b, cols, x, xq, st);
+        pair ? launch_typed<4, true>(type, b, cols, xp, st) : launch_typed<4, false>(type, b, cols, xp, st);
     } else if (tile_rows_budget >= 2) {
-        pair ? launch_typed<2, true>(type, b, cols, x, xq, st) : launch_typed<2, false>(type, b, cols, x, xq, st);
+        pair ? launch_typed<2, true>(type, b, cols, xp, st) : launch_typed<2, false>(type, b, cols, xp, st);
     } else {
-        pair ? launch_typed<1, true>(type, b, cols, x, xq, st) : launch_typed<1, false>(type, b, cols, x, xq, st);
+        pair ? launch_typed<1, true>(type, b, cols, xp, st) : launch_typed<1, false>(type, b, cols, xp, st);
+    }
+}
+
+void prepare_x_form(int type, int cols, const float* x, const XPrep& xp, hipStream_t st) {
+    switch (gemv_input_form(type, cols)) {
+    case 1: launch_quantize_x(x, cols, xp.q8, st); break;
+    case 2: launch_x_digits(x, cols, xp.dig, st); break;
+    default: break;
     }
 }
 

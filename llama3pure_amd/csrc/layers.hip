@@ -4,45 +4,14 @@
 // sampler.  Arithmetic follows llama3pure-c-engine.c (cited per kernel); the
 // library is built with -ffp-contract=off so elementwise expressions round
 // exactly as the reference's scalar C does.
+#include "device_common.h"
 #include "model.h"
-
-#include <hip/hip_fp16.h>
 
 namespace {
 
 constexpr int kTC = 64;   // positions per attention chunk (one per lane)
 
-__device__ __forceinline__ float h2f(uint32_t h) {
-    return __half2float(__ushort_as_half((unsigned short)(h & 0xffffu)));
-}
-__device__ __forceinline__ float h2f_exact(uint32_t h) {
-    h &= 0xffffu;
-    if (((h >> 10) & 31u) == 31u)
-        return __uint_as_float(((h & 0x8000u) << 16) | 0x7f800000u | ((h & 0x3ffu) << 13));
-    return h2f(h);
-}
-__device__ __forceinline__ uint32_t f2h_trunc(float f) {   // c:585-599
-    uint32_t b = __float_as_uint(f);
-    uint32_t sign = (b >> 16) & 0x8000u;
-    int e = (int)((b >> 23) & 0xffu) - 112;
-    uint32_t m = (b >> 13) & 0x3ffu;
-    if (e <= 0) {
-        if (e < -10) return sign;
-        return sign | ((m | 0x400u) >> (1 - e));
-    }
-    if (e >= 31) return sign | 0x7c00u;
-    return sign | ((uint32_t)e << 10) | m;
-}
-__device__ __forceinline__ uint32_t shr64(uint32_t lo, uint32_t hi, uint32_t sh) {
-    return (uint32_t)((((uint64_t)hi << 32) | lo) >> sh);
-}
-__device__ __forceinline__ float ref_fast_tanhf(float x) {   // c:3089-3095
-    if (x < -4.0f) return -1.0f;
-    if (x > 4.0f) return 1.0f;
-    float x2 = x * x;
-    return (x * (135135.0f + x2 * (17325.0f + x2 * (378.0f + x2)))) /
-           (135135.0f + x2 * (62370.0f + x2 * (3150.0f + 28.0f * x2)));
-}
+using namespace l3pd;
 
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
@@ -67,33 +36,6 @@ __device__ float block_sum(float v, float* sh) {
     return s;
 }
 
-// Q8_0 quantization of 32 values (quantize_row_q8_0, c:1508-1528): truncated
-// fp16 scale d = amax/127, q = roundf(x * (127/amax)).
-struct QBlock {
-    uint32_t dh;
-    int8_t q[32];
-    int sum;
-};
-__device__ __forceinline__ void quantize32(const float* v, QBlock& o) {
-    float amax = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 32; ++j) {
-        float a = v[j] < 0 ? -v[j] : v[j];
-        if (a > amax) amax = a;
-    }
-    const float d = amax / 127.0f;
-    const float id = d > 0.0f ? 127.0f / amax : 0.0f;
-    o.dh = f2h_trunc(d);
-    int s = 0;
-#pragma unroll
-    for (int j = 0; j < 32; ++j) {
-        int qi = (int)roundf(v[j] * id);
-        qi = qi > 127 ? 127 : (qi < -128 ? -128 : qi);
-        o.q[j] = (int8_t)qi;
-        s += qi;
-    }
-    o.sum = s;
-}
 __device__ __forceinline__ void store_block34(uint8_t* dst, const QBlock& b) {
     dst[0] = (uint8_t)(b.dh & 0xff);
     dst[1] = (uint8_t)(b.dh >> 8);
@@ -103,12 +45,13 @@ __device__ __forceinline__ void store_block34(uint8_t* dst, const QBlock& b) {
 
 // ---------------------------------------------------------------------------
 // RMSNorm (c:3117-3129), optional fused embedding scale (Gemma first layer,
-// c:3132-3148) and optional Q8_0 quantization of the output for the integer
-// GEMV path.  One workgroup.
+// c:3132-3148), and the output also written in the form the next GEMV
+// consumes (form 1: Q8_0 for Q4_0 weights; form 2: digits for Q8_0 weights).
+// One workgroup.
 // ---------------------------------------------------------------------------
 __global__ void __launch_bounds__(1024) rmsnorm_kernel(const float* __restrict__ xin, float* xscale, float scale,
                                                        const float* __restrict__ w, int n, float inv_n, float eps,
-                                                       float* out, XQ8 xq, int do_q) {
+                                                       float* out, XQ8 xq, XDig xd, int form) {
     __shared__ float sh[16];
     const int t = threadIdx.x, nt = blockDim.x;
     float ss = 0.0f;
@@ -130,13 +73,26 @@ __global__ void __launch_bounds__(1024) rmsnorm_kernel(const float* __restrict__
         for (int j = 0; j < 32; ++j) o[j] = w[32 * b + j] * (r * xs[32 * b + j]);
 #pragma unroll
         for (int j = 0; j < 32; ++j) out[32 * b + j] = o[j];
-        if (do_q) {
+        if (form == 1) {
             QBlock qb;
             quantize32(o, qb);
-#pragma unroll
-            for (int j = 0; j < 32; ++j) xq.qs[32 * b + j] = qb.q[j];
+            int4* dq = reinterpret_cast<int4*>(xq.qs + 32 * b);
+            const int* qi = reinterpret_cast<const int*>(qb.q);
+            dq[0] = make_int4(qi[0], qi[1], qi[2], qi[3]);
+            dq[1] = make_int4(qi[4], qi[5], qi[6], qi[7]);
             xq.d[b] = h2f_exact(qb.dh);
             xq.sum[b] = qb.sum;
+        } else if (form == 2) {
+            int8_t dg[4][32];
+            const float sc = digits32(o, dg);
+            int4* dd = reinterpret_cast<int4*>(xd.dg + 128 * b);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int* p = reinterpret_cast<const int*>(dg[k]);
+                dd[2 * k] = make_int4(p[0], p[1], p[2], p[3]);
+                dd[2 * k + 1] = make_int4(p[4], p[5], p[6], p[7]);
+            }
+            xd.s[b] = sc;
         }
     }
 }
@@ -247,8 +203,9 @@ __global__ void __launch_bounds__(64) rope_kv_kernel(RopeArgs a) {
 struct AttnKArgs {
     const int8_t* qq;
     const float* qd;
-    const uint8_t* kc;
-    const uint8_t* vc;
+    const uint8_t* kc;      // allocation base of the K cache (256-byte aligned)
+    const uint8_t* vc;      // allocation base of the V cache
+    size_t layer_off;       // byte offset of this layer in both caches
     float* att;
     float* part_acc;
     unsigned* counters;
@@ -266,16 +223,18 @@ __global__ void __launch_bounds__(1024) attn_scores_kernel(AttnKArgs a) {
     const int i = c * kTC + lane;         // position index relative to t0
     if (i < a.na) {
         const int t = a.t0 + i;
-        const uint8_t* row = a.kc + (size_t)g * a.head_seq + (size_t)t * a.hq8;
-        const uint32_t* rw = reinterpret_cast<const uint32_t*>(row);   // rows are 4-byte aligned
+        // absolute byte offset of the K row from the (256-byte aligned) cache base
+        const size_t rowoff = a.layer_off + (size_t)g * a.head_seq + (size_t)t * a.hq8;
+        const uint32_t* cw = reinterpret_cast<const uint32_t*>(a.kc);
         const int8_t* qh = a.qq + (size_t)h * a.hs;
         float sum = 0.0f;
         for (int b = 0; b < nb; ++b) {
-            const uint32_t off = 34u * b;
-            const uint32_t E = off >> 2, sh = (off & 2u) ? 32u : 16u;
+            const size_t off = rowoff + 34u * b;
+            const size_t E = off >> 2;
+            const uint32_t sh = (off & 2u) ? 32u : 16u;
             uint32_t dw[9];
 #pragma unroll
-            for (int k = 0; k < 9; ++k) dw[k] = rw[E + k];
+            for (int k = 0; k < 9; ++k) dw[k] = cw[E + k];
             const float db = h2f(dw[0] >> ((off & 2u) ? 16u : 0u));
             const int4* qp = reinterpret_cast<const int4*>(qh + 32 * b);
             const int4 qa = qp[0], qb4 = qp[1];
@@ -317,16 +276,18 @@ __global__ void __launch_bounds__(1024) attn_values_kernel(AttnKArgs a) {
     const int g = blockIdx.x, c = blockIdx.y;
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int h = g * a.kv_mul + w;
-    const int per = a.hs / 64;                 // outputs per lane (2 or 4)
+    const int per = (a.hs + 63) / 64;          // outputs per lane (1, 2 or 4)
     const int i0 = lane * per;                 // first output element of this lane
-    const int b = i0 >> 5;                     // its 32-block
+    const bool act = i0 < a.hs;
+    const int b = act ? i0 >> 5 : 0;           // its 32-block
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     const float* att = a.att + (size_t)h * a.seq;
-    const uint8_t* vbase = a.vc + (size_t)g * a.head_seq + 34 * b;
+    const uint8_t* vbase = a.vc + a.layer_off + (size_t)g * a.head_seq + 34 * b;
     const int jbeg = c * kTC, jend = min(a.na, jbeg + kTC);
     for (int j = jbeg; j < jend; ++j) {
         const float wt = att[j];
         if (wt > -1e-8f && wt < 1e-8f) continue;
+        if (!act) continue;
         const uint8_t* blk = vbase + (size_t)(a.t0 + j) * a.hq8;
         const float scale = h2f((uint32_t)blk[0] | ((uint32_t)blk[1] << 8)) * wt;
         const int8_t* qs = reinterpret_cast<const int8_t*>(blk + 2 + (i0 & 31));
@@ -334,23 +295,27 @@ __global__ void __launch_bounds__(1024) attn_values_kernel(AttnKArgs a) {
     }
     float* out = a.out + (size_t)h * a.hs + i0;
     if (a.n_chunks == 1) {
-        for (int e = 0; e < per; ++e) out[e] = acc[e];
+        if (act)
+            for (int e = 0; e < per; ++e) out[e] = acc[e];
         return;
     }
     float* pa = a.part_acc + ((size_t)h * a.n_chunks + c) * a.hs + i0;
-    for (int e = 0; e < per; ++e) pa[e] = acc[e];
+    if (act)
+        for (int e = 0; e < per; ++e) pa[e] = acc[e];
     __threadfence();
     __syncthreads();
     if (threadIdx.x == 0) last = atomicAdd(&a.counters[g], 1u) == (unsigned)(a.n_chunks - 1);
     __syncthreads();
     if (!last) return;
     __threadfence();
-    float tot[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int cc = 0; cc < a.n_chunks; ++cc) {
-        const float* p = a.part_acc + ((size_t)h * a.n_chunks + cc) * a.hs + i0;
-        for (int e = 0; e < per; ++e) tot[e] += p[e];
+    if (act) {
+        float tot[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int cc = 0; cc < a.n_chunks; ++cc) {
+            const float* p = a.part_acc + ((size_t)h * a.n_chunks + cc) * a.hs + i0;
+            for (int e = 0; e < per; ++e) tot[e] += p[e];
+        }
+        for (int e = 0; e < per; ++e) out[e] = tot[e];
     }
-    for (int e = 0; e < per; ++e) out[e] = tot[e];
     __syncthreads();
     if (threadIdx.x == 0) a.counters[g] = 0;
 }
@@ -404,87 +369,95 @@ __global__ void argmax_final_kernel(const float* cv, const int* ci, int nc, int*
     if (threadIdx.x == 0) *out = bi == 0x7fffffff ? 0 : bi;
 }
 
-// Top-k / temperature / top-p (c:4803-4907).  Stage 1 sorts chunks of 1024
-// logits in LDS (value descending, index ascending) and keeps each chunk's
-// best k; stage 2 sorts the candidates and runs the reference's sampling
-// arithmetic on the best k in descending order.
-constexpr int kChunk = 1024;
-constexpr int kMaxK = 128;
+// Top-k selection exactly as generate_token performs it (c:4818-4848): the
+// k slots start as logits[0..k); scanning i = k..n-1, logits[i] replaces the
+// slot holding the current minimum (the lowest slot among equal minima) when
+// it is strictly greater.  The final slot order matters to the reference's
+// later arithmetic (its pre-sort sum and, with top_p >= 1, its CDF walk), so
+// it is reproduced, not just the top-k set.  Kernel 1 computes the maximum of
+// every group of 64 logits (indices >= k); kernel 2, one wave, walks the
+// groups in order and only visits groups whose maximum beats the current
+// minimum.
+constexpr int kSlotsPerLane = 16;            // k <= 1024
 
-__device__ void bitonic_sort_desc(float* v, int* id, int n) {   // n power of two
-    for (int size = 2; size <= n; size <<= 1) {
-        for (int stride = size >> 1; stride > 0; stride >>= 1) {
-            __syncthreads();
-            for (int i = threadIdx.x; i < n / 2; i += blockDim.x) {
-                const int lo = 2 * i - (i & (stride - 1));
-                const int hi = lo + stride;
-                const bool desc = ((lo & size) == 0);
-                const bool swap = desc ? better(v[hi], id[hi], v[lo], id[lo]) : better(v[lo], id[lo], v[hi], id[hi]);
-                if (swap) {
-                    float tv = v[lo]; v[lo] = v[hi]; v[hi] = tv;
-                    int ti = id[lo]; id[lo] = id[hi]; id[hi] = ti;
+__global__ void __launch_bounds__(1024) topk_groupmax_kernel(const float* __restrict__ l, int n, int k, int ng,
+                                                             float* gmax) {
+    const int g = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int i = 64 * g + lane;
+    float v = (i >= k && i < n) ? l[i] : -INFINITY;
+    v = wave_max(v);
+    if (lane == 0 && g < ng) gmax[g] = v;
+}
+
+__device__ __forceinline__ bool slot_less(float v, int s, float bv, int bs) {
+    return v < bv || (v == bv && s < bs);
+}
+
+__global__ void __launch_bounds__(64) topk_scan_kernel(const float* __restrict__ l, int n, int k,
+                                                       const float* __restrict__ gmax, int ng, float* out_v,
+                                                       int* out_i) {
+    const int lane = threadIdx.x;
+    float sv[kSlotsPerLane];
+    int si[kSlotsPerLane];
+#pragma unroll
+    for (int j = 0; j < kSlotsPerLane; ++j) {
+        const int s = lane + 64 * j;
+        sv[j] = s < k ? l[s] : INFINITY;
+        si[j] = s < k ? s : -1;
+    }
+    // current minimum over slots: (value, slot) with the lowest slot on ties
+    auto find_min = [&](float& mv, int& ms) {
+        float bv = INFINITY;
+        int bs = 0x7fffffff;
+#pragma unroll
+        for (int j = 0; j < kSlotsPerLane; ++j) {
+            const int s = lane + 64 * j;
+            if (s < k && slot_less(sv[j], s, bv, bs)) { bv = sv[j]; bs = s; }
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            const float ov = __shfl_xor(bv, o, 64);
+            const int os = __shfl_xor(bs, o, 64);
+            if (slot_less(ov, os, bv, bs)) { bv = ov; bs = os; }
+        }
+        mv = bv;
+        ms = bs;
+    };
+    float cur;
+    int cur_slot;
+    find_min(cur, cur_slot);
+    for (int g0 = 0; g0 < ng; g0 += 64) {
+        const float gm = (g0 + lane < ng) ? gmax[g0 + lane] : -INFINITY;
+        uint64_t flagged = __ballot(gm > cur);
+        while (flagged) {
+            const int j = __ffsll((unsigned long long)flagged) - 1;
+            flagged &= flagged - 1;
+            if (!(__shfl(gm, j, 64) > cur)) continue;
+            const int base = 64 * (g0 + j);
+            const int i = base + lane;
+            const float v = (i >= k && i < n) ? l[i] : -INFINITY;
+            uint64_t cand = __ballot(v > cur);
+            while (cand) {
+                const int c = __ffsll((unsigned long long)cand) - 1;
+                cand &= cand - 1;
+                const float bv = __shfl(v, c, 64);
+                if (bv > cur) {
+                    if (lane == (cur_slot & 63)) {
+#pragma unroll
+                        for (int jj = 0; jj < kSlotsPerLane; ++jj)
+                            if (jj == (cur_slot >> 6)) { sv[jj] = bv; si[jj] = base + c; }
+                    }
+                    find_min(cur, cur_slot);
                 }
             }
         }
     }
-    __syncthreads();
-}
-
-__global__ void __launch_bounds__(1024) topk_stage1_kernel(const float* __restrict__ l, int n, int k, float* cv, int* ci) {
-    __shared__ float v[kChunk];
-    __shared__ int id[kChunk];
-    const int base = blockIdx.x * kChunk;
-    for (int i = threadIdx.x; i < kChunk; i += blockDim.x) {
-        const int gi = base + i;
-        v[i] = gi < n ? l[gi] : -INFINITY;
-        id[i] = gi < n ? gi : 0x7fffffff;
+#pragma unroll
+    for (int j = 0; j < kSlotsPerLane; ++j) {
+        const int s = lane + 64 * j;
+        if (s < k) { out_v[s] = sv[j]; out_i[s] = si[j]; }
     }
-    bitonic_sort_desc(v, id, kChunk);
-    for (int i = threadIdx.x; i < k; i += blockDim.x) {
-        cv[blockIdx.x * k + i] = v[i];
-        ci[blockIdx.x * k + i] = id[i];
-    }
-}
-
-__global__ void __launch_bounds__(1024) topk_stage2_kernel(const float* cv, const int* ci, int nc, int np2, int k,
-                                                           float temperature, float top_p, float r, int* out) {
-    extern __shared__ float smem[];
-    float* v = smem;
-    int* id = reinterpret_cast<int*>(smem + np2);
-    for (int i = threadIdx.x; i < np2; i += blockDim.x) {
-        v[i] = i < nc ? cv[i] : -INFINITY;
-        id[i] = i < nc ? ci[i] : 0x7fffffff;
-    }
-    bitonic_sort_desc(v, id, np2);
-    if (threadIdx.x != 0) return;
-    // the reference's arithmetic on the k best, in descending order
-    const float inv_t = 1.0f / temperature;
-    const float max_vt = v[0] * inv_t;
-    float sum = 0.0f;
-    for (int i = 0; i < k; ++i) {
-        const float e = expf(v[i] * inv_t - max_vt);
-        v[i] = e;
-        sum += e;
-    }
-    int keep = k;
-    if (top_p < 1.0f) {
-        float cum = 0.0f;
-        const float thr = top_p * sum;
-        for (int i = 0; i < k; ++i) {
-            cum += v[i];
-            if (cum >= thr) { keep = i + 1; break; }
-        }
-        sum = 0.0f;
-        for (int i = 0; i < keep; ++i) sum += v[i];
-    }
-    const float rr = r * sum;
-    float cdf = 0.0f;
-    int s = keep - 1;
-    for (int i = 0; i < keep; ++i) {
-        cdf += v[i];
-        if (rr < cdf) { s = i; break; }
-    }
-    *out = id[s];
 }
 
 }  // namespace
@@ -497,10 +470,11 @@ void launch_embed(const Mat& emb, int token, float* x, hipStream_t s) {
 }
 
 void launch_rmsnorm(const float* xin, float* xscale, float scale, const float* w, int n, float inv_n, float eps,
-                    float* out, const XQ8* xq, hipStream_t s) {
-    XQ8 q = xq ? *xq : XQ8{};
-    hipLaunchKernelGGL(rmsnorm_kernel, dim3(1), dim3(1024), 0, s, xin, xscale, scale, w, n, inv_n, eps, out, q,
-                       xq ? 1 : 0);
+                    float* out, const XPrep* xp, int form, hipStream_t s) {
+    const XQ8 q = xp ? xp->q8 : XQ8{};
+    const XDig d = xp ? xp->dig : XDig{};
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(1), dim3(1024), 0, s, xin, xscale, scale, w, n, inv_n, eps, out, q, d,
+                       xp ? form : 0);
     L3P_HIP(hipGetLastError());
 }
 
@@ -544,6 +518,7 @@ void launch_attention(const AttnArgs& x, hipStream_t s) {
     a.qd = x.qd;
     a.kc = x.kc;
     a.vc = x.vc;
+    a.layer_off = x.layer_off;
     a.att = x.att;
     a.part_acc = x.part_acc;
     a.counters = x.counters;
@@ -569,8 +544,8 @@ void launch_softcap(float* l, int n, float cap, hipStream_t s) {
     L3P_HIP(hipGetLastError());
 }
 
-int sample_num_blocks(int n) { return (n + kChunk - 1) / kChunk; }
-int sample_candidates_per_block() { return kMaxK; }
+int sample_groups(int n) { return (n + 63) / 64; }
+int sample_max_k() { return 64 * kSlotsPerLane; }
 
 void launch_argmax(const float* l, int n, int* out, hipStream_t s, float* cv, int* ci) {
     const int nb = 256;
@@ -580,19 +555,12 @@ void launch_argmax(const float* l, int n, int* out, hipStream_t s, float* cv, in
     L3P_HIP(hipGetLastError());
 }
 
-void launch_sample_topk(const float* l, int n, float temperature, int k, float top_p, float r, float* cv, int* ci,
-                        int* out, hipStream_t s) {
-    L3P_REQUIRE(k >= 1 && k <= kMaxK, L3P_E_UNSUPPORTED, "sampler: top_k=%d outside [1, %d]", k, kMaxK);
-    const int nb = sample_num_blocks(n);
-    hipLaunchKernelGGL(topk_stage1_kernel, dim3(nb), dim3(1024), 0, s, l, n, k, cv, ci);
+void launch_topk_slots(const float* l, int n, int k, float* gmax, float* out_v, int* out_i, hipStream_t s) {
+    L3P_REQUIRE(k >= 1 && k <= 64 * kSlotsPerLane && k <= n, L3P_E_UNSUPPORTED, "sampler: top_k=%d outside [1, %d]",
+                k, 64 * kSlotsPerLane);
+    const int ng = sample_groups(n);
+    hipLaunchKernelGGL(topk_groupmax_kernel, dim3((ng + 15) / 16), dim3(1024), 0, s, l, n, k, ng, gmax);
     L3P_HIP(hipGetLastError());
-    const int nc = nb * k;
-    int np2 = 1;
-    while (np2 < nc) np2 <<= 1;
-    const size_t lds = (size_t)np2 * 8;
-    L3P_REQUIRE(lds <= 160 * 1024, L3P_E_UNSUPPORTED, "sampler: %d candidates exceed LDS", nc);
-    if (lds > 65536)
-        L3P_HIP(hipFuncSetAttribute((const void*)topk_stage2_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-    hipLaunchKernelGGL(topk_stage2_kernel, dim3(1), dim3(1024), lds, s, cv, ci, nc, np2, k, temperature, top_p, r, out);
+    hipLaunchKernelGGL(topk_scan_kernel, dim3(1), dim3(64), 0, s, l, n, k, gmax, ng, out_v, out_i);
     L3P_HIP(hipGetLastError());
 }

@@ -30,6 +30,8 @@ void* Model::dalloc(size_t bytes) {
 Model::~Model() {
     for (void* p : allocs) hipFree(p);
     if (out_token_host) hipHostFree(out_token_host);
+    if (slot_val_host) hipHostFree(slot_val_host);
+    if (slot_idx_host) hipHostFree(slot_idx_host);
 }
 
 // ---------------------------------------------------------------------------
@@ -265,7 +267,8 @@ static Model* load_model(l3p_ctx* c, const void* bytes, size_t len, const l3p_lo
                 "GGUF: bad dimensions");
     L3P_REQUIRE(m.n_kv > 0 && m.n_heads % m.n_kv == 0, L3P_E_UNSUPPORTED, "n_heads %d not a multiple of n_kv %d",
                 m.n_heads, m.n_kv);
-    L3P_REQUIRE(m.hs % 64 == 0 && m.hs <= 256, L3P_E_UNSUPPORTED, "head_dim %d unsupported (need 64..256, /64)", m.hs);
+    L3P_REQUIRE(m.hs % 32 == 0 && m.hs >= 32 && m.hs <= 256, L3P_E_UNSUPPORTED,
+                "head_dim %d unsupported (need a multiple of 32 up to 256)", m.hs);
     L3P_REQUIRE(m.n_heads / m.n_kv <= 16, L3P_E_UNSUPPORTED, "GQA group of %d heads unsupported", m.n_heads / m.n_kv);
     m.kv_dim = m.n_kv * m.hs;
     m.q_dim = m.n_heads * m.hs;
@@ -396,16 +399,20 @@ static Model* load_model(l3p_ctx* c, const void* bytes, size_t len, const l3p_lo
     m.xq.qs = (int8_t*)m.dalloc((size_t)maxin);
     m.xq.d = (float*)m.dalloc((size_t)maxin / 32 * 4);
     m.xq.sum = (int32_t*)m.dalloc((size_t)maxin / 32 * 4);
+    m.xd.dg = (int8_t*)m.dalloc((size_t)maxin / 32 * 128);
+    m.xd.s = (float*)m.dalloc((size_t)maxin / 32 * 4);
     m.att = (float*)m.dalloc((size_t)m.n_heads * m.seq_len * 4);
     m.max_chunks = (m.seq_len + 63) / 64;
     m.part_acc = (float*)m.dalloc((size_t)m.n_heads * m.max_chunks * m.hs * 4);
     m.counters = (unsigned*)m.dalloc((size_t)m.n_kv * sizeof(unsigned));
     L3P_HIP(hipMemsetAsync(m.counters, 0, (size_t)m.n_kv * sizeof(unsigned), s));
-    const int ncand = std::max(256, sample_num_blocks(m.vocab) * sample_candidates_per_block());
+    const int ncand = std::max(256, sample_groups(m.vocab)) + sample_max_k();
     m.cand_val = (float*)m.dalloc((size_t)ncand * 4);
-    m.cand_idx = (int*)m.dalloc((size_t)ncand * 4);
+    m.cand_idx = (int*)m.dalloc((size_t)std::max(256, sample_max_k()) * 4);
     m.out_token = (int*)m.dalloc(16);
     L3P_HIP(hipHostMalloc((void**)&m.out_token_host, 16, hipHostMallocDefault));
+    L3P_HIP(hipHostMalloc((void**)&m.slot_val_host, (size_t)sample_max_k() * 4, hipHostMallocDefault));
+    L3P_HIP(hipHostMalloc((void**)&m.slot_idx_host, (size_t)sample_max_k() * 4, hipHostMallocDefault));
     L3P_HIP(hipStreamSynchronize(s));
     return mp.release();
 }
@@ -413,17 +420,110 @@ static Model* load_model(l3p_ctx* c, const void* bytes, size_t len, const l3p_lo
 // ---------------------------------------------------------------------------
 // forward (transformer, c:3190-3435)
 // ---------------------------------------------------------------------------
-static void gemv_into(const Model& m, const Mat& W, const float* x, float* y, int epi, hipStream_t s) {
+void prepare_x(int type, int cols, const float* x, const XPrep& xp, hipStream_t s) {
+    prepare_x_form(type, cols, x, xp, s);
+}
+
+// ---------------------------------------------------------------------------
+// GEMV launch timing
+// ---------------------------------------------------------------------------
+hipEvent_t Profiler::event() {
+    if (!pool.empty()) {
+        hipEvent_t e = pool.back();
+        pool.pop_back();
+        return e;
+    }
+    hipEvent_t e;
+    L3P_HIP(hipEventCreate(&e));
+    return e;
+}
+int Profiler::stat(const std::string& name, double bytes) {
+    for (size_t i = 0; i < stats.size(); ++i)
+        if (stats[i].name == name) return (int)i;
+    Stat st;
+    st.name = name;
+    st.bytes = bytes;
+    stats.push_back(st);
+    return (int)stats.size() - 1;
+}
+void Profiler::collect() {
+    for (const Pending& q : pending) {
+        float ms = 0.0f;
+        if (hipEventElapsedTime(&ms, q.a, q.b) == hipSuccess) {
+            stats[q.stat].ms += ms;
+            stats[q.stat].launches += 1;
+        }
+        pool.push_back(q.a);
+        pool.push_back(q.b);
+    }
+    pending.clear();
+}
+void Profiler::reset() {
+    for (const Pending& q : pending) {
+        pool.push_back(q.a);
+        pool.push_back(q.b);
+    }
+    pending.clear();
+    stats.clear();
+}
+void Profiler::release() {
+    reset();
+    for (hipEvent_t e : pool) hipEventDestroy(e);
+    pool.clear();
+}
+ProfRange::ProfRange(Profiler& pr, hipStream_t stream, const std::string& name, double bytes) {
+    if (!pr.on) return;
+    p = &pr;
+    s = stream;
+    st = pr.stat(name, bytes);
+    a = pr.event();
+    b = pr.event();
+    L3P_HIP(hipEventRecord(a, s));
+}
+ProfRange::~ProfRange() {
+    if (!p) return;
+    if (hipEventRecord(b, s) == hipSuccess) p->pending.push_back({st, a, b});
+    else {
+        p->pool.push_back(a);
+        p->pool.push_back(b);
+    }
+}
+
+static const char* type_name(int t) {
+    switch (t) {
+    case L3P_Q4_0: return "q4_0";
+    case L3P_Q8_0: return "q8_0";
+    case L3P_Q4_K: return "q4_k";
+    case L3P_Q6_K: return "q6_k";
+    case L3P_F16: return "f16";
+    case L3P_BF16: return "bf16";
+    case L3P_F32: return "f32";
+    default: return "other";
+    }
+}
+
+// Timing label "<type> gemv <what> <rows>x<cols>" and the algorithmic bytes of
+// one launch: the weight blocks, the fp32 input and the fp32 outputs.
+static std::string gemv_label(const char* what, int type, int rows, int cols) {
+    char b[96];
+    snprintf(b, sizeof b, "%s gemv %s %dx%d", type_name(type), what, rows, cols);
+    return b;
+}
+static double gemv_bytes(int type, int rows, int cols, int out_rows) {
+    return (double)rows * (double)type_row_bytes(type, cols) + 4.0 * cols + 4.0 * out_rows;
+}
+
+static void gemv_into(l3p_ctx* c, const Mat& W, const float* x, float* y, int epi, const char* what) {
+    const Model& m = *c->model;
+    hipStream_t s = c->stream;
     GemvBatch b{};
     b.seg[0] = GemvSegment{W.w, y, W.rows};
     b.nseg = 1;
     b.epilogue = epi;
-    if (q8_class(W.type)) {
-        launch_quantize_x(x, W.cols, m.xq, s);
-        launch_gemv(W.type, b, W.cols, x, &m.xq, s);
-    } else {
-        launch_gemv(W.type, b, W.cols, x, nullptr, s);
-    }
+    const XPrep xp = m.prep(x);
+    prepare_x(W.type, W.cols, x, xp, s);
+    ProfRange r(c->prof, s, gemv_label(what, W.type, W.rows, W.cols), gemv_bytes(W.type, W.rows, W.cols, W.rows));
+    launch_gemv(W.type, b, W.cols, xp, s);
 }
 
 static void forward_impl(l3p_ctx* c, int token, int pos, bool with_logits) {
@@ -433,12 +533,14 @@ static void forward_impl(l3p_ctx* c, int token, int pos, bool with_logits) {
     launch_embed(m.emb, token, m.x, s);                          // c:3204-3207
     for (int l = 0; l < m.n_layers; ++l) {
         const Layer& L = m.layers[l];
-        const bool qkv_q8 = q8_class(L.wq.type);
-        // attention rmsnorm (c:3211-3217); Q4_0 weights take the Q8_0 x (c:3221-3225)
+        // attention rmsnorm (c:3211-3217), written also in the form the q/k/v
+        // weights consume (Q4_0 takes the Q8_0 x, c:3221-3225)
+        const XPrep xb_prep = m.prep(m.xb);
+        const int qkv_form = gemv_input_form(L.wq.type, m.dim);
         if (m.is_gemma && l == 0)
-            launch_rmsnorm(m.x, m.x, m.embed_scale, L.att_norm, m.dim, m.inv_dim, eps, m.xb, qkv_q8 ? &m.xq : nullptr, s);
+            launch_rmsnorm(m.x, m.x, m.embed_scale, L.att_norm, m.dim, m.inv_dim, eps, m.xb, &xb_prep, qkv_form, s);
         else
-            launch_rmsnorm(m.x, nullptr, 0.0f, L.att_norm, m.dim, m.inv_dim, eps, m.xb, qkv_q8 ? &m.xq : nullptr, s);
+            launch_rmsnorm(m.x, nullptr, 0.0f, L.att_norm, m.dim, m.inv_dim, eps, m.xb, &xb_prep, qkv_form, s);
         // q, k, v in one launch when the three share a type (c:3221-3230)
         if (L.wq.type == L.wk.type && L.wq.type == L.wv.type) {
             GemvBatch b{};
@@ -447,7 +549,9 @@ static void forward_impl(l3p_ctx* c, int token, int pos, bool with_logits) {
             b.seg[2] = GemvSegment{L.wv.w, m.v, L.wv.rows};
             b.nseg = 3;
             b.epilogue = EPI_STORE;
-            launch_gemv(L.wq.type, b, m.dim, m.xb, qkv_q8 ? &m.xq : nullptr, s);
+            const int rows = L.wq.rows + L.wk.rows + L.wv.rows;
+            ProfRange r(c->prof, s, gemv_label("qkv", L.wq.type, rows, m.dim), gemv_bytes(L.wq.type, rows, m.dim, rows));
+            launch_gemv(L.wq.type, b, m.dim, xb_prep, s);
         } else {
             const Mat* W3[3] = {&L.wq, &L.wk, &L.wv};
             float* Y3[3] = {m.q, m.k, m.v};
@@ -456,7 +560,11 @@ static void forward_impl(l3p_ctx* c, int token, int pos, bool with_logits) {
                 b.seg[0] = GemvSegment{W3[i]->w, Y3[i], W3[i]->rows};
                 b.nseg = 1;
                 b.epilogue = EPI_STORE;
-                launch_gemv(W3[i]->type, b, m.dim, m.xb, qkv_q8 ? &m.xq : nullptr, s);
+                if (i > 0 && gemv_input_form(W3[i]->type, m.dim) != qkv_form) prepare_x(W3[i]->type, m.dim, m.xb, xb_prep, s);
+                static const char* nm[3] = {"q", "k", "v"};
+                ProfRange r(c->prof, s, gemv_label(nm[i], W3[i]->type, W3[i]->rows, m.dim),
+                            gemv_bytes(W3[i]->type, W3[i]->rows, m.dim, W3[i]->rows));
+                launch_gemv(W3[i]->type, b, m.dim, xb_prep, s);
             }
         }
         // QK-norm, RoPE, KV write, Q quantization (c:3232-3312)
@@ -468,8 +576,9 @@ static void forward_impl(l3p_ctx* c, int token, int pos, bool with_logits) {
         AttnArgs a;
         a.qq = m.qq;
         a.qd = m.qd;
-        a.kc = m.kc + (size_t)l * m.layer_kv;
-        a.vc = m.vc + (size_t)l * m.layer_kv;
+        a.kc = m.kc;
+        a.vc = m.vc;
+        a.layer_off = (size_t)l * m.layer_kv;
         a.att = m.att;
         a.part_acc = m.part_acc;
         a.counters = m.counters;
@@ -486,14 +595,14 @@ static void forward_impl(l3p_ctx* c, int token, int pos, bool with_logits) {
         launch_attention(a, s);
         // output projection + residual (c:3362-3371)
         if (m.is_gemma) {
-            gemv_into(m, L.wo, m.xb, m.xb2, EPI_STORE, s);
+            gemv_into(c, L.wo, m.xb, m.xb2, EPI_STORE, "wo");
             launch_rmsnorm_add(m.xb2, L.post_att, m.dim, m.inv_dim, eps, m.x, s);
         } else {
-            gemv_into(m, L.wo, m.xb, m.x, EPI_ADD, s);
+            gemv_into(c, L.wo, m.xb, m.x, EPI_ADD, "wo");
         }
         // FFN (c:3373-3417)
-        const bool ffn_q8 = q8_class(L.w1.type);
-        launch_rmsnorm(m.x, nullptr, 0.0f, L.ffn_norm, m.dim, m.inv_dim, eps, m.xb, ffn_q8 ? &m.xq : nullptr, s);
+        const int ffn_form = gemv_input_form(L.w1.type, m.dim);
+        launch_rmsnorm(m.x, nullptr, 0.0f, L.ffn_norm, m.dim, m.inv_dim, eps, m.xb, &xb_prep, ffn_form, s);
         {
             GemvBatch b{};
             b.seg[0] = GemvSegment{L.w1.w, m.hb, L.w1.rows};
@@ -501,19 +610,21 @@ static void forward_impl(l3p_ctx* c, int token, int pos, bool with_logits) {
             b.nseg = 2;
             b.pair = 1;
             b.epilogue = m.is_gemma ? EPI_GEGLU : EPI_SWIGLU;
-            launch_gemv(L.w1.type, b, m.dim, m.xb, ffn_q8 ? &m.xq : nullptr, s);
+            ProfRange r(c->prof, s, gemv_label("gate|up", L.w1.type, 2 * L.w1.rows, m.dim),
+                        gemv_bytes(L.w1.type, 2 * L.w1.rows, m.dim, L.w1.rows));
+            launch_gemv(L.w1.type, b, m.dim, xb_prep, s);
         }
         if (m.is_gemma) {
-            gemv_into(m, L.w2, m.hb, m.xb, EPI_STORE, s);
+            gemv_into(c, L.w2, m.hb, m.xb, EPI_STORE, "down");
             launch_rmsnorm_add(m.xb, L.post_ffn, m.dim, m.inv_dim, eps, m.x, s);
         } else {
-            gemv_into(m, L.w2, m.hb, m.x, EPI_ADD, s);
+            gemv_into(c, L.w2, m.hb, m.x, EPI_ADD, "down");
         }
     }
     // final rmsnorm in place (c:3420), classifier (c:3423-3433)
-    launch_rmsnorm(m.x, nullptr, 0.0f, m.final_norm, m.dim, m.inv_dim, eps, m.x, nullptr, s);
+    launch_rmsnorm(m.x, nullptr, 0.0f, m.final_norm, m.dim, m.inv_dim, eps, m.x, nullptr, 0, s);
     if (with_logits) {
-        gemv_into(m, m.wcls, m.x, m.logits, EPI_STORE, s);
+        gemv_into(c, m.wcls, m.x, m.logits, EPI_STORE, "lm_head");
         if (m.is_gemma && m.softcap > 0.0f) launch_softcap(m.logits, m.vocab, m.softcap, s);
     }
 }
@@ -527,20 +638,84 @@ static float rng_f32(uint64_t* st) {
     return (u >> 8) / 16777216.0f;
 }
 
+// The reference's arithmetic on the k top-k slots, in slot order
+// (c:4850-4907): temperature softmax with expf, stable insertion sort by
+// probability when top_p < 1, the top-p cut, and one xorshift64* draw.  It runs
+// on the host with the same C library expf as the reference, so given the same
+// logits the chosen token is the reference's.
+static int sample_slots(float* val, const int* idx, int k, float temperature, float top_p, uint64_t* rng) {
+    const float inv_temp = 1.0f / temperature;
+    float max_v = val[0];
+    for (int i = 1; i < k; ++i)
+        if (val[i] > max_v) max_v = val[i];
+    const float max_vt = max_v * inv_temp;
+    float sum = 0.0f;
+    for (int i = 0; i < k; ++i) {
+        const float e = expf(val[i] * inv_temp - max_vt);
+        val[i] = e;
+        sum += e;
+    }
+    std::vector<int> id(idx, idx + k);
+    int n = k;
+    if (top_p < 1.0f) {
+        for (int i = 1; i < k; ++i) {
+            const float kv = val[i];
+            const int ki = id[i];
+            int j = i - 1;
+            while (j >= 0 && val[j] < kv) {
+                val[j + 1] = val[j];
+                id[j + 1] = id[j];
+                --j;
+            }
+            val[j + 1] = kv;
+            id[j + 1] = ki;
+        }
+        float cum = 0.0f;
+        const float thr = top_p * sum;
+        n = k;
+        for (int i = 0; i < k; ++i) {
+            cum += val[i];
+            if (cum >= thr) {
+                n = i + 1;
+                break;
+            }
+        }
+        sum = 0.0f;
+        for (int i = 0; i < n; ++i) sum += val[i];
+    }
+    const float r = rng_f32(rng) * sum;
+    float cdf = 0.0f;
+    int s = n - 1;
+    for (int i = 0; i < n; ++i) {
+        cdf += val[i];
+        if (r < cdf) {
+            s = i;
+            break;
+        }
+    }
+    return id[s];
+}
+
 static void sample_impl(l3p_ctx* c, const float* logits, int n, const l3p_sampler* sp, uint64_t* rng, int32_t* out) {
     Model& m = *c->model;
     hipStream_t s = c->stream;
-    if (sp->temperature == 0.0f) {                               // c:4812-4813
+    if (sp->temperature == 0.0f) {                               // argmax (c:4812-4813)
         launch_argmax(logits, n, m.out_token, s, m.cand_val, m.cand_idx);
-    } else {
-        L3P_REQUIRE(rng, L3P_E_INVALID, "sampler: rng state is NULL");
-        const int k = std::min(sp->top_k, n);
-        const float r = rng_f32(rng);
-        launch_sample_topk(logits, n, sp->temperature, k, sp->top_p, r, m.cand_val, m.cand_idx, m.out_token, s);
+        L3P_HIP(hipMemcpyAsync(m.out_token_host, m.out_token, 4, hipMemcpyDeviceToHost, s));
+        L3P_HIP(hipStreamSynchronize(s));
+        *out = m.out_token_host[0];
+        return;
     }
-    L3P_HIP(hipMemcpyAsync(m.out_token_host, m.out_token, 4, hipMemcpyDeviceToHost, s));
+    L3P_REQUIRE(rng, L3P_E_INVALID, "sampler: rng state is NULL");
+    L3P_REQUIRE(sp->top_k >= 1, L3P_E_INVALID, "sampler: top_k=%d", sp->top_k);
+    const int k = std::min(sp->top_k, n);                        // c:4815-4816
+    const int ng = std::max(256, sample_groups(m.vocab));
+    float* slot_v = m.cand_val + ng;
+    launch_topk_slots(logits, n, k, m.cand_val, slot_v, m.cand_idx, s);
+    L3P_HIP(hipMemcpyAsync(m.slot_val_host, slot_v, (size_t)k * 4, hipMemcpyDeviceToHost, s));
+    L3P_HIP(hipMemcpyAsync(m.slot_idx_host, m.cand_idx, (size_t)k * 4, hipMemcpyDeviceToHost, s));
     L3P_HIP(hipStreamSynchronize(s));
-    *out = m.out_token_host[0];
+    *out = sample_slots(m.slot_val_host, m.slot_idx_host, k, sp->temperature, sp->top_p, rng);
 }
 
 // ---------------------------------------------------------------------------
@@ -554,13 +729,12 @@ void run_gemm(l3p_ctx* c, int type, const uint8_t* w, int rows, int cols, const 
         gb.nseg = 1;
         gb.epilogue = EPI_STORE;
         const float* xb = x + (size_t)b * in_stride;
-        if (q8_class(type)) {
-            XQ8 xq = c->scratch.xq(cols);
-            launch_quantize_x(xb, cols, xq, c->stream);
-            launch_gemv(type, gb, cols, xb, &xq, c->stream);
-        } else {
-            launch_gemv(type, gb, cols, xb, nullptr, c->stream);
-        }
+        XPrep xp;
+        xp.x = xb;
+        xp.q8 = c->scratch.xq(cols);
+        xp.dig = c->scratch.xdig(cols);
+        prepare_x_form(type, cols, xb, xp, c->stream);
+        launch_gemv(type, gb, cols, xp, c->stream);
     }
 }
 
@@ -618,6 +792,7 @@ int l3p_forward(l3p_ctx* c, int32_t token, int32_t pos, int compute_logits, floa
         if (compute_logits && logits_host)
             L3P_HIP(hipMemcpyAsync(logits_host, m.logits, (size_t)m.vocab * 4, hipMemcpyDeviceToHost, c->stream));
         L3P_HIP(hipStreamSynchronize(c->stream));
+        c->prof.collect();
     });
 }
 
@@ -632,6 +807,7 @@ int l3p_prefill(l3p_ctx* c, const int32_t* tokens, int n, int32_t start) {
                         tokens[i]);
         for (int i = 0; i < n; ++i) forward_impl(c, tokens[i], start + i, false);
         L3P_HIP(hipStreamSynchronize(c->stream));
+        c->prof.collect();
     });
 }
 
@@ -643,6 +819,7 @@ int l3p_decode(l3p_ctx* c, int32_t token, int32_t pos, const l3p_sampler* sp, ui
         L3P_REQUIRE(pos >= 0 && pos < m.seq_len, L3P_E_INVALID, "pos %d out of range [0, %d)", pos, m.seq_len);
         forward_impl(c, token, pos, true);
         sample_impl(c, m.logits, m.vocab, sp, rng, out);
+        c->prof.collect();
     });
 }
 
@@ -669,6 +846,31 @@ int l3p_copy_kv(l3p_ctx* c, int layer, int which_v, void* dst, size_t cap) {
         const uint8_t* src = (which_v ? m.vc : m.kc) + (size_t)layer * m.layer_kv;
         L3P_HIP(hipMemcpyAsync(dst, src, m.layer_kv, hipMemcpyDeviceToHost, c->stream));
         L3P_HIP(hipStreamSynchronize(c->stream));
+    });
+}
+
+int l3p_profile(l3p_ctx* c, int on) {
+    return mguard(c, false, [&] {
+        L3P_HIP(hipStreamSynchronize(c->stream));
+        c->prof.reset();
+        c->prof.on = on != 0;
+    });
+}
+
+int l3p_profile_read(l3p_ctx* c, l3p_kernel_stat* out, int cap, int* n) {
+    return mguard(c, false, [&] {
+        L3P_REQUIRE(n && (cap <= 0 || out), L3P_E_INVALID, "profile_read: bad arguments");
+        L3P_HIP(hipStreamSynchronize(c->stream));
+        c->prof.collect();
+        *n = (int)c->prof.stats.size();
+        for (int i = 0; i < *n && i < cap; ++i) {
+            const Profiler::Stat& st = c->prof.stats[i];
+            memset(&out[i], 0, sizeof out[i]);
+            snprintf(out[i].name, sizeof out[i].name, "%s", st.name.c_str());
+            out[i].launches = st.launches;
+            out[i].total_ms = st.ms;
+            out[i].bytes_per_launch = st.bytes;
+        }
     });
 }
 

@@ -12,8 +12,9 @@ struct DevBuf {
 };
 
 struct Scratch {
-    DevBuf xq_buf, gemm_buf;
+    DevBuf xq_buf, xd_buf, gemm_buf;
     XQ8 xq(int cols);
+    XDig xdig(int cols);
     void release();
 };
 
@@ -34,8 +35,9 @@ struct Layer {
 struct AttnArgs {
     const int8_t* qq;      // [n_heads][hs] Q8_0 query quants
     const float* qd;       // [n_heads][hs/32] their scales (fp32 value of the fp16 scale)
-    const uint8_t* kc;     // layer base of the K cache [n_kv][seq][hq8]
-    const uint8_t* vc;     // layer base of the V cache
+    const uint8_t* kc;     // K cache allocation base; layer at kc + layer_off, [n_kv][seq][hq8]
+    const uint8_t* vc;     // V cache allocation base
+    size_t layer_off;
     float* att;            // [n_heads][seq] scores, then exp
     float* part_acc;       // [n_heads][max_chunks][hs] chunk outputs
     unsigned* counters;    // [n_heads] combine counters (kept at zero between calls)
@@ -68,17 +70,63 @@ struct Model {
     int8_t* qq = nullptr;          // Q8_0 query [n_heads][hs]
     float* qd = nullptr;           // [n_heads][hs/32]
     XQ8 xq{};
+    XDig xd{};
+    XPrep prep(const float* x) const {
+        XPrep p;
+        p.x = x;
+        p.q8 = xq;
+        p.dig = xd;
+        return p;
+    }
     float *att = nullptr, *part_acc = nullptr;
     unsigned* counters = nullptr;
     int max_chunks = 0;
     // sampler scratch
-    float* cand_val = nullptr;
-    int* cand_idx = nullptr;
+    float* cand_val = nullptr;     // device: group maxima, then top-k slot values
+    int* cand_idx = nullptr;       // device: top-k slot indices
     int* out_token = nullptr;      // device
     int* out_token_host = nullptr; // pinned
+    float* slot_val_host = nullptr;   // pinned, top-k slot values
+    int* slot_idx_host = nullptr;     // pinned, top-k slot indices
 
     void* dalloc(size_t bytes);
     ~Model();
+};
+
+// Per-kernel timing of the GEMV launches of a forward step, with HIP events
+// recorded on the launching stream around each launch.
+struct Profiler {
+    bool on = false;
+    struct Stat {
+        std::string name;
+        int64_t launches = 0;
+        double ms = 0.0;
+        double bytes = 0.0;   // algorithmic bytes per launch
+    };
+    struct Pending {
+        int stat;
+        hipEvent_t a, b;
+    };
+    std::vector<Stat> stats;
+    std::vector<Pending> pending;
+    std::vector<hipEvent_t> pool;
+
+    hipEvent_t event();
+    int stat(const std::string& name, double bytes);
+    void reset();                    // drops stats, keeps the event pool
+    void collect();                  // after the stream has drained
+    void release();
+};
+
+// RAII range around one launch: records a start event on construction and an
+// end event on destruction when profiling is on.
+struct ProfRange {
+    Profiler* p = nullptr;
+    int st = -1;
+    hipEvent_t a{}, b{};
+    hipStream_t s{};
+    ProfRange(Profiler& pr, hipStream_t stream, const std::string& name, double bytes);
+    ~ProfRange();
 };
 
 struct l3p_ctx {
@@ -87,21 +135,23 @@ struct l3p_ctx {
     std::string err;
     Scratch scratch;
     Model* model = nullptr;
+    Profiler prof;
 };
 
 // layers.hip
 void launch_embed(const Mat& emb, int token, float* x, hipStream_t s);
 void launch_rmsnorm(const float* x_in, float* x_scale_inplace, float scale, const float* w, int n, float inv_n,
-                    float eps, float* out, const XQ8* xq, hipStream_t s);
+                    float eps, float* out, const XPrep* xp, int form, hipStream_t s);
+// Launch the kernel that writes x in the form `type` consumes (none for fp32).
+void prepare_x(int type, int cols, const float* x, const XPrep& xp, hipStream_t s);
 void launch_rmsnorm_add(const float* y, const float* w, int n, float inv_n, float eps, float* x, hipStream_t s);
 void launch_rope_kv(const Model& m, int layer, int pos, hipStream_t s);
 void launch_attention(const AttnArgs& a, hipStream_t s);
 void launch_softcap(float* logits, int n, float cap, hipStream_t s);
 void launch_argmax(const float* logits, int n, int* out, hipStream_t s, float* cv, int* ci);
-void launch_sample_topk(const float* logits, int n, float temperature, int top_k, float top_p, float r,
-                        float* cand_val, int* cand_idx, int* out, hipStream_t s);
-int sample_candidates_per_block();
-int sample_num_blocks(int n);
+void launch_topk_slots(const float* logits, int n, int k, float* gmax, float* out_v, int* out_i, hipStream_t s);
+int sample_groups(int n);
+int sample_max_k();
 
 // model.cpp
 void run_gemm(l3p_ctx* c, int type, const uint8_t* w, int rows, int cols, const float* x, int batch, int in_stride,

@@ -134,28 +134,44 @@ def _kv(key: str, val) -> bytes:
     raise TypeError(type(val))
 
 
-def write_gguf(meta: dict, tensors: list, alignment: int = 32) -> bytes:
-    """tensors: list of (name, qtype, ne (cols, rows) or (n,), raw uint8 bytes)."""
-    head = bytearray(b"GGUF" + struct.pack("<IQQ", 3, len(tensors), len(meta)))
+def _gguf_header(meta: dict, specs: list, alignment: int):
+    """Header bytes and the data offset of every tensor (relative to the data start)."""
+    head = bytearray(b"GGUF" + struct.pack("<IQQ", 3, len(specs), len(meta)))
     for k, v in meta.items():
         head += _kv(k, v)
     off = 0
     offsets = []
-    for name, qtype, ne, raw in tensors:
+    for name, qtype, ne, nbytes in specs:
         off = (off + alignment - 1) // alignment * alignment
         offsets.append(off)
         head += _s(name.encode()) + struct.pack("<I", len(ne))
         for n in ne:
             head += struct.pack("<Q", n)
         head += struct.pack("<IQ", qtype, off)
-        off += len(raw)
-    pad = (-len(head)) % alignment
-    out = bytearray(head) + bytes(pad)
-    base = len(out)
-    for (name, qtype, ne, raw), o in zip(tensors, offsets):
-        out += bytes(base + o - len(out))
-        out += bytes(raw)
-    return bytes(out)
+        off += nbytes
+    head += bytes((-len(head)) % alignment)
+    return bytes(head), offsets, off
+
+
+def build_gguf(meta: dict, specs: list, fill, alignment: int = 32) -> np.ndarray:
+    """GGUF v3 image in one preallocated uint8 array.  specs: (name, qtype, ne, nbytes);
+    fill(i, view) writes tensor i's raw bytes into view (called in spec order)."""
+    head, offsets, data = _gguf_header(meta, specs, alignment)
+    out = np.zeros(len(head) + data, np.uint8)
+    out[:len(head)] = np.frombuffer(head, np.uint8)
+    for i, ((name, qtype, ne, nbytes), o) in enumerate(zip(specs, offsets)):
+        fill(i, out[len(head) + o: len(head) + o + nbytes])
+    return out
+
+
+def write_gguf(meta: dict, tensors: list, alignment: int = 32) -> bytes:
+    """tensors: list of (name, qtype, ne (cols, rows) or (n,), raw uint8 bytes)."""
+    specs = [(n, q, ne, len(raw)) for n, q, ne, raw in tensors]
+
+    def fill(i, view):
+        view[:] = np.frombuffer(bytes(tensors[i][3]), np.uint8)
+
+    return build_gguf(meta, specs, fill, alignment).tobytes()
 
 
 def synthetic_model(arch: str = "llama", dim: int = 256, hidden: int = 512, n_layers: int = 2,
@@ -163,9 +179,13 @@ def synthetic_model(arch: str = "llama", dim: int = 256, hidden: int = 512, n_la
                     ctx: int = 256, qtype: int = Q8_0, std: float = 0.02, seed: int = 0,
                     rope_theta: float = 500000.0, eps: float = 1e-5, tied: bool = False,
                     softcap: float = 0.0, swa_window: int = 0, rope_theta_swa: float = 10000.0,
-                    norm_jitter: float = 0.0) -> bytes:
+                    norm_jitter: float = 0.0, qtypes: dict | None = None, make_mat=None):
     """A random-init model in GGUF form.  arch 'llama' (Llama-3 layout) or
-    'gemma3' (Gemma layout: QK-norm, post norms, NEOX RoPE, GeGLU)."""
+    'gemma3' (Gemma layout: QK-norm, post norms, NEOX RoPE, GeGLU).
+    qtypes overrides the type per tensor-name suffix (e.g. {"ffn_down": Q4_0}).
+    make_mat(qtype, rows, cols, std, view), when given, writes the quantized
+    bytes of each matrix into view (e.g. generated on a GPU for multi-GB
+    models) and the image is returned as a uint8 array instead of bytes."""
     rng = np.random.default_rng(seed)
     hd = head_dim or dim // n_heads
     qd, kvd = n_heads * hd, n_kv * hd
@@ -191,34 +211,55 @@ def synthetic_model(arch: str = "llama", dim: int = 256, hidden: int = 512, n_la
     meta["tokenizer.ggml.bos_token_id"] = 1
     meta["tokenizer.ggml.eos_token_id"] = 2
 
-    def mat(rows, cols):
-        w = rng.normal(0, std, (rows, cols)).astype(np.float32)
-        return (qtype, (cols, rows), quantize(w, qtype).ravel())
+    def qtype_of(name):
+        t = qtype
+        for k, v in (qtypes or {}).items():
+            if k in name:
+                t = v
+        return t
 
-    def norm(n):
-        v = np.ones(n, np.float32)
-        if norm_jitter:
-            v += rng.normal(0, norm_jitter, n).astype(np.float32)
-        return (F32, (n,), v.view(np.uint8))
-
-    tensors = [("token_embd.weight",) + mat(vocab, dim)]
+    # (name, kind, rows, cols): kind "mat" (quantized, ne = (cols, rows)) or "norm" (F32, ne = (n,))
+    layout = [("token_embd.weight", "mat", vocab, dim)]
     for l in range(n_layers):
         p = f"blk.{l}."
-        tensors += [(p + "attn_norm.weight",) + norm(dim),
-                    (p + "attn_q.weight",) + mat(qd, dim),
-                    (p + "attn_k.weight",) + mat(kvd, dim),
-                    (p + "attn_v.weight",) + mat(kvd, dim),
-                    (p + "attn_output.weight",) + mat(dim, qd),
-                    (p + "ffn_norm.weight",) + norm(dim),
-                    (p + "ffn_gate.weight",) + mat(hidden, dim),
-                    (p + "ffn_down.weight",) + mat(dim, hidden),
-                    (p + "ffn_up.weight",) + mat(hidden, dim)]
+        layout += [(p + "attn_norm.weight", "norm", dim, 1),
+                   (p + "attn_q.weight", "mat", qd, dim),
+                   (p + "attn_k.weight", "mat", kvd, dim),
+                   (p + "attn_v.weight", "mat", kvd, dim),
+                   (p + "attn_output.weight", "mat", dim, qd),
+                   (p + "ffn_norm.weight", "norm", dim, 1),
+                   (p + "ffn_gate.weight", "mat", hidden, dim),
+                   (p + "ffn_down.weight", "mat", dim, hidden),
+                   (p + "ffn_up.weight", "mat", hidden, dim)]
         if pre == "gemma3":
-            tensors += [(p + "attn_q_norm.weight",) + norm(hd),
-                        (p + "attn_k_norm.weight",) + norm(hd),
-                        (p + "post_attention_norm.weight",) + norm(dim),
-                        (p + "post_ffw_norm.weight",) + norm(dim)]
-    tensors.append(("output_norm.weight",) + norm(dim))
+            layout += [(p + "attn_q_norm.weight", "norm", hd, 1),
+                       (p + "attn_k_norm.weight", "norm", hd, 1),
+                       (p + "post_attention_norm.weight", "norm", dim, 1),
+                       (p + "post_ffw_norm.weight", "norm", dim, 1)]
+    layout.append(("output_norm.weight", "norm", dim, 1))
     if not tied:
-        tensors.append(("output.weight",) + mat(vocab, dim))
-    return write_gguf(meta, tensors)
+        layout.append(("output.weight", "mat", vocab, dim))
+
+    specs = []
+    for name, kind, rows, cols in layout:
+        if kind == "mat":
+            t = qtype_of(name)
+            specs.append((name, t, (cols, rows), rows * row_bytes(t, cols)))
+        else:
+            specs.append((name, F32, (rows,), 4 * rows))
+
+    def fill(i, view):
+        name, kind, rows, cols = layout[i]
+        if kind == "norm":
+            v = np.ones(rows, np.float32)
+            if norm_jitter:
+                v += rng.normal(0, norm_jitter, rows).astype(np.float32)
+            view[:] = v.view(np.uint8)
+        elif make_mat is not None:
+            make_mat(specs[i][1], rows, cols, std, view)
+        else:
+            w = rng.normal(0, std, (rows, cols)).astype(np.float32)
+            view[:] = quantize(w, specs[i][1]).ravel()
+
+    out = build_gguf(meta, specs, fill)
+    return out if make_mat is not None else out.tobytes()

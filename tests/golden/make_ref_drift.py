@@ -1,0 +1,94 @@
+"""Writes ref_drift.json: how far the reference engine's own optimised build
+(Makefile "fast"/OpenMP line: gcc -Ofast -fopenmp, which vectorises and
+reorders its fp32 sums) drifts from its plain build (bit-identical to the
+oracle) on the synthetic models of test_gpu_model.py, under the same
+teacher-forced protocol as test_teacher_forced_logits_and_kv.
+
+The GPU path reorders fp32 sums too, so its logits are held to a tolerance
+derived from this drift: it may differ from the oracle by as much as the
+reference differs from itself across its own supported builds.
+
+Needs oracle/_ref/libref_omp.so (``make -C oracle ref``).  One model per
+subprocess because the reference keeps its model in process globals.
+
+usage: python tests/golden/make_ref_drift.py        (rewrites ref_drift.json)
+"""
+import json
+import os
+import subprocess
+import sys
+import tempfile
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(os.path.dirname(HERE))
+sys.path.insert(0, ROOT)
+sys.path.insert(0, os.path.dirname(HERE))
+
+STEPS = 24
+
+
+def measure(name: str) -> dict:
+    import oracle
+    from llama3pure_amd import synth
+    import model_cases as T
+
+    g = synth.synthetic_model(**T.MODELS[name])
+    fd, path = tempfile.mkstemp(suffix=".gguf")
+    with os.fdopen(fd, "wb") as f:
+        f.write(g)
+    try:
+        ref = oracle.Ref(oracle.REF_OMP_SO)
+        assert ref.lib.ref_model_open(path.encode(), 0) == 0
+        m = oracle.CpuRef().open_model(g)
+        prompt = T.teacher_prompt(m)
+        n = len(prompt) - 1
+        pos = 0
+        while pos < n:  # the reference's prefill batches of 32 (c:5277-5287)
+            bs = min(32, n - pos)
+            ref.lib.ref_prefill(oracle._vp(prompt), pos, bs)
+            m.prefill(prompt, pos, bs)
+            pos += bs
+        tok = int(prompt[-1])
+        out = np.empty(m.vocab, np.float32)
+        rel = []
+        for _ in range(STEPS):
+            lo = m.forward(tok, pos)
+            ref.lib.ref_forward(tok, pos, 1, oracle._vp(out))
+            rel.append(float(np.abs(lo - out).max()) / T.rms(lo))
+            tok, pos = int(np.argmax(lo)), pos + 1
+        kv = {}
+        for layer in (0, m.n_layers - 1):
+            for wv in (0, 1):
+                b = m.kv(layer, bool(wv))
+                a = np.empty(b.size, np.uint8)
+                ref.lib.ref_copy_kv(layer, wv, oracle._vp(a), a.size)
+                d = T.kv_quant_diff(a, b, m, pos)
+                kv[f"{layer}/{'v' if wv else 'k'}"] = {"max": int(d.max()), "mean": float(d.mean())}
+        return {"max_rel": max(rel), "per_step": rel, "kv": kv}
+    finally:
+        os.unlink(path)
+
+
+def main():
+    if len(sys.argv) == 3 and sys.argv[1] == "--one":
+        print(json.dumps(measure(sys.argv[2])))
+        return
+    import model_cases as T
+
+    out = {"build": "gcc -Ofast -fopenmp -march=x86-64-v3 (reference Makefile OpenMP line)",
+           "protocol": f"teacher-forced, prompt of 20, {STEPS} decode steps; max|dlogit|/rms(logits)",
+           "models": {}}
+    env = dict(os.environ, OMP_NUM_THREADS=os.environ.get("OMP_NUM_THREADS", "4"))
+    for name in T.MODELS:
+        r = subprocess.run([sys.executable, __file__, "--one", name], check=True, capture_output=True, text=True,
+                           env=env)
+        out["models"][name] = json.loads(r.stdout.strip().splitlines()[-1])
+        print(name, f"{out['models'][name]['max_rel']:.3e}")
+    with open(os.path.join(HERE, "ref_drift.json"), "w") as f:
+        json.dump(out, f, indent=1)
+
+
+if __name__ == "__main__":
+    main()

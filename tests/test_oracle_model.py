@@ -10,6 +10,7 @@ import os
 import subprocess
 import sys
 
+import numpy as np
 import pytest
 
 import oracle
@@ -52,3 +53,15 @@ def test_sampler_bit_identical(tmp_path):
     r = run(tmp_path, CASES["llama_q8_0"], n_pre=8, n_dec=16, sample=(0.9, 40, 0.9))
     assert r["ok"], r
     assert len(set(r["sampled"])) > 1   # genuinely sampling, not argmax
+
+
+@pytest.mark.skipif(not oracle.have_ref(), reason="oracle/_ref not built (make -C oracle ref)")
+def test_ref_drift_fixture_reproduces():
+    """tests/golden/ref_drift.json is what the reference's -Ofast -fopenmp build gives now."""
+    here = os.path.dirname(os.path.abspath(__file__))
+    with open(os.path.join(here, "golden", "ref_drift.json")) as f:
+        want = json.load(f)["models"]["llama_q8_0"]
+    r = subprocess.run([sys.executable, os.path.join(here, "golden", "make_ref_drift.py"), "--one", "llama_q8_0"],
+                       check=True, capture_output=True, text=True, timeout=600)
+    got = json.loads(r.stdout.strip().splitlines()[-1])
+    assert np.allclose(got["per_step"], want["per_step"], rtol=1e-6, atol=0)
