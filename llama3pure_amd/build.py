@@ -1,4 +1,5 @@
-"""Builds libl3p.so (HIP, gfx950) in-tree with hipcc.
+"""Builds libl3p.so (HIP, gfx950) in-tree with hipcc, and the Node.js N-API
+addon js/l3p_napi.node over it when Node's headers are installed.
 
     python -m llama3pure_amd.build
 
@@ -55,7 +56,36 @@ def build() -> str:
         sys.stderr.write(r.stdout + r.stderr)
         raise RuntimeError("link failed")
     os.replace(tmp, OUT)
+    build_napi()
     return OUT
+
+
+NAPI_SRC = os.path.join(HERE, "..", "js", "l3p_napi.c")
+NAPI_OUT = os.path.join(HERE, "..", "js", "l3p_napi.node")
+
+
+def node_include() -> str | None:
+    for d in ("/usr/include/node", "/usr/local/include/node"):
+        if os.path.exists(os.path.join(d, "node_api.h")):
+            return d
+    return None
+
+
+def build_napi() -> str | None:
+    """js/l3p_napi.node, linked against libl3p.so through an $ORIGIN rpath."""
+    inc = node_include()
+    if inc is None:
+        sys.stderr.write("node_api.h not found: the N-API addon is not built\n")
+        return None
+    tmp = NAPI_OUT + ".tmp"
+    cmd = ["gcc", "-O2", "-Wall", "-shared", "-fPIC", "-DNODE_GYP_MODULE_NAME=l3p_napi", f"-I{inc}", NAPI_SRC,
+           "-o", tmp, f"-L{HERE}", "-l:libl3p.so", "-Wl,-rpath,$ORIGIN/../llama3pure_amd"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        sys.stderr.write(r.stdout + r.stderr)
+        raise RuntimeError("N-API addon build failed")
+    os.replace(tmp, NAPI_OUT)
+    return NAPI_OUT
 
 
 if __name__ == "__main__":
