@@ -148,12 +148,7 @@ int l3p_gemv(l3p_ctx* c, int type, const void* w, int rows, int cols, const floa
         b.seg[0] = GemvSegment{(const uint8_t*)w, y, rows};
         b.nseg = 1;
         b.epilogue = EPI_STORE;
-        XPrep xp;
-        xp.x = x;
-        xp.q8 = c->scratch.xq(cols);
-        xp.dig = c->scratch.xdig(cols);
-        prepare_x_form(type, cols, x, xp, c->stream);
-        launch_gemv(type, b, cols, xp, c->stream);
+        gemv_plain(c, type, b, cols, x);
     });
 }
 

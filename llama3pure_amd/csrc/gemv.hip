@@ -518,6 +518,14 @@ __global__ void dequant_kernel(int type, const uint8_t* __restrict__ s, int64_t 
     if (i < n) y[i] = deq_elem(type, s, i);
 }
 
+// Embedding row times a scale (Gemma's sqrt(dim), which the reference applies
+// to x in place before the first norm, c:3132-3140; x*scale rounds the same).
+__global__ void embed_scaled_kernel(int type, const uint8_t* __restrict__ s, int n, float scale,
+                                    float* __restrict__ y) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) y[i] = deq_elem(type, s, i) * scale;
+}
+
 // ---------------------------------------------------------------------------
 // launch helpers
 // ---------------------------------------------------------------------------
@@ -643,5 +651,10 @@ void launch_quantize_q8_0_blocks(const float* x, int64_t n, uint8_t* dst, hipStr
 void launch_dequant(int type, const uint8_t* src, int64_t n, float* dst, hipStream_t st) {
     if (n == 0) return;
     hipLaunchKernelGGL(dequant_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, type, src, n, dst);
+    L3P_HIP(hipGetLastError());
+}
+
+void launch_embed_scaled(int type, const uint8_t* row, int n, float scale, float* dst, hipStream_t st) {
+    hipLaunchKernelGGL(embed_scaled_kernel, dim3((n + 255) / 256), dim3(256), 0, st, type, row, n, scale, dst);
     L3P_HIP(hipGetLastError());
 }

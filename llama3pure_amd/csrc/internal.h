@@ -134,4 +134,9 @@ void prepare_x_form(int type, int cols, const float* x, const XPrep& xp, hipStre
 void launch_quantize_x(const float* x, int cols, const XQ8& xq, hipStream_t s);
 void launch_quantize_q8_0_blocks(const float* x, int64_t n, uint8_t* dst, hipStream_t s);
 void launch_dequant(int type, const uint8_t* src, int64_t n, float* dst, hipStream_t s);
+void launch_embed_scaled(int type, const uint8_t* row, int n, float scale, float* dst, hipStream_t s);
+// gemv4.hip: Q8_0 / Q4_0 GEMV with an optional fused RMSNorm of x (norm != null)
+bool gemv4_supported(int type, int cols);
+void launch_gemv4(int type, const GemvBatch& b, int cols, const float* x, const float* norm, float eps,
+                  hipStream_t s);
 bool gemv_supported(int type, int cols);

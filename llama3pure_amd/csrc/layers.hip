@@ -10,6 +10,7 @@
 namespace {
 
 constexpr int kTC = 64;   // positions per attention chunk (one per lane)
+typedef __attribute__((address_space(3))) void lds_void;
 
 using namespace l3pd;
 
@@ -192,13 +193,19 @@ __global__ void __launch_bounds__(64) rope_kv_kernel(RopeArgs a) {
 
 // ---------------------------------------------------------------------------
 // Attention over the Q8_0 cache (c:3314-3359), split over chunks of 64
-// positions.  Kernel 1: integer scores per position, bit-exact with
-// dot_q8_0_q8_0_cache (c:1574-1597); the last chunk of each KV group to
-// finish runs the softmax (c:3167-3186) for the group's query heads and
-// stores the normalized weights.  Kernel 2: weighted V accumulation
-// (accum_q8_0_cache, c:1600-1622, weights |w| < 1e-8 skipped) per chunk; the
-// last chunk of a group sums the chunk partials in chunk order.
-// Workgroup = kv_mul waves (one per query head of the group) x one chunk.
+// positions; workgroup = kv_mul waves (one per query head of a KV group) x
+// one chunk.
+//   attn_scores_kernel: lane = position; the score is the reference's
+//     dot_q8_0_q8_0_cache (c:1574-1597): exact integer block dots, fp32 sum
+//     over blocks in block order, so scores are bit-exact.
+//     Each chunk also leaves its maximum and its sum of expf(s - chunk max).
+//   attn_values_kernel: every workgroup combines the chunk maxima and sums
+//     into the head's softmax max M and sum S (softmax, c:3167-3186; the same
+//     order in every workgroup), forms its chunk's weights
+//     w = expf(s - M) * (1/S), and
+//     accum_q8_0_cache (c:1600-1622: out += q * (d * w), |w| < 1e-8 skipped)
+//     over its chunk's V rows staged in LDS, into a per-chunk partial;
+//   attn_combine_kernel: adds the chunk partials in chunk order.
 // ---------------------------------------------------------------------------
 struct AttnKArgs {
     const int8_t* qq;
@@ -208,116 +215,153 @@ struct AttnKArgs {
     size_t layer_off;       // byte offset of this layer in both caches
     float* att;
     float* part_acc;
-    unsigned* counters;
+    float* part_ms;         // [n_heads][2][n_chunks]: chunk max, chunk sum of expf(s - max)
     float* out;
     size_t head_seq;
     int n_heads, kv_mul, hs, hq8, seq, t0, na, n_chunks;
 };
 
 __global__ void __launch_bounds__(1024) attn_scores_kernel(AttnKArgs a) {
-    __shared__ unsigned last;
     const int g = blockIdx.x, c = blockIdx.y;
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int h = g * a.kv_mul + w;
     const int nb = a.hs / 32;
     const int i = c * kTC + lane;         // position index relative to t0
     if (i < a.na) {
-        const int t = a.t0 + i;
-        // absolute byte offset of the K row from the (256-byte aligned) cache base
-        const size_t rowoff = a.layer_off + (size_t)g * a.head_seq + (size_t)t * a.hq8;
-        const uint32_t* cw = reinterpret_cast<const uint32_t*>(a.kc);
-        const int8_t* qh = a.qq + (size_t)h * a.hs;
-        float sum = 0.0f;
-        for (int b = 0; b < nb; ++b) {
-            const size_t off = rowoff + 34u * b;
-            const size_t E = off >> 2;
-            const uint32_t sh = (off & 2u) ? 32u : 16u;
-            uint32_t dw[9];
+    const int t = a.t0 + i;
+    // absolute byte offset of the K row from the (256-byte aligned) cache base
+    const size_t rowoff = a.layer_off + (size_t)g * a.head_seq + (size_t)t * a.hq8;
+    const uint32_t* cw = reinterpret_cast<const uint32_t*>(a.kc);
+    const int8_t* qh = a.qq + (size_t)h * a.hs;
+    float sum = 0.0f;
+#pragma unroll 8
+    for (int b = 0; b < nb; ++b) {
+        const size_t off = rowoff + 34u * b;
+        const size_t E = off >> 2;
+        const uint32_t sh = (off & 2u) ? 32u : 16u;
+        uint32_t dw[9];
 #pragma unroll
-            for (int k = 0; k < 9; ++k) dw[k] = cw[E + k];
-            const float db = h2f(dw[0] >> ((off & 2u) ? 16u : 0u));
-            const int4* qp = reinterpret_cast<const int4*>(qh + 32 * b);
-            const int4 qa = qp[0], qb4 = qp[1];
-            const int qv[8] = {qa.x, qa.y, qa.z, qa.w, qb4.x, qb4.y, qb4.z, qb4.w};
-            int isum = 0;
+        for (int k = 0; k < 9; ++k) dw[k] = cw[E + k];
+        const float db = h2f(dw[0] >> ((off & 2u) ? 16u : 0u));
+        const int4* qp = reinterpret_cast<const int4*>(qh + 32 * b);
+        const int4 qa = qp[0], qb4 = qp[1];
+        const int qv[8] = {qa.x, qa.y, qa.z, qa.w, qb4.x, qb4.y, qb4.z, qb4.w};
+        int isum = 0;
 #pragma unroll
-            for (int k = 0; k < 8; ++k) isum = __builtin_amdgcn_sdot4(qv[k], (int)shr64(dw[k], dw[k + 1], sh), isum, false);
-            const float da = a.qd[h * nb + b];
-            sum += da * db * (float)isum;
-        }
-        a.att[(size_t)h * a.seq + i] = sum;
+        for (int k = 0; k < 8; ++k) isum = __builtin_amdgcn_sdot4(qv[k], (int)shr64(dw[k], dw[k + 1], sh), isum, false);
+        const float da = a.qd[h * nb + b];
+        sum += da * db * (float)isum;
     }
-    // the last chunk of this KV group runs the softmax for the group's heads
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) last = atomicAdd(&a.counters[g], 1u) == (unsigned)(a.n_chunks - 1);
-    __syncthreads();
-    if (!last) return;
-    __threadfence();
-    float* att = a.att + (size_t)h * a.seq;
-    float m = -INFINITY;
-    for (int j = lane; j < a.na; j += 64) m = fmaxf(m, att[j]);
-    m = wave_max(m);
-    float s = 0.0f;
-    for (int j = lane; j < a.na; j += 64) {
-        const float e = expf(att[j] - m);
-        att[j] = e;
-        s += e;
+    a.att[(size_t)h * a.seq + i] = sum;
     }
-    s = wave_sum(s);
-    const float inv = 1.0f / s;
-    for (int j = lane; j < a.na; j += 64) att[j] *= inv;
-    __syncthreads();
-    if (threadIdx.x == 0) a.counters[g] = 0;
+    // chunk statistics for the softmax
+    const float v = i < a.na ? a.att[(size_t)h * a.seq + i] : -INFINITY;
+    const float cm = wave_max(v);
+    const float cs = wave_sum(i < a.na ? expf(v - cm) : 0.0f);
+    if (lane == 0) {
+        a.part_ms[((size_t)h * 2) * a.n_chunks + c] = cm;
+        a.part_ms[((size_t)h * 2 + 1) * a.n_chunks + c] = cs;
+    }
 }
 
 __global__ void __launch_bounds__(1024) attn_values_kernel(AttnKArgs a) {
-    __shared__ unsigned last;
+    extern __shared__ __align__(16) float smem[];
     const int g = blockIdx.x, c = blockIdx.y;
-    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, nt = blockDim.x;
     const int h = g * a.kv_mul + w;
+    const float* att = a.att + (size_t)h * a.seq;
+
+    // V rows of this chunk -> LDS, copied HBM -> LDS by global_load_lds_dword
+    // (64 dwords per instruction) from the 4-byte aligned start, all issued
+    // before anything waits
+    const int jbeg = c * kTC, jend = min(a.na, jbeg + kTC);
+    const size_t start = a.layer_off + (size_t)g * a.head_seq + (size_t)(a.t0 + jbeg) * a.hq8;
+    const size_t end = start + (size_t)(jend - jbeg) * a.hq8;
+    const size_t s4 = start & ~(size_t)3;
+    const int nd = (int)((end - s4 + 3) >> 2);
+    float* wts = smem;                                                      // [kv_mul][8][kTC]
+    uint32_t* vb = reinterpret_cast<uint32_t*>(smem + a.kv_mul * 8 * kTC);  // chunk V rows
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(a.vc) + (s4 >> 2);
+    const int nw = nt >> 6;
+    for (int i = w; i * 64 < nd; i += nw) {
+        if (i * 64 + lane < nd)
+            __builtin_amdgcn_global_load_lds(src + i * 64 + lane, (lds_void*)(vb + i * 64), 4, 0, 0);
+    }
+
+    // softmax max and sum of head h (c:3167-3186) from the chunk statistics
+    const float* pm = a.part_ms + ((size_t)h * 2) * a.n_chunks;
+    const float* ps = pm + a.n_chunks;
+    float m = -INFINITY;
+    for (int cc = lane; cc < a.n_chunks; cc += 64) m = fmaxf(m, pm[cc]);
+    m = wave_max(m);
+    float ssum = 0.0f;
+    for (int cc = lane; cc < a.n_chunks; cc += 64) ssum += ps[cc] * expf(pm[cc] - m);
+    ssum = wave_sum(ssum);
+    const float inv = 1.0f / ssum;
+    const float wt = jbeg + lane < jend ? expf(att[jbeg + lane] - m) * inv : 0.0f;
+    __builtin_amdgcn_s_waitcnt(0x0070);   // vmcnt(0) lgkmcnt(0): this wave's V copies have landed
+    __syncthreads();
+
+    // f[b][j] = d(row j, block b) * w_j, or 0 where the reference skips
+    // position j (|w| < 1e-8); then out[i] += q[j][i] * f[b(i)][j]
+    // (accum_q8_0_cache, c:1600-1622: scale = d * w, out += q * scale)
+    const int nbk = a.hs / 32;
+    const uint8_t* rows = reinterpret_cast<const uint8_t*>(vb) + (start - s4);
+    float* f = wts + (size_t)w * 8 * kTC;     // [8][kTC] for this head
+    if (jbeg + lane < jend) {
+        const bool skip = wt > -1e-8f && wt < 1e-8f;
+        for (int bb = 0; bb < nbk; ++bb) {
+            const uint8_t* sc = rows + (size_t)lane * a.hq8 + 34 * bb;
+            const float d = h2f((uint32_t)sc[0] | ((uint32_t)sc[1] << 8));
+            f[bb * kTC + lane] = skip ? 0.0f : d * wt;
+        }
+    }
+    __syncthreads();
     const int per = (a.hs + 63) / 64;          // outputs per lane (1, 2 or 4)
     const int i0 = lane * per;                 // first output element of this lane
     const bool act = i0 < a.hs;
     const int b = act ? i0 >> 5 : 0;           // its 32-block
+    const uint8_t* qrow = rows + 34 * b + 2 + (i0 & 31);
+    const float* fb = f + b * kTC;
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    const float* att = a.att + (size_t)h * a.seq;
-    const uint8_t* vbase = a.vc + a.layer_off + (size_t)g * a.head_seq + 34 * b;
-    const int jbeg = c * kTC, jend = min(a.na, jbeg + kTC);
-    for (int j = jbeg; j < jend; ++j) {
-        const float wt = att[j];
-        if (wt > -1e-8f && wt < 1e-8f) continue;
-        if (!act) continue;
-        const uint8_t* blk = vbase + (size_t)(a.t0 + j) * a.hq8;
-        const float scale = h2f((uint32_t)blk[0] | ((uint32_t)blk[1] << 8)) * wt;
-        const int8_t* qs = reinterpret_cast<const int8_t*>(blk + 2 + (i0 & 31));
-        for (int e = 0; e < per; ++e) acc[e] += (float)qs[e] * scale;
-    }
-    float* out = a.out + (size_t)h * a.hs + i0;
-    if (a.n_chunks == 1) {
-        if (act)
-            for (int e = 0; e < per; ++e) out[e] = acc[e];
-        return;
-    }
-    float* pa = a.part_acc + ((size_t)h * a.n_chunks + c) * a.hs + i0;
-    if (act)
-        for (int e = 0; e < per; ++e) pa[e] = acc[e];
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) last = atomicAdd(&a.counters[g], 1u) == (unsigned)(a.n_chunks - 1);
-    __syncthreads();
-    if (!last) return;
-    __threadfence();
+    const int cnt = jend - jbeg;
     if (act) {
-        float tot[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        for (int cc = 0; cc < a.n_chunks; ++cc) {
-            const float* p = a.part_acc + ((size_t)h * a.n_chunks + cc) * a.hs + i0;
-            for (int e = 0; e < per; ++e) tot[e] += p[e];
+        if (per == 2) {
+#pragma unroll 8
+            for (int j = 0; j < cnt; ++j) {
+                const uint32_t q = *reinterpret_cast<const uint16_t*>(qrow + (size_t)j * a.hq8);
+                const float fj = fb[j];
+                acc[0] += (float)(int8_t)(q & 0xffu) * fj;
+                acc[1] += (float)(int8_t)(q >> 8) * fj;
+            }
+        } else {
+#pragma unroll 4
+            for (int j = 0; j < cnt; ++j) {
+                const int8_t* qs = reinterpret_cast<const int8_t*>(qrow + (size_t)j * a.hq8);
+                const float fj = fb[j];
+                for (int e = 0; e < per; ++e) acc[e] += (float)qs[e] * fj;
+            }
         }
-        for (int e = 0; e < per; ++e) out[e] = tot[e];
     }
-    __syncthreads();
-    if (threadIdx.x == 0) a.counters[g] = 0;
+    float* dst = a.n_chunks == 1 ? a.out + (size_t)h * a.hs + i0
+                                 : a.part_acc + ((size_t)h * a.n_chunks + c) * a.hs + i0;
+    if (act)
+        for (int e = 0; e < per; ++e) dst[e] = acc[e];
+}
+
+// Sum of the chunk partials of every head in chunk order.  A kernel of its
+// own: a cross-workgroup handoff inside the values kernel would need
+// device-scope fences, which write back L2 on this GPU.
+__global__ void __launch_bounds__(256) attn_combine_kernel(const float* __restrict__ part, int n_chunks, int hs,
+                                                           float* __restrict__ out) {
+    const int h = blockIdx.x;
+    for (int i = threadIdx.x; i < hs; i += blockDim.x) {
+        const float* p = part + (size_t)h * n_chunks * hs + i;
+        float tot = 0.0f;
+#pragma unroll 8
+        for (int cc = 0; cc < n_chunks; ++cc) tot += p[(size_t)cc * hs];
+        out[(size_t)h * hs + i] = tot;
+    }
 }
 
 // Final logit soft-cap (Gemma, c:3425-3433).
@@ -521,7 +565,7 @@ void launch_attention(const AttnArgs& x, hipStream_t s) {
     a.layer_off = x.layer_off;
     a.att = x.att;
     a.part_acc = x.part_acc;
-    a.counters = x.counters;
+    a.part_ms = x.part_ms;
     a.out = x.out;
     a.head_seq = x.head_seq;
     a.n_heads = x.n_heads;
@@ -535,8 +579,16 @@ void launch_attention(const AttnArgs& x, hipStream_t s) {
     const dim3 grid(x.n_heads / x.kv_mul, a.n_chunks), block(64 * x.kv_mul);
     hipLaunchKernelGGL(attn_scores_kernel, grid, block, 0, s, a);
     L3P_HIP(hipGetLastError());
-    hipLaunchKernelGGL(attn_values_kernel, grid, block, 0, s, a);
+    // LDS: per-head block factors [kv_mul][8][kTC], then the chunk's V rows
+    // (+8 bytes of alignment slack)
+    const size_t lds = (size_t)x.kv_mul * 8 * kTC * 4 + (size_t)kTC * x.hq8 + 8;
+    hipLaunchKernelGGL(attn_values_kernel, grid, block, lds, s, a);
     L3P_HIP(hipGetLastError());
+    if (a.n_chunks > 1) {
+        hipLaunchKernelGGL(attn_combine_kernel, dim3(x.n_heads), dim3(std::min(256, (x.hs + 63) / 64 * 64)), 0, s,
+                           (const float*)a.part_acc, a.n_chunks, a.hs, a.out);
+        L3P_HIP(hipGetLastError());
+    }
 }
 
 void launch_softcap(float* l, int n, float cap, hipStream_t s) {

@@ -357,8 +357,10 @@ static Model* load_model(l3p_ctx* c, const void* bytes, size_t len, const l3p_lo
     L3P_REQUIRE(type_block_elems(m.emb.type) > 0, L3P_E_UNSUPPORTED, "embedding type unsupported");
 
     // KV cache, zeroed like calloc (c:365-372)
-    m.kc = (uint8_t*)m.dalloc((size_t)m.n_layers * m.layer_kv);
-    m.vc = (uint8_t*)m.dalloc((size_t)m.n_layers * m.layer_kv);
+    // +64 bytes: the attention kernels read whole dwords around 34-byte
+    // blocks, up to 4 bytes past the last row
+    m.kc = (uint8_t*)m.dalloc((size_t)m.n_layers * m.layer_kv + 64);
+    m.vc = (uint8_t*)m.dalloc((size_t)m.n_layers * m.layer_kv + 64);
     L3P_HIP(hipMemsetAsync(m.kc, 0, (size_t)m.n_layers * m.layer_kv, s));
     L3P_HIP(hipMemsetAsync(m.vc, 0, (size_t)m.n_layers * m.layer_kv, s));
 
@@ -404,8 +406,7 @@ static Model* load_model(l3p_ctx* c, const void* bytes, size_t len, const l3p_lo
     m.att = (float*)m.dalloc((size_t)m.n_heads * m.seq_len * 4);
     m.max_chunks = (m.seq_len + 63) / 64;
     m.part_acc = (float*)m.dalloc((size_t)m.n_heads * m.max_chunks * m.hs * 4);
-    m.counters = (unsigned*)m.dalloc((size_t)m.n_kv * sizeof(unsigned));
-    L3P_HIP(hipMemsetAsync(m.counters, 0, (size_t)m.n_kv * sizeof(unsigned), s));
+    m.part_ms = (float*)m.dalloc((size_t)m.n_heads * 2 * m.max_chunks * 4);
     const int ncand = std::max(256, sample_groups(m.vocab)) + sample_max_k();
     m.cand_val = (float*)m.dalloc((size_t)ncand * 4);
     m.cand_idx = (int*)m.dalloc((size_t)std::max(256, sample_max_k()) * 4);
@@ -513,35 +514,76 @@ static double gemv_bytes(int type, int rows, int cols, int out_rows) {
     return (double)rows * (double)type_row_bytes(type, cols) + 4.0 * cols + 4.0 * out_rows;
 }
 
-static void gemv_into(l3p_ctx* c, const Mat& W, const float* x, float* y, int epi, const char* what) {
-    const Model& m = *c->model;
+static bool v4_ok(int type, const GemvBatch& b, int cols) {
+    if (!gemv4_supported(type, cols)) return false;
+    for (int i = 0; i < b.nseg; ++i)
+        if (((uintptr_t)b.seg[i].w & 15) != 0) return false;
+    return true;
+}
+
+// b's segments = W . rmsnorm(x) (norm != null) or W . x, all of one type.
+// Q8_0/Q4_0 run the streaming kernel with the norm and the activation's
+// integer form computed in its prologue; other types take the norm kernel
+// (into xb), the input preparation and the generic GEMV.
+static void gemv_batch(l3p_ctx* c, int type, const GemvBatch& b, int cols, const float* x, const float* norm,
+                       const char* what) {
+    Model& m = *c->model;
     hipStream_t s = c->stream;
+    const float eps = m.eps > 0 ? m.eps : 1e-5f;   // c:3198
+    int rows = 0;
+    for (int i = 0; i < (b.pair ? 2 : b.nseg); ++i) rows += b.seg[i].rows;
+    const int out_rows = b.pair ? b.seg[0].rows : rows;
+    const std::string label = gemv_label(what, type, rows, cols);
+    const double bytes = gemv_bytes(type, rows, cols, out_rows);
+    if (v4_ok(type, b, cols)) {
+        ProfRange r(c->prof, s, label, bytes);
+        launch_gemv4(type, b, cols, x, norm, eps, s);
+        return;
+    }
+    const float* in = x;
+    XPrep xp = m.prep(m.xb);
+    if (norm) {
+        launch_rmsnorm(x, nullptr, 0.0f, norm, cols, 1.0f / (float)cols, eps, m.xb, &xp, gemv_input_form(type, cols), s);
+        in = m.xb;
+    } else {
+        prepare_x(type, cols, x, xp, s);
+    }
+    xp.x = in;
+    ProfRange r(c->prof, s, label, bytes);
+    launch_gemv(type, b, cols, xp, s);
+}
+
+void gemv_plain(l3p_ctx* c, int type, const GemvBatch& b, int cols, const float* x) {
+    if (v4_ok(type, b, cols)) {
+        launch_gemv4(type, b, cols, x, nullptr, 0.0f, c->stream);
+        return;
+    }
+    XPrep xp;
+    xp.x = x;
+    xp.q8 = c->scratch.xq(cols);
+    xp.dig = c->scratch.xdig(cols);
+    prepare_x_form(type, cols, x, xp, c->stream);
+    launch_gemv(type, b, cols, xp, c->stream);
+}
+
+static GemvBatch one(const Mat& W, float* y, int epi) {
     GemvBatch b{};
     b.seg[0] = GemvSegment{W.w, y, W.rows};
     b.nseg = 1;
     b.epilogue = epi;
-    const XPrep xp = m.prep(x);
-    prepare_x(W.type, W.cols, x, xp, s);
-    ProfRange r(c->prof, s, gemv_label(what, W.type, W.rows, W.cols), gemv_bytes(W.type, W.rows, W.cols, W.rows));
-    launch_gemv(W.type, b, W.cols, xp, s);
+    return b;
 }
 
 static void forward_impl(l3p_ctx* c, int token, int pos, bool with_logits) {
     Model& m = *c->model;
     hipStream_t s = c->stream;
     const float eps = m.eps > 0 ? m.eps : 1e-5f;                 // c:3198
-    launch_embed(m.emb, token, m.x, s);                          // c:3204-3207
+    // embedding row (c:3204-3207); Gemma scales it by sqrt(dim) (c:3212-3214)
+    if (m.is_gemma) launch_embed_scaled(m.emb.type, m.emb.w + (size_t)token * m.emb.rb, m.dim, m.embed_scale, m.x, s);
+    else launch_embed(m.emb, token, m.x, s);
     for (int l = 0; l < m.n_layers; ++l) {
         const Layer& L = m.layers[l];
-        // attention rmsnorm (c:3211-3217), written also in the form the q/k/v
-        // weights consume (Q4_0 takes the Q8_0 x, c:3221-3225)
-        const XPrep xb_prep = m.prep(m.xb);
-        const int qkv_form = gemv_input_form(L.wq.type, m.dim);
-        if (m.is_gemma && l == 0)
-            launch_rmsnorm(m.x, m.x, m.embed_scale, L.att_norm, m.dim, m.inv_dim, eps, m.xb, &xb_prep, qkv_form, s);
-        else
-            launch_rmsnorm(m.x, nullptr, 0.0f, L.att_norm, m.dim, m.inv_dim, eps, m.xb, &xb_prep, qkv_form, s);
-        // q, k, v in one launch when the three share a type (c:3221-3230)
+        // q, k, v = W . rmsnorm(x) (c:3211-3230), one launch when the three share a type
         if (L.wq.type == L.wk.type && L.wq.type == L.wv.type) {
             GemvBatch b{};
             b.seg[0] = GemvSegment{L.wq.w, m.q, L.wq.rows};
@@ -549,23 +591,11 @@ static void forward_impl(l3p_ctx* c, int token, int pos, bool with_logits) {
             b.seg[2] = GemvSegment{L.wv.w, m.v, L.wv.rows};
             b.nseg = 3;
             b.epilogue = EPI_STORE;
-            const int rows = L.wq.rows + L.wk.rows + L.wv.rows;
-            ProfRange r(c->prof, s, gemv_label("qkv", L.wq.type, rows, m.dim), gemv_bytes(L.wq.type, rows, m.dim, rows));
-            launch_gemv(L.wq.type, b, m.dim, xb_prep, s);
+            gemv_batch(c, L.wq.type, b, m.dim, m.x, L.att_norm, "qkv");
         } else {
-            const Mat* W3[3] = {&L.wq, &L.wk, &L.wv};
-            float* Y3[3] = {m.q, m.k, m.v};
-            for (int i = 0; i < 3; ++i) {
-                GemvBatch b{};
-                b.seg[0] = GemvSegment{W3[i]->w, Y3[i], W3[i]->rows};
-                b.nseg = 1;
-                b.epilogue = EPI_STORE;
-                if (i > 0 && gemv_input_form(W3[i]->type, m.dim) != qkv_form) prepare_x(W3[i]->type, m.dim, m.xb, xb_prep, s);
-                static const char* nm[3] = {"q", "k", "v"};
-                ProfRange r(c->prof, s, gemv_label(nm[i], W3[i]->type, W3[i]->rows, m.dim),
-                            gemv_bytes(W3[i]->type, W3[i]->rows, m.dim, W3[i]->rows));
-                launch_gemv(W3[i]->type, b, m.dim, xb_prep, s);
-            }
+            gemv_batch(c, L.wq.type, one(L.wq, m.q, EPI_STORE), m.dim, m.x, L.att_norm, "q");
+            gemv_batch(c, L.wk.type, one(L.wk, m.k, EPI_STORE), m.dim, m.x, L.att_norm, "k");
+            gemv_batch(c, L.wv.type, one(L.wv, m.v, EPI_STORE), m.dim, m.x, L.att_norm, "v");
         }
         // QK-norm, RoPE, KV write, Q quantization (c:3232-3312)
         launch_rope_kv(m, l, pos, s);
@@ -581,7 +611,7 @@ static void forward_impl(l3p_ctx* c, int token, int pos, bool with_logits) {
         a.layer_off = (size_t)l * m.layer_kv;
         a.att = m.att;
         a.part_acc = m.part_acc;
-        a.counters = m.counters;
+        a.part_ms = m.part_ms;
         a.out = m.xb;
         a.n_heads = m.n_heads;
         a.kv_mul = m.kv_mul;
@@ -595,14 +625,12 @@ static void forward_impl(l3p_ctx* c, int token, int pos, bool with_logits) {
         launch_attention(a, s);
         // output projection + residual (c:3362-3371)
         if (m.is_gemma) {
-            gemv_into(c, L.wo, m.xb, m.xb2, EPI_STORE, "wo");
+            gemv_batch(c, L.wo.type, one(L.wo, m.xb2, EPI_STORE), m.q_dim, m.xb, nullptr, "wo");
             launch_rmsnorm_add(m.xb2, L.post_att, m.dim, m.inv_dim, eps, m.x, s);
         } else {
-            gemv_into(c, L.wo, m.xb, m.x, EPI_ADD, "wo");
+            gemv_batch(c, L.wo.type, one(L.wo, m.x, EPI_ADD), m.q_dim, m.xb, nullptr, "wo");
         }
-        // FFN (c:3373-3417)
-        const int ffn_form = gemv_input_form(L.w1.type, m.dim);
-        launch_rmsnorm(m.x, nullptr, 0.0f, L.ffn_norm, m.dim, m.inv_dim, eps, m.xb, &xb_prep, ffn_form, s);
+        // FFN (c:3373-3417): gate/up with the norm and the activation fused
         {
             GemvBatch b{};
             b.seg[0] = GemvSegment{L.w1.w, m.hb, L.w1.rows};
@@ -610,21 +638,18 @@ static void forward_impl(l3p_ctx* c, int token, int pos, bool with_logits) {
             b.nseg = 2;
             b.pair = 1;
             b.epilogue = m.is_gemma ? EPI_GEGLU : EPI_SWIGLU;
-            ProfRange r(c->prof, s, gemv_label("gate|up", L.w1.type, 2 * L.w1.rows, m.dim),
-                        gemv_bytes(L.w1.type, 2 * L.w1.rows, m.dim, L.w1.rows));
-            launch_gemv(L.w1.type, b, m.dim, xb_prep, s);
+            gemv_batch(c, L.w1.type, b, m.dim, m.x, L.ffn_norm, "gate|up");
         }
         if (m.is_gemma) {
-            gemv_into(c, L.w2, m.hb, m.xb, EPI_STORE, "down");
+            gemv_batch(c, L.w2.type, one(L.w2, m.xb, EPI_STORE), m.hidden, m.hb, nullptr, "down");
             launch_rmsnorm_add(m.xb, L.post_ffn, m.dim, m.inv_dim, eps, m.x, s);
         } else {
-            gemv_into(c, L.w2, m.hb, m.x, EPI_ADD, "down");
+            gemv_batch(c, L.w2.type, one(L.w2, m.x, EPI_ADD), m.hidden, m.hb, nullptr, "down");
         }
     }
-    // final rmsnorm in place (c:3420), classifier (c:3423-3433)
-    launch_rmsnorm(m.x, nullptr, 0.0f, m.final_norm, m.dim, m.inv_dim, eps, m.x, nullptr, 0, s);
+    // final rmsnorm (c:3420) fused into the classifier (c:3423-3433)
     if (with_logits) {
-        gemv_into(c, m.wcls, m.x, m.logits, EPI_STORE, "lm_head");
+        gemv_batch(c, m.wcls.type, one(m.wcls, m.logits, EPI_STORE), m.dim, m.x, m.final_norm, "lm_head");
         if (m.is_gemma && m.softcap > 0.0f) launch_softcap(m.logits, m.vocab, m.softcap, s);
     }
 }
@@ -728,13 +753,7 @@ void run_gemm(l3p_ctx* c, int type, const uint8_t* w, int rows, int cols, const 
         gb.seg[0] = GemvSegment{w, y + (size_t)b * out_stride, rows};
         gb.nseg = 1;
         gb.epilogue = EPI_STORE;
-        const float* xb = x + (size_t)b * in_stride;
-        XPrep xp;
-        xp.x = xb;
-        xp.q8 = c->scratch.xq(cols);
-        xp.dig = c->scratch.xdig(cols);
-        prepare_x_form(type, cols, xb, xp, c->stream);
-        launch_gemv(type, gb, cols, xp, c->stream);
+        gemv_plain(c, type, gb, cols, x + (size_t)b * in_stride);
     }
 }
 

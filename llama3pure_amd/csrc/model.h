@@ -40,7 +40,7 @@ struct AttnArgs {
     size_t layer_off;
     float* att;            // [n_heads][seq] scores, then exp
     float* part_acc;       // [n_heads][max_chunks][hs] chunk outputs
-    unsigned* counters;    // [n_heads] combine counters (kept at zero between calls)
+    float* part_ms;        // [n_heads][2][max_chunks] chunk softmax max and sum
     float* out;            // [n_heads][hs]
     int n_heads, kv_mul, hs, hq8, seq, t0, na, n_chunks;
     size_t head_seq;
@@ -78,8 +78,7 @@ struct Model {
         p.dig = xd;
         return p;
     }
-    float *att = nullptr, *part_acc = nullptr;
-    unsigned* counters = nullptr;
+    float *att = nullptr, *part_acc = nullptr, *part_ms = nullptr;
     int max_chunks = 0;
     // sampler scratch
     float* cand_val = nullptr;     // device: group maxima, then top-k slot values
@@ -137,6 +136,9 @@ struct l3p_ctx {
     Model* model = nullptr;
     Profiler prof;
 };
+
+// y = W . x through the fastest kernel for the type (model.cpp)
+void gemv_plain(l3p_ctx* c, int type, const GemvBatch& b, int cols, const float* x);
 
 // layers.hip
 void launch_embed(const Mat& emb, int token, float* x, hipStream_t s);

@@ -138,6 +138,11 @@ def _check_gemv(ctx, torch, cpuref, qtype, rows, cols, seed=0, sample_rows=None)
     (l3p.Q6_K, 2048, 4096),
     (l3p.Q8_0, 2304, 2304),        # Gemma-2-2B dims
     (l3p.Q8_0, 2304, 9216),
+    (l3p.Q4_0, 2304, 2304),        # last column chunk of 8 blocks
+    (l3p.Q4_0, 1000, 9216),
+    (l3p.Q8_0, 300, 256),          # one partial chunk
+    (l3p.Q4_0, 77, 1536),
+    (l3p.Q8_0, 128256 // 64, 4096),
 ])
 def test_gemv_parity(ctx, torch_gpu, cpuref, qtype, rows, cols):
     _check_gemv(ctx, torch_gpu, cpuref, qtype, rows, cols, seed=rows + cols, sample_rows=min(rows, 768))
