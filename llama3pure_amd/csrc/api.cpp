@@ -58,6 +58,7 @@ void l3p_destroy(l3p_ctx* c) {
     if (!c) return;
     hipSetDevice(c->device);
     hipStreamSynchronize(c->stream);
+    c->drop_graphs();
     delete c->model;
     c->model = nullptr;
     c->scratch.release();
@@ -196,17 +197,7 @@ XQ8 Scratch::xq(int cols) {
     return q;
 }
 
-XDig Scratch::xdig(int cols) {
-    const size_t nb = (size_t)cols / 32;
-    xd_buf.ensure(nb * 128 + nb * 4 + 64);
-    XDig d;
-    d.dg = (int8_t*)xd_buf.p;
-    d.s = (float*)((char*)xd_buf.p + nb * 128);
-    return d;
-}
-
 void Scratch::release() {
-    xd_buf.release();
     xq_buf.release();
     gemm_buf.release();
 }

@@ -94,27 +94,4 @@ __device__ __forceinline__ void quantize32(const float* v, QBlock& o) {
     o.sum = s;
 }
 
-// Four int8 digits of 32 values against a power-of-two scale:
-// v = s * (d0 + d1/2^7 + d2/2^14 + d3/2^21) + r with |r| <= 2^-27 * max|v|,
-// where s = 2^(e-6) and max|v| < 2^e.  Every step is exact in fp32.
-__device__ __forceinline__ float digits32(const float* v, int8_t (*dg)[32]) {
-    float amax = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(v[j]));
-    int e = 0;
-    if (amax > 0.0f) frexpf(amax, &e);
-    const float up = amax > 0.0f ? ldexpf(1.0f, 6 - e) : 0.0f;
-#pragma unroll
-    for (int j = 0; j < 32; ++j) {
-        float r = v[j] * up;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const float d = rintf(r);
-            dg[k][j] = (int8_t)(int)d;
-            r = (r - d) * 128.0f;
-        }
-    }
-    return amax > 0.0f ? ldexpf(1.0f, e - 6) : 0.0f;
-}
-
 }  // namespace l3pd

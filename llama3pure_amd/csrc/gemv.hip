@@ -518,12 +518,21 @@ __global__ void dequant_kernel(int type, const uint8_t* __restrict__ s, int64_t 
     if (i < n) y[i] = deq_elem(type, s, i);
 }
 
-// Embedding row times a scale (Gemma's sqrt(dim), which the reference applies
-// to x in place before the first norm, c:3132-3140; x*scale rounds the same).
-__global__ void embed_scaled_kernel(int type, const uint8_t* __restrict__ s, int n, float scale,
-                                    float* __restrict__ y) {
+// Embedding row (c:3204-3207), times a scale when non-zero (Gemma's sqrt(dim),
+// which the reference applies to x in place before the first norm,
+// c:3132-3140; x*scale rounds the same), and the step record {token, pos}
+// that the kernels of the step read.
+__global__ void embed_step_kernel(int type, const uint8_t* __restrict__ s, int n, float scale, float* __restrict__ y,
+                                  int token, int pos, int* step) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) y[i] = deq_elem(type, s, i) * scale;
+    if (i < n) {
+        const float v = deq_elem(type, s, i);
+        y[i] = scale != 0.0f ? v * scale : v;
+    }
+    if (i == 0) {
+        step[0] = token;
+        step[1] = pos;
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -601,18 +610,13 @@ bool gemv_supported(int type, int cols) {
 }
 
 int gemv_input_form(int type, int cols) {
-    if (type == L3P_Q4_0) return 1;
-    if (type == L3P_Q8_0 && gemv2_supported(type, cols)) return 2;
-    return 0;
+    (void)cols;
+    return type == L3P_Q4_0 ? 1 : 0;
 }
 
 void launch_gemv(int type, const GemvBatch& b, int cols, const XPrep& xp, hipStream_t st) {
     L3P_REQUIRE(gemv_supported(type, cols), L3P_E_UNSUPPORTED, "gemv: type %d with %d columns not supported",
                 type, cols);
-    if (gemv2_supported(type, cols)) {
-        launch_gemv2(type, b, cols, xp, st);
-        return;
-    }
     L3P_REQUIRE(type != L3P_Q4_0 || xp.q8.qs, L3P_E_INVALID, "gemv: Q4_0 needs the quantized activation");
     const size_t rb = type_row_bytes(type, cols);
     const bool pair = b.pair != 0;
@@ -630,7 +634,6 @@ void launch_gemv(int type, const GemvBatch& b, int cols, const XPrep& xp, hipStr
 void prepare_x_form(int type, int cols, const float* x, const XPrep& xp, hipStream_t st) {
     switch (gemv_input_form(type, cols)) {
     case 1: launch_quantize_x(x, cols, xp.q8, st); break;
-    case 2: launch_x_digits(x, cols, xp.dig, st); break;
     default: break;
     }
 }
@@ -654,7 +657,9 @@ void launch_dequant(int type, const uint8_t* src, int64_t n, float* dst, hipStre
     L3P_HIP(hipGetLastError());
 }
 
-void launch_embed_scaled(int type, const uint8_t* row, int n, float scale, float* dst, hipStream_t st) {
-    hipLaunchKernelGGL(embed_scaled_kernel, dim3((n + 255) / 256), dim3(256), 0, st, type, row, n, scale, dst);
+void launch_embed_row(int type, const uint8_t* row, int n, float scale, float* dst, int token, int pos, int* step,
+                      hipStream_t st) {
+    hipLaunchKernelGGL(embed_step_kernel, dim3((n + 255) / 256), dim3(256), 0, st, type, row, n, scale, dst, token,
+                       pos, step);
     L3P_HIP(hipGetLastError());
 }

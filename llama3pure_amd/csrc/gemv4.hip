@@ -16,15 +16,12 @@
 // waits for a chunk with its own vmcnt: no workgroup barrier inside the row
 // loop.  The only barrier is per row group, for the cross-wave sum.
 //
-// Arithmetic.  Integer dot4 (v_dot4_i32_i8) on every block:
-//   Q4_0: against the Q8_0 activation, exactly the reference's
-//         vec_dot_q4_0_q8_0 (llama3pure-c-engine.c:1625-1643), block result
-//         dw*dx*(float)isum;
-//   Q8_0: against x as four int8 digits per 32-block,
-//         x = 2^(e-6) (d0 + d1/2^7 + d2/2^14 + d3/2^21), exact to 2^-27 of the
-//         block maximum; the four integer block dots are exact and combined
-//         in fp32 (the reference dequantizes exactly and sums fp32 products,
-//         c:2136-2176).
+// Arithmetic per block:
+//   Q4_0: integer dot4 (v_dot4_i32_i8) against the Q8_0 activation, exactly
+//         the reference's vec_dot_q4_0_q8_0 (llama3pure-c-engine.c:1625-1643),
+//         block result dw*dx*(float)isum;
+//   Q8_0: d * sum_j q_j x_j with fp32 FMAs on the fp32 activation (the
+//         reference dequantizes exactly and sums fp32 products, c:2136-2176).
 // Row totals: per-lane partials of the G rows are transposed-reduced across
 // the wave, then summed over the NC waves in chunk order, so results do not
 // depend on timing.
@@ -94,21 +91,31 @@ __device__ __forceinline__ void wait_vm() {
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
-// HBM -> LDS copy of one chunk (nbytes <= kChunkBytes, a 16-byte multiple)
-// into this wave's buffer dst.  Always exactly kX4 + 1 instructions, every
-// lane active: lanes past nbytes re-read the chunk's last bytes (the copy
-// lands beyond nbytes in the buffer and is never read), so the number of
-// outstanding copies per chunk is a constant the waits can count on.  Rows
-// past the end of the matrix (a ragged last group) copy a valid dummy chunk.
+// Byte offsets this lane copies within a chunk of nbytes (<= kChunkBytes, a
+// 16-byte multiple; the same for every row a wave copies): kX4 dwordx4
+// pieces and one dword piece, clamped so lanes past nbytes re-read the
+// chunk's last bytes (that copy lands past nbytes in the buffer and is never
+// read).  Every chunk is therefore exactly kX4 + 1 instructions with all
+// lanes active, a constant the waits count on.
+struct DmaLane {
+    int o0, o1;   // the dwordx4 pieces (o1 unused for Q4_0's single one)
+    int ot;       // the dword piece
+};
 template <int QT>
-__device__ __forceinline__ void chunk_dma(uint32_t* dst, const uint8_t* __restrict__ src, int nbytes, int lane) {
-#pragma unroll
-    for (int j = 0; j < Fmt<QT>::kX4; ++j) {
-        const int o = min(j * 1024 + lane * 16, nbytes - 16);
-        __builtin_amdgcn_global_load_lds(src + o, (lds_void*)(dst + j * 256), 16, 0, 2);
-    }
-    const int o = min(Fmt<QT>::kX4 * 1024 + lane * 4, nbytes - 4);
-    __builtin_amdgcn_global_load_lds(src + o, (lds_void*)(dst + Fmt<QT>::kX4 * 256), 4, 0, 2);
+__device__ __forceinline__ DmaLane dma_lane(int lane, int nbytes) {
+    DmaLane d;
+    d.o0 = min(lane * 16, nbytes - 16);
+    d.o1 = min(1024 + lane * 16, nbytes - 16);
+    d.ot = min(Fmt<QT>::kX4 * 1024 + lane * 4, nbytes - 4);
+    return d;
+}
+// HBM -> LDS copy of one chunk into this wave's buffer dst (lane i of an
+// instruction writes the instruction's LDS base + 16 i, or + 4 i for the dword piece).
+template <int QT>
+__device__ __forceinline__ void chunk_dma(uint32_t* dst, const uint8_t* src, DmaLane d) {
+    __builtin_amdgcn_global_load_lds(src + d.o0, (lds_void*)dst, 16, 0, 2);
+    if (Fmt<QT>::kX4 > 1) __builtin_amdgcn_global_load_lds(src + d.o1, (lds_void*)(dst + 256), 16, 0, 2);
+    __builtin_amdgcn_global_load_lds(src + d.ot, (lds_void*)(dst + Fmt<QT>::kX4 * 256), 4, 0, 2);
 }
 
 template <int N>
@@ -181,107 +188,128 @@ __device__ __forceinline__ void seg_of(const Gemv4Args& a, int i, int& s, int& r
     }
 }
 
+// The rows a wave streams, as wave-uniform values.
+struct Cursor {
+    const uint8_t *w0, *w1, *w2;
+    int rows0, rows1, rows_total, ngroups, bid, gdim;
+    uint32_t rb;      // row bytes
+    uint32_t coff;    // byte offset of this wave's chunk column in a row
+};
+
 // Row-chunk k of this workgroup's sequence: group j = blockIdx.x + (k / G) *
 // gridDim.x, row slot i = k % G.  Pair mode: slots [0, G/2) are gate rows,
-// [G/2, G) the matching up rows.  Sets src/nbytes to the chunk's bytes and
-// returns true for a real row; past the end it returns false with src/nbytes
-// pointing at the first chunk of the first matrix (a valid dummy copy).
+// [G/2, G) the matching up rows.  Sets src to the chunk and returns true for
+// a real row; past the end it returns false with src at the same chunk column
+// of the first row (a valid dummy copy of the same size).
 template <int G, bool PAIR>
-__device__ __forceinline__ bool chunk_src(const Gemv4Args& a, int k, int c, uint32_t rb, int chunk_bytes,
-                                          const uint8_t*& src, int& nbytes) {
-    const int j = blockIdx.x + (k / G) * gridDim.x;
+__device__ __forceinline__ bool chunk_src(const Cursor& cc, int k, const uint8_t*& src) {
+    const int j = cc.bid + (k / G) * cc.gdim;
     const int i = k % G;
-    int s = 0, r = 0;
-    bool ok = j < a.ngroups;
-    if (ok) {
-        if (PAIR) {
-            s = i < G / 2 ? 0 : 1;
-            r = j * (G / 2) + (i % (G / 2));
-            ok = r < a.rows[0];
-        } else {
-            const int gi = j * G + i;
-            ok = gi < a.rows_total;
-            if (ok) seg_of(a, gi, s, r);
+    const uint8_t* base = cc.w0;
+    int r;
+    bool ok = j < cc.ngroups;
+    if (PAIR) {
+        r = j * (G / 2) + (i % (G / 2));
+        if (i >= G / 2) base = cc.w1;
+        ok = ok && r < cc.rows0;
+    } else {
+        r = j * G + i;
+        ok = ok && r < cc.rows_total;
+        if (r >= cc.rows0) {
+            r -= cc.rows0;
+            base = cc.w1;
+            if (r >= cc.rows1) {
+                r -= cc.rows1;
+                base = cc.w2;
+            }
         }
     }
     if (!ok) {
-        s = 0;
+        base = cc.w0;
         r = 0;
-        c = 0;
     }
-    const uint32_t off = (uint32_t)c * (uint32_t)chunk_bytes;
-    nbytes = (int)min((uint32_t)chunk_bytes, rb - off);
-    src = a.w[s] + (size_t)r * rb + off;
+    src = base + (size_t)r * cc.rb + cc.coff;
     return ok;
 }
 
 // Activation of one 32-block in the form the weight type consumes.
 struct XBlock {
-    int q[4][8];   // Q8_0 weights: four digit planes; Q4_0 weights: q[0] = Q8_0 quants
-    float s;       // Q8_0: digit scale; Q4_0: fp32 value of the Q8_0 scale
+    float x[32];   // Q8_0 weights: the fp32 values
+    int q[8];      // Q4_0 weights: the Q8_0 quants, four per dword
+    float s;       // Q4_0: fp32 value of the Q8_0 scale
     int sum8;      // Q4_0: 8 * sum of quants
 };
 
 template <int QT>
 __device__ __forceinline__ void prepare_block(const float* v, XBlock& xb) {
     if (QT == L3P_Q8_0) {
-        int8_t dg[4][32];
-        xb.s = digits32(v, dg);
 #pragma unroll
-        for (int k = 0; k < 4; ++k)
-#pragma unroll
-            for (int e = 0; e < 8; ++e)
-                xb.q[k][e] = (int)((uint32_t)(uint8_t)dg[k][4 * e] | ((uint32_t)(uint8_t)dg[k][4 * e + 1] << 8) |
-                                   ((uint32_t)(uint8_t)dg[k][4 * e + 2] << 16) |
-                                   ((uint32_t)(uint8_t)dg[k][4 * e + 3] << 24));
-        xb.sum8 = 0;
+        for (int j = 0; j < 32; ++j) xb.x[j] = v[j];
     } else {
         QBlock qb;
         quantize32(v, qb);
 #pragma unroll
         for (int e = 0; e < 8; ++e)
-            xb.q[0][e] = (int)((uint32_t)(uint8_t)qb.q[4 * e] | ((uint32_t)(uint8_t)qb.q[4 * e + 1] << 8) |
-                               ((uint32_t)(uint8_t)qb.q[4 * e + 2] << 16) |
-                               ((uint32_t)(uint8_t)qb.q[4 * e + 3] << 24));
+            xb.q[e] = (int)((uint32_t)(uint8_t)qb.q[4 * e] | ((uint32_t)(uint8_t)qb.q[4 * e + 1] << 8) |
+                            ((uint32_t)(uint8_t)qb.q[4 * e + 2] << 16) | ((uint32_t)(uint8_t)qb.q[4 * e + 3] << 24));
         xb.s = h2f_exact(qb.dh);
         xb.sum8 = 8 * qb.sum;
     }
 }
 
-// Dot of the block at LDS byte offset `boff` (2-byte aligned) with the lane's
-// activation block.
+// Where lane l's block sits in a chunk buffer: its fp16 scale is the
+// halfword at byte BB*l; its quants start at byte BB*l + 2, which is
+// dword-aligned for odd l and 2 bytes into a dword for even l.  Reading nine
+// dwords from `first` and taking alignbyte(dw[k+1], dw[k], shift) gives the
+// k-th quant dword for both parities with one instruction and no branch.
+struct LaneBlock {
+    uint32_t half;    // halfword index of the scale
+    uint32_t first;   // dword index of the first dword read
+    uint32_t shift;   // byte shift for v_alignbyte: 2 (even l) or 0 (odd l)
+};
 template <int QT>
-__device__ __forceinline__ float block_dot(const uint32_t* lds, uint32_t boff, const XBlock& xb) {
-    const uint32_t E = boff >> 2;
-    const bool odd = (boff & 2u) != 0;   // block starts 2 bytes into a dword
+__device__ __forceinline__ LaneBlock lane_block(int lane) {
+    const uint32_t b = (uint32_t)lane * Fmt<QT>::kBlockBytes;
+    const bool odd = (b & 2u) != 0;
+    return LaneBlock{b >> 1, (b >> 2) + (odd ? 1u : 0u), odd ? 0u : 2u};
+}
+
+// Dot of the lane's block in the chunk buffer `buf` with the lane's activation:
+//   Q8_0: d * sum_j q_j x_j with fp32 FMAs (the reference dequantizes exactly,
+//         q*d, and sums fp32 products, c:2136-2176; fp32 summation order is
+//         the only difference);
+//   Q4_0: the reference's integer block dot against the Q8_0 activation,
+//         dw*dx*(float)isum (vec_dot_q4_0_q8_0, c:1625-1643).
+template <int QT>
+__device__ __forceinline__ float block_dot(const uint32_t* buf, const LaneBlock& lb, const XBlock& xb) {
+    const float d = h2f(reinterpret_cast<const uint16_t*>(buf)[lb.half]);
+    const uint32_t* p = buf + lb.first;
     if (QT == L3P_Q8_0) {
         uint32_t dw[9];
 #pragma unroll
-        for (int k = 0; k < 9; ++k) dw[k] = lds[E + k];
-        const float d = h2f(odd ? (dw[0] >> 16) : dw[0]);
-        int I[4] = {0, 0, 0, 0};
+        for (int k = 0; k < 9; ++k) dw[k] = p[k];
+        float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
-            const int q = (int)(odd ? dw[k + 1] : __builtin_amdgcn_alignbyte(dw[k + 1], dw[k], 2));
-#pragma unroll
-            for (int g = 0; g < 4; ++g) I[g] = __builtin_amdgcn_sdot4(q, xb.q[g][k], I[g], false);
+            const uint32_t q = __builtin_amdgcn_alignbyte(dw[k + 1], dw[k], lb.shift);
+            s0 = fmaf((float)(int8_t)(q & 0xffu), xb.x[4 * k], s0);
+            s1 = fmaf((float)(int8_t)((q >> 8) & 0xffu), xb.x[4 * k + 1], s1);
+            s2 = fmaf((float)(int8_t)((q >> 16) & 0xffu), xb.x[4 * k + 2], s2);
+            s3 = fmaf((float)(int8_t)(q >> 24), xb.x[4 * k + 3], s3);
         }
-        const float c7 = 0.0078125f;
-        const float f = (float)I[0] + ((float)I[1] + ((float)I[2] + (float)I[3] * c7) * c7) * c7;
-        return f * (d * xb.s);
+        return ((s0 + s1) + (s2 + s3)) * d;
     } else {
         uint32_t dw[5];
 #pragma unroll
-        for (int k = 0; k < 5; ++k) dw[k] = lds[E + k];
-        const float dwt = h2f(odd ? (dw[0] >> 16) : dw[0]);
+        for (int k = 0; k < 5; ++k) dw[k] = p[k];
         int isum = -xb.sum8;
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-            const uint32_t q = odd ? dw[k + 1] : __builtin_amdgcn_alignbyte(dw[k + 1], dw[k], 2);
-            isum = __builtin_amdgcn_sdot4((int)(q & 0x0f0f0f0fu), xb.q[0][k], isum, false);
-            isum = __builtin_amdgcn_sdot4((int)((q >> 4) & 0x0f0f0f0fu), xb.q[0][4 + k], isum, false);
+            const uint32_t q = __builtin_amdgcn_alignbyte(dw[k + 1], dw[k], lb.shift);
+            isum = __builtin_amdgcn_sdot4((int)(q & 0x0f0f0f0fu), xb.q[k], isum, false);
+            isum = __builtin_amdgcn_sdot4((int)((q >> 4) & 0x0f0f0f0fu), xb.q[4 + k], isum, false);
         }
-        return dwt * xb.s * (float)isum;
+        return d * xb.s * (float)isum;
     }
 }
 
@@ -293,10 +321,24 @@ __global__ void __launch_bounds__(1024) gemv4_kernel(Gemv4Args a) {
     constexpr int CI = Fmt<QT>::kX4 + 1;   // copy instructions per chunk
     constexpr int NOUT = PAIR ? G / 2 : G;
     extern __shared__ __align__(16) uint32_t lds[];
-    const int t = threadIdx.x, w = t >> 6, lane = t & 63, nw = blockDim.x >> 6;
+    const int t = threadIdx.x, lane = t & 63, nw = blockDim.x >> 6;
+    const int w = __builtin_amdgcn_readfirstlane(t >> 6);
     const int nb = a.cols >> 5;
     const uint32_t rb = (uint32_t)nb * BB;
     uint32_t* ring = lds + (size_t)w * NB * CDW;                          // this wave's chunk buffers
+    Cursor cc;
+    cc.w0 = a.w[0];
+    cc.w1 = a.w[1];
+    cc.w2 = a.w[2];
+    cc.rows0 = a.rows[0];
+    cc.rows1 = a.rows[1];
+    cc.rows_total = a.rows_total;
+    cc.ngroups = a.ngroups;
+    cc.bid = blockIdx.x;
+    cc.gdim = gridDim.x;
+    cc.rb = rb;
+    cc.coff = (uint32_t)w * (uint32_t)CB;
+    const DmaLane dl = dma_lane<QT>(lane, (int)min((uint32_t)CB, rb - cc.coff));
     float* red = reinterpret_cast<float*>(lds + (size_t)nw * NB * CDW);   // [2][nw][G]
     float* ssred = red + 2 * nw * G;                                      // [nw]
     float* out_lds = ssred + nw;                                          // [groups of this WG][NOUT]
@@ -332,9 +374,8 @@ __global__ void __launch_bounds__(1024) gemv4_kernel(Gemv4Args a) {
     for (int b = 0; b < NB - 1; ++b) {
         if (b < nk) {
             const uint8_t* src;
-            int nbytes;
-            chunk_src<G, PAIR>(a, b, w, rb, CB, src, nbytes);
-            chunk_dma<QT>(ring + b * CDW, src, nbytes, lane);
+            chunk_src<G, PAIR>(cc, b, src);
+            chunk_dma<QT>(ring + b * CDW, src, dl);
         }
     }
 
@@ -364,6 +405,7 @@ __global__ void __launch_bounds__(1024) gemv4_kernel(Gemv4Args a) {
     }
     XBlock xb;
     prepare_block<QT>(v, xb);
+    const LaneBlock lb = lane_block<QT>(lane);
 
     // ---- row loop: G rows per group, chunk k = gl*G + i of this WG's sequence
     for (int gl = 0; gl < ngroups_mine; ++gl) {
@@ -376,15 +418,19 @@ __global__ void __launch_bounds__(1024) gemv4_kernel(Gemv4Args a) {
             if (k + NB - 2 < nk) wait_vm<(NB - 2) * CI>();
             else wait_vm<0>();
             const uint8_t* src;
-            int nbytes;
-            const bool real = chunk_src<G, PAIR>(a, k, w, rb, CB, src, nbytes);
-            float d = 0.0f;
-            if (real && active) d = block_dot<QT>(ring + (k % NB) * CDW, (uint32_t)lane * BB, xb);
+            const bool real = chunk_src<G, PAIR>(cc, k, src);
+            // every lane reads inside the buffer, so the dot runs unconditionally
+            // and lanes past the row or rows past the matrix drop their value
+            float dv = block_dot<QT>(ring + (k % NB) * CDW, lb, xb);
+            // pin the dot here: left alone, the compiler sinks every dot of the
+            // group to its end and keeps all their quants live in registers
+            asm volatile("" : "+v"(dv));
+            const float d = (real && active) ? dv : 0.0f;
             wait_lgkm();   // this chunk's LDS reads are done before its buffer is refilled
             const int kn = k + NB - 1;
             if (kn < nk) {
-                chunk_src<G, PAIR>(a, kn, w, rb, CB, src, nbytes);
-                chunk_dma<QT>(ring + (kn % NB) * CDW, src, nbytes, lane);
+                chunk_src<G, PAIR>(cc, kn, src);
+                chunk_dma<QT>(ring + (kn % NB) * CDW, src, dl);
             }
             acc[i] = d;
         }
@@ -486,6 +532,7 @@ void launch4_nb(Gemv4Args a, int nbuf, hipStream_t st) {
     switch (nbuf) {
     case 3: launch4<QT, G, 3, PAIR>(a, st); break;
     case 6: launch4<QT, G, 6, PAIR>(a, st); break;
+    case 8: launch4<QT, G, 8, PAIR>(a, st); break;
     default: launch4<QT, G, 4, PAIR>(a, st); break;
     }
 }
@@ -495,6 +542,17 @@ void launch4_type(Gemv4Args a, bool pair, int G, int nbuf, hipStream_t st) {
     const int units = pair ? a.rows[0] : a.rows_total;
     const int per = pair ? G / 2 : G;
     a.ngroups = (units + per - 1) / per;
+    // the deepest ring (3, 4, 6, 8 or 12 buffers per wave) not above nbuf
+    // whose buffers fit the 160 KB of LDS with room for the result slots
+    const int nw = (a.cols / 32 + kChunkBlocks - 1) / kChunkBlocks;
+    static const int depths[] = {8, 6, 4, 3};
+    int nb = 3;
+    for (int d : depths)
+        if (d <= nbuf && (size_t)nw * d * Fmt<QT>::kBufBytes + 16384 <= 160 * 1024) {
+            nb = d;
+            break;
+        }
+    nbuf = nb;
     if (pair) {   // G counts gate and up rows together: 2 or 4 output rows per group
         switch (G) {
         case 4: launch4_nb<QT, 4, true>(a, nbuf, st); break;
@@ -537,11 +595,23 @@ void launch_gemv4(int type, const GemvBatch& b, int cols, const float* x, const 
     a.norm = norm;
     a.eps = eps;
     a.inv_n = 1.0f / (float)cols;
-    // rows per group: enough groups to give every CU work, then the largest
+    // Rows per group G: the largest of 16, 8, 4 that still gives about six
+    // waves per CU (groups x column chunks); ring depth 3 at G = 4, else 4.
+    // (Measured on MI355X at the Llama-3-8B shapes.)
+    const int nw = (cols / 32 + kChunkBlocks - 1) / kChunkBlocks;
     const int units = a.rows_total;
+    const int per_g = b.pair ? 2 : 1;   // pair groups hold G/2 rows of each matrix
+    auto waves = [&](int g) { return (long)(units * per_g + g - 1) / g * nw; };
     int G = env_int("L3P_GEMV4_G", 0);
-    if (G != 4 && G != 8 && G != 16) G = units >= 16 * 4 * cus() ? 16 : units >= 8 * 2 * cus() ? 8 : 4;
-    const int nbuf = env_int("L3P_GEMV4_NB", 4);
+    if (G != 4 && G != 8 && G != 16) {
+        G = 4;
+        for (int g : {16, 8})
+            if ((!b.pair || g <= 8) && waves(g) >= 6L * cus()) {
+                G = g;
+                break;
+            }
+    }
+    const int nbuf = env_int("L3P_GEMV4_NB", G == 4 ? 3 : 4);
     if (type == L3P_Q8_0) launch4_type<L3P_Q8_0>(a, b.pair != 0, G, nbuf, st);
     else launch4_type<L3P_Q4_0>(a, b.pair != 0, G, nbuf, st);
 }

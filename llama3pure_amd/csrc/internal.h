@@ -106,35 +106,23 @@ struct XQ8 {
     int32_t* sum;   // [cols/32]
 };
 
-// Activation in digit form for the Q8_0 GEMV: per 32-block, four int8 digit
-// planes (dg[b][k][j], 128 bytes) and the power-of-two scale s[b]:
-//   x[32b+j] ~= s[b] * (d0 + d1/2^7 + d2/2^14 + d3/2^21), to 2^-27 of the block max.
-struct XDig {
-    int8_t* dg;   // [cols/32][4][32]
-    float* s;     // [cols/32]
-};
-
-// A GEMV input in the forms the kernels consume: fp32 (K-quants), Q8_0 (Q4_0
-// weights) and digits (Q8_0 weights).  Only the form the weight type needs
-// has to be filled in.
+// A GEMV input in the forms the generic kernels consume: fp32, and Q8_0 for
+// Q4_0 weights.  Only the form the weight type needs has to be filled in.
 struct XPrep {
     const float* x = nullptr;
     XQ8 q8{};
-    XDig dig{};
 };
 
-// launchers (gemv.hip, gemv2.hip)
+// launchers (gemv.hip)
 void launch_gemv(int type, const GemvBatch& b, int cols, const XPrep& x, hipStream_t s);
-bool gemv2_supported(int type, int cols);
-void launch_gemv2(int type, const GemvBatch& b, int cols, const XPrep& x, hipStream_t s);
-void launch_x_digits(const float* x, int cols, const XDig& xd, hipStream_t s);
-// Which activation form a weight type consumes: 0 fp32, 1 Q8_0, 2 digits.
+// Which activation form a weight type consumes: 0 fp32, 1 Q8_0.
 int gemv_input_form(int type, int cols);
 void prepare_x_form(int type, int cols, const float* x, const XPrep& xp, hipStream_t s);
 void launch_quantize_x(const float* x, int cols, const XQ8& xq, hipStream_t s);
 void launch_quantize_q8_0_blocks(const float* x, int64_t n, uint8_t* dst, hipStream_t s);
 void launch_dequant(int type, const uint8_t* src, int64_t n, float* dst, hipStream_t s);
-void launch_embed_scaled(int type, const uint8_t* row, int n, float scale, float* dst, hipStream_t s);
+void launch_embed_row(int type, const uint8_t* row, int n, float scale, float* dst, int token, int pos, int* step,
+                      hipStream_t s);
 // gemv4.hip: Q8_0 / Q4_0 GEMV with an optional fused RMSNorm of x (norm != null)
 bool gemv4_supported(int type, int cols);
 void launch_gemv4(int type, const GemvBatch& b, int cols, const float* x, const float* norm, float eps,

@@ -25,6 +25,21 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
+// Q8_0 quantization with one value per lane, 32 lanes per block: the
+// reference's quantize_row_q8_0 (c:1508-1528) per element.  Returns the
+// quant; dh is the block's truncated fp16 scale (the same in its 32 lanes).
+__device__ __forceinline__ int8_t quant_lane(float v, uint32_t& dh) {
+    float amax = fabsf(v);
+#pragma unroll
+    for (int o = 16; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+    const float d = amax / 127.0f;
+    const float id = d > 0.0f ? 127.0f / amax : 0.0f;
+    dh = f2h_trunc(d);
+    int qi = (int)roundf(v * id);
+    qi = qi > 127 ? 127 : (qi < -128 ? -128 : qi);
+    return (int8_t)qi;
+}
+
 // Sum over the workgroup (any size that is a multiple of 64, <= 1024).
 __device__ float block_sum(float v, float* sh) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
@@ -37,22 +52,16 @@ __device__ float block_sum(float v, float* sh) {
     return s;
 }
 
-__device__ __forceinline__ void store_block34(uint8_t* dst, const QBlock& b) {
-    dst[0] = (uint8_t)(b.dh & 0xff);
-    dst[1] = (uint8_t)(b.dh >> 8);
-#pragma unroll
-    for (int j = 0; j < 32; ++j) dst[2 + j] = (uint8_t)b.q[j];
-}
 
 // ---------------------------------------------------------------------------
 // RMSNorm (c:3117-3129), optional fused embedding scale (Gemma first layer,
 // c:3132-3148), and the output also written in the form the next GEMV
-// consumes (form 1: Q8_0 for Q4_0 weights; form 2: digits for Q8_0 weights).
+// consumes (form 1: Q8_0 for Q4_0 weights).
 // One workgroup.
 // ---------------------------------------------------------------------------
 __global__ void __launch_bounds__(1024) rmsnorm_kernel(const float* __restrict__ xin, float* xscale, float scale,
                                                        const float* __restrict__ w, int n, float inv_n, float eps,
-                                                       float* out, XQ8 xq, XDig xd, int form) {
+                                                       float* out, XQ8 xq, int form) {
     __shared__ float sh[16];
     const int t = threadIdx.x, nt = blockDim.x;
     float ss = 0.0f;
@@ -83,17 +92,6 @@ __global__ void __launch_bounds__(1024) rmsnorm_kernel(const float* __restrict__
             dq[1] = make_int4(qi[4], qi[5], qi[6], qi[7]);
             xq.d[b] = h2f_exact(qb.dh);
             xq.sum[b] = qb.sum;
-        } else if (form == 2) {
-            int8_t dg[4][32];
-            const float sc = digits32(o, dg);
-            int4* dd = reinterpret_cast<int4*>(xd.dg + 128 * b);
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const int* p = reinterpret_cast<const int*>(dg[k]);
-                dd[2 * k] = make_int4(p[0], p[1], p[2], p[3]);
-                dd[2 * k + 1] = make_int4(p[4], p[5], p[6], p[7]);
-            }
-            xd.s[b] = sc;
         }
     }
 }
@@ -112,219 +110,270 @@ __global__ void __launch_bounds__(1024) rmsnorm_add_kernel(const float* __restri
 }
 
 // ---------------------------------------------------------------------------
-// Per head: Gemma QK-norm (c:3151-3165), RoPE with attn_scale fused into Q
-// (c:3240-3296), Q8_0 quantization of K and V into the cache at pos
-// (c:3301-3308) and of Q for the integer scores (c:3311-3312).
-// Workgroup = one wave; blocks [0, n_heads) are query heads, then KV heads.
+// Attention of one decode step over the Q8_0 KV cache (c:3232-3359), as
+// flash-decoding over chunks of kTC positions.  attn_chunk_kernel: workgroup
+// = one KV group (kv_mul waves, one per query head) x one chunk:
+//   * Gemma QK-norm (c:3151-3165), RoPE with attn_scale fused into Q
+//     (c:3240-3296) and Q8_0 quantization of Q (c:3311-3312) for the
+//     group's query heads; the chunk holding the step's position also
+//     quantizes K and V into the cache there (c:3301-3308);
+//   * the chunk's K and V rows are copied HBM -> LDS;
+//   * scores are the reference's dot_q8_0_q8_0_cache (c:1574-1597): exact
+//     integer block dots summed in fp32 in block order (bit-exact);
+//   * the chunk's softmax max m and sum l of e = expf(s - m), and the
+//     unnormalized V accumulation sum_t q_t * (d_t * e_t) (accum_q8_0_cache,
+//     c:1600-1622).  A position is skipped when e < 1e-8: its normalized
+//     weight expf(s - M) / S is then below 1e-8 too, the reference's skip
+//     threshold (c:1602).
+// attn_merge_kernel then forms the reference's softmax max M and sum S from
+// the chunk statistics (softmax, c:3167-3186) and the output
+// sum_c acc_c * expf(m_c - M) / S.
 // ---------------------------------------------------------------------------
-struct RopeArgs {
-    float *q, *k;
-    const float* v;
-    const float *q_norm, *k_norm;
-    const float *cos, *sin;      // rows for this position
-    uint8_t *kc, *vc;            // cache slots [n_kv][seq][hq8] at this position (layer base + pos*hq8)
+struct AttnCArgs {
+    const float *q, *k, *v;          // this step's projections [heads][hs]
+    const float *q_norm, *k_norm;    // Gemma QK-norm weights (null otherwise)
+    const float *cos, *sin;          // RoPE tables [seq][hs/2]; the step's row is used
+    uint8_t *kc, *vc;                // this layer's caches [n_kv][seq][hq8]
+    const int* step;                 // device {token, pos}
+    float* part;                     // [n_heads][n_chunks][hs + 2]: chunk output, max, sum
+    float* out;                      // [n_heads][hs]
     size_t head_seq;
-    int8_t* qq;                  // [n_heads][hs]
-    float* qd;                   // [n_heads][hs/32]
-    int n_heads, hs, neox;
+    int n_heads, kv_mul, hs, hq8, window, neox;
     float attn_scale, eps, inv_hs;
 };
 
-__global__ void __launch_bounds__(64) rope_kv_kernel(RopeArgs a) {
-    __shared__ float hv[256 + 8];
-    const int lane = threadIdx.x;
-    const bool isq = (int)blockIdx.x < a.n_heads;
-    const int head = isq ? blockIdx.x : blockIdx.x - a.n_heads;
-    const int hs = a.hs, half = hs / 2;
-    float* src = (isq ? a.q : a.k) + (size_t)head * hs;
-
-    // QK-norm (per-head rmsnorm) when weights are present
-    const float* nw = isq ? a.q_norm : a.k_norm;
-    for (int j = lane; j < hs; j += 64) hv[j] = src[j];
-    __syncthreads();
-    if (nw) {
-        float ss = 0.0f;
-        for (int j = lane; j < hs; j += 64) ss += hv[j] * hv[j];
-        ss = wave_sum(ss);
-        const float r = 1.0f / sqrtf(ss * a.inv_hs + a.eps);
-        __syncthreads();
-        for (int j = lane; j < hs; j += 64) hv[j] = nw[j] * (r * hv[j]);
-        __syncthreads();
-    }
-    // RoPE
-    for (int p = lane; p < half; p += 64) {
-        const float c = a.cos[p], s = a.sin[p];
-        const int i0 = a.neox ? p : 2 * p;
-        const int i1 = a.neox ? p + half : 2 * p + 1;
-        const float v0 = hv[i0], v1 = hv[i1];
-        if (isq) {
-            hv[i0] = (v0 * c - v1 * s) * a.attn_scale;
-            hv[i1] = (v0 * s + v1 * c) * a.attn_scale;
-        } else {
-            hv[i0] = v0 * c - v1 * s;
-            hv[i1] = v0 * s + v1 * c;
-        }
-    }
-    __syncthreads();
-    for (int j = lane; j < hs; j += 64) src[j] = hv[j];
-    const int nb = hs / 32;
-    if (lane < nb) {
-        QBlock qb;
-        quantize32(hv + 32 * lane, qb);
-        if (isq) {
-            int8_t* dq = a.qq + (size_t)head * hs + 32 * lane;
-#pragma unroll
-            for (int j = 0; j < 32; ++j) dq[j] = qb.q[j];
-            a.qd[head * nb + lane] = h2f_exact(qb.dh);
-        } else {
-            store_block34(a.kc + (size_t)head * a.head_seq + 34 * lane, qb);
-        }
-    } else if (!isq && lane >= 32 && lane < 32 + nb) {
-        const int b = lane - 32;
-        float vv[32];
-        const float* vs = a.v + (size_t)head * hs + 32 * b;
-#pragma unroll
-        for (int j = 0; j < 32; ++j) vv[j] = vs[j];
-        QBlock qb;
-        quantize32(vv, qb);
-        store_block34(a.vc + (size_t)head * a.head_seq + 34 * b, qb);
-    }
-}
-
-// ---------------------------------------------------------------------------
-// Attention over the Q8_0 cache (c:3314-3359), split over chunks of 64
-// positions; workgroup = kv_mul waves (one per query head of a KV group) x
-// one chunk.
-//   attn_scores_kernel: lane = position; the score is the reference's
-//     dot_q8_0_q8_0_cache (c:1574-1597): exact integer block dots, fp32 sum
-//     over blocks in block order, so scores are bit-exact.
-//     Each chunk also leaves its maximum and its sum of expf(s - chunk max).
-//   attn_values_kernel: every workgroup combines the chunk maxima and sums
-//     into the head's softmax max M and sum S (softmax, c:3167-3186; the same
-//     order in every workgroup), forms its chunk's weights
-//     w = expf(s - M) * (1/S), and
-//     accum_q8_0_cache (c:1600-1622: out += q * (d * w), |w| < 1e-8 skipped)
-//     over its chunk's V rows staged in LDS, into a per-chunk partial;
-//   attn_combine_kernel: adds the chunk partials in chunk order.
-// ---------------------------------------------------------------------------
-struct AttnKArgs {
-    const int8_t* qq;
-    const float* qd;
-    const uint8_t* kc;      // allocation base of the K cache (256-byte aligned)
-    const uint8_t* vc;      // allocation base of the V cache
-    size_t layer_off;       // byte offset of this layer in both caches
-    float* att;
-    float* part_acc;
-    float* part_ms;         // [n_heads][2][n_chunks]: chunk max, chunk sum of expf(s - max)
-    float* out;
-    size_t head_seq;
-    int n_heads, kv_mul, hs, hq8, seq, t0, na, n_chunks;
+// Positions this step attends to: [t0, pos], in chunks of kTC (c:3316-3322).
+struct Span {
+    int pos, t0, na, n_chunks;
 };
-
-__global__ void __launch_bounds__(1024) attn_scores_kernel(AttnKArgs a) {
-    const int g = blockIdx.x, c = blockIdx.y;
-    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int h = g * a.kv_mul + w;
-    const int nb = a.hs / 32;
-    const int i = c * kTC + lane;         // position index relative to t0
-    if (i < a.na) {
-    const int t = a.t0 + i;
-    // absolute byte offset of the K row from the (256-byte aligned) cache base
-    const size_t rowoff = a.layer_off + (size_t)g * a.head_seq + (size_t)t * a.hq8;
-    const uint32_t* cw = reinterpret_cast<const uint32_t*>(a.kc);
-    const int8_t* qh = a.qq + (size_t)h * a.hs;
-    float sum = 0.0f;
-#pragma unroll 8
-    for (int b = 0; b < nb; ++b) {
-        const size_t off = rowoff + 34u * b;
-        const size_t E = off >> 2;
-        const uint32_t sh = (off & 2u) ? 32u : 16u;
-        uint32_t dw[9];
-#pragma unroll
-        for (int k = 0; k < 9; ++k) dw[k] = cw[E + k];
-        const float db = h2f(dw[0] >> ((off & 2u) ? 16u : 0u));
-        const int4* qp = reinterpret_cast<const int4*>(qh + 32 * b);
-        const int4 qa = qp[0], qb4 = qp[1];
-        const int qv[8] = {qa.x, qa.y, qa.z, qa.w, qb4.x, qb4.y, qb4.z, qb4.w};
-        int isum = 0;
-#pragma unroll
-        for (int k = 0; k < 8; ++k) isum = __builtin_amdgcn_sdot4(qv[k], (int)shr64(dw[k], dw[k + 1], sh), isum, false);
-        const float da = a.qd[h * nb + b];
-        sum += da * db * (float)isum;
-    }
-    a.att[(size_t)h * a.seq + i] = sum;
-    }
-    // chunk statistics for the softmax
-    const float v = i < a.na ? a.att[(size_t)h * a.seq + i] : -INFINITY;
-    const float cm = wave_max(v);
-    const float cs = wave_sum(i < a.na ? expf(v - cm) : 0.0f);
-    if (lane == 0) {
-        a.part_ms[((size_t)h * 2) * a.n_chunks + c] = cm;
-        a.part_ms[((size_t)h * 2 + 1) * a.n_chunks + c] = cs;
-    }
+__device__ __forceinline__ Span span_of(const int* step, int window) {
+    Span s;
+    s.pos = step[1];
+    s.t0 = window > 0 ? max(0, s.pos - window + 1) : 0;
+    s.na = s.pos - s.t0 + 1;
+    s.n_chunks = (s.na + kTC - 1) / kTC;
+    return s;
 }
 
-__global__ void __launch_bounds__(1024) attn_values_kernel(AttnKArgs a) {
+// Q8_0 block `b` of a cache row starting at byte offset `off` of a dword
+// array (LDS here): fp16 scale and the 32 quants as eight dwords.
+__device__ __forceinline__ float row_block(const uint32_t* base, uint32_t off, uint32_t (&q)[8]) {
+    const uint32_t E = off >> 2;
+    const bool odd = (off & 2u) != 0;   // block starts 2 bytes into a dword
+    uint32_t dw[9];
+#pragma unroll
+    for (int k = 0; k < 9; ++k) dw[k] = base[E + k];
+    // quants: dwords E+1.. when odd, two bytes into dword E otherwise
+#pragma unroll
+    for (int k = 0; k < 8; ++k) q[k] = odd ? dw[k + 1] : __builtin_amdgcn_alignbyte(dw[k + 1], dw[k], 2);
+    return h2f(odd ? (dw[0] >> 16) : dw[0]);
+}
+
+__global__ void __launch_bounds__(1024) attn_chunk_kernel(AttnCArgs a) {
     extern __shared__ __align__(16) float smem[];
     const int g = blockIdx.x, c = blockIdx.y;
+    const Span sp = span_of(a.step, a.window);
+    if (c >= sp.n_chunks) return;   // the grid covers the longest context
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, nt = blockDim.x;
-    const int h = g * a.kv_mul + w;
-    const float* att = a.att + (size_t)h * a.seq;
+    const int hs = a.hs, nb = hs / 32, half = hs / 2, km = a.kv_mul;
+    const int h = g * km + w;
+    const int jbeg = c * kTC, jend = min(sp.na, jbeg + kTC), cnt = jend - jbeg;
+    const bool has_pos = c == sp.n_chunks - 1;   // the chunk holding the step's position
 
-    // V rows of this chunk -> LDS, copied HBM -> LDS by global_load_lds_dword
-    // (64 dwords per instruction) from the 4-byte aligned start, all issued
-    // before anything waits
-    const int jbeg = c * kTC, jend = min(a.na, jbeg + kTC);
-    const size_t start = a.layer_off + (size_t)g * a.head_seq + (size_t)(a.t0 + jbeg) * a.hq8;
-    const size_t end = start + (size_t)(jend - jbeg) * a.hq8;
-    const size_t s4 = start & ~(size_t)3;
-    const int nd = (int)((end - s4 + 3) >> 2);
-    float* wts = smem;                                                      // [kv_mul][8][kTC]
-    uint32_t* vb = reinterpret_cast<uint32_t*>(smem + a.kv_mul * 8 * kTC);  // chunk V rows
-    const uint32_t* src = reinterpret_cast<const uint32_t*>(a.vc) + (s4 >> 2);
-    const int nw = nt >> 6;
-    for (int i = w; i * 64 < nd; i += nw) {
-        if (i * 64 + lane < nd)
-            __builtin_amdgcn_global_load_lds(src + i * 64 + lane, (lds_void*)(vb + i * 64), 4, 0, 0);
+    // LDS: [kv_mul][hs] q rows, [2][hs] k and v rows, [kv_mul][8][kTC] V
+    // factors, [kv_mul][hs] int8 q, [kv_mul][8] q scales, then the chunk's K
+    // rows and V rows (kTC * hq8 bytes + 8 each, dword aligned)
+    float* qh = smem;
+    float* kvh = qh + km * hs;
+    float* f = kvh + 2 * hs;
+    int8_t* qq = reinterpret_cast<int8_t*>(f + km * 8 * kTC);
+    float* qd = reinterpret_cast<float*>(qq + km * hs);
+    const int rowdw = (kTC * a.hq8 + 8 + 3) / 4;
+    uint32_t* krows = reinterpret_cast<uint32_t*>(qd + km * 8);
+    uint32_t* vrows = krows + rowdw;
+
+    // this step's q (and k, v) rows, RoPE factors and norm weights go to
+    // registers first: everything is issued before the row copies below, so
+    // waiting for these loads never waits for the copies (hs <= 256)
+    const float* cosr = a.cos + (size_t)sp.pos * half;
+    const float* sinr = a.sin + (size_t)sp.pos * half;
+    float qv[4], kv2[8], cs[2], sn[2], qn[4], kn[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int j = lane + 64 * k;
+        qv[k] = j < hs ? a.q[(size_t)h * hs + j] : 0.0f;
+        qn[k] = (a.q_norm && j < hs) ? a.q_norm[j] : 0.0f;
+        kn[k] = (a.k_norm && j < hs) ? a.k_norm[j] : 0.0f;
+    }
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int p = lane + 64 * k;
+        cs[k] = p < half ? cosr[p] : 0.0f;
+        sn[k] = p < half ? sinr[p] : 0.0f;
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {   // k then v over the workgroup (2*hs <= 8*64)
+        const int j = threadIdx.x + nt * k;
+        kv2[k] = (has_pos && j < 2 * hs) ? (j < hs ? a.k[(size_t)g * hs + j] : a.v[(size_t)g * hs + j - hs]) : 0.0f;
     }
 
-    // softmax max and sum of head h (c:3167-3186) from the chunk statistics
-    const float* pm = a.part_ms + ((size_t)h * 2) * a.n_chunks;
-    const float* ps = pm + a.n_chunks;
-    float m = -INFINITY;
-    for (int cc = lane; cc < a.n_chunks; cc += 64) m = fmaxf(m, pm[cc]);
-    m = wave_max(m);
-    float ssum = 0.0f;
-    for (int cc = lane; cc < a.n_chunks; cc += 64) ssum += ps[cc] * expf(pm[cc] - m);
-    ssum = wave_sum(ssum);
-    const float inv = 1.0f / ssum;
-    const float wt = jbeg + lane < jend ? expf(att[jbeg + lane] - m) * inv : 0.0f;
-    __builtin_amdgcn_s_waitcnt(0x0070);   // vmcnt(0) lgkmcnt(0): this wave's V copies have landed
-    __syncthreads();
+    // the chunk's K and V rows, HBM -> LDS (dword copies from the 4-byte
+    // aligned start; the row at the step's position is replaced below)
+    const size_t start = (size_t)g * a.head_seq + (size_t)(sp.t0 + jbeg) * a.hq8;
+    const size_t s4 = start & ~(size_t)3;
+    const int nd = (int)((start + (size_t)cnt * a.hq8 - s4 + 3) >> 2);
+    {
+        const uint32_t* ks = reinterpret_cast<const uint32_t*>(a.kc) + (s4 >> 2);
+        const uint32_t* vs = reinterpret_cast<const uint32_t*>(a.vc) + (s4 >> 2);
+        const int nw = nt >> 6;
+        for (int i = w; i * 64 < nd; i += nw) {
+            if (i * 64 + lane < nd) {
+                __builtin_amdgcn_global_load_lds(ks + i * 64 + lane, (lds_void*)(krows + i * 64), 4, 0, 0);
+                __builtin_amdgcn_global_load_lds(vs + i * 64 + lane, (lds_void*)(vrows + i * 64), 4, 0, 0);
+            }
+        }
+    }
+    const uint32_t roff = (uint32_t)(start - s4);   // byte offset of row 0 in krows / vrows
 
-    // f[b][j] = d(row j, block b) * w_j, or 0 where the reference skips
-    // position j (|w| < 1e-8); then out[i] += q[j][i] * f[b(i)][j]
-    // (accum_q8_0_cache, c:1600-1622: scale = d * w, out += q * scale)
-    const int nbk = a.hs / 32;
-    const uint8_t* rows = reinterpret_cast<const uint8_t*>(vb) + (start - s4);
-    float* f = wts + (size_t)w * 8 * kTC;     // [8][kTC] for this head
-    if (jbeg + lane < jend) {
-        const bool skip = wt > -1e-8f && wt < 1e-8f;
-        for (int bb = 0; bb < nbk; ++bb) {
-            const uint8_t* sc = rows + (size_t)lane * a.hq8 + 34 * bb;
-            const float d = h2f((uint32_t)sc[0] | ((uint32_t)sc[1] << 8));
-            f[bb * kTC + lane] = skip ? 0.0f : d * wt;
+    // QK-norm + RoPE + Q8_0 of the group's query heads (and of K, V at pos)
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+        if (lane + 64 * k < hs) qh[w * hs + lane + 64 * k] = qv[k];
+    if (has_pos)
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+            if (threadIdx.x + nt * k < 2 * hs) kvh[threadIdx.x + nt * k] = kv2[k];
+    __syncthreads();
+    if (a.q_norm) {   // per-head rmsnorm (c:3151-3165); every wave also forms K's factor
+        float ssq = 0.0f, ssk = 0.0f;
+        for (int j = lane; j < hs; j += 64) {
+            ssq += qh[w * hs + j] * qh[w * hs + j];
+            ssk += kvh[j] * kvh[j];
+        }
+        ssq = wave_sum(ssq);
+        ssk = wave_sum(ssk);
+        const float rq = 1.0f / sqrtf(ssq * a.inv_hs + a.eps);
+        const float rk = 1.0f / sqrtf(ssk * a.inv_hs + a.eps);
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int j = lane + 64 * k;
+            if (j < hs) {
+                qh[w * hs + j] = qn[k] * (rq * qh[w * hs + j]);
+                if (has_pos && w == 0) kvh[j] = kn[k] * (rk * kvh[j]);
+            }
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {   // RoPE: NEOX (Gemma) or interleaved pairs
+        const int p = lane + 64 * k;
+        if (p < half) {
+            const int i0 = a.neox ? p : 2 * p;
+            const int i1 = a.neox ? p + half : 2 * p + 1;
+            const float v0 = qh[w * hs + i0], v1 = qh[w * hs + i1];
+            qh[w * hs + i0] = (v0 * cs[k] - v1 * sn[k]) * a.attn_scale;
+            qh[w * hs + i1] = (v0 * sn[k] + v1 * cs[k]) * a.attn_scale;
+            if (has_pos && w == 0) {
+                const float k0 = kvh[i0], k1 = kvh[i1];
+                kvh[i0] = k0 * cs[k] - k1 * sn[k];
+                kvh[i1] = k0 * sn[k] + k1 * cs[k];
+            }
         }
     }
     __syncthreads();
-    const int per = (a.hs + 63) / 64;          // outputs per lane (1, 2 or 4)
-    const int i0 = lane * per;                 // first output element of this lane
-    const bool act = i0 < a.hs;
-    const int b = act ? i0 >> 5 : 0;           // its 32-block
-    const uint8_t* qrow = rows + 34 * b + 2 + (i0 & 31);
-    const float* fb = f + b * kTC;
+    // Q8_0 of the head's q, one value per lane (c:3311-3312)
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int j = lane + 64 * k;
+        if (k * 64 < hs) {
+            uint32_t dh;
+            const int8_t qv8 = quant_lane(j < hs ? qh[w * hs + j] : 0.0f, dh);   // all lanes take part
+            if (j < hs) {
+                qq[w * hs + j] = qv8;
+                if ((lane & 31) == 0) qd[w * 8 + (j >> 5)] = h2f_exact(dh);
+            }
+        }
+    }
+    // K (wave 0) and V (wave 1, or 0 for one-wave groups) of the step, quantized
+    // here one value per lane; the copy replaces the copied row in LDS and goes
+    // to the cache at the end of the kernel (c:3301-3308)
+    const int kvsel = w == 0 ? 0 : (w == 1 ? 1 : -1);
+    const bool kv_wave = has_pos && (kvsel >= 0 || km == 1);
+    uint32_t kvq[2][4], kvdh[2][4];
+    if (kv_wave) {
+#pragma unroll
+        for (int sel = 0; sel < 2; ++sel) {
+            if (km > 1 && sel != kvsel) continue;
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                if (k * 64 < hs)
+                    kvq[sel][k] = (uint8_t)quant_lane(lane + 64 * k < hs ? kvh[sel * hs + lane + 64 * k] : 0.0f,
+                                                      kvdh[sel][k]);
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0x0070);   // vmcnt(0) lgkmcnt(0): this wave's row copies have landed
+    __syncthreads();
+    if (kv_wave) {   // the step's own K/V row replaces the copied one
+#pragma unroll
+        for (int sel = 0; sel < 2; ++sel) {
+            if (km > 1 && sel != kvsel) continue;
+            uint8_t* rb = reinterpret_cast<uint8_t*>(sel ? vrows : krows) + roff + (size_t)(cnt - 1) * a.hq8;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int j = lane + 64 * k;
+                if (j < hs) {
+                    const int b = j >> 5;
+                    rb[34 * b + 2 + (j & 31)] = (uint8_t)kvq[sel][k];
+                    if ((lane & 31) == 0) {
+                        rb[34 * b] = (uint8_t)(kvdh[sel][k] & 0xff);
+                        rb[34 * b + 1] = (uint8_t)(kvdh[sel][k] >> 8);
+                    }
+                }
+            }
+        }
+    }
+    __syncthreads();
+
+    // scores of head h: lane = position
+    float sc = -INFINITY;
+    if (lane < cnt) {
+        float sum = 0.0f;
+        const int8_t* qw = qq + w * hs;
+        for (int b = 0; b < nb; ++b) {
+            uint32_t kq[8];
+            const float db = row_block(krows, roff + (uint32_t)lane * a.hq8 + 34u * b, kq);
+            int isum = 0;
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+                isum = __builtin_amdgcn_sdot4(*reinterpret_cast<const int*>(qw + 32 * b + 4 * k), (int)kq[k], isum, false);
+            sum += qd[w * 8 + b] * db * (float)isum;
+        }
+        sc = sum;
+    }
+    const float m = wave_max(sc);
+    const float e = lane < cnt ? expf(sc - m) : 0.0f;
+    const float l = wave_sum(e);
+
+    // f[b][j] = d(V row j, block b) * e_j, 0 for skipped positions
+    const uint8_t* vbytes = reinterpret_cast<const uint8_t*>(vrows) + roff;
+    float* fw = f + (size_t)w * 8 * kTC;
+    if (lane < cnt) {
+        const bool skip = e < 1e-8f;
+        for (int bb = 0; bb < nb; ++bb) {
+            const uint8_t* s2 = vbytes + (size_t)lane * a.hq8 + 34 * bb;
+            const float d = h2f((uint32_t)s2[0] | ((uint32_t)s2[1] << 8));
+            fw[bb * kTC + lane] = skip ? 0.0f : d * e;
+        }
+    }
+    __syncthreads();
+    const int per = (hs + 63) / 64;            // outputs per lane (1, 2 or 4)
+    const int i0 = lane * per;
+    const bool act = i0 < hs;
+    const int b = act ? i0 >> 5 : 0;
+    const uint8_t* qrow = vbytes + 34 * b + 2 + (i0 & 31);
+    const float* fb = fw + b * kTC;
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    const int cnt = jend - jbeg;
     if (act) {
         if (per == 2) {
 #pragma unroll 8
@@ -339,28 +388,78 @@ __global__ void __launch_bounds__(1024) attn_values_kernel(AttnKArgs a) {
             for (int j = 0; j < cnt; ++j) {
                 const int8_t* qs = reinterpret_cast<const int8_t*>(qrow + (size_t)j * a.hq8);
                 const float fj = fb[j];
-                for (int e = 0; e < per; ++e) acc[e] += (float)qs[e] * fj;
+                for (int e2 = 0; e2 < per; ++e2) acc[e2] += (float)qs[e2] * fj;
             }
         }
     }
-    float* dst = a.n_chunks == 1 ? a.out + (size_t)h * a.hs + i0
-                                 : a.part_acc + ((size_t)h * a.n_chunks + c) * a.hs + i0;
+    float* dst = a.part + ((size_t)h * sp.n_chunks + c) * (hs + 2);
     if (act)
-        for (int e = 0; e < per; ++e) dst[e] = acc[e];
+        for (int e2 = 0; e2 < per; ++e2) dst[i0 + e2] = acc[e2];
+    if (lane == 0) {
+        dst[hs] = m;
+        dst[hs + 1] = l;
+    }
+    if (kv_wave) {   // K and V of the step into the cache (c:3301-3308)
+#pragma unroll
+        for (int sel = 0; sel < 2; ++sel) {
+            if (km > 1 && sel != kvsel) continue;
+            uint8_t* cd = (sel ? a.vc : a.kc) + (size_t)g * a.head_seq + (size_t)sp.pos * a.hq8;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int j = lane + 64 * k;
+                if (j < hs) {
+                    const int b = j >> 5;
+                    cd[34 * b + 2 + (j & 31)] = (uint8_t)kvq[sel][k];
+                    if ((lane & 31) == 0) {
+                        cd[34 * b] = (uint8_t)(kvdh[sel][k] & 0xff);
+                        cd[34 * b + 1] = (uint8_t)(kvdh[sel][k] >> 8);
+                    }
+                }
+            }
+        }
+    }
 }
 
-// Sum of the chunk partials of every head in chunk order.  A kernel of its
-// own: a cross-workgroup handoff inside the values kernel would need
-// device-scope fences, which write back L2 on this GPU.
-__global__ void __launch_bounds__(256) attn_combine_kernel(const float* __restrict__ part, int n_chunks, int hs,
-                                                           float* __restrict__ out) {
-    const int h = blockIdx.x;
-    for (int i = threadIdx.x; i < hs; i += blockDim.x) {
-        const float* p = part + (size_t)h * n_chunks * hs + i;
-        float tot = 0.0f;
-#pragma unroll 8
-        for (int cc = 0; cc < n_chunks; ++cc) tot += p[(size_t)cc * hs];
-        out[(size_t)h * hs + i] = tot;
+// out = sum_c acc_c * expf(m_c - M) / S with M = max m_c, S = sum l_c expf(m_c - M).
+// Every load is issued before anything waits: the first wave reads the
+// chunk maxima and sums (lane = chunk) while each thread reads its output's
+// chunk partials; the weights expf(m_c - M) / S go through LDS.
+__global__ void __launch_bounds__(256) attn_merge_kernel(AttnCArgs a) {
+    __shared__ float wc[256];
+    const Span sp = span_of(a.step, a.window);
+    const int h = blockIdx.x, hs = a.hs, nch = sp.n_chunks, t = threadIdx.x;
+    const float* part = a.part + (size_t)h * nch * (hs + 2);
+    for (int c0 = 0; c0 < nch; c0 += 64) {   // 64 chunks (4096 positions) per round
+        const int nc = min(64, nch - c0);
+        float pv[64];
+        const int i = t;   // this thread's output element (hs <= 256 = blockDim)
+#pragma unroll
+        for (int k = 0; k < 64; ++k) pv[k] = (k < nc && i < hs) ? part[(size_t)(c0 + k) * (hs + 2) + i] : 0.0f;
+        if (t < 64) {
+            const bool ok = t < nch;
+            // the statistics of every chunk (not only this round's), for M and S
+            float mx = -INFINITY;
+            for (int c = t; c < nch; c += 64) mx = fmaxf(mx, part[(size_t)c * (hs + 2) + hs]);
+            mx = wave_max(mx);
+            float ssum = 0.0f;
+            for (int c = t; c < nch; c += 64) {
+                const float* pc = part + (size_t)c * (hs + 2);
+                ssum += pc[hs + 1] * expf(pc[hs] - mx);
+            }
+            ssum = wave_sum(ssum);
+            const float inv = 1.0f / ssum;
+            if (t < nc) wc[t] = expf(part[(size_t)(c0 + t) * (hs + 2) + hs] - mx) * inv;
+            (void)ok;
+        }
+        __syncthreads();
+        if (i < hs) {
+            float tot = c0 == 0 ? 0.0f : a.out[(size_t)h * hs + i];
+#pragma unroll
+            for (int k = 0; k < 64; ++k)
+                if (k < nc) tot += pv[k] * wc[k];
+            a.out[(size_t)h * hs + i] = tot;
+        }
+        __syncthreads();
     }
 }
 
@@ -509,15 +608,14 @@ __global__ void __launch_bounds__(64) topk_scan_kernel(const float* __restrict__
 // ---------------------------------------------------------------------------
 // launchers
 // ---------------------------------------------------------------------------
-void launch_embed(const Mat& emb, int token, float* x, hipStream_t s) {
-    launch_dequant(emb.type, emb.w + (size_t)token * emb.rb, emb.cols, x, s);
+void launch_embed_step(const Mat& emb, int token, int pos, float scale, float* x, int* step, hipStream_t s) {
+    launch_embed_row(emb.type, emb.w + (size_t)token * emb.rb, emb.cols, scale, x, token, pos, step, s);
 }
 
 void launch_rmsnorm(const float* xin, float* xscale, float scale, const float* w, int n, float inv_n, float eps,
                     float* out, const XPrep* xp, int form, hipStream_t s) {
     const XQ8 q = xp ? xp->q8 : XQ8{};
-    const XDig d = xp ? xp->dig : XDig{};
-    hipLaunchKernelGGL(rmsnorm_kernel, dim3(1), dim3(1024), 0, s, xin, xscale, scale, w, n, inv_n, eps, out, q, d,
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(1), dim3(1024), 0, s, xin, xscale, scale, w, n, inv_n, eps, out, q,
                        xp ? form : 0);
     L3P_HIP(hipGetLastError());
 }
@@ -527,68 +625,46 @@ void launch_rmsnorm_add(const float* y, const float* w, int n, float inv_n, floa
     L3P_HIP(hipGetLastError());
 }
 
-void launch_rope_kv(const Model& m, int l, int pos, hipStream_t s) {
+void launch_attention(const Model& m, int l, float* out, hipStream_t s) {
     const Layer& L = m.layers[l];
     const bool swa = m.swa_pattern > 0 && (l % m.swa_pattern < m.swa_pattern - 1);   // c:3247
-    const bool use_swa_tables = m.is_gemma && swa;
-    const int half = m.hs / 2;
-    RopeArgs a;
+    const bool use_swa = m.is_gemma && swa;
+    AttnCArgs a;
     a.q = m.q;
     a.k = m.k;
     a.v = m.v;
     a.q_norm = m.is_gemma ? L.q_norm : nullptr;
     a.k_norm = m.is_gemma ? L.k_norm : nullptr;
-    a.cos = (use_swa_tables ? m.cos_s : m.cos_d) + (size_t)pos * half;
-    a.sin = (use_swa_tables ? m.sin_s : m.sin_d) + (size_t)pos * half;
-    const size_t loff = (size_t)l * m.layer_kv + (size_t)pos * m.hq8;
-    a.kc = m.kc + loff;
-    a.vc = m.vc + loff;
+    a.cos = use_swa ? m.cos_s : m.cos_d;
+    a.sin = use_swa ? m.sin_s : m.sin_d;
+    a.kc = m.kc + (size_t)l * m.layer_kv;
+    a.vc = m.vc + (size_t)l * m.layer_kv;
+    a.step = m.step;
+    a.part = m.part_acc;
+    a.out = out;
     a.head_seq = m.head_seq;
-    a.qq = m.qq;
-    a.qd = m.qd;
     a.n_heads = m.n_heads;
+    a.kv_mul = m.kv_mul;
     a.hs = m.hs;
+    a.hq8 = m.hq8;
+    a.window = (use_swa && m.swa_window > 0) ? m.swa_window : 0;   // c:3316-3321
     a.neox = m.is_gemma;
     a.attn_scale = m.attn_scale;
     a.eps = m.eps > 0 ? m.eps : 1e-5f;
     a.inv_hs = m.inv_hs;
-    hipLaunchKernelGGL(rope_kv_kernel, dim3(m.n_heads + m.n_kv), dim3(64), 0, s, a);
-    L3P_HIP(hipGetLastError());
-}
-
-void launch_attention(const AttnArgs& x, hipStream_t s) {
-    AttnKArgs a;
-    a.qq = x.qq;
-    a.qd = x.qd;
-    a.kc = x.kc;
-    a.vc = x.vc;
-    a.layer_off = x.layer_off;
-    a.att = x.att;
-    a.part_acc = x.part_acc;
-    a.part_ms = x.part_ms;
-    a.out = x.out;
-    a.head_seq = x.head_seq;
-    a.n_heads = x.n_heads;
-    a.kv_mul = x.kv_mul;
-    a.hs = x.hs;
-    a.hq8 = x.hq8;
-    a.seq = x.seq;
-    a.t0 = x.t0;
-    a.na = x.na;
-    a.n_chunks = (x.na + kTC - 1) / kTC;
-    const dim3 grid(x.n_heads / x.kv_mul, a.n_chunks), block(64 * x.kv_mul);
-    hipLaunchKernelGGL(attn_scores_kernel, grid, block, 0, s, a);
-    L3P_HIP(hipGetLastError());
-    // LDS: per-head block factors [kv_mul][8][kTC], then the chunk's V rows
-    // (+8 bytes of alignment slack)
-    const size_t lds = (size_t)x.kv_mul * 8 * kTC * 4 + (size_t)kTC * x.hq8 + 8;
-    hipLaunchKernelGGL(attn_values_kernel, grid, block, lds, s, a);
-    L3P_HIP(hipGetLastError());
-    if (a.n_chunks > 1) {
-        hipLaunchKernelGGL(attn_combine_kernel, dim3(x.n_heads), dim3(std::min(256, (x.hs + 63) / 64 * 64)), 0, s,
-                           (const float*)a.part_acc, a.n_chunks, a.hs, a.out);
-        L3P_HIP(hipGetLastError());
+    const int rowdw = (kTC * m.hq8 + 8 + 3) / 4;
+    const size_t lds = (size_t)m.kv_mul * m.hs * 4 + 2 * (size_t)m.hs * 4 + (size_t)m.kv_mul * 8 * kTC * 4 +
+                       (size_t)m.kv_mul * m.hs + (size_t)m.kv_mul * 8 * 4 + 2 * (size_t)rowdw * 4 + 16;
+    const dim3 grid(m.n_kv, m.max_chunks), block(64 * m.kv_mul);
+    static size_t lds_set = 65536;   // dynamic LDS above 64 KB must be allowed first
+    if (lds > lds_set) {
+        L3P_HIP(hipFuncSetAttribute((const void*)attn_chunk_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+        lds_set = lds;
     }
+    hipLaunchKernelGGL(attn_chunk_kernel, grid, block, lds, s, a);
+    L3P_HIP(hipGetLastError());
+    hipLaunchKernelGGL(attn_merge_kernel, dim3(m.n_heads), dim3((m.hs + 63) / 64 * 64), 0, s, a);
+    L3P_HIP(hipGetLastError());
 }
 
 void launch_softcap(float* l, int n, float cap, hipStream_t s) {

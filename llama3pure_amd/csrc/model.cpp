@@ -401,12 +401,10 @@ static Model* load_model(l3p_ctx* c, const void* bytes, size_t len, const l3p_lo
     m.xq.qs = (int8_t*)m.dalloc((size_t)maxin);
     m.xq.d = (float*)m.dalloc((size_t)maxin / 32 * 4);
     m.xq.sum = (int32_t*)m.dalloc((size_t)maxin / 32 * 4);
-    m.xd.dg = (int8_t*)m.dalloc((size_t)maxin / 32 * 128);
-    m.xd.s = (float*)m.dalloc((size_t)maxin / 32 * 4);
-    m.att = (float*)m.dalloc((size_t)m.n_heads * m.seq_len * 4);
     m.max_chunks = (m.seq_len + 63) / 64;
-    m.part_acc = (float*)m.dalloc((size_t)m.n_heads * m.max_chunks * m.hs * 4);
-    m.part_ms = (float*)m.dalloc((size_t)m.n_heads * 2 * m.max_chunks * 4);
+    L3P_REQUIRE(m.max_chunks <= 4096, L3P_E_UNSUPPORTED, "context length %d exceeds 262144", m.seq_len);
+    m.part_acc = (float*)m.dalloc((size_t)m.n_heads * m.max_chunks * (m.hs + 2) * 4);
+    m.step = (int*)m.dalloc(4 * sizeof(int));
     const int ncand = std::max(256, sample_groups(m.vocab)) + sample_max_k();
     m.cand_val = (float*)m.dalloc((size_t)ncand * 4);
     m.cand_idx = (int*)m.dalloc((size_t)std::max(256, sample_max_k()) * 4);
@@ -561,7 +559,6 @@ void gemv_plain(l3p_ctx* c, int type, const GemvBatch& b, int cols, const float*
     XPrep xp;
     xp.x = x;
     xp.q8 = c->scratch.xq(cols);
-    xp.dig = c->scratch.xdig(cols);
     prepare_x_form(type, cols, x, xp, c->stream);
     launch_gemv(type, b, cols, xp, c->stream);
 }
@@ -574,13 +571,13 @@ static GemvBatch one(const Mat& W, float* y, int epi) {
     return b;
 }
 
-static void forward_impl(l3p_ctx* c, int token, int pos, bool with_logits) {
+// The layer stack and the classifier of one step (c:3209-3434).  Reads the
+// token and position from the device step record only, so a capture of it
+// replays for any position.
+static void layers_impl(l3p_ctx* c, bool with_logits) {
     Model& m = *c->model;
     hipStream_t s = c->stream;
     const float eps = m.eps > 0 ? m.eps : 1e-5f;                 // c:3198
-    // embedding row (c:3204-3207); Gemma scales it by sqrt(dim) (c:3212-3214)
-    if (m.is_gemma) launch_embed_scaled(m.emb.type, m.emb.w + (size_t)token * m.emb.rb, m.dim, m.embed_scale, m.x, s);
-    else launch_embed(m.emb, token, m.x, s);
     for (int l = 0; l < m.n_layers; ++l) {
         const Layer& L = m.layers[l];
         // q, k, v = W . rmsnorm(x) (c:3211-3230), one launch when the three share a type
@@ -597,32 +594,8 @@ static void forward_impl(l3p_ctx* c, int token, int pos, bool with_logits) {
             gemv_batch(c, L.wk.type, one(L.wk, m.k, EPI_STORE), m.dim, m.x, L.att_norm, "k");
             gemv_batch(c, L.wv.type, one(L.wv, m.v, EPI_STORE), m.dim, m.x, L.att_norm, "v");
         }
-        // QK-norm, RoPE, KV write, Q quantization (c:3232-3312)
-        launch_rope_kv(m, l, pos, s);
-        // attention (c:3314-3359)
-        const bool swa = m.swa_pattern > 0 && (l % m.swa_pattern < m.swa_pattern - 1);
-        int t0 = 0;
-        if (m.is_gemma && swa && m.swa_window > 0) t0 = std::max(0, pos - m.swa_window + 1);
-        AttnArgs a;
-        a.qq = m.qq;
-        a.qd = m.qd;
-        a.kc = m.kc;
-        a.vc = m.vc;
-        a.layer_off = (size_t)l * m.layer_kv;
-        a.att = m.att;
-        a.part_acc = m.part_acc;
-        a.part_ms = m.part_ms;
-        a.out = m.xb;
-        a.n_heads = m.n_heads;
-        a.kv_mul = m.kv_mul;
-        a.hs = m.hs;
-        a.hq8 = m.hq8;
-        a.seq = m.seq_len;
-        a.t0 = t0;
-        a.na = pos - t0 + 1;
-        a.n_chunks = (a.na + 63) / 64;
-        a.head_seq = m.head_seq;
-        launch_attention(a, s);
+        // QK-norm, RoPE, KV write, Q quantization and attention (c:3232-3359)
+        launch_attention(m, l, m.xb, s);
         // output projection + residual (c:3362-3371)
         if (m.is_gemma) {
             gemv_batch(c, L.wo.type, one(L.wo, m.xb2, EPI_STORE), m.q_dim, m.xb, nullptr, "wo");
@@ -652,6 +625,54 @@ static void forward_impl(l3p_ctx* c, int token, int pos, bool with_logits) {
         gemv_batch(c, m.wcls.type, one(m.wcls, m.logits, EPI_STORE), m.dim, m.x, m.final_norm, "lm_head");
         if (m.is_gemma && m.softcap > 0.0f) launch_softcap(m.logits, m.vocab, m.softcap, s);
     }
+}
+
+void l3p_ctx::drop_graphs() {
+    for (int i = 0; i < 2; ++i) {
+        if (graph[i]) hipGraphExecDestroy(graph[i]);
+        graph[i] = nullptr;
+        graph_runs[i] = 0;
+    }
+}
+
+static bool graphs_enabled() {
+    static int on = -1;
+    if (on < 0) {
+        const char* e = getenv("L3P_GRAPH");
+        on = e ? atoi(e) != 0 : 1;
+    }
+    return on != 0;
+}
+
+// One step of transformer() (c:3190-3435): the embedding row and the step
+// record are written by an eager launch; the layers run as a replayed HIP
+// graph from the second step of each variant on (the first, eager, step also
+// settles every launch configuration).  Per-launch timing runs eagerly.
+static void forward_impl(l3p_ctx* c, int token, int pos, bool with_logits) {
+    Model& m = *c->model;
+    hipStream_t s = c->stream;
+    launch_embed_step(m.emb, token, pos, m.is_gemma ? m.embed_scale : 0.0f, m.x, m.step, s);
+    const int v = with_logits ? 1 : 0;
+    if (c->prof.on || !graphs_enabled() || c->graph_runs[v]++ == 0) {
+        layers_impl(c, with_logits);
+        return;
+    }
+    if (!c->graph[v]) {
+        hipGraph_t g = nullptr;
+        L3P_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+        try {
+            layers_impl(c, with_logits);
+        } catch (...) {
+            hipStreamEndCapture(s, &g);
+            if (g) hipGraphDestroy(g);
+            throw;
+        }
+        L3P_HIP(hipStreamEndCapture(s, &g));
+        hipError_t e = hipGraphInstantiate(&c->graph[v], g, nullptr, nullptr, 0);
+        hipGraphDestroy(g);
+        L3P_HIP(e);
+    }
+    L3P_HIP(hipGraphLaunch(c->graph[v], s));
 }
 
 // xorshift64* (c:4266-4276)
@@ -783,6 +804,7 @@ int l3p_load_gguf(l3p_ctx* c, const void* bytes, size_t len, const l3p_load_opts
     return mguard(c, false, [&] {
         L3P_REQUIRE(bytes, L3P_E_INVALID, "gguf pointer is NULL");
         L3P_HIP(hipStreamSynchronize(c->stream));
+        c->drop_graphs();
         delete c->model;
         c->model = nullptr;
         c->model = load_model(c, bytes, len, opts);

@@ -12,9 +12,8 @@ struct DevBuf {
 };
 
 struct Scratch {
-    DevBuf xq_buf, xd_buf, gemm_buf;
+    DevBuf xq_buf, gemm_buf;
     XQ8 xq(int cols);
-    XDig xdig(int cols);
     void release();
 };
 
@@ -29,21 +28,6 @@ struct Layer {
     Mat wq, wk, wv, wo, w1, w2, w3;
     float *att_norm = nullptr, *ffn_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr;
     float *post_att = nullptr, *post_ffn = nullptr;
-};
-
-// Attention launch parameters shared by the attention kernels.
-struct AttnArgs {
-    const int8_t* qq;      // [n_heads][hs] Q8_0 query quants
-    const float* qd;       // [n_heads][hs/32] their scales (fp32 value of the fp16 scale)
-    const uint8_t* kc;     // K cache allocation base; layer at kc + layer_off, [n_kv][seq][hq8]
-    const uint8_t* vc;     // V cache allocation base
-    size_t layer_off;
-    float* att;            // [n_heads][seq] scores, then exp
-    float* part_acc;       // [n_heads][max_chunks][hs] chunk outputs
-    float* part_ms;        // [n_heads][2][max_chunks] chunk softmax max and sum
-    float* out;            // [n_heads][hs]
-    int n_heads, kv_mul, hs, hq8, seq, t0, na, n_chunks;
-    size_t head_seq;
 };
 
 struct Model {
@@ -70,15 +54,14 @@ struct Model {
     int8_t* qq = nullptr;          // Q8_0 query [n_heads][hs]
     float* qd = nullptr;           // [n_heads][hs/32]
     XQ8 xq{};
-    XDig xd{};
     XPrep prep(const float* x) const {
         XPrep p;
         p.x = x;
         p.q8 = xq;
-        p.dig = xd;
         return p;
     }
-    float *att = nullptr, *part_acc = nullptr, *part_ms = nullptr;
+    float* part_acc = nullptr;     // [n_heads][max_chunks][hs + 2] attention chunk partials
+    int* step = nullptr;           // device {token, pos} of the step being computed
     int max_chunks = 0;
     // sampler scratch
     float* cand_val = nullptr;     // device: group maxima, then top-k slot values
@@ -135,20 +118,28 @@ struct l3p_ctx {
     Scratch scratch;
     Model* model = nullptr;
     Profiler prof;
+    // the layer stack of one forward step, captured once per variant
+    // (index: with logits) and replayed; dropped when the model changes
+    hipGraphExec_t graph[2] = {nullptr, nullptr};
+    int graph_runs[2] = {0, 0};
+    void drop_graphs();
 };
 
 // y = W . x through the fastest kernel for the type (model.cpp)
 void gemv_plain(l3p_ctx* c, int type, const GemvBatch& b, int cols, const float* x);
 
 // layers.hip
-void launch_embed(const Mat& emb, int token, float* x, hipStream_t s);
+// x = embedding row of `token` (times `scale` when non-zero) and the device
+// step record {token, pos} that the layer kernels read.
+void launch_embed_step(const Mat& emb, int token, int pos, float scale, float* x, int* step, hipStream_t s);
 void launch_rmsnorm(const float* x_in, float* x_scale_inplace, float scale, const float* w, int n, float inv_n,
                     float eps, float* out, const XPrep* xp, int form, hipStream_t s);
 // Launch the kernel that writes x in the form `type` consumes (none for fp32).
 void prepare_x(int type, int cols, const float* x, const XPrep& xp, hipStream_t s);
 void launch_rmsnorm_add(const float* y, const float* w, int n, float inv_n, float eps, float* x, hipStream_t s);
-void launch_rope_kv(const Model& m, int layer, int pos, hipStream_t s);
-void launch_attention(const AttnArgs& a, hipStream_t s);
+// QK-norm, RoPE, the K/V cache write and attention of one layer for the
+// step's position (c:3232-3359); out = [n_heads][head_dim].
+void launch_attention(const Model& m, int layer, float* out, hipStream_t s);
 void launch_softcap(float* logits, int n, float cap, hipStream_t s);
 void launch_argmax(const float* logits, int n, int* out, hipStream_t s, float* cv, int* ci);
 void launch_topk_slots(const float* logits, int n, int k, float* gmax, float* out_v, int* out_i, hipStream_t s);

@@ -160,3 +160,57 @@ def test_sampler_matches_oracle(pair, ctx, cpuref, torch_gpu):
         seed = s_ref
     t_gpu, _ = ctx.sample(torch_gpu.from_numpy(lo).cuda(), m.vocab, temperature=0.0)
     assert t_gpu == int(np.argmax(lo))
+
+
+def test_graph_replay_equals_eager(torch_gpu):
+    """From the second step on, the layer stack replays a captured HIP graph.
+    Every replay must give exactly the eager logits and KV cache; the eager
+    reference is a context with launch timing on (which runs eagerly), and
+    unrelated eager GEMVs run between the replays."""
+    g = synth.synthetic_model(**dict(MODELS["gemma_q8_0"], n_layers=3))
+    rng = np.random.default_rng(14)
+    toks = rng.integers(0, 2048, 24).astype(np.int32)
+    w = torch_gpu.from_numpy(synth.random_blocks(synth.Q8_0, 256, 512, seed=3)).cuda()
+    xg = torch_gpu.from_numpy(synth.random_x(512, seed=4)).cuda()
+    yg = torch_gpu.empty(256, device="cuda")
+    with l3p.Context(0) as eager, l3p.Context(0) as graphed:
+        eager.load_gguf(g)
+        graphed.load_gguf(g)
+        eager.profile(True)
+        for c in (eager, graphed):
+            c.prefill(toks[:16], 0)
+        for i in range(16, 24):
+            a = eager.forward(int(toks[i]), i)
+            graphed.gemv(synth.Q8_0, w, 256, 512, xg, yg)       # eager work between replays
+            b = graphed.forward(int(toks[i]), i)
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"step {i}"
+        for layer in range(3):
+            for wv in (False, True):
+                assert np.array_equal(eager.copy_kv(layer, wv), graphed.copy_kv(layer, wv))
+
+
+@pytest.mark.parametrize("dim,heads,kv", [(256, 8, 8), (768, 8, 4), (512, 16, 1), (256, 4, 1)])
+def test_head_shapes(torch_gpu, cpuref, dim, heads, kv):
+    """Head sizes 32, 96, 32 and 64 with KV groups of 1, 2, 16 and 4 heads,
+    across more than one 64-position chunk: logits within the full-model
+    tolerance and the layer-0 KV cache equal up to one-step quant flips (the
+    K/V projections sum in another fp32 order, so a value on a rounding
+    boundary may quantize one step apart)."""
+    g = synth.synthetic_model(arch="llama", dim=dim, hidden=256, n_layers=2, n_heads=heads, n_kv=kv, vocab=512,
+                              ctx=256, qtype=synth.Q8_0, seed=dim + heads, norm_jitter=0.1)
+    toks = np.random.default_rng(dim).integers(0, 512, 75).astype(np.int32)
+    with l3p.Context(0) as c2:
+        c2.load_gguf(g)
+        m = cpuref.open_model(g)
+        c2.prefill(toks[:70], 0)
+        m.prefill(toks, 0, 32)
+        m.prefill(toks, 32, 32)
+        m.prefill(toks, 64, 6)
+        for i in range(70, 75):
+            a = m.forward(int(toks[i]), i)
+            b = c2.forward(int(toks[i]), i)
+            assert float(np.max(np.abs(a - b))) <= 1e-2 * rms(a), (dim, heads, kv, i)
+        for wv in (False, True):
+            d = kv_quant_diff(c2.copy_kv(0, wv), m.kv(0, wv), m, 75)
+            assert d.max() <= 1 and d.mean() < 0.01, (dim, heads, kv, wv, int(d.max()), float(d.mean()))
+        m.close()
