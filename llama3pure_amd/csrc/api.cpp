@@ -61,7 +61,6 @@ void l3p_destroy(l3p_ctx* c) {
     c->drop_graphs();
     delete c->model;
     c->model = nullptr;
-    c->scratch.release();
     c->prof.release();
     hipStreamDestroy(c->stream);
     delete c;
@@ -169,35 +168,3 @@ int l3p_gemm(l3p_ctx* c, int type, const void* w, int rows, int cols, const floa
 }
 
 }  // extern "C"
-
-// ---------------------------------------------------------------------------
-// scratch
-// ---------------------------------------------------------------------------
-void DevBuf::ensure(size_t n) {
-    if (n <= cap) return;
-    release();
-    hipError_t e = hipMalloc(&p, n);
-    if (e == hipErrorOutOfMemory) throw L3pError{L3P_E_NOMEM, "scratch: out of device memory"};
-    L3P_HIP(e);
-    cap = n;
-}
-void DevBuf::release() {
-    if (p) hipFree(p);
-    p = nullptr;
-    cap = 0;
-}
-
-XQ8 Scratch::xq(int cols) {
-    const size_t nb = (size_t)cols / 32;
-    xq_buf.ensure(cols + nb * 8 + 64);
-    XQ8 q;
-    q.qs = (int8_t*)xq_buf.p;
-    q.d = (float*)((char*)xq_buf.p + (cols + 15) / 16 * 16);
-    q.sum = (int32_t*)((char*)q.d + nb * 4);
-    return q;
-}
-
-void Scratch::release() {
-    xq_buf.release();
-    gemm_buf.release();
-}

@@ -1,665 +1,805 @@
-// gemv.hip — decode GEMVs over GGUF blocks in their native layout (gfx950).
+// gemv.hip — streaming decode GEMVs over GGUF Q8_0, Q4_0, Q4_K and Q6_K rows
+// (gfx950), split over 2048-element column chunks, with the activation's
+// RMSNorm (and, for Q4_0, its Q8_0 form) computed in the prologue.
 //
-// One workgroup owns a tile of R consecutive rows of a matrix and the whole
-// K extent.  Thread t owns block column t (32 consecutive inputs; for K-quants
-// the 32-input sub-block t), keeps its 32 inputs of x in registers and walks
-// the R rows of the tile:
+// Work split.  A row of `cols` elements is cut into NC = ceil(cols/2048)
+// chunks of 2048 elements: 64 Q8_0 / Q4_0 blocks (2176 / 1152 B) or 8 Q4_K /
+// Q6_K super-blocks (1152 / 1680 B).  A workgroup has NC waves; wave c owns
+// chunk column c of every row it processes, and lane l owns the 32 elements
+// [2048c + 32l, +32) (a Q8_0/Q4_0 block, a Q4_K sub-block, a quarter of a
+// Q6_K half super-block), so the activation of those elements is prepared
+// once and kept in registers for the whole kernel.  Workgroups walk groups of
+// G consecutive rows (persistent over the grid).
 //
-//   1. the tile, R*row_bytes contiguous bytes of HBM, is copied into LDS with
-//      coalesced 16-byte loads (rows are 16-byte multiples for every shape of
-//      the Llama-3 / Gemma dimensions);
-//   2. each thread reads its block of every row back from LDS as aligned
-//      dwords and realigns it in registers (Q8_0 and Q4_0 blocks are 34 and
-//      18 bytes, so odd columns start 2 bytes into a dword);
-//   3. partial sums are reduced across the workgroup (wave butterfly, then a
-//      fixed-order sum over waves), so results are deterministic.
+// Streaming.  Each wave copies its own chunks HBM -> LDS with
+// global_load_lds (dwordx4 pieces and a dword piece, cache policy nt: the
+// weights are read once per call) into a private ring of NB buffers, keeping
+// NB-1 chunks in flight, and waits for a chunk with its own vmcnt: no
+// workgroup barrier inside the row loop.  The only barrier is per row group,
+// for the cross-wave sum.
 //
-// Arithmetic per type follows the reference's matmul_quantized dispatch
-// (llama3pure-c-engine.c:2091-2133): Q8_0/Q4_K/Q6_K weights are dequantized
-// exactly and multiplied with fp32 x (matmul_deq_4row, c:2136-2176); Q4_0
-// takes x quantized to Q8_0 and exact integer block dots (c:1625-1643).
-// Only the fp32 summation order differs from the reference's sequential loop.
+// Row alignment.  When a row's length in bytes is a multiple of 16 (cols a
+// multiple of 256 for Q8_0/Q4_0, of 2048 for Q6_K, always for Q4_K) every
+// chunk starts 16-byte aligned.  Otherwise (UA kernels) a chunk is copied from
+// its address rounded down to 16, its data lands `sh` = address % 16 bytes
+// into the buffer, and each lane recomputes where its elements sit.  Copies
+// then reach at most to the end of the 16-byte granule that holds the row's
+// last byte, which lies in the same page as that byte.
+//
+// Arithmetic per lane (32 elements j):
+//   Q8_0: d * sum q_j x_j, fp32 FMAs on the fp32 activation (the reference
+//         dequantizes exactly, q*d, and sums fp32 products, c:2136-2176);
+//   Q4_0: the reference's integer block dot against the Q8_0 activation,
+//         dw*dx*(float)isum (vec_dot_q4_0_q8_0, c:1625-1643);
+//   Q4_K: (d*sc) * sum q_j x_j - (dmin*m) * sum x_j with the sub-block's
+//         6-bit scale and min (get_scale_min_k4 + dequantize_row_q4_K,
+//         c:705-746);
+//   Q6_K: d * sum over the two 16-element halves of sc_h * (sum u_j x_j -
+//         32 sum x_j), u = q + 32 the 6-bit code (dequantize_row_q6_K,
+//         c:873-904).
+// The reference rounds w_j = dequant(q_j) and then sums w_j x_j in fp32; the
+// factored forms differ from it only in fp32 rounding order.
+// Row totals: per-lane partials of the G rows are transposed-reduced across
+// the wave, then summed over the NC waves in chunk order, so results do not
+// depend on timing.
+//
+// Prologue (optional RMSNorm, c:3117-3129): every workgroup computes
+// ss = sum(x^2) in one fixed order and r = 1/sqrt(ss/n + eps); lane l then
+// forms w[j] * (r * x[j]) for its elements and prepares them.  The lane's x
+// and norm loads are issued first, then the first weight copies, so HBM is
+// busy while the activation is prepared.
 #include "device_common.h"
 #include "internal.h"
 
+#include <map>
+#include <mutex>
+#include <tuple>
+
 namespace {
 
-constexpr int kMaxThreads = 1024;
-
 using namespace l3pd;
+typedef __attribute__((address_space(3))) void lds_void;
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
+constexpr int kChunkElems = 2048;   // 64 lanes x 32 elements
+constexpr int kMaxWaves = 16;       // chunk columns per row: cols <= 32768
+constexpr int kMaxOut = 4096;       // per-workgroup result slots kept in LDS
 
-// Copy `nbytes` (a multiple of 4) from 16-byte aligned global memory to LDS.
-// Weights are streamed once per call, so the loads are marked non-temporal.
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ void tile_to_lds(uint32_t* lds, const uint8_t* __restrict__ src, int nbytes,
-                                            int t, int nt) {
-    const int n16 = nbytes >> 4;
-    const u32x4* s = reinterpret_cast<const u32x4*>(src);
-    u32x4* d = reinterpret_cast<u32x4*>(lds);
-    int c = t;
-    for (; c + 3 * nt < n16; c += 4 * nt) {
-        u32x4 a0 = __builtin_nontemporal_load(s + c);
-        u32x4 a1 = __builtin_nontemporal_load(s + c + nt);
-        u32x4 a2 = __builtin_nontemporal_load(s + c + 2 * nt);
-        u32x4 a3 = __builtin_nontemporal_load(s + c + 3 * nt);
-        d[c] = a0;
-        d[c + nt] = a1;
-        d[c + 2 * nt] = a2;
-        d[c + 3 * nt] = a3;
-    }
-    for (; c < n16; c += nt) d[c] = __builtin_nontemporal_load(s + c);
-    const int rem = (nbytes & 15) >> 2;
-    if (t < rem) lds[(n16 << 2) + t] = reinterpret_cast<const uint32_t*>(src)[(n16 << 2) + t];
-}
-
-// Locate the workgroup's segment and first row.  In pair mode both segments
-// share the row range.
-struct TileLoc {
-    int seg, r0, nr;
+// Storage unit of a type (a block or super-block) and how a chunk is copied:
+// kX4 dwordx4 instructions (1024 B each) and, with kTail, one dword
+// instruction (256 B).  The pieces cover kChunkBytes + 14 (the largest start
+// offset of an unaligned chunk); clamped lanes write past the data, so a
+// buffer is kBufBytes long.
+template <int UE, int UB, int X4, int TAIL>
+struct FmtBase {
+    static constexpr int kUnitElems = UE;
+    static constexpr int kUnitBytes = UB;
+    static constexpr int kChunkBytes = kChunkElems / UE * UB;
+    static constexpr int kX4 = X4;
+    static constexpr int kTail = TAIL;
+    static constexpr int kCI = X4 + TAIL;   // copy instructions per chunk
+    static constexpr int kBufBytes = X4 * 1024 + TAIL * 256;
+    static_assert(kChunkBytes + 14 <= kBufBytes, "copy pieces must cover an unaligned chunk");
 };
-template <int R, bool PAIR>
-__device__ __forceinline__ TileLoc locate(const GemvBatch& B) {
-    int bid = blockIdx.x, s = 0;
-    if (!PAIR) {
-        while (s < B.nseg - 1) {
-            int nt = (B.seg[s].rows + R - 1) / R;
-            if (bid < nt) break;
-            bid -= nt;
-            ++s;
-        }
-    }
-    TileLoc L;
-    L.seg = s;
-    L.r0 = bid * R;
-    L.nr = min(R, B.seg[s].rows - L.r0);
-    return L;
+template <int QT>
+struct Fmt;
+template <> struct Fmt<L3P_Q8_0> : FmtBase<32, 34, 2, 1> {};    // 2176 B chunks
+template <> struct Fmt<L3P_Q4_0> : FmtBase<32, 18, 1, 1> {};    // 1152 B
+template <> struct Fmt<L3P_Q4_K> : FmtBase<256, 144, 1, 1> {};  // 1152 B, always aligned
+template <> struct Fmt<L3P_Q6_K> : FmtBase<256, 210, 2, 0> {};  // 1680 B
+
+template <int QT>
+__host__ __device__ __forceinline__ uint32_t row_bytes(int cols) {
+    return (uint32_t)(cols / Fmt<QT>::kUnitElems) * Fmt<QT>::kUnitBytes;
 }
 
-// Reduce acc[NRR] over the workgroup and apply the epilogue.
-template <int R, bool PAIR>
-__device__ __forceinline__ void finish(const GemvBatch& B, const TileLoc& L, float* acc, float* red) {
-    constexpr int NRR = PAIR ? 2 * R : R;
-    const int t = threadIdx.x, lane = t & 63, w = t >> 6, nw = blockDim.x >> 6;
+// Barrier for LDS traffic only (no wait on outstanding vector memory, which
+// __syncthreads' release fence would add).
+__device__ __forceinline__ void lds_sync() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+__device__ __forceinline__ void wait_lgkm() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// Wait until at most N of this wave's vector-memory operations are outstanding
+// (s_waitcnt on gfx9: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] << 14).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// Byte offsets this lane copies, from the copy base, for a chunk whose data
+// is bytes [0, span) of the copy: dwordx4 pieces over [0, 1024 kX4), the
+// dword piece over [1024 kX4, +256).  Offsets are clamped to the last whole
+// piece that ends within span rounded up to 16 (or 4), so lanes past the data
+// re-read its last bytes (landing past span in the buffer, never read).
+// Every chunk is therefore exactly kCI instructions with all lanes active, a
+// constant the waits count on.
+struct DmaLane {
+    int o0, o1;   // the dwordx4 pieces (o1 unused when kX4 == 1)
+    int ot;       // the dword piece (unused without a tail)
+};
+template <int QT>
+__device__ __forceinline__ DmaLane dma_lane(int lane, int span) {
+    const int e16 = ((span + 15) & ~15) - 16, e4 = ((span + 3) & ~3) - 4;
+    DmaLane d;
+    d.o0 = min(lane * 16, e16);
+    d.o1 = min(1024 + lane * 16, e16);
+    d.ot = min(Fmt<QT>::kX4 * 1024 + lane * 4, e4);
+    return d;
+}
+// HBM -> LDS copy of one chunk into this wave's buffer dst (lane i of an
+// instruction writes the instruction's LDS base + 16 i, or + 4 i for the dword piece).
+template <int QT>
+__device__ __forceinline__ void chunk_dma(uint32_t* dst, const uint8_t* src, DmaLane d) {
+    __builtin_amdgcn_global_load_lds(src + d.o0, (lds_void*)dst, 16, 0, 2);
+    if (Fmt<QT>::kX4 > 1) __builtin_amdgcn_global_load_lds(src + d.o1, (lds_void*)(dst + 256), 16, 0, 2);
+    if (Fmt<QT>::kTail)
+        __builtin_amdgcn_global_load_lds(src + d.ot, (lds_void*)(dst + Fmt<QT>::kX4 * 256), 4, 0, 2);
+}
+
+template <int N>
+__device__ __forceinline__ constexpr int log2c() {
+    return N >= 32 ? 5 : N >= 16 ? 4 : N >= 8 ? 3 : N >= 4 ? 2 : N >= 2 ? 1 : 0;
+}
+// Lane group of `lane` after xreduce<N>: which of the N values it holds.
+template <int N>
+__device__ __forceinline__ int rowof(int lane) {
+    constexpr int L = log2c<N>();
+    int r = 0;
 #pragma unroll
-    for (int i = 0; i < NRR; ++i) {
-        float v = wave_sum(acc[i]);
-        if (lane == 0) red[w * NRR + i] = v;
+    for (int s = 0; s < L; ++s) r |= ((lane >> (5 - s)) & 1) << (L - 1 - s);
+    return r;
+}
+// Transpose-reduce N per-lane values over the wave: afterwards every lane of
+// group g (64/N consecutive lanes) holds the wave total of value rowof<N>(lane).
+template <int N>
+__device__ __forceinline__ float xreduce(float (&v)[N], int lane) {
+    constexpr int L = log2c<N>();
+#pragma unroll
+    for (int s = 0; s < L; ++s) {
+        const int m = 32 >> s;
+        const bool up = (lane & m) != 0;
+        const int half = N >> (s + 1);
+#pragma unroll
+        for (int i = 0; i < (N >> 1); ++i) {
+            if (i < half) {
+                float lo = v[i], hi = v[i + half];
+                // keep both as register values: a select between two array
+                // elements would otherwise become a per-lane indexed load
+                asm volatile("" : "+v"(lo), "+v"(hi));
+                const float send = up ? lo : hi;
+                const float keep = up ? hi : lo;
+                v[i] = keep + __shfl_xor(send, m, 64);
+            }
+        }
     }
-    __syncthreads();
-    if (t < L.nr) {
+    float r = v[0];
+#pragma unroll
+    for (int m = 32 >> L; m > 0; m >>= 1) r += __shfl_xor(r, m, 64);
+    return r;
+}
+
+struct GemvArgs {
+    const uint8_t* w[3];
+    float* y[3];
+    int rows[3];        // rows per segment; pair mode: rows[0] == rows[1]
+    int nseg;
+    int epilogue;       // GemvEpilogue
+    int cols;
+    int rows_total;     // sum of rows (pair: rows[0])
+    int ngroups;
+    const float* x;     // fp32 activation
+    const float* norm;  // RMSNorm weights, or null for x as is
+    float eps, inv_n;
+};
+
+// Row `i` of the concatenated row space -> (segment, local row).
+__device__ __forceinline__ void seg_of(const GemvArgs& a, int i, int& s, int& r) {
+    s = 0;
+    r = i;
+    if (a.nseg > 1 && r >= a.rows[0]) {
+        r -= a.rows[0];
+        s = 1;
+        if (a.nseg > 2 && r >= a.rows[1]) {
+            r -= a.rows[1];
+            s = 2;
+        }
+    }
+}
+
+// The rows a wave streams, as wave-uniform values.
+struct Cursor {
+    const uint8_t *w0, *w1, *w2;
+    int rows0, rows1, rows_total, ngroups, bid, gdim;
+    uint32_t rb;      // row bytes
+    uint32_t coff;    // byte offset of this wave's chunk column in a row
+};
+
+// Row-chunk k of this workgroup's sequence: group j = blockIdx.x + (k / G) *
+// gridDim.x, row slot i = k % G.  Pair mode: slots [0, G/2) are gate rows,
+// [G/2, G) the matching up rows.  Sets src to the chunk and returns true for
+// a real row; past the end it returns false with src at the same chunk column
+// of the first row (a valid dummy copy of the same size).
+template <int G, bool PAIR>
+__device__ __forceinline__ bool chunk_src(const Cursor& cc, int k, const uint8_t*& src) {
+    const int j = cc.bid + (k / G) * cc.gdim;
+    const int i = k % G;
+    const uint8_t* base = cc.w0;
+    int r;
+    bool ok = j < cc.ngroups;
+    if (PAIR) {
+        r = j * (G / 2) + (i % (G / 2));
+        if (i >= G / 2) base = cc.w1;
+        ok = ok && r < cc.rows0;
+    } else {
+        r = j * G + i;
+        ok = ok && r < cc.rows_total;
+        if (r >= cc.rows0) {
+            r -= cc.rows0;
+            base = cc.w1;
+            if (r >= cc.rows1) {
+                r -= cc.rows1;
+                base = cc.w2;
+            }
+        }
+    }
+    if (!ok) {
+        base = cc.w0;
+        r = 0;
+    }
+    src = base + (size_t)r * cc.rb + cc.coff;
+    return ok;
+}
+
+// Activation of one lane's 32 elements in the form the weight type consumes.
+struct XBlock {
+    float x[32];    // Q8_0, Q4_K, Q6_K: the fp32 values
+    int q[8];       // Q4_0: the Q8_0 quants, four per dword
+    float s;        // Q4_0: fp32 value of the Q8_0 scale
+    int sum8;       // Q4_0: 8 * sum of quants
+    float xs;       // Q4_K: sum of the 32 values
+    float xs0, xs1; // Q6_K: sums of values 0..15 and 16..31
+};
+
+template <int QT>
+__device__ __forceinline__ void prepare_block(const float* v, XBlock& xb) {
+    if (QT == L3P_Q4_0) {
+        QBlock qb;
+        quantize32(v, qb);
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            xb.q[e] = (int)((uint32_t)(uint8_t)qb.q[4 * e] | ((uint32_t)(uint8_t)qb.q[4 * e + 1] << 8) |
+                            ((uint32_t)(uint8_t)qb.q[4 * e + 2] << 16) | ((uint32_t)(uint8_t)qb.q[4 * e + 3] << 24));
+        xb.s = h2f_exact(qb.dh);
+        xb.sum8 = 8 * qb.sum;
+    } else {
+#pragma unroll
+        for (int j = 0; j < 32; ++j) xb.x[j] = v[j];
         float a = 0.0f, b = 0.0f;
-        for (int k = 0; k < nw; ++k) {
-            a += red[k * NRR + t];
-            if (PAIR) b += red[k * NRR + R + t];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            a += v[j];
+            b += v[16 + j];
         }
-        const int r = L.r0 + t;
-        if (PAIR) {
-            B.seg[0].y[r] = B.epilogue == EPI_GEGLU ? ref_geglu(a, b) : ref_swiglu(a, b);
-        } else {
-            float* y = B.seg[L.seg].y;
-            if (B.epilogue == EPI_ADD) y[r] += a;
-            else y[r] = a;
-        }
+        xb.xs0 = a;
+        xb.xs1 = b;
+        xb.xs = a + b;
     }
 }
 
-// ---------------------------------------------------------------------------
-// Q8_0: 34-byte blocks {fp16 d; int8 q[32]} (c:127-130), w = q*d exactly.
-// ---------------------------------------------------------------------------
-template <int R, bool PAIR>
-__global__ void __launch_bounds__(kMaxThreads) gemv_q8_0_kernel(GemvBatch B, int cols,
-                                                                 const float* __restrict__ x) {
-    extern __shared__ __align__(16) uint32_t lds[];
-    constexpr int NRR = PAIR ? 2 * R : R;
-    const int nb = cols >> 5;
-    const uint32_t rb = (uint32_t)nb * 34u;
-    const int t = threadIdx.x, nt = blockDim.x;
-    const TileLoc L = locate<R, PAIR>(B);
+// Where a lane's 32 elements sit in a chunk buffer whose data starts at byte
+// sh (0 for aligned rows), and their dot with the lane's activation.
+//
+// Q8_0 / Q4_0: the lane's block starts at byte b = sh + BB*lane.  Its fp16
+// scale is the halfword b/2 (b is even: blocks and rows have even lengths);
+// its quants start at b + 2, which is dword-aligned when b % 4 == 2 and 2
+// bytes into a dword otherwise.  Reading dwords from `first` and taking
+// alignbyte(dw[k+1], dw[k], shift) gives the k-th quant dword in both cases
+// with one instruction and no branch.
+template <int QT>
+struct Lane {
+    uint32_t half, first, shift;
 
-    tile_to_lds(lds, B.seg[L.seg].w + (size_t)L.r0 * rb, L.nr * rb, t, nt);
-    if (PAIR) tile_to_lds(lds + (R * rb >> 2), B.seg[1].w + (size_t)L.r0 * rb, L.nr * rb, t, nt);
-
-    const bool active = t < nb;
-    float xv[32];
-    if (active) {
-        const float4* xp = reinterpret_cast<const float4*>(x + 32 * t);
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            float4 v = xp[k];
-            xv[4 * k] = v.x; xv[4 * k + 1] = v.y; xv[4 * k + 2] = v.z; xv[4 * k + 3] = v.w;
-        }
+    __device__ __forceinline__ void at(int lane, uint32_t sh) {
+        const uint32_t b = sh + (uint32_t)lane * Fmt<QT>::kUnitBytes;
+        const bool odd = (b & 2u) != 0;
+        half = b >> 1;
+        first = (b >> 2) + (odd ? 1u : 0u);
+        shift = odd ? 0u : 2u;
     }
-    __syncthreads();
 
-    float acc[NRR];
-    // Even columns start dword-aligned: d in the low half, quants 2 bytes in.
-    // Odd columns start 2 bytes into a dword: d in the high half, quants
-    // dword-aligned one dword later.
-    const uint32_t qsh = (t & 1) ? 32u : 16u;
-    const uint32_t dsh = (t & 1) ? 16u : 0u;
-#pragma unroll
-    for (int i = 0; i < NRR; ++i) {
-        float a = 0.0f;
-        if (active && (i % R) < L.nr) {
-            const uint32_t E = ((uint32_t)i * rb + 34u * (uint32_t)t) >> 2;
+    //   Q8_0: d * sum_j q_j x_j with fp32 FMAs;
+    //   Q4_0: dw*dx*(float)isum, isum the exact integer dot.
+    __device__ __forceinline__ float dot(const uint32_t* buf, const XBlock& xb) const {
+        const float d = h2f(reinterpret_cast<const uint16_t*>(buf)[half]);
+        const uint32_t* p = buf + first;
+        if (QT == L3P_Q8_0) {
             uint32_t dw[9];
 #pragma unroll
-            for (int k = 0; k < 9; ++k) dw[k] = lds[E + k];
-            const float d = h2f(dw[0] >> dsh);
-            float s0 = 0.0f, s1 = 0.0f;
+            for (int k = 0; k < 9; ++k) dw[k] = p[k];
+            float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
 #pragma unroll
             for (int k = 0; k < 8; ++k) {
-                const uint32_t q = shr64(dw[k], dw[k + 1], qsh);
-                s0 = fmaf((float)(int8_t)(q), xv[4 * k + 0], s0);
-                s1 = fmaf((float)(int8_t)(q >> 8), xv[4 * k + 1], s1);
-                s0 = fmaf((float)(int8_t)(q >> 16), xv[4 * k + 2], s0);
-                s1 = fmaf((float)(int8_t)(q >> 24), xv[4 * k + 3], s1);
+                const uint32_t q = __builtin_amdgcn_alignbyte(dw[k + 1], dw[k], shift);
+                s0 = fmaf((float)(int8_t)(q & 0xffu), xb.x[4 * k], s0);
+                s1 = fmaf((float)(int8_t)((q >> 8) & 0xffu), xb.x[4 * k + 1], s1);
+                s2 = fmaf((float)(int8_t)((q >> 16) & 0xffu), xb.x[4 * k + 2], s2);
+                s3 = fmaf((float)(int8_t)(q >> 24), xb.x[4 * k + 3], s3);
             }
-            a = (s0 + s1) * d;
-        }
-        acc[i] = a;
-    }
-    float* red = reinterpret_cast<float*>(lds) + ((PAIR ? 2 : 1) * R * rb + 15) / 16 * 4;
-    finish<R, PAIR>(B, L, acc, red);
-}
-
-// ---------------------------------------------------------------------------
-// Q4_0: 18-byte blocks {fp16 d; u8 qs[16]} (c:151-154) against Q8_0 x.
-// Per block: isum = sum xq*(q-8) exactly, term = dw*dx*(float)isum
-// (vec_dot_q4_0_q8_0, c:1625-1643).
-// ---------------------------------------------------------------------------
-template <int R, bool PAIR>
-__global__ void __launch_bounds__(kMaxThreads) gemv_q4_0_kernel(GemvBatch B, int cols, XQ8 xq) {
-    extern __shared__ __align__(16) uint32_t lds[];
-    constexpr int NRR = PAIR ? 2 * R : R;
-    const int nb = cols >> 5;
-    const uint32_t rb = (uint32_t)nb * 18u;
-    const int t = threadIdx.x, nt = blockDim.x;
-    const TileLoc L = locate<R, PAIR>(B);
-
-    tile_to_lds(lds, B.seg[L.seg].w + (size_t)L.r0 * rb, L.nr * rb, t, nt);
-    if (PAIR) tile_to_lds(lds + (R * rb >> 2), B.seg[1].w + (size_t)L.r0 * rb, L.nr * rb, t, nt);
-
-    const bool active = t < nb;
-    int xw[8];
-    float dx = 0.0f;
-    int xsum8 = 0;
-    if (active) {
-        const int4* xp = reinterpret_cast<const int4*>(xq.qs + 32 * t);
-        int4 a = xp[0], b = xp[1];
-        xw[0] = a.x; xw[1] = a.y; xw[2] = a.z; xw[3] = a.w;
-        xw[4] = b.x; xw[5] = b.y; xw[6] = b.z; xw[7] = b.w;
-        dx = xq.d[t];
-        xsum8 = 8 * xq.sum[t];
-    }
-    __syncthreads();
-
-    float acc[NRR];
-    const uint32_t qsh = (t & 1) ? 32u : 16u;
-    const uint32_t dsh = (t & 1) ? 16u : 0u;
-#pragma unroll
-    for (int i = 0; i < NRR; ++i) {
-        float a = 0.0f;
-        if (active && (i % R) < L.nr) {
-            const uint32_t E = ((uint32_t)i * rb + 18u * (uint32_t)t) >> 2;
+            return ((s0 + s1) + (s2 + s3)) * d;
+        } else {
             uint32_t dw[5];
 #pragma unroll
-            for (int k = 0; k < 5; ++k) dw[k] = lds[E + k];
-            const float dw16 = h2f(dw[0] >> dsh);
-            int isum = -xsum8;
+            for (int k = 0; k < 5; ++k) dw[k] = p[k];
+            int isum = -xb.sum8;
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
-                const uint32_t q = shr64(dw[k], dw[k + 1], qsh);
-                isum = __builtin_amdgcn_sdot4((int)(q & 0x0f0f0f0fu), xw[k], isum, false);
-                isum = __builtin_amdgcn_sdot4((int)((q >> 4) & 0x0f0f0f0fu), xw[4 + k], isum, false);
+                const uint32_t q = __builtin_amdgcn_alignbyte(dw[k + 1], dw[k], shift);
+                isum = __builtin_amdgcn_sdot4((int)(q & 0x0f0f0f0fu), xb.q[k], isum, false);
+                isum = __builtin_amdgcn_sdot4((int)((q >> 4) & 0x0f0f0f0fu), xb.q[4 + k], isum, false);
             }
-            a = dw16 * dx * (float)isum;
-        }
-        acc[i] = a;
-    }
-    float* red = reinterpret_cast<float*>(lds) + ((PAIR ? 2 : 1) * R * rb + 15) / 16 * 4;
-    finish<R, PAIR>(B, L, acc, red);
-}
-
-// ---------------------------------------------------------------------------
-// Q4_K: 144-byte super-blocks {fp16 d, dmin; u8 scales[12]; u8 qs[128]}
-// (c:157-162), 8 sub-blocks of 32 with 6-bit scale/min (c:705-746):
-// w = (d*sc)*q - dmin*m.  Thread t owns sub-block j = t%8 of super-block
-// t/8 and evaluates d1*sum(q*x) - m1*sum(x), with d1 = d*sc and m1 =
-// dmin*m exact products.
-// ---------------------------------------------------------------------------
-template <int R, bool PAIR>
-__global__ void __launch_bounds__(kMaxThreads) gemv_q4_k_kernel(GemvBatch B, int cols,
-                                                                 const float* __restrict__ x) {
-    extern __shared__ __align__(16) uint32_t lds[];
-    constexpr int NRR = PAIR ? 2 * R : R;
-    const int nsub = cols >> 5;
-    const uint32_t rb = (uint32_t)(cols >> 8) * 144u;
-    const int t = threadIdx.x, nt = blockDim.x;
-    const TileLoc L = locate<R, PAIR>(B);
-
-    tile_to_lds(lds, B.seg[L.seg].w + (size_t)L.r0 * rb, L.nr * rb, t, nt);
-    if (PAIR) tile_to_lds(lds + (R * rb >> 2), B.seg[1].w + (size_t)L.r0 * rb, L.nr * rb, t, nt);
-
-    const bool active = t < nsub;
-    const int j = t & 7;           // sub-block within the super-block
-    const int sb = t >> 3;
-    float xv[32];
-    float xs = 0.0f;
-    if (active) {
-        const float4* xp = reinterpret_cast<const float4*>(x + 32 * t);
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            float4 v = xp[k];
-            xv[4 * k] = v.x; xv[4 * k + 1] = v.y; xv[4 * k + 2] = v.z; xv[4 * k + 3] = v.w;
-        }
-#pragma unroll
-        for (int k = 0; k < 32; ++k) xs += xv[k];
-    }
-    __syncthreads();
-
-    float acc[NRR];
-    const uint32_t nsh = (j & 1) ? 4u : 0u;
-#pragma unroll
-    for (int i = 0; i < NRR; ++i) {
-        float a = 0.0f;
-        if (active && (i % R) < L.nr) {
-            const uint32_t E = ((uint32_t)i * rb + 144u * (uint32_t)sb) >> 2;
-            const uint4 hdr = *reinterpret_cast<const uint4*>(lds + E);   // d,dmin,scales[12]
-            const float d = h2f(hdr.x), dmin = h2f(hdr.x >> 16);
-            // 6-bit scale/min of sub-block j (get_scale_min_k4, c:705-714)
-            const uint32_t bs = 8u * (uint32_t)(j & 3);
-            const uint32_t b0 = (hdr.y >> bs) & 0xffu, b1 = (hdr.z >> bs) & 0xffu, b2 = (hdr.w >> bs) & 0xffu;
-            const uint32_t sc = j < 4 ? (b0 & 63u) : ((b2 & 0x0fu) | ((b0 >> 6) << 4));
-            const uint32_t mn = j < 4 ? (b1 & 63u) : ((b2 >> 4) | ((b1 >> 6) << 4));
-            const float d1 = d * (float)sc, m1 = dmin * (float)mn;
-            const uint4* qp = reinterpret_cast<const uint4*>(lds + E + 4 + 8 * (j >> 1));
-            const uint4 qa = qp[0], qb = qp[1];
-            const uint32_t qw[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
-            float s0 = 0.0f, s1 = 0.0f;
-#pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                const uint32_t q = (qw[k] >> nsh) & 0x0f0f0f0fu;
-                s0 = fmaf((float)(q & 0xffu), xv[4 * k + 0], s0);
-                s1 = fmaf((float)((q >> 8) & 0xffu), xv[4 * k + 1], s1);
-                s0 = fmaf((float)((q >> 16) & 0xffu), xv[4 * k + 2], s0);
-                s1 = fmaf((float)(q >> 24), xv[4 * k + 3], s1);
-            }
-            a = d1 * (s0 + s1) - m1 * xs;
-        }
-        acc[i] = a;
-    }
-    float* red = reinterpret_cast<float*>(lds) + ((PAIR ? 2 : 1) * R * rb + 15) / 16 * 4;
-    finish<R, PAIR>(B, L, acc, red);
-}
-
-// ---------------------------------------------------------------------------
-// Q6_K: 210-byte super-blocks {u8 ql[128]; u8 qh[64]; i8 sc[16]; fp16 d}
-// (c:190-195), w = d*sc*(q-32) exactly (c:873-904).  Thread t owns, in
-// super-block t/8, half h = (t%8)/4 and l in [8c, 8c+8) with c = t%4: four
-// runs of 8 elements (offsets 0, 32, 64, 96 of the half), each run sharing
-// one sub-scale.  Per run: (d*sc) * (sum(q*x) - 32*sum(x)).
-// ---------------------------------------------------------------------------
-template <int R, bool PAIR>
-__global__ void __launch_bounds__(kMaxThreads) gemv_q6_k_kernel(GemvBatch B, int cols,
-                                                                 const float* __restrict__ x) {
-    extern __shared__ __align__(16) uint32_t lds[];
-    constexpr int NRR = PAIR ? 2 * R : R;
-    const int nthr = cols >> 5;
-    const uint32_t rb = (uint32_t)(cols >> 8) * 210u;
-    const int t = threadIdx.x, nt = blockDim.x;
-    const TileLoc L = locate<R, PAIR>(B);
-
-    tile_to_lds(lds, B.seg[L.seg].w + (size_t)L.r0 * rb, L.nr * rb, t, nt);
-    if (PAIR) tile_to_lds(lds + (R * rb >> 2), B.seg[1].w + (size_t)L.r0 * rb, L.nr * rb, t, nt);
-
-    const bool active = t < nthr;
-    const int sb = t >> 3, h = (t >> 2) & 1, c = t & 3;
-    float xv[32];     // xv[8*g + e] = x[256*sb + 128*h + 32*g + 8*c + e]
-    float xs[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (active) {
-        const float* xb = x + 256 * sb + 128 * h + 8 * c;
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            const float4* xp = reinterpret_cast<const float4*>(xb + 32 * g);
-            float4 v0 = xp[0], v1 = xp[1];
-            xv[8 * g + 0] = v0.x; xv[8 * g + 1] = v0.y; xv[8 * g + 2] = v0.z; xv[8 * g + 3] = v0.w;
-            xv[8 * g + 4] = v1.x; xv[8 * g + 5] = v1.y; xv[8 * g + 6] = v1.z; xv[8 * g + 7] = v1.w;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) xs[g] += xv[8 * g + e];
+            return d * xb.s * (float)isum;
         }
     }
-    __syncthreads();
-
-    float acc[NRR];
-#pragma unroll
-    for (int i = 0; i < NRR; ++i) {
-        float a = 0.0f;
-        if (active && (i % R) < L.nr) {
-            const uint32_t base = (uint32_t)i * rb + 210u * (uint32_t)sb;   // even bytes
-            const uint32_t sh = (base & 2u) ? 16u : 0u;
-            // 2-dword loads realigned: ql[64h+8c..+8], ql[64h+32+8c..+8], qh[32h+8c..+8]
-            auto ld2 = [&](uint32_t byteoff, uint32_t& lo, uint32_t& hi) {
-                const uint32_t E = (base + byteoff) >> 2;
-                const uint32_t a0 = lds[E], a1 = lds[E + 1], a2 = lds[E + 2];
-                lo = shr64(a0, a1, sh);
-                hi = shr64(a1, a2, sh);
-            };
-            uint32_t la0, la1, lb0, lb1, h0, h1;
-            ld2(64u * h + 8u * c, la0, la1);
-            ld2(64u * h + 32u + 8u * c, lb0, lb1);
-            ld2(128u + 32u * h + 8u * c, h0, h1);
-            uint32_t s0w, s1w, dd;
-            {
-                // scales sc[8h + c/2 + {0,2,4,6}] and d at byte 208
-                const uint32_t E = (base + 192u) >> 2;
-                const uint32_t a0 = lds[E], a1 = lds[E + 1], a2 = lds[E + 2], a3 = lds[E + 3],
-                               a4 = lds[E + 4];
-                const uint32_t w0 = shr64(a0, a1, sh), w1 = shr64(a1, a2, sh), w2 = shr64(a2, a3, sh),
-                               w3 = shr64(a3, a4, sh);
-                // bytes 192..207 = sc[0..15] in w0..w3; bytes 208..209 = d in low half of next
-                s0w = h ? w2 : w0;
-                s1w = h ? w3 : w1;
-                dd = a4 >> sh;
-            }
-            const float d = h2f(dd);
-            const int cs = c >> 1;
-            // sc index within the half: cs + 2g  -> byte (cs + 2g) of (s0w, s1w)
-            auto scv = [&](int g) -> float {
-                const int k = cs + 2 * g;
-                const uint32_t w = k < 4 ? s0w : s1w;
-                return (float)(int8_t)(w >> (8 * (k & 3)));
-            };
-            const uint32_t ql[4][2] = {{la0, la1}, {lb0, lb1}, {la0 >> 4, la1 >> 4}, {lb0 >> 4, lb1 >> 4}};
-            float tot = 0.0f;
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                float s = 0.0f;
-#pragma unroll
-                for (int hw = 0; hw < 2; ++hw) {
-                    const uint32_t hb = hw ? h1 : h0;
-                    const uint32_t q = (ql[g][hw] & 0x0f0f0f0fu) | (((hb >> (2 * g)) & 0x03030303u) << 4);
-                    s = fmaf((float)(q & 0xffu), xv[8 * g + 4 * hw + 0], s);
-                    s = fmaf((float)((q >> 8) & 0xffu), xv[8 * g + 4 * hw + 1], s);
-                    s = fmaf((float)((q >> 16) & 0xffu), xv[8 * g + 4 * hw + 2], s);
-                    s = fmaf((float)(q >> 24), xv[8 * g + 4 * hw + 3], s);
-                }
-                tot = fmaf(d * scv(g), s - 32.0f * xs[g], tot);
-            }
-            a = tot;
-        }
-        acc[i] = a;
-    }
-    float* red = reinterpret_cast<float*>(lds) + ((PAIR ? 2 : 1) * R * rb + 15) / 16 * 4;
-    finish<R, PAIR>(B, L, acc, red);
-}
-
-// ---------------------------------------------------------------------------
-// Activation quantization (quantize_row_q8_0, c:1508-1528), bit-exact.
-// ---------------------------------------------------------------------------
-__global__ void quantize_x_kernel(const float* __restrict__ x, int nb, XQ8 out) {
-    const int b = blockIdx.x * blockDim.x + threadIdx.x;
-    if (b >= nb) return;
-    float v[32];
-#pragma unroll
-    for (int j = 0; j < 32; ++j) v[j] = x[32 * b + j];
-    QBlock qb;
-    quantize32(v, qb);
-    int4* dst = reinterpret_cast<int4*>(out.qs + 32 * b);
-    const int* qi = reinterpret_cast<const int*>(qb.q);
-    dst[0] = make_int4(qi[0], qi[1], qi[2], qi[3]);
-    dst[1] = make_int4(qi[4], qi[5], qi[6], qi[7]);
-    out.d[b] = h2f_exact(qb.dh);
-    out.sum[b] = qb.sum;
-}
-
-__global__ void quantize_blocks_kernel(const float* __restrict__ x, int64_t nb, uint8_t* __restrict__ dst) {
-    const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (b >= nb) return;
-    float v[32];
-#pragma unroll
-    for (int j = 0; j < 32; ++j) v[j] = x[32 * b + j];
-    QBlock qb;
-    quantize32(v, qb);
-    uint8_t* o = dst + 34 * b;
-    o[0] = (uint8_t)(qb.dh & 0xff);
-    o[1] = (uint8_t)(qb.dh >> 8);
-#pragma unroll
-    for (int j = 0; j < 32; ++j) o[2 + j] = (uint8_t)qb.q[j];
-}
-
-// ---------------------------------------------------------------------------
-// Dequantization, one element per thread, bit-exact with dequantize_row
-// (c:611-934) for the types listed in l3p.h.
-// ---------------------------------------------------------------------------
-__device__ __forceinline__ float ldh(const uint8_t* p) { return h2f_exact((uint32_t)p[0] | ((uint32_t)p[1] << 8)); }
-
-__device__ float deq_elem(int type, const uint8_t* __restrict__ s, int64_t i) {
-    switch (type) {
-    case L3P_F32: return reinterpret_cast<const float*>(s)[i];
-    case L3P_F16: return ldh(s + 2 * i);
-    case L3P_BF16:
-        return __uint_as_float(((uint32_t)s[2 * i] | ((uint32_t)s[2 * i + 1] << 8)) << 16);
-    case L3P_Q4_0: {
-        const uint8_t* b = s + (i >> 5) * 18;
-        const int j = (int)(i & 31);
-        const int q = j < 16 ? (b[2 + j] & 0x0f) : (b[2 + j - 16] >> 4);
-        return (float)(q - 8) * ldh(b);
-    }
-    case L3P_Q4_1: {
-        const uint8_t* b = s + (i >> 5) * 20;
-        const int j = (int)(i & 31);
-        const int q = j < 16 ? (b[4 + j] & 0x0f) : (b[4 + j - 16] >> 4);
-        return (float)q * ldh(b) + ldh(b + 2);
-    }
-    case L3P_Q5_0: case L3P_Q5_1: {
-        const bool one = type == L3P_Q5_1;
-        const uint8_t* b = s + (i >> 5) * (one ? 24 : 22);
-        const uint8_t* qhp = b + (one ? 4 : 2);
-        const uint32_t qh = (uint32_t)qhp[0] | ((uint32_t)qhp[1] << 8) | ((uint32_t)qhp[2] << 16) |
-                            ((uint32_t)qhp[3] << 24);
-        const uint8_t* qs = qhp + 4;
-        const int j = (int)(i & 31);
-        const int q = j < 16 ? ((qs[j] & 0x0f) | (int)(((qh >> j) & 1u) << 4))
-                             : ((qs[j - 16] >> 4) | (int)(((qh >> j) & 1u) << 4));
-        return one ? (float)q * ldh(b) + ldh(b + 2) : (float)(q - 16) * ldh(b);
-    }
-    case L3P_Q8_0: {
-        const uint8_t* b = s + (i >> 5) * 34;
-        return (float)(int8_t)b[2 + (i & 31)] * ldh(b);
-    }
-    case L3P_IQ4_NL: {
-        const int8_t kv[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
-        const uint8_t* b = s + (i >> 5) * 18;
-        const int j = (int)(i & 31);
-        const int q = j < 16 ? (b[2 + j] & 0x0f) : (b[2 + j - 16] >> 4);
-        return ldh(b) * (float)kv[q];
-    }
-    case L3P_Q4_K: {
-        const uint8_t* b = s + (i >> 8) * 144;
-        const int e = (int)(i & 255), g = e >> 6, hi = (e >> 5) & 1, l = e & 31;
-        const int js = 2 * g + hi;
-        const uint8_t* sc = b + 4;
-        int scv, mnv;
-        if (js < 4) {
-            scv = sc[js] & 63;
-            mnv = sc[js + 4] & 63;
-        } else {
-            scv = (sc[js + 4] & 0x0f) | ((sc[js - 4] >> 6) << 4);
-            mnv = (sc[js + 4] >> 4) | ((sc[js] >> 6) << 4);
-        }
-        const float d1 = ldh(b) * (float)scv, m1 = ldh(b + 2) * (float)mnv;
-        const int q = hi ? (b[16 + 32 * g + l] >> 4) : (b[16 + 32 * g + l] & 0x0f);
-        return d1 * (float)q - m1;
-    }
-    case L3P_Q6_K: {
-        const uint8_t* b = s + (i >> 8) * 210;
-        const int e = (int)(i & 255), half = e >> 7, r = e & 127, g = r >> 5, l = r & 31;
-        const uint8_t* ql = b + 64 * half;
-        const uint8_t* qh = b + 128 + 32 * half;
-        const int8_t* sc = reinterpret_cast<const int8_t*>(b + 192 + 8 * half);
-        const int lo = (g & 1) ? ql[l + 32] : ql[l];
-        const int nib = (g & 2) ? (lo >> 4) : (lo & 0x0f);
-        const int q = (nib | (((qh[l] >> (2 * g)) & 3) << 4)) - 32;
-        return ldh(b + 208) * (float)sc[l / 16 + 2 * g] * (float)q;
-    }
-    default: return 0.0f;
-    }
-}
-
-__global__ void dequant_kernel(int type, const uint8_t* __restrict__ s, int64_t n, float* __restrict__ y) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) y[i] = deq_elem(type, s, i);
-}
-
-// Embedding row (c:3204-3207), times a scale when non-zero (Gemma's sqrt(dim),
-// which the reference applies to x in place before the first norm,
-// c:3132-3140; x*scale rounds the same), and the step record {token, pos}
-// that the kernels of the step read.
-__global__ void embed_step_kernel(int type, const uint8_t* __restrict__ s, int n, float scale, float* __restrict__ y,
-                                  int token, int pos, int* step) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) {
-        const float v = deq_elem(type, s, i);
-        y[i] = scale != 0.0f ? v * scale : v;
-    }
-    if (i == 0) {
-        step[0] = token;
-        step[1] = pos;
-    }
-}
-
-// ---------------------------------------------------------------------------
-// launch helpers
-// ---------------------------------------------------------------------------
-template <typename K>
-void set_lds(K kern, size_t bytes) {
-    if (bytes > 65536) L3P_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes));
-}
-
-struct Shape {
-    int threads;     // workgroup size
-    uint32_t rb;     // row bytes
 };
 
-Shape shape_of(int type, int cols) {
-    Shape s{0, (uint32_t)type_row_bytes(type, cols)};
-    int lanes = 0;
-    switch (type) {
-    case L3P_Q8_0: case L3P_Q4_0: lanes = cols / 32; break;
-    case L3P_Q4_K: case L3P_Q6_K: lanes = cols / 32; break;
-    default: break;
+// Q4_K super-block {fp16 d, dmin; u8 scales[12]; u8 qs[128]} (c:157-162),
+// 144 B at byte 144*sb of the buffer (16-byte aligned).  Lane = sub-block
+// j = lane % 8 of super-block sb = lane / 8: the low (j even) or high (j odd)
+// nibbles of qs[32*(j/2) .. +32].  High nibbles are used in place, masked,
+// as 16*q, and the sum is scaled back by 1/16 (exact).
+template <>
+struct Lane<L3P_Q4_K> {
+    uint32_t hdr;    // dword index of {d, dmin, scales[12]}
+    uint32_t qs;     // dword index of the lane's 32 quant bytes
+    uint32_t mask;   // 0x0f0f0f0f or 0xf0f0f0f0
+    uint32_t bs;     // bit offset of scale byte j % 4 within its dword
+    float fs;        // 1 or 1/16
+    bool hi;         // j >= 4
+
+    __device__ __forceinline__ void at(int lane, uint32_t /*sh: always 0*/) {
+        const uint32_t sb = (uint32_t)lane >> 3, j = (uint32_t)lane & 7u;
+        hdr = 36u * sb;
+        qs = hdr + 4u + 8u * (j >> 1);
+        mask = (j & 1u) ? 0xf0f0f0f0u : 0x0f0f0f0fu;
+        fs = (j & 1u) ? 0.0625f : 1.0f;
+        bs = 8u * (j & 3u);
+        hi = j >= 4u;
     }
-    s.threads = (lanes + 63) / 64 * 64;
-    return s;
+
+    __device__ __forceinline__ float dot(const uint32_t* buf, const XBlock& xb) const {
+        // dword reads (merged into ds_read_b128 by the compiler): a uint4
+        // read here makes the compiler wait for every copy in flight
+        uint4 h;
+        h.x = buf[hdr];
+        h.y = buf[hdr + 1];
+        h.z = buf[hdr + 2];
+        h.w = buf[hdr + 3];
+        const float d = h2f(h.x), dmin = h2f(h.x >> 16);
+        // get_scale_min_k4 (c:705-714) for sub-block j, from bytes s[j%4] (in
+        // h.y), s[j%4+4] (h.z) and s[j%4+8] (h.w), as bit-field extracts and
+        // selects (no divergent branch):
+        //   j < 4:  sc = s[j] & 63,                          m = s[j+4] & 63
+        //   j >= 4: sc = (s[j+4] & 15) | (s[j-4] >> 6) << 4,  m = (s[j+4] >> 4) | (s[j] >> 6) << 4
+        const uint32_t sc = __builtin_amdgcn_ubfe(hi ? h.w : h.y, bs, hi ? 4u : 6u) |
+                            (hi ? __builtin_amdgcn_ubfe(h.y, bs + 6u, 2u) << 4 : 0u);
+        const uint32_t mn = __builtin_amdgcn_ubfe(hi ? h.w : h.z, hi ? bs + 4u : bs, hi ? 4u : 6u) |
+                            (hi ? __builtin_amdgcn_ubfe(h.z, bs + 6u, 2u) << 4 : 0u);
+        uint32_t qw[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) qw[k] = buf[qs + k];
+        float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const uint32_t q = qw[k] & mask;
+            s0 = fmaf((float)(q & 0xffu), xb.x[4 * k], s0);
+            s1 = fmaf((float)((q >> 8) & 0xffu), xb.x[4 * k + 1], s1);
+            s2 = fmaf((float)((q >> 16) & 0xffu), xb.x[4 * k + 2], s2);
+            s3 = fmaf((float)(q >> 24), xb.x[4 * k + 3], s3);
+        }
+        const float s = ((s0 + s1) + (s2 + s3)) * fs;
+        return (d * (float)sc) * s - (dmin * (float)mn) * xb.xs;
+    }
+};
+
+// Q6_K super-block {u8 ql[128]; u8 qh[64]; i8 scales[16]; fp16 d}
+// (c:190-195), 210 B at byte base = sh + 210*sb of the buffer (even).  Lane
+// = quarter g = lane % 4 of half h = (lane / 4) % 2 of super-block
+// sb = lane / 8, i.e. elements 128h + 32g + e, e < 32 (c:873-904):
+//   u_e = nibble (g / 2 ? high : low) of ql[64h + 32(g%2) + e]
+//         | ((qh[32h + e] >> 2g) & 3) << 4,   q_e = u_e - 32,
+//   scale sc[8h + 2g + e/16].
+// Each quant dword is one v_alignbit from a pair of buffer dwords: the ql
+// stream is read from bit 8*pos + 4*(g/2) (nibble at bits 0..3 of each
+// byte), the qh stream from bit 8*pos + 2g - 4 (code bits at 4..5), so
+// u = (ql' & 0x0f) | (qh' & 0x30) per byte.
+template <>
+struct Lane<L3P_Q6_K> {
+    uint32_t qlf, qln;   // first dword and bit offset of the ql stream
+    uint32_t qhf, qhn;   // same for qh
+    uint32_t sch, dh;    // halfword indices of {sc[8h+2g], sc[8h+2g+1]} and d
+
+    __device__ __forceinline__ void at(int lane, uint32_t sh) {
+        const uint32_t sb = (uint32_t)lane >> 3, h = ((uint32_t)lane >> 2) & 1u, g = (uint32_t)lane & 3u;
+        const uint32_t base = sh + 210u * sb;
+        const uint32_t pl = 8u * (base + 64u * h + 32u * (g & 1u)) + 4u * (g >> 1);
+        const uint32_t ph = 8u * (base + 128u + 32u * h) + 2u * g - 4u;
+        qlf = pl >> 5;
+        qln = pl & 31u;
+        qhf = ph >> 5;
+        qhn = ph & 31u;
+        sch = (base + 192u + 8u * h + 2u * g) >> 1;
+        dh = (base + 208u) >> 1;
+    }
+
+    __device__ __forceinline__ float dot(const uint32_t* buf, const XBlock& xb) const {
+        uint32_t l[9], hb[9];
+#pragma unroll
+        for (int k = 0; k < 9; ++k) {
+            l[k] = buf[qlf + k];
+            hb[k] = buf[qhf + k];
+        }
+        const uint16_t* hw = reinterpret_cast<const uint16_t*>(buf);
+        const uint32_t scw = hw[sch];
+        const float d = h2f(hw[dh]);
+        float a0 = 0.0f, a1 = 0.0f, b0 = 0.0f, b1 = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const uint32_t ql = __builtin_amdgcn_alignbit(l[k + 1], l[k], qln);
+            const uint32_t qh = __builtin_amdgcn_alignbit(hb[k + 1], hb[k], qhn);
+            const uint32_t u = (ql & 0x0f0f0f0fu) | (qh & 0x30303030u);
+            if (k < 4) {
+                a0 = fmaf((float)(u & 0xffu), xb.x[4 * k], a0);
+                a1 = fmaf((float)((u >> 8) & 0xffu), xb.x[4 * k + 1], a1);
+                a0 = fmaf((float)((u >> 16) & 0xffu), xb.x[4 * k + 2], a0);
+                a1 = fmaf((float)(u >> 24), xb.x[4 * k + 3], a1);
+            } else {
+                b0 = fmaf((float)(u & 0xffu), xb.x[4 * k], b0);
+                b1 = fmaf((float)((u >> 8) & 0xffu), xb.x[4 * k + 1], b1);
+                b0 = fmaf((float)((u >> 16) & 0xffu), xb.x[4 * k + 2], b0);
+                b1 = fmaf((float)(u >> 24), xb.x[4 * k + 3], b1);
+            }
+        }
+        const float sc0 = (float)(int8_t)(scw & 0xffu), sc1 = (float)(int8_t)(scw >> 8);
+        return d * (sc0 * ((a0 + a1) - 32.0f * xb.xs0) + sc1 * ((b0 + b1) - 32.0f * xb.xs1));
+    }
+};
+
+template <int QT, int G, int NB, bool PAIR, bool UA>
+__global__ void __launch_bounds__(1024) gemv_kernel(GemvArgs a) {
+    constexpr int CB = Fmt<QT>::kChunkBytes;
+    constexpr int CDW = Fmt<QT>::kBufBytes / 4;
+    constexpr int CI = Fmt<QT>::kCI;
+    constexpr int NOUT = PAIR ? G / 2 : G;
+    extern __shared__ __align__(16) uint32_t lds[];
+    const int t = threadIdx.x, lane = t & 63, nw = blockDim.x >> 6;
+    const int w = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int nb = a.cols >> 5;   // 32-element lane slots of a row
+    const uint32_t rb = row_bytes<QT>(a.cols);
+    uint32_t* ring = lds + (size_t)w * NB * CDW;                          // this wave's chunk buffers
+    Cursor cc;
+    cc.w0 = a.w[0];
+    cc.w1 = a.w[1];
+    cc.w2 = a.w[2];
+    cc.rows0 = a.rows[0];
+    cc.rows1 = a.rows[1];
+    cc.rows_total = a.rows_total;
+    cc.ngroups = a.ngroups;
+    cc.bid = blockIdx.x;
+    cc.gdim = gridDim.x;
+    cc.rb = rb;
+    cc.coff = (uint32_t)w * (uint32_t)CB;
+    const int nbytes = (int)min((uint32_t)CB, rb - cc.coff);   // this wave's chunk length
+    const DmaLane dl = dma_lane<QT>(lane, nbytes);
+    // copy row-chunk k of the sequence into ring slot `slot`
+    auto issue = [&](int k, int slot) {
+        const uint8_t* src;
+        chunk_src<G, PAIR>(cc, k, src);
+        if (UA) {
+            const uint32_t sh = (uint32_t)(uintptr_t)src & 15u;
+            chunk_dma<QT>(ring + slot * CDW, src - sh, dma_lane<QT>(lane, (int)sh + nbytes));
+        } else {
+            chunk_dma<QT>(ring + slot * CDW, src, dl);
+        }
+    };
+    float* red = reinterpret_cast<float*>(lds + (size_t)nw * NB * CDW);   // [2][nw][G]
+    float* ssred = red + 2 * nw * G;                                      // [nw]
+    float* out_lds = ssred + nw;                                          // [groups of this WG][NOUT]
+
+    // ---- this lane's activation block (and the norm weights), issued first:
+    // they come from L2 while the weight copies below are in flight
+    const int blk = w * 64 + lane;
+    const bool active = blk < nb;
+    float v[32];
+    float4 nv[8];
+    if (active) {
+        const float4* xp = reinterpret_cast<const float4*>(a.x + 32 * blk);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float4 q = xp[e];
+            v[4 * e] = q.x; v[4 * e + 1] = q.y; v[4 * e + 2] = q.z; v[4 * e + 3] = q.w;
+        }
+        if (a.norm) {
+            const float4* np = reinterpret_cast<const float4*>(a.norm + 32 * blk);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) nv[e] = np[e];
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 32; ++j) v[j] = 0.0f;
+    }
+    // ---- weight copies: the first NB-1 chunks of this workgroup's sequence,
+    // CI instructions each.  nk = number of row-chunks this wave processes.
+    const int ngroups_mine =
+        a.ngroups > (int)blockIdx.x ? (a.ngroups - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x : 0;
+    const int nk = ngroups_mine * G;
+#pragma unroll
+    for (int b = 0; b < NB - 1; ++b)
+        if (b < nk) issue(b, b);
+
+    // ---- optional RMSNorm.  Every block of x belongs to exactly one lane, so
+    // ss = sum over lanes of the lane's 32 squares, then over lanes and waves
+    // in a fixed order: the same value in every workgroup.
+    if (a.norm) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 32; ++j) ss += v[j] * v[j];
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+        if (lane == 0) ssred[w] = ss;
+        lds_sync();
+        ss = 0.0f;
+        for (int i = 0; i < nw; ++i) ss += ssred[i];
+        const float r = 1.0f / sqrtf(ss * a.inv_n + a.eps);
+        if (active) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                v[4 * e] = nv[e].x * (r * v[4 * e]);
+                v[4 * e + 1] = nv[e].y * (r * v[4 * e + 1]);
+                v[4 * e + 2] = nv[e].z * (r * v[4 * e + 2]);
+                v[4 * e + 3] = nv[e].w * (r * v[4 * e + 3]);
+            }
+        }
+    }
+    XBlock xb;
+    prepare_block<QT>(v, xb);
+    Lane<QT> ln;
+    ln.at(lane, 0u);
+
+    // ---- row loop: G rows per group, chunk k = gl*G + i of this WG's sequence
+    for (int gl = 0; gl < ngroups_mine; ++gl) {
+        float acc[G];
+#pragma unroll
+        for (int i = 0; i < G; ++i) {
+            const int k = gl * G + i;
+            // chunk k is in LDS once only the younger chunks' copies remain:
+            // NB-2 of them in steady state, none near the end of the sequence
+            if (k + NB - 2 < nk) wait_vm<(NB - 2) * CI>();
+            else wait_vm<0>();
+            const uint8_t* src;
+            const bool real = chunk_src<G, PAIR>(cc, k, src);
+            if (UA) ln.at(lane, (uint32_t)(uintptr_t)src & 15u);
+            // every lane reads inside the buffer, so the dot runs unconditionally
+            // and lanes past the row or rows past the matrix drop their value
+            float dv = ln.dot(ring + (k % NB) * CDW, xb);
+            // pin the dot here: left alone, the compiler sinks every dot of the
+            // group to its end and keeps all their quants live in registers
+            asm volatile("" : "+v"(dv));
+            const float d = (real && active) ? dv : 0.0f;
+            wait_lgkm();   // this chunk's LDS reads are done before its buffer is refilled
+            const int kn = k + NB - 1;
+            if (kn < nk) issue(kn, kn % NB);
+            acc[i] = d;
+        }
+        // group done: wave totals -> LDS -> sum over the chunk waves in order
+        float* rd = red + (gl & 1) * nw * G;
+        const float tot = xreduce<G>(acc, lane);
+        if ((lane & ((64 / G) - 1)) == 0) rd[w * G + rowof<G>(lane)] = tot;
+        lds_sync();
+        if (t < NOUT) {
+            float s0 = 0.0f;
+            for (int c = 0; c < nw; ++c) s0 += rd[c * G + t];
+            float res = s0;
+            if (PAIR) {
+                float s1 = 0.0f;
+                for (int c = 0; c < nw; ++c) s1 += rd[c * G + G / 2 + t];
+                res = a.epilogue == EPI_GEGLU ? ref_geglu(s0, s1) : ref_swiglu(s0, s1);
+            }
+            out_lds[gl * NOUT + t] = res;
+        }
+    }
+    // ---- results of this workgroup's groups (every copy has been waited for)
+    lds_sync();
+    for (int j = t; j < ngroups_mine * NOUT; j += blockDim.x) {
+        const int gk = j / NOUT, i = j % NOUT;
+        const int grp = blockIdx.x + gk * gridDim.x;
+        if (PAIR) {
+            const int row = grp * NOUT + i;
+            if (row < a.rows[0]) a.y[0][row] = out_lds[j];
+        } else {
+            const int gi = grp * G + i;
+            if (gi >= a.rows_total) continue;
+            int s, row;
+            seg_of(a, gi, s, row);
+            float* y = a.y[s] + row;
+            if (a.epilogue == EPI_ADD) *y += out_lds[j];
+            else *y = out_lds[j];
+        }
+    }
 }
 
-template <int R, bool PAIR>
-void launch_typed(int type, const GemvBatch& b, int cols, const XPrep& xp, hipStream_t st) {
-    const float* x = xp.x;
-    const XQ8* xq = &xp.q8;
-    const Shape sh = shape_of(type, cols);
-    const int nrr = PAIR ? 2 * R : R;
-    const size_t lds = ((size_t)(PAIR ? 2 : 1) * R * sh.rb + 15) / 16 * 16 + (size_t)(sh.threads / 64) * nrr * 4;
-    int tiles = 0;
-    if (PAIR) tiles = (b.seg[0].rows + R - 1) / R;
-    else for (int s = 0; s < b.nseg; ++s) tiles += (b.seg[s].rows + R - 1) / R;
-    if (tiles == 0) return;
-    dim3 grid(tiles), block(sh.threads);
-    switch (type) {
-    case L3P_Q8_0:
-        set_lds(gemv_q8_0_kernel<R, PAIR>, lds);
-        hipLaunchKernelGGL((gemv_q8_0_kernel<R, PAIR>), grid, block, lds, st, b, cols, x);
-        break;
-    case L3P_Q4_0:
-        set_lds(gemv_q4_0_kernel<R, PAIR>, lds);
-        hipLaunchKernelGGL((gemv_q4_0_kernel<R, PAIR>), grid, block, lds, st, b, cols, *xq);
-        break;
-    case L3P_Q4_K:
-        set_lds(gemv_q4_k_kernel<R, PAIR>, lds);
-        hipLaunchKernelGGL((gemv_q4_k_kernel<R, PAIR>), grid, block, lds, st, b, cols, x);
-        break;
-    case L3P_Q6_K:
-        set_lds(gemv_q6_k_kernel<R, PAIR>, lds);
-        hipLaunchKernelGGL((gemv_q6_k_kernel<R, PAIR>), grid, block, lds, st, b, cols, x);
-        break;
-    default:
-        throw L3pError{L3P_E_UNSUPPORTED, "gemv: unsupported type"};
+// ---------------------------------------------------------------------------
+// launch
+// ---------------------------------------------------------------------------
+int cus() {
+    static int n = 0;
+    if (!n) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            n = 0;
+        if (n <= 0) n = 256;
     }
+    return n;
+}
+
+template <typename K>
+int occupancy(K kern, int threads, size_t lds) {
+    static std::mutex mu;
+    static std::map<std::tuple<const void*, int, size_t>, int> cache;
+    std::lock_guard<std::mutex> g(mu);
+    auto key = std::make_tuple((const void*)kern, threads, lds);
+    auto it = cache.find(key);
+    if (it != cache.end()) return it->second;
+    if (lds > 65536)
+        L3P_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    int n = 0;
+    L3P_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, threads, lds));
+    if (n < 1) n = 1;
+    cache[key] = n;
+    return n;
+}
+
+int env_int(const char* name, int dflt) {
+    const char* e = getenv(name);
+    return e ? atoi(e) : dflt;
+}
+
+template <int QT, int G, int NB, bool PAIR, bool UA>
+void launch_rows(GemvArgs a, hipStream_t st) {
+    constexpr int NOUT = PAIR ? G / 2 : G;
+    const int nb = a.cols / 32;
+    const int nw = (nb + 63) / 64;
+    const int threads = nw * 64;
+    const size_t base = (size_t)nw * NB * Fmt<QT>::kBufBytes + (size_t)2 * nw * G * 4 + (size_t)nw * 4;
+    auto lds_for = [&](int grid) { return base + (size_t)((a.ngroups + grid - 1) / grid) * NOUT * 4; };
+    auto kern = gemv_kernel<QT, G, NB, PAIR, UA>;
+    const int per_cu = occupancy(kern, threads, lds_for(cus()));
+    int grid = std::min(a.ngroups, per_cu * cus());
+    grid = std::max(grid, (a.ngroups * NOUT + kMaxOut - 1) / kMaxOut);
+    const size_t lds = lds_for(grid);
+    if (lds > 65536)
+        L3P_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(threads), lds, st, a);
     L3P_HIP(hipGetLastError());
+}
+
+template <int QT, int G, bool PAIR, bool UA>
+void launch_nb(GemvArgs a, int nbuf, hipStream_t st) {
+    switch (nbuf) {
+    case 3: launch_rows<QT, G, 3, PAIR, UA>(a, st); break;
+    case 6: launch_rows<QT, G, 6, PAIR, UA>(a, st); break;
+    default: launch_rows<QT, G, 4, PAIR, UA>(a, st); break;
+    }
+}
+
+template <int QT, bool UA>
+void launch_g(GemvArgs a, bool pair, int G, int nbuf, hipStream_t st) {
+    if (pair) {   // G counts gate and up rows together: 2 or 4 output rows per group
+        switch (G) {
+        case 4: launch_nb<QT, 4, true, UA>(a, nbuf, st); break;
+        default: launch_nb<QT, 8, true, UA>(a, nbuf, st); break;
+        }
+    } else {
+        switch (G) {
+        case 4: launch_nb<QT, 4, false, UA>(a, nbuf, st); break;
+        case 16: launch_nb<QT, 16, false, UA>(a, nbuf, st); break;
+        default: launch_nb<QT, 8, false, UA>(a, nbuf, st); break;
+        }
+    }
+}
+
+template <int QT>
+void launch_type(GemvArgs a, bool pair, int G, int nbuf, hipStream_t st) {
+    const int units = pair ? a.rows[0] : a.rows_total;
+    const int per = pair ? G / 2 : G;
+    a.ngroups = (units + per - 1) / per;
+    // the deepest ring (3, 4 or 6 buffers per wave) not above nbuf whose
+    // buffers fit the 160 KB of LDS with room for the result slots
+    const int nw = (a.cols / 32 + 63) / 64;
+    static const int depths[] = {6, 4, 3};
+    int nb = 3;
+    for (int d : depths)
+        if (d <= nbuf && (size_t)nw * d * Fmt<QT>::kBufBytes + 16384 <= 160 * 1024) {
+            nb = d;
+            break;
+        }
+    if (row_bytes<QT>(a.cols) % 16 == 0) {
+        launch_g<QT, false>(a, pair, G, nb, st);
+    } else {
+        // Q4_K rows (144 B super-blocks, cols % 256 == 0) are always 16-byte multiples
+        if constexpr (QT != L3P_Q4_K) launch_g<QT, true>(a, pair, G, nb, st);
+    }
 }
 
 }  // namespace
 
 bool gemv_supported(int type, int cols) {
-    // Rows must be 16-byte multiples (tiles are copied with 16-byte loads and
-    // every row then starts with the same dword alignment).
+    int unit;
     switch (type) {
-    case L3P_Q8_0: case L3P_Q4_0: case L3P_Q4_K: case L3P_Q6_K:
-        return cols > 0 && cols % type_block_elems(type) == 0 && type_row_bytes(type, cols) % 16 == 0 &&
-               cols / 32 <= kMaxThreads;
-    default:
-        return false;
+    case L3P_Q8_0: case L3P_Q4_0: unit = 32; break;
+    case L3P_Q4_K: case L3P_Q6_K: unit = 256; break;
+    default: return false;
     }
+    return cols > 0 && cols % unit == 0 && cols <= kMaxWaves * kChunkElems;
 }
 
-int gemv_input_form(int type, int cols) {
-    (void)cols;
-    return type == L3P_Q4_0 ? 1 : 0;
-}
-
-void launch_gemv(int type, const GemvBatch& b, int cols, const XPrep& xp, hipStream_t st) {
+void launch_gemv(int type, const GemvBatch& b, int cols, const float* x, const float* norm, float eps,
+                  hipStream_t st) {
     L3P_REQUIRE(gemv_supported(type, cols), L3P_E_UNSUPPORTED, "gemv: type %d with %d columns not supported",
                 type, cols);
-    L3P_REQUIRE(type != L3P_Q4_0 || xp.q8.qs, L3P_E_INVALID, "gemv: Q4_0 needs the quantized activation");
-    const size_t rb = type_row_bytes(type, cols);
-    const bool pair = b.pair != 0;
-    // Rows per tile: keep the LDS tile within 64 KB.
-    const size_t tile_rows_budget = 65536 / ((pair ? 2 : 1) * rb);
-    if (tile_rows_budget >= 4) {
-        pair ? launch_typed<4, true>(type, b, cols, xp, st) : launch_typed<4, false>(type, b, cols, xp, st);
-    } else if (tile_rows_budget >= 2) {
-        pair ? launch_typed<2, true>(type, b, cols, xp, st) : launch_typed<2, false>(type, b, cols, xp, st);
-    } else {
-        pair ? launch_typed<1, true>(type, b, cols, xp, st) : launch_typed<1, false>(type, b, cols, xp, st);
+    L3P_REQUIRE(((uintptr_t)x & 15) == 0 && ((uintptr_t)norm & 15) == 0, L3P_E_INVALID,
+                "gemv: activation and norm weights must be 16-byte aligned");
+    GemvArgs a{};
+    for (int s = 0; s < b.nseg; ++s) {
+        a.w[s] = b.seg[s].w;
+        a.y[s] = b.seg[s].y;
+        a.rows[s] = b.seg[s].rows;
+        L3P_REQUIRE(((uintptr_t)a.w[s] & 15) == 0, L3P_E_INVALID, "gemv: weights must be 16-byte aligned");
     }
-}
-
-void prepare_x_form(int type, int cols, const float* x, const XPrep& xp, hipStream_t st) {
-    switch (gemv_input_form(type, cols)) {
-    case 1: launch_quantize_x(x, cols, xp.q8, st); break;
-    default: break;
+    a.nseg = b.nseg;
+    a.epilogue = b.epilogue;
+    a.cols = cols;
+    a.rows_total = 0;
+    if (b.pair) a.rows_total = b.seg[0].rows;
+    else
+        for (int s = 0; s < b.nseg; ++s) a.rows_total += b.seg[s].rows;
+    if (a.rows_total == 0) return;
+    a.x = x;
+    a.norm = norm;
+    a.eps = eps;
+    a.inv_n = 1.0f / (float)cols;
+    // Rows per group G: the largest of 16, 8, 4 that still gives about six
+    // waves per CU (groups x column chunks); ring depth 3 at G = 4, else 4.
+    // (Measured on MI355X at the Llama-3-8B shapes.)
+    const int nw = (cols / 32 + 63) / 64;
+    const int units = a.rows_total;
+    const int per_g = b.pair ? 2 : 1;   // pair groups hold G/2 rows of each matrix
+    auto waves = [&](int g) { return (long)(units * per_g + g - 1) / g * nw; };
+    int G = env_int("L3P_GEMV_G", 0);
+    if (G != 4 && G != 8 && G != 16) {
+        G = 4;
+        for (int g : {16, 8})
+            if ((!b.pair || g <= 8) && waves(g) >= 6L * cus()) {
+                G = g;
+                break;
+            }
     }
-}
-
-void launch_quantize_x(const float* x, int cols, const XQ8& xq, hipStream_t st) {
-    const int nb = cols / 32;
-    hipLaunchKernelGGL(quantize_x_kernel, dim3((nb + 255) / 256), dim3(256), 0, st, x, nb, xq);
-    L3P_HIP(hipGetLastError());
-}
-
-void launch_quantize_q8_0_blocks(const float* x, int64_t n, uint8_t* dst, hipStream_t st) {
-    const int64_t nb = n / 32;
-    if (nb == 0) return;
-    hipLaunchKernelGGL(quantize_blocks_kernel, dim3((unsigned)((nb + 255) / 256)), dim3(256), 0, st, x, nb, dst);
-    L3P_HIP(hipGetLastError());
-}
-
-void launch_dequant(int type, const uint8_t* src, int64_t n, float* dst, hipStream_t st) {
-    if (n == 0) return;
-    hipLaunchKernelGGL(dequant_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, type, src, n, dst);
-    L3P_HIP(hipGetLastError());
-}
-
-void launch_embed_row(int type, const uint8_t* row, int n, float scale, float* dst, int token, int pos, int* step,
-                      hipStream_t st) {
-    hipLaunchKernelGGL(embed_step_kernel, dim3((n + 255) / 256), dim3(256), 0, st, type, row, n, scale, dst, token,
-                       pos, step);
-    L3P_HIP(hipGetLastError());
+    const int nbuf = env_int("L3P_GEMV_NB", G == 4 ? 3 : 4);
+    switch (type) {
+    case L3P_Q8_0: launch_type<L3P_Q8_0>(a, b.pair != 0, G, nbuf, st); break;
+    case L3P_Q4_0: launch_type<L3P_Q4_0>(a, b.pair != 0, G, nbuf, st); break;
+    case L3P_Q4_K: launch_type<L3P_Q4_K>(a, b.pair != 0, G, nbuf, st); break;
+    default: launch_type<L3P_Q6_K>(a, b.pair != 0, G, nbuf, st); break;
+    }
 }

@@ -96,35 +96,14 @@ struct GemvBatch {
     int epilogue;  // GemvEpilogue
 };
 
-// Activation in the Q8_0 form used by the integer-dot path (Q4_0 weights):
-// int8 quants, the fp32 value of the truncated fp16 scale, and the per-block
-// sum of quants.  Same numbers as the reference's block_q8_0, laid out for
-// aligned loads.
-struct XQ8 {
-    int8_t* qs;     // [cols]
-    float* d;       // [cols/32]
-    int32_t* sum;   // [cols/32]
-};
-
-// A GEMV input in the forms the generic kernels consume: fp32, and Q8_0 for
-// Q4_0 weights.  Only the form the weight type needs has to be filled in.
-struct XPrep {
-    const float* x = nullptr;
-    XQ8 q8{};
-};
-
-// launchers (gemv.hip)
-void launch_gemv(int type, const GemvBatch& b, int cols, const XPrep& x, hipStream_t s);
-// Which activation form a weight type consumes: 0 fp32, 1 Q8_0.
-int gemv_input_form(int type, int cols);
-void prepare_x_form(int type, int cols, const float* x, const XPrep& xp, hipStream_t s);
-void launch_quantize_x(const float* x, int cols, const XQ8& xq, hipStream_t s);
+// gemv.hip: the decode GEMV over Q8_0 / Q4_0 / Q4_K / Q6_K rows, with an
+// optional RMSNorm of x fused into its prologue (norm != null).  Weights, x
+// and norm must be 16-byte aligned.
+bool gemv_supported(int type, int cols);
+void launch_gemv(int type, const GemvBatch& b, int cols, const float* x, const float* norm, float eps,
+                 hipStream_t s);
+// blocks.hip
 void launch_quantize_q8_0_blocks(const float* x, int64_t n, uint8_t* dst, hipStream_t s);
 void launch_dequant(int type, const uint8_t* src, int64_t n, float* dst, hipStream_t s);
 void launch_embed_row(int type, const uint8_t* row, int n, float scale, float* dst, int token, int pos, int* step,
                       hipStream_t s);
-// gemv4.hip: Q8_0 / Q4_0 GEMV with an optional fused RMSNorm of x (norm != null)
-bool gemv4_supported(int type, int cols);
-void launch_gemv4(int type, const GemvBatch& b, int cols, const float* x, const float* norm, float eps,
-                  hipStream_t s);
-bool gemv_supported(int type, int cols);

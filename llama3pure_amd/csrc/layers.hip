@@ -53,49 +53,6 @@ __device__ float block_sum(float v, float* sh) {
 }
 
 
-// ---------------------------------------------------------------------------
-// RMSNorm (c:3117-3129), optional fused embedding scale (Gemma first layer,
-// c:3132-3148), and the output also written in the form the next GEMV
-// consumes (form 1: Q8_0 for Q4_0 weights).
-// One workgroup.
-// ---------------------------------------------------------------------------
-__global__ void __launch_bounds__(1024) rmsnorm_kernel(const float* __restrict__ xin, float* xscale, float scale,
-                                                       const float* __restrict__ w, int n, float inv_n, float eps,
-                                                       float* out, XQ8 xq, int form) {
-    __shared__ float sh[16];
-    const int t = threadIdx.x, nt = blockDim.x;
-    float ss = 0.0f;
-    for (int j = t; j < n; j += nt) {
-        float v = xin[j];
-        if (xscale) {
-            v = v * scale;
-            xscale[j] = v;
-        }
-        ss += v * v;
-    }
-    ss = block_sum(ss, sh);
-    const float r = 1.0f / sqrtf(ss * inv_n + eps);
-    const float* xs = xscale ? xscale : xin;
-    __syncthreads();
-    for (int b = t; b < n / 32; b += nt) {
-        float o[32];
-#pragma unroll
-        for (int j = 0; j < 32; ++j) o[j] = w[32 * b + j] * (r * xs[32 * b + j]);
-#pragma unroll
-        for (int j = 0; j < 32; ++j) out[32 * b + j] = o[j];
-        if (form == 1) {
-            QBlock qb;
-            quantize32(o, qb);
-            int4* dq = reinterpret_cast<int4*>(xq.qs + 32 * b);
-            const int* qi = reinterpret_cast<const int*>(qb.q);
-            dq[0] = make_int4(qi[0], qi[1], qi[2], qi[3]);
-            dq[1] = make_int4(qi[4], qi[5], qi[6], qi[7]);
-            xq.d[b] = h2f_exact(qb.dh);
-            xq.sum[b] = qb.sum;
-        }
-    }
-}
-
 // x += rmsnorm(y) (Gemma post-attention / post-FFN norm then residual,
 // c:3364-3371, c:3411-3417).
 __global__ void __launch_bounds__(1024) rmsnorm_add_kernel(const float* __restrict__ y, const float* __restrict__ w,
@@ -610,14 +567,6 @@ __global__ void __launch_bounds__(64) topk_scan_kernel(const float* __restrict__
 // ---------------------------------------------------------------------------
 void launch_embed_step(const Mat& emb, int token, int pos, float scale, float* x, int* step, hipStream_t s) {
     launch_embed_row(emb.type, emb.w + (size_t)token * emb.rb, emb.cols, scale, x, token, pos, step, s);
-}
-
-void launch_rmsnorm(const float* xin, float* xscale, float scale, const float* w, int n, float inv_n, float eps,
-                    float* out, const XPrep* xp, int form, hipStream_t s) {
-    const XQ8 q = xp ? xp->q8 : XQ8{};
-    hipLaunchKernelGGL(rmsnorm_kernel, dim3(1), dim3(1024), 0, s, xin, xscale, scale, w, n, inv_n, eps, out, q,
-                       xp ? form : 0);
-    L3P_HIP(hipGetLastError());
 }
 
 void launch_rmsnorm_add(const float* y, const float* w, int n, float inv_n, float eps, float* x, hipStream_t s) {

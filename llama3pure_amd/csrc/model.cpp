@@ -386,7 +386,6 @@ static Model* load_model(l3p_ctx* c, const void* bytes, size_t len, const l3p_lo
     }
 
     // run state
-    const int maxin = std::max(m.max_dim, m.hidden);
     m.x = (float*)m.dalloc((size_t)m.dim * 4);
     m.xb = (float*)m.dalloc((size_t)m.max_dim * 4);
     m.xb2 = (float*)m.dalloc((size_t)m.dim * 4);
@@ -396,11 +395,6 @@ static Model* load_model(l3p_ctx* c, const void* bytes, size_t len, const l3p_lo
     m.hb = (float*)m.dalloc((size_t)m.hidden * 4);
     m.hb2 = (float*)m.dalloc((size_t)m.hidden * 4);
     m.logits = (float*)m.dalloc((size_t)m.vocab * 4);
-    m.qq = (int8_t*)m.dalloc((size_t)m.q_dim);
-    m.qd = (float*)m.dalloc((size_t)m.q_dim / 32 * 4);
-    m.xq.qs = (int8_t*)m.dalloc((size_t)maxin);
-    m.xq.d = (float*)m.dalloc((size_t)maxin / 32 * 4);
-    m.xq.sum = (int32_t*)m.dalloc((size_t)maxin / 32 * 4);
     m.max_chunks = (m.seq_len + 63) / 64;
     L3P_REQUIRE(m.max_chunks <= 4096, L3P_E_UNSUPPORTED, "context length %d exceeds 262144", m.seq_len);
     m.part_acc = (float*)m.dalloc((size_t)m.n_heads * m.max_chunks * (m.hs + 2) * 4);
@@ -419,10 +413,6 @@ static Model* load_model(l3p_ctx* c, const void* bytes, size_t len, const l3p_lo
 // ---------------------------------------------------------------------------
 // forward (transformer, c:3190-3435)
 // ---------------------------------------------------------------------------
-void prepare_x(int type, int cols, const float* x, const XPrep& xp, hipStream_t s) {
-    prepare_x_form(type, cols, x, xp, s);
-}
-
 // ---------------------------------------------------------------------------
 // GEMV launch timing
 // ---------------------------------------------------------------------------
@@ -512,17 +502,8 @@ static double gemv_bytes(int type, int rows, int cols, int out_rows) {
     return (double)rows * (double)type_row_bytes(type, cols) + 4.0 * cols + 4.0 * out_rows;
 }
 
-static bool v4_ok(int type, const GemvBatch& b, int cols) {
-    if (!gemv4_supported(type, cols)) return false;
-    for (int i = 0; i < b.nseg; ++i)
-        if (((uintptr_t)b.seg[i].w & 15) != 0) return false;
-    return true;
-}
-
-// b's segments = W . rmsnorm(x) (norm != null) or W . x, all of one type.
-// Q8_0/Q4_0 run the streaming kernel with the norm and the activation's
-// integer form computed in its prologue; other types take the norm kernel
-// (into xb), the input preparation and the generic GEMV.
+// b's segments = W . rmsnorm(x) (norm != null) or W . x, all of one type,
+// in one launch of the streaming GEMV (the norm runs in its prologue).
 static void gemv_batch(l3p_ctx* c, int type, const GemvBatch& b, int cols, const float* x, const float* norm,
                        const char* what) {
     Model& m = *c->model;
@@ -531,36 +512,12 @@ static void gemv_batch(l3p_ctx* c, int type, const GemvBatch& b, int cols, const
     int rows = 0;
     for (int i = 0; i < (b.pair ? 2 : b.nseg); ++i) rows += b.seg[i].rows;
     const int out_rows = b.pair ? b.seg[0].rows : rows;
-    const std::string label = gemv_label(what, type, rows, cols);
-    const double bytes = gemv_bytes(type, rows, cols, out_rows);
-    if (v4_ok(type, b, cols)) {
-        ProfRange r(c->prof, s, label, bytes);
-        launch_gemv4(type, b, cols, x, norm, eps, s);
-        return;
-    }
-    const float* in = x;
-    XPrep xp = m.prep(m.xb);
-    if (norm) {
-        launch_rmsnorm(x, nullptr, 0.0f, norm, cols, 1.0f / (float)cols, eps, m.xb, &xp, gemv_input_form(type, cols), s);
-        in = m.xb;
-    } else {
-        prepare_x(type, cols, x, xp, s);
-    }
-    xp.x = in;
-    ProfRange r(c->prof, s, label, bytes);
-    launch_gemv(type, b, cols, xp, s);
+    ProfRange r(c->prof, s, gemv_label(what, type, rows, cols), gemv_bytes(type, rows, cols, out_rows));
+    launch_gemv(type, b, cols, x, norm, eps, s);
 }
 
 void gemv_plain(l3p_ctx* c, int type, const GemvBatch& b, int cols, const float* x) {
-    if (v4_ok(type, b, cols)) {
-        launch_gemv4(type, b, cols, x, nullptr, 0.0f, c->stream);
-        return;
-    }
-    XPrep xp;
-    xp.x = x;
-    xp.q8 = c->scratch.xq(cols);
-    prepare_x_form(type, cols, x, xp, c->stream);
-    launch_gemv(type, b, cols, xp, c->stream);
+    launch_gemv(type, b, cols, x, nullptr, 0.0f, c->stream);
 }
 
 static GemvBatch one(const Mat& W, float* y, int epi) {

@@ -3,20 +3,6 @@
 
 #include "internal.h"
 
-struct DevBuf {
-    void* p = nullptr;
-    size_t cap = 0;
-    void ensure(size_t n);
-    void release();
-    ~DevBuf() { release(); }
-};
-
-struct Scratch {
-    DevBuf xq_buf, gemm_buf;
-    XQ8 xq(int cols);
-    void release();
-};
-
 // One weight matrix in HBM, native GGUF block layout (QuantizedTensor, c:238-249).
 struct Mat {
     const uint8_t* w = nullptr;
@@ -51,15 +37,6 @@ struct Model {
     // run state (RunState, c:281-343), device resident
     float *x = nullptr, *xb = nullptr, *xb2 = nullptr, *q = nullptr, *k = nullptr, *v = nullptr;
     float *hb = nullptr, *hb2 = nullptr, *logits = nullptr;
-    int8_t* qq = nullptr;          // Q8_0 query [n_heads][hs]
-    float* qd = nullptr;           // [n_heads][hs/32]
-    XQ8 xq{};
-    XPrep prep(const float* x) const {
-        XPrep p;
-        p.x = x;
-        p.q8 = xq;
-        return p;
-    }
     float* part_acc = nullptr;     // [n_heads][max_chunks][hs + 2] attention chunk partials
     int* step = nullptr;           // device {token, pos} of the step being computed
     int max_chunks = 0;
@@ -115,7 +92,6 @@ struct l3p_ctx {
     int device = 0;
     hipStream_t stream = nullptr;
     std::string err;
-    Scratch scratch;
     Model* model = nullptr;
     Profiler prof;
     // the layer stack of one forward step, captured once per variant
@@ -132,10 +108,6 @@ void gemv_plain(l3p_ctx* c, int type, const GemvBatch& b, int cols, const float*
 // x = embedding row of `token` (times `scale` when non-zero) and the device
 // step record {token, pos} that the layer kernels read.
 void launch_embed_step(const Mat& emb, int token, int pos, float scale, float* x, int* step, hipStream_t s);
-void launch_rmsnorm(const float* x_in, float* x_scale_inplace, float scale, const float* w, int n, float inv_n,
-                    float eps, float* out, const XPrep* xp, int form, hipStream_t s);
-// Launch the kernel that writes x in the form `type` consumes (none for fp32).
-void prepare_x(int type, int cols, const float* x, const XPrep& xp, hipStream_t s);
 void launch_rmsnorm_add(const float* y, const float* w, int n, float inv_n, float eps, float* x, hipStream_t s);
 // QK-norm, RoPE, the K/V cache write and attention of one layer for the
 // step's position (c:3232-3359); out = [n_heads][head_dim].

@@ -99,11 +99,81 @@ def quantize_q4_0(w: np.ndarray) -> np.ndarray:
     return out.reshape(rows, -1)
 
 
+def _round_div(a: np.ndarray, b: np.ndarray, lo: int, hi: int) -> np.ndarray:
+    """clip(round(a / b), lo, hi) with 0 where b == 0."""
+    with np.errstate(divide="ignore", invalid="ignore"):
+        r = np.where(b > 0, np.rint(a / np.where(b > 0, b, 1)), 0)
+    return np.clip(r, lo, hi).astype(np.int64)
+
+
+def quantize_q4_k(w: np.ndarray) -> np.ndarray:
+    """fp32 [rows, cols] -> Q4_K bytes [rows, cols/256*144].  A plain min/max
+    quantizer (not llama.cpp's iterative search): per 32-element sub-block
+    scale (max-min)/15 and offset -min, both stored as 6-bit multiples of the
+    fp16 super-block d / dmin; fields packed as get_scale_min_k4 reads them
+    (llama3pure-c-engine.c:705-746)."""
+    rows, cols = w.shape
+    nsb = cols // 256
+    b = w.reshape(rows, nsb, 8, 32).astype(np.float32)
+    mn = np.minimum(b.min(axis=3), 0)
+    scale = (b.max(axis=3) - mn) / np.float32(15)
+    off = -mn
+    d = (scale.max(axis=2) / np.float32(63)).astype(np.float16)
+    dmin = (off.max(axis=2) / np.float32(63)).astype(np.float16)
+    dd, dm = d.astype(np.float32), dmin.astype(np.float32)
+    sc = _round_div(scale, dd[:, :, None], 0, 63)
+    m = _round_div(off, dm[:, :, None], 0, 63)
+    d1 = (dd[:, :, None] * sc).astype(np.float32)
+    m1 = (dm[:, :, None] * m).astype(np.float32)
+    q = _round_div(b + m1[..., None], d1[..., None], 0, 15)
+    out = np.empty((rows, nsb, 144), np.uint8)
+    out[:, :, 0:2] = np.ascontiguousarray(d).view(np.uint8).reshape(rows, nsb, 2)
+    out[:, :, 2:4] = np.ascontiguousarray(dmin).view(np.uint8).reshape(rows, nsb, 2)
+    s = np.empty((rows, nsb, 12), np.int64)
+    s[:, :, 0:4] = (sc[:, :, 0:4] & 63) | ((sc[:, :, 4:8] >> 4) << 6)
+    s[:, :, 4:8] = (m[:, :, 0:4] & 63) | ((m[:, :, 4:8] >> 4) << 6)
+    s[:, :, 8:12] = (sc[:, :, 4:8] & 15) | ((m[:, :, 4:8] & 15) << 4)
+    out[:, :, 4:16] = s.astype(np.uint8)
+    qs = q[:, :, 0::2, :] | (q[:, :, 1::2, :] << 4)          # [rows, nsb, 4, 32]
+    out[:, :, 16:] = qs.reshape(rows, nsb, 128).astype(np.uint8)
+    return out.reshape(rows, -1)
+
+
+def quantize_q6_k(w: np.ndarray) -> np.ndarray:
+    """fp32 [rows, cols] -> Q6_K bytes [rows, cols/256*210]: per 16-element
+    group scale max|w|/31 stored as an int8 multiple of the fp16 d, quants
+    q = round(w / (d*sc)) in [-32, 31] kept as u = q + 32 in the ql/qh
+    layout dequantize_row_q6_K reads (llama3pure-c-engine.c:873-904)."""
+    rows, cols = w.shape
+    nsb = cols // 256
+    b = w.reshape(rows, nsb, 16, 16).astype(np.float32)
+    s = np.abs(b).max(axis=3) / np.float32(31)
+    d = (s.max(axis=2) / np.float32(127)).astype(np.float16)
+    dd = d.astype(np.float32)
+    sc = _round_div(s, dd[:, :, None], -128, 127)
+    ds = (dd[:, :, None] * sc).astype(np.float32)
+    u = (_round_div(b, ds[..., None], -32, 31) + 32).reshape(rows, nsb, 2, 4, 32)   # [.., h, g, l]
+    out = np.empty((rows, nsb, 210), np.uint8)
+    ql = np.empty((rows, nsb, 2, 64), np.int64)
+    ql[..., :32] = (u[:, :, :, 0] & 15) | ((u[:, :, :, 2] & 15) << 4)
+    ql[..., 32:] = (u[:, :, :, 1] & 15) | ((u[:, :, :, 3] & 15) << 4)
+    qh = (u[:, :, :, 0] >> 4) | ((u[:, :, :, 1] >> 4) << 2) | ((u[:, :, :, 2] >> 4) << 4) | ((u[:, :, :, 3] >> 4) << 6)
+    out[:, :, 0:128] = ql.reshape(rows, nsb, 128).astype(np.uint8)
+    out[:, :, 128:192] = qh.reshape(rows, nsb, 64).astype(np.uint8)
+    out[:, :, 192:208] = sc.astype(np.int8).view(np.uint8)
+    out[:, :, 208:210] = np.ascontiguousarray(d).view(np.uint8).reshape(rows, nsb, 2)
+    return out.reshape(rows, -1)
+
+
 def quantize(w: np.ndarray, qtype: int) -> np.ndarray:
     if qtype == Q8_0:
         return quantize_q8_0(w)
     if qtype == Q4_0:
         return quantize_q4_0(w)
+    if qtype == Q4_K:
+        return quantize_q4_k(w)
+    if qtype == Q6_K:
+        return quantize_q6_k(w)
     if qtype == F32:
         return np.ascontiguousarray(w, np.float32).view(np.uint8).reshape(w.shape[0], -1)
     raise ValueError(f"no weight quantizer for type {qtype}")

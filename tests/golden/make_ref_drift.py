@@ -1,8 +1,9 @@
 """Writes ref_drift.json: how far the reference engine's own optimised build
 (Makefile "fast"/OpenMP line: gcc -Ofast -fopenmp, which vectorises and
 reorders its fp32 sums) drifts from its plain build (bit-identical to the
-oracle) on the synthetic models of test_gpu_model.py, under the same
-teacher-forced protocol as test_teacher_forced_logits_and_kv.
+oracle) on the synthetic models of test_gpu_model.py: the full models under
+the teacher-forced protocol of test_teacher_forced_logits_and_kv, and the
+one-layer models of test_single_layer_position0_tight per token.
 
 The GPU path reorders fp32 sums too, so its logits are held to a tolerance
 derived from this drift: it may differ from the oracle by as much as the
@@ -71,9 +72,37 @@ def measure(name: str) -> dict:
         os.unlink(path)
 
 
+def measure_single(case: str) -> list:
+    """Per token of SINGLE_TOKENS: max|dlogit|/rms of the reference's two
+    builds on the one-layer model `case` at position 0."""
+    import oracle
+    import model_cases as T
+
+    g = T.single_layer_model(case)
+    fd, path = tempfile.mkstemp(suffix=".gguf")
+    with os.fdopen(fd, "wb") as f:
+        f.write(g)
+    try:
+        ref = oracle.Ref(oracle.REF_OMP_SO)
+        assert ref.lib.ref_model_open(path.encode(), 0) == 0
+        m = oracle.CpuRef().open_model(g)
+        out = np.empty(m.vocab, np.float32)
+        rel = []
+        for tok in T.SINGLE_TOKENS:
+            lo = m.forward(tok, 0)
+            ref.lib.ref_forward(tok, 0, 1, oracle._vp(out))
+            rel.append(float(np.abs(lo - out).max()) / T.rms(lo))
+        return rel
+    finally:
+        os.unlink(path)
+
+
 def main():
     if len(sys.argv) == 3 and sys.argv[1] == "--one":
         print(json.dumps(measure(sys.argv[2])))
+        return
+    if len(sys.argv) == 3 and sys.argv[1] == "--single":
+        print(json.dumps(measure_single(sys.argv[2])))
         return
     import model_cases as T
 
@@ -86,6 +115,12 @@ def main():
                            env=env)
         out["models"][name] = json.loads(r.stdout.strip().splitlines()[-1])
         print(name, f"{out['models'][name]['max_rel']:.3e}")
+    out["single_layer"] = {}
+    for case in T.SINGLE_LAYER:
+        r = subprocess.run([sys.executable, __file__, "--single", case], check=True, capture_output=True, text=True,
+                           env=env)
+        out["single_layer"][case] = json.loads(r.stdout.strip().splitlines()[-1])
+        print(case, " ".join(f"{v:.1e}" for v in out["single_layer"][case]))
     with open(os.path.join(HERE, "ref_drift.json"), "w") as f:
         json.dump(out, f, indent=1)
 

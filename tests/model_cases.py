@@ -15,7 +15,36 @@ MODELS = {
     "gemma_q8_0": dict(arch="gemma3", dim=512, hidden=1536, n_layers=7, n_heads=4, n_kv=2, head_dim=256,
                        vocab=2048, ctx=256, qtype=synth.Q8_0, seed=3, softcap=30.0, swa_window=16,
                        norm_jitter=0.1, tied=True),
+    "llama_q4_k_m": dict(arch="llama", dim=512, hidden=1024, n_layers=4, n_heads=8, n_kv=2, vocab=2048, ctx=256,
+                         qtype=synth.Q4_K, seed=4, norm_jitter=0.1,
+                         qtypes={"ffn_down": synth.Q6_K, "attn_v": synth.Q6_K, "output": synth.Q6_K}),
 }
+
+
+_GEMMA = dict(arch="gemma3", head_dim=256, softcap=30.0, swa_window=16, tied=True)
+_KMIX = {"ffn_down": synth.Q6_K, "attn_v": synth.Q6_K, "output": synth.Q6_K}
+
+# One-layer models compared at position 0 (test_single_layer_position0_tight).
+SINGLE_LAYER = {
+    "llama_q8_0": dict(qtype=synth.Q8_0),
+    "llama_q4_0": dict(qtype=synth.Q4_0),
+    "gemma_q8_0": dict(qtype=synth.Q8_0, **_GEMMA),
+    # Q4_K with Q6_K down / V / output projections, as in Q4_K_M files
+    "llama_q4_k_m": dict(qtype=synth.Q4_K, qtypes=_KMIX),
+    # rows that are not 16-byte multiples: Gemma-3-1B width 1152 (Q8_0 rows
+    # of 1224 B), Gemma-3-270M width 640 (Q4_0 rows of 360 B), Q6_K at
+    # widths 768 and 1280 (rows of 630 and 1050 B)
+    "gemma_q8_0_1152": dict(qtype=synth.Q8_0, dim=1152, hidden=1536, n_heads=4, n_kv=1, **_GEMMA),
+    "llama_q4_0_640": dict(qtype=synth.Q4_0, dim=640, hidden=2048, n_heads=5, n_kv=1),
+    "llama_q6_k_768": dict(qtype=synth.Q6_K, dim=768, hidden=1280, n_heads=6, n_kv=2),
+}
+SINGLE_TOKENS = (0, 7, 1234, 42, 555, 1000, 1999, 2047)
+
+
+def single_layer_model(case):
+    kw = dict(arch="llama", dim=512, hidden=1024, n_heads=8, n_kv=2)
+    kw.update(SINGLE_LAYER[case])
+    return synth.synthetic_model(n_layers=1, vocab=2048, ctx=64, seed=21, norm_jitter=0.1, **kw)
 
 
 def rms(lo):
@@ -34,14 +63,16 @@ def kv_quant_diff(a, b, m, pos):
     return np.abs(qa.astype(np.int32) - qb.astype(np.int32))
 
 
-def _load_drift():
+def _load_drift(key):
     p = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "ref_drift.json")
     if not os.path.exists(p):
         return {}
     with open(p) as f:
-        return json.load(f)["models"]
+        return json.load(f).get(key, {})
 
 
 # name -> drift of the reference's -Ofast -fopenmp build from its plain build:
 #   max_rel: max|dlogit|/rms(logits); kv["layer/k|v"]: max and mean |quant diff|
-REF_DRIFT = _load_drift()
+REF_DRIFT = _load_drift("models")
+# single-layer case -> max|dlogit|/rms(logits) per token of SINGLE_TOKENS at position 0
+SINGLE_DRIFT = _load_drift("single_layer")

@@ -8,8 +8,10 @@ blocks, the truncated fp16 block scales, the Q8_0 activations of Q4_0
 weights) a last-bit difference occasionally moves a quant by one step or a
 scale by one fp16 ulp (2^-10 relative).  The stated tolerances:
 
-  * single layer at position 0 (no attention history):
-        |logit_gpu - logit_oracle| <= 1e-4 * rms(logits)
+  * single layer at position 0 (no attention history), per token:
+        |logit_gpu - logit_oracle| <= max(1e-4, 2 * drift) * rms(logits)
+    with drift the reference's own build-to-build difference on that token
+    (~5e-7 unless a quantized value sits on a rounding boundary);
   * full models after prefill:
         |logit_gpu - logit_oracle| <= max(1e-2, 2 * drift) * rms(logits)
     where drift is the largest max|dlogit|/rms by which the reference's own
@@ -36,7 +38,8 @@ import pytest
 
 import llama3pure_amd as l3p
 from llama3pure_amd import synth
-from model_cases import MODELS, REF_DRIFT, kv_quant_diff, rms, teacher_prompt
+from model_cases import (MODELS, REF_DRIFT, SINGLE_DRIFT, SINGLE_LAYER, SINGLE_TOKENS, kv_quant_diff, rms,
+                         single_layer_model, teacher_prompt)
 
 pytestmark = pytest.mark.gpu
 
@@ -79,20 +82,29 @@ def test_rope_tables_bit_exact(pair, ctx):
             assert np.array_equal(s.view(np.uint32), rs.view(np.uint32))
 
 
-@pytest.mark.parametrize("arch,qtype", [("llama", synth.Q8_0), ("llama", synth.Q4_0), ("gemma3", synth.Q8_0)])
-def test_single_layer_position0_tight(torch_gpu, cpuref, arch, qtype):
-    """No attention history and one layer: only fp32 summation order differs."""
-    extra = dict(head_dim=256, softcap=30.0, swa_window=16, tied=True) if arch == "gemma3" else {}
-    g = synth.synthetic_model(arch=arch, dim=512, hidden=1024, n_layers=1, n_heads=8, n_kv=2, vocab=2048, ctx=64,
-                              qtype=qtype, seed=21, norm_jitter=0.1, **extra)
+@pytest.mark.parametrize("case", list(SINGLE_LAYER))
+def test_single_layer_position0_tight(torch_gpu, cpuref, case):
+    """No attention history and one layer: only fp32 summation order differs.
+
+    Per token, max|dlogit| <= max(1e-4, 2 * drift) * rms(logits), where drift
+    is what the reference's -Ofast -fopenmp build shows against its plain
+    build on the same token (tests/golden/ref_drift.json, "single_layer").
+    The drift is ~5e-7 except where a quantized value (a Q8_0 activation of
+    Q4_0 weights, a K/V quant) sits on a rounding boundary; there either build
+    may round one step the other way and logits move by up to a few percent."""
+    g = single_layer_model(case)
+    drift = SINGLE_DRIFT[case]
     with l3p.Context(0) as c2:
         c2.load_gguf(g)
         m = cpuref.open_model(g)
-        for tok in (0, 7, 1234):
+        rel = []
+        for tok in SINGLE_TOKENS:
             a = m.forward(tok, 0)
             b = c2.forward(tok, 0)
-            assert float(np.max(np.abs(a - b))) <= 1e-4 * rms(a)
+            rel.append(float(np.max(np.abs(a - b))) / rms(a))
         m.close()
+    for tok, r, d in zip(SINGLE_TOKENS, rel, drift):
+        assert r <= max(1e-4, 2.0 * d), (case, tok, r, d)
 
 
 def test_teacher_forced_logits_and_kv(pair, ctx):

@@ -143,6 +143,21 @@ def _check_gemv(ctx, torch, cpuref, qtype, rows, cols, seed=0, sample_rows=None)
     (l3p.Q8_0, 300, 256),          # one partial chunk
     (l3p.Q4_0, 77, 1536),
     (l3p.Q8_0, 128256 // 64, 4096),
+    # rows that are not 16-byte multiples (copied from 16-byte aligned-down
+    # addresses): Gemma-3-1B / 270M widths, tiny rows, Q6_K off 2048-multiples
+    (l3p.Q8_0, 2048, 1152),
+    (l3p.Q8_0, 1025, 640),
+    (l3p.Q8_0, 99, 96),
+    (l3p.Q4_0, 2048, 1152),
+    (l3p.Q4_0, 333, 160),
+    (l3p.Q6_K, 1000, 2304),
+    (l3p.Q6_K, 512, 1536),
+    (l3p.Q6_K, 301, 256),
+    (l3p.Q6_K, 4097, 14336),
+    # Q4_K: partial last chunk (9 super-blocks), one super-block, FFN down
+    (l3p.Q4_K, 2304, 2304),
+    (l3p.Q4_K, 100, 256),
+    (l3p.Q4_K, 4096, 14336),
 ])
 def test_gemv_parity(ctx, torch_gpu, cpuref, qtype, rows, cols):
     _check_gemv(ctx, torch_gpu, cpuref, qtype, rows, cols, seed=rows + cols, sample_rows=min(rows, 768))

@@ -25,6 +25,10 @@ CASES = {
                             qtype=synth.Q4_0, seed=2, tied=True),
     "gemma_swa": dict(arch="gemma3", dim=256, hidden=768, n_layers=7, n_heads=4, n_kv=2, head_dim=64, vocab=512,
                       ctx=128, qtype=synth.Q8_0, seed=3, softcap=30.0, swa_window=12, norm_jitter=0.1, tied=True),
+    # Q4_K with Q6_K down / V / output projections (a Q4_K_M-style mix)
+    "llama_q4_k_m": dict(arch="llama", dim=256, hidden=512, n_layers=2, n_heads=8, n_kv=2, vocab=512, ctx=128,
+                         qtype=synth.Q4_K, seed=4, norm_jitter=0.1,
+                         qtypes={"ffn_down": synth.Q6_K, "attn_v": synth.Q6_K, "output": synth.Q6_K}),
 }
 
 
