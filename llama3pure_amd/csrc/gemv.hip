@@ -13,9 +13,10 @@
 //
 // Streaming.  Each wave copies its own chunks HBM -> LDS with
 // global_load_lds (dwordx4 pieces and a dword piece, cache policy nt: the
-// weights are read once per call) into a private ring of NB buffers, keeping
-// NB-1 chunks in flight, and waits for a chunk with its own vmcnt: no
-// workgroup barrier inside the row loop.  The only barrier is per row group,
+// weights are read once per call) into a private ring of NB buffers.  Before
+// computing chunk k it refills the buffer of chunk k-1 with chunk k+NB-1, so
+// NB-1 chunks are in flight during the compute, and waits for chunk k with
+// its own vmcnt: no workgroup barrier inside the row loop.  The only barrier is per row group,
 // for the cross-wave sum.
 //
 // Row alignment.  When a row's length in bytes is a multiple of 16 (cols a
@@ -44,10 +45,12 @@
 // depend on timing.
 //
 // Prologue (optional RMSNorm, c:3117-3129): every workgroup computes
-// ss = sum(x^2) in one fixed order and r = 1/sqrt(ss/n + eps); lane l then
-// forms w[j] * (r * x[j]) for its elements and prepares them.  The lane's x
-// and norm loads are issued first, then the first weight copies, so HBM is
-// busy while the activation is prepared.
+// ss = sum(x^2) in one fixed order and r = 1/sqrt(ss/n + eps).  Q4_0 lanes
+// form w[j] * (r * x[j]) and quantize it as the reference does; the fp32
+// types use w[j] * x[j] and multiply each row total by r (the product is
+// linear in x), so no wave waits for the others before its first chunk.
+// The lane's x and norm loads are issued first, then the first weight
+// copies, so HBM is busy while the activation is prepared.
 #include "device_common.h"
 #include "internal.h"
 
@@ -115,6 +118,19 @@ __device__ __forceinline__ void wait_vm() {
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// Wait for the copy of a chunk when `younger` copies (CI instructions each)
+// were issued after it: vmcnt(min(younger, J) * CI), as a chain of scalar
+// compares that ends at the first hit (the common case is younger >= J).
+template <int J, int CI>
+__device__ __forceinline__ void wait_chunk(int younger) {
+    if constexpr (J == 0) {
+        wait_vm<0>();
+    } else {
+        if (younger >= J) wait_vm<J * CI>();
+        else wait_chunk<J - 1, CI>(younger);
+    }
 }
 
 // Byte offsets this lane copies, from the copy base, for a chunk whose data
@@ -549,7 +565,12 @@ __global__ void __launch_bounds__(1024) gemv_kernel(GemvArgs a) {
 
     // ---- optional RMSNorm.  Every block of x belongs to exactly one lane, so
     // ss = sum over lanes of the lane's 32 squares, then over lanes and waves
-    // in a fixed order: the same value in every workgroup.
+    // in a fixed order: the same value in every workgroup.  For fp32
+    // activations the GEMV is linear in x, so the lanes take w[j] * x[j] and
+    // the row totals are scaled by r after the first group's cross-wave sum:
+    // nothing here waits for the other waves.  Q4_0 quantizes w[j] * (r *
+    // x[j]) exactly as the reference does, so it forms r first.
+    constexpr bool kLateScale = QT != L3P_Q4_0;
     if (a.norm) {
         float ss = 0.0f;
 #pragma unroll
@@ -557,20 +578,31 @@ __global__ void __launch_bounds__(1024) gemv_kernel(GemvArgs a) {
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
         if (lane == 0) ssred[w] = ss;
-        lds_sync();
-        ss = 0.0f;
-        for (int i = 0; i < nw; ++i) ss += ssred[i];
-        const float r = 1.0f / sqrtf(ss * a.inv_n + a.eps);
+        float r = 1.0f;
+        if (!kLateScale) {
+            lds_sync();
+            ss = 0.0f;
+            for (int i = 0; i < nw; ++i) ss += ssred[i];
+            r = 1.0f / sqrtf(ss * a.inv_n + a.eps);
+        }
         if (active) {
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                v[4 * e] = nv[e].x * (r * v[4 * e]);
-                v[4 * e + 1] = nv[e].y * (r * v[4 * e + 1]);
-                v[4 * e + 2] = nv[e].z * (r * v[4 * e + 2]);
-                v[4 * e + 3] = nv[e].w * (r * v[4 * e + 3]);
+                if (kLateScale) {
+                    v[4 * e] = nv[e].x * v[4 * e];
+                    v[4 * e + 1] = nv[e].y * v[4 * e + 1];
+                    v[4 * e + 2] = nv[e].z * v[4 * e + 2];
+                    v[4 * e + 3] = nv[e].w * v[4 * e + 3];
+                } else {
+                    v[4 * e] = nv[e].x * (r * v[4 * e]);
+                    v[4 * e + 1] = nv[e].y * (r * v[4 * e + 1]);
+                    v[4 * e + 2] = nv[e].z * (r * v[4 * e + 2]);
+                    v[4 * e + 3] = nv[e].w * (r * v[4 * e + 3]);
+                }
             }
         }
     }
+    float rscale = 1.0f;   // late RMSNorm scale of the row totals (threads t < NOUT)
     XBlock xb;
     prepare_block<QT>(v, xb);
     Lane<QT> ln;
@@ -582,10 +614,14 @@ __global__ void __launch_bounds__(1024) gemv_kernel(GemvArgs a) {
 #pragma unroll
         for (int i = 0; i < G; ++i) {
             const int k = gl * G + i;
+            // refill first: chunk k+NB-1 goes to the buffer of chunk k-1, whose
+            // LDS reads finished in the previous step, so NB-1 copies stay in
+            // flight while chunk k is computed
+            const int kn = k + NB - 1;
+            if (kn < nk) issue(kn, kn % NB);
             // chunk k is in LDS once only the younger chunks' copies remain:
-            // NB-2 of them in steady state, none near the end of the sequence
-            if (k + NB - 2 < nk) wait_vm<(NB - 2) * CI>();
-            else wait_vm<0>();
+            // NB-1 of them in steady state, fewer near the end of the sequence
+            wait_chunk<NB - 1, CI>(nk - 1 - k);
             const uint8_t* src;
             const bool real = chunk_src<G, PAIR>(cc, k, src);
             if (UA) ln.at(lane, (uint32_t)(uintptr_t)src & 15u);
@@ -597,8 +633,6 @@ __global__ void __launch_bounds__(1024) gemv_kernel(GemvArgs a) {
             asm volatile("" : "+v"(dv));
             const float d = (real && active) ? dv : 0.0f;
             wait_lgkm();   // this chunk's LDS reads are done before its buffer is refilled
-            const int kn = k + NB - 1;
-            if (kn < nk) issue(kn, kn % NB);
             acc[i] = d;
         }
         // group done: wave totals -> LDS -> sum over the chunk waves in order
@@ -607,12 +641,19 @@ __global__ void __launch_bounds__(1024) gemv_kernel(GemvArgs a) {
         if ((lane & ((64 / G) - 1)) == 0) rd[w * G + rowof<G>(lane)] = tot;
         lds_sync();
         if (t < NOUT) {
+            if (kLateScale && a.norm && gl == 0) {   // every wave's ss is in LDS by now
+                float ss = 0.0f;
+                for (int i = 0; i < nw; ++i) ss += ssred[i];
+                rscale = 1.0f / sqrtf(ss * a.inv_n + a.eps);
+            }
             float s0 = 0.0f;
             for (int c = 0; c < nw; ++c) s0 += rd[c * G + t];
+            s0 *= rscale;
             float res = s0;
             if (PAIR) {
                 float s1 = 0.0f;
                 for (int c = 0; c < nw; ++c) s1 += rd[c * G + G / 2 + t];
+                s1 *= rscale;
                 res = a.epilogue == EPI_GEGLU ? ref_geglu(s0, s1) : ref_swiglu(s0, s1);
             }
             out_lds[gl * NOUT + t] = res;
@@ -684,8 +725,19 @@ void launch_rows(GemvArgs a, hipStream_t st) {
     const size_t base = (size_t)nw * NB * Fmt<QT>::kBufBytes + (size_t)2 * nw * G * 4 + (size_t)nw * 4;
     auto lds_for = [&](int grid) { return base + (size_t)((a.ngroups + grid - 1) / grid) * NOUT * 4; };
     auto kern = gemv_kernel<QT, G, NB, PAIR, UA>;
-    const int per_cu = occupancy(kern, threads, lds_for(cus()));
-    int grid = std::min(a.ngroups, per_cu * cus());
+    // Every workgroup reads the whole activation (and the norm weights when
+    // fused), so workgroups per CU are also capped to keep that traffic near
+    // 128 KB per CU: more workgroups than this only add x reads that compete
+    // with the weight stream (measured on MI355X at the Llama-3-8B shapes).
+    const int xbytes = a.cols * 4 * (a.norm ? 2 : 1);
+    const int per_cu = std::min(occupancy(kern, threads, lds_for(cus())), std::max(1, (128 << 10) / xbytes));
+    const int cap = per_cu * cus();
+    int grid = std::min(a.ngroups, cap);
+    if (env_int("L3P_GEMV_BAL", 1)) {
+        // the same number of groups (k, or k-1 for the last few) per workgroup
+        const int k = (a.ngroups + cap - 1) / cap;
+        grid = (a.ngroups + k - 1) / k;
+    }
     grid = std::max(grid, (a.ngroups * NOUT + kMaxOut - 1) / kMaxOut);
     const size_t lds = lds_for(grid);
     if (lds > 65536)
@@ -755,7 +807,7 @@ bool gemv_supported(int type, int cols) {
 }
 
 void launch_gemv(int type, const GemvBatch& b, int cols, const float* x, const float* norm, float eps,
-                  hipStream_t st) {
+                 hipStream_t st) {
     L3P_REQUIRE(gemv_supported(type, cols), L3P_E_UNSUPPORTED, "gemv: type %d with %d columns not supported",
                 type, cols);
     L3P_REQUIRE(((uintptr_t)x & 15) == 0 && ((uintptr_t)norm & 15) == 0, L3P_E_INVALID,
@@ -780,13 +832,14 @@ void launch_gemv(int type, const GemvBatch& b, int cols, const float* x, const f
     a.eps = eps;
     a.inv_n = 1.0f / (float)cols;
     // Rows per group G: the largest of 16, 8, 4 that still gives about six
-    // waves per CU (groups x column chunks); ring depth 3 at G = 4, else 4.
-    // (Measured on MI355X at the Llama-3-8B shapes.)
+    // waves per CU (groups x column chunks); ring depth 3.  (Measured on
+    // MI355X at the Llama-3-8B shapes.)
     const int nw = (cols / 32 + 63) / 64;
     const int units = a.rows_total;
     const int per_g = b.pair ? 2 : 1;   // pair groups hold G/2 rows of each matrix
     auto waves = [&](int g) { return (long)(units * per_g + g - 1) / g * nw; };
     int G = env_int("L3P_GEMV_G", 0);
+    if (b.pair && G == 16) G = 8;   // pair kernels exist for G = 4, 8
     if (G != 4 && G != 8 && G != 16) {
         G = 4;
         for (int g : {16, 8})
@@ -795,7 +848,7 @@ void launch_gemv(int type, const GemvBatch& b, int cols, const float* x, const f
                 break;
             }
     }
-    const int nbuf = env_int("L3P_GEMV_NB", G == 4 ? 3 : 4);
+    const int nbuf = env_int("L3P_GEMV_NB", 3);
     switch (type) {
     case L3P_Q8_0: launch_type<L3P_Q8_0>(a, b.pair != 0, G, nbuf, st); break;
     case L3P_Q4_0: launch_type<L3P_Q4_0>(a, b.pair != 0, G, nbuf, st); break;
