@@ -20,7 +20,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "libl3p.so")
 BUILD = os.path.join(HERE, "_build")
-SOURCES = ["gemv.hip", "blocks.hip", "layers.hip", "api.cpp", "model.cpp"]
+SOURCES = ["gemv.hip", "gemm.hip", "blocks.hip", "layers.hip", "api.cpp", "model.cpp"]
 ARCH = os.environ.get("L3P_ARCH", "gfx950")
 
 FLAGS = [f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",

@@ -1,0 +1,178 @@
+// gemm.hip — the prefill GEMM on the fp32 matrix cores (gfx950):
+//   Y[m][n] (=|+=) sum_k W[n][k] * X[m][k]
+// for M prompt tokens, N output features and K inputs, with W in its GGUF
+// block layout.  It replaces matmul_quantized_batch (llama3pure-c-engine.c:
+// 2291-2331) for the types the reference dequantizes before its batched dot
+// (matmul_deq_batch_4row, c:2179-2273): every weight is expanded exactly to
+// fp32 (dequantize_row_*, c:611-934) and multiplied with the fp32
+// activation, so the products are the reference's and only the fp32
+// summation order differs.
+//
+// Tiling.  A workgroup owns a 64 x 64 tile of Y and walks K in steps of 64:
+//   1. the 64 x 64 X tile (fp32, from L2) and the dequantized 64 x 64 W tile
+//      go to LDS, rows padded to 68 floats;
+//   2. four waves each compute a 32 x 32 quarter with v_mfma_f32_16x16x4_f32
+//      (2 x 2 tiles of 16 x 16).  The instruction contracts over 4 k-slots,
+//      slot g held by lanes 16g..16g+15; here slot g of step s is
+//      k = kk + 4g + s, the same for A (X) and B (W), so each lane fetches
+//      its four k values of a 16-wide slab with one ds_read_b128.
+// Several workgroups per CU hide the load and dequantization latency.
+#include "dequant.h"
+#include "device_common.h"
+#include "internal.h"
+
+namespace {
+
+using namespace l3pd;
+
+constexpr int kBM = 64, kBN = 64, kBK = 64;
+constexpr int kLDK = kBK + 4;   // LDS row stride in floats (b128 reads spread over the banks)
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+struct GemmArgs {
+    const uint8_t* w;
+    size_t rb;        // bytes per weight row
+    int n, k, m;      // output features, inputs, batch rows
+    const float* x;
+    int ldx;
+    float* y;
+    int ldy;
+    int add;          // 1: Y += W.X (residual), 0: Y = W.X
+};
+
+// Rows [n0, n0+64) x columns [k0, k0+64) of W, dequantized into ws[r][c].
+// Q8_0 (blocks of 32, 34 B): thread t expands 16 values of one block,
+// (float)q * d as in dequantize_row_q8_0 (c:691-702).  Other types go
+// element by element through the reference-exact dequantizer.
+template <int QT>
+__device__ __forceinline__ void load_w_tile(float* ws, const GemmArgs& a, int n0, int k0, int t) {
+    if (QT == L3P_Q8_0) {
+        const int r = t >> 2, blk = (t >> 1) & 1, half = t & 1;
+        const int n = n0 + r, kb = (k0 >> 5) + blk;
+        float v[16];
+        if (n < a.n && 32 * kb < a.k) {
+            const uint8_t* b = a.w + (size_t)n * a.rb + (size_t)kb * 34;
+            const float d = ldh(b);
+            const uint16_t* q = reinterpret_cast<const uint16_t*>(b + 2 + 16 * half);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const uint32_t u = q[j];
+                v[2 * j] = (float)(int8_t)(u & 0xffu) * d;
+                v[2 * j + 1] = (float)(int8_t)(u >> 8) * d;
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) v[j] = 0.0f;
+        }
+        float4* dst = reinterpret_cast<float4*>(ws + r * kLDK + 32 * blk + 16 * half);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) dst[j] = make_float4(v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
+    } else {
+        // 4096 values, 16 per thread: row t/4, columns 16*(t%4) .. +16
+        const int r = t >> 2, c0 = 16 * (t & 3);
+        const int n = n0 + r;
+        const bool ok = n < a.n;
+        const uint8_t* row = a.w + (size_t)(ok ? n : 0) * a.rb;
+#pragma unroll 4
+        for (int j = 0; j < 16; ++j) {
+            const int kk = k0 + c0 + j;
+            ws[r * kLDK + c0 + j] = (ok && kk < a.k) ? deq_elem(QT, row, kk) : 0.0f;
+        }
+    }
+}
+
+template <int QT>
+__global__ void __launch_bounds__(256) gemm_kernel(GemmArgs a) {
+    __shared__ __align__(16) float xs[kBM * kLDK];
+    __shared__ __align__(16) float ws[kBN * kLDK];
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const int n0 = blockIdx.x * kBN, m0 = blockIdx.y * kBM;
+    const int wm = w >> 1, wn = w & 1;      // this wave's 32 x 32 quarter
+    const int g = lane >> 4, i16 = lane & 15;
+    floatx4 acc[2][2];
+#pragma unroll
+    for (int im = 0; im < 2; ++im)
+#pragma unroll
+        for (int in = 0; in < 2; ++in) acc[im][in] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    for (int k0 = 0; k0 < a.k; k0 += kBK) {
+        // X tile: 64 rows x 16 float4, four per thread
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int i = t + 256 * u, r = i >> 4, c = i & 15;
+            const int m = m0 + r, kk = k0 + 4 * c;
+            float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (m < a.m && kk < a.k) v = *reinterpret_cast<const float4*>(a.x + (size_t)m * a.ldx + kk);
+            *reinterpret_cast<float4*>(xs + r * kLDK + 4 * c) = v;
+        }
+        load_w_tile<QT>(ws, a, n0, k0, t);
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < kBK; kk += 16) {
+            float4 af[2], bf[2];
+#pragma unroll
+            for (int im = 0; im < 2; ++im)
+                af[im] = *reinterpret_cast<const float4*>(xs + (32 * wm + 16 * im + i16) * kLDK + kk + 4 * g);
+#pragma unroll
+            for (int in = 0; in < 2; ++in)
+                bf[in] = *reinterpret_cast<const float4*>(ws + (32 * wn + 16 * in + i16) * kLDK + kk + 4 * g);
+            const float a0[4] = {af[0].x, af[0].y, af[0].z, af[0].w};
+            const float a1[4] = {af[1].x, af[1].y, af[1].z, af[1].w};
+            const float b0[4] = {bf[0].x, bf[0].y, bf[0].z, bf[0].w};
+            const float b1[4] = {bf[1].x, bf[1].y, bf[1].z, bf[1].w};
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                acc[0][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0[s], b0[s], acc[0][0], 0, 0, 0);
+                acc[0][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0[s], b1[s], acc[0][1], 0, 0, 0);
+                acc[1][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1[s], b0[s], acc[1][0], 0, 0, 0);
+                acc[1][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1[s], b1[s], acc[1][1], 0, 0, 0);
+            }
+        }
+        __syncthreads();
+    }
+    // D layout of the 16 x 16 tile: lane (g, i16) holds rows 4g..4g+3 of column i16
+#pragma unroll
+    for (int im = 0; im < 2; ++im)
+#pragma unroll
+        for (int in = 0; in < 2; ++in) {
+            const int n = n0 + 32 * wn + 16 * in + i16;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int m = m0 + 32 * wm + 16 * im + 4 * g + r;
+                if (m < a.m && n < a.n) {
+                    float* p = a.y + (size_t)m * a.ldy + n;
+                    const float v = acc[im][in][r];
+                    *p = a.add ? *p + v : v;
+                }
+            }
+        }
+}
+
+template <int QT>
+void launch_typed(const GemmArgs& a, hipStream_t st) {
+    const dim3 grid((a.n + kBN - 1) / kBN, (a.m + kBM - 1) / kBM);
+    hipLaunchKernelGGL(gemm_kernel<QT>, grid, dim3(256), 0, st, a);
+    L3P_HIP(hipGetLastError());
+}
+
+}  // namespace
+
+bool gemm_mfma_supported(int type) {
+    return type == L3P_Q8_0 || type == L3P_Q4_K || type == L3P_Q6_K;
+}
+
+void launch_gemm(int type, const uint8_t* w, int n, int k, const float* x, int m, int ldx, float* y, int ldy,
+                 bool add, hipStream_t st) {
+    L3P_REQUIRE(gemm_mfma_supported(type), L3P_E_UNSUPPORTED, "gemm: type %d has no MFMA path", type);
+    L3P_REQUIRE(k % 32 == 0 && ldx % 4 == 0 && ((uintptr_t)x & 15) == 0, L3P_E_INVALID,
+                "gemm: x rows must be 16-byte aligned");
+    L3P_REQUIRE(m <= 65535 * kBM, L3P_E_INVALID, "gemm: batch %d too large", m);
+    if (m == 0 || n == 0) return;
+    GemmArgs a{w, type_row_bytes(type, k), n, k, m, x, ldx, y, ldy, add ? 1 : 0};
+    switch (type) {
+    case L3P_Q8_0: launch_typed<L3P_Q8_0>(a, st); break;
+    case L3P_Q4_K: launch_typed<L3P_Q4_K>(a, st); break;
+    default: launch_typed<L3P_Q6_K>(a, st); break;
+    }
+}

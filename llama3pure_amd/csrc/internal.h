@@ -102,6 +102,12 @@ struct GemvBatch {
 bool gemv_supported(int type, int cols);
 void launch_gemv(int type, const GemvBatch& b, int cols, const float* x, const float* norm, float eps,
                  hipStream_t s);
+// gemm.hip: Y[m][n] (=|+=) W[n,:] . X[m,:] on the fp32 matrix cores, for the
+// types the reference dequantizes before its batched dot (Q8_0, Q4_K, Q6_K).
+// x rows must be 16-byte aligned (ldx a multiple of 4).
+bool gemm_mfma_supported(int type);
+void launch_gemm(int type, const uint8_t* w, int n, int k, const float* x, int m, int ldx, float* y, int ldy,
+                 bool add, hipStream_t s);
 // blocks.hip
 void launch_quantize_q8_0_blocks(const float* x, int64_t n, uint8_t* dst, hipStream_t s);
 void launch_dequant(int type, const uint8_t* src, int64_t n, float* dst, hipStream_t s);

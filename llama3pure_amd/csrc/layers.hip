@@ -1,9 +1,11 @@
-// layers.hip — the fused per-layer kernels of the decode path (gfx950):
-// RMSNorm (+ activation quantization), QK-norm + RoPE + Q8_0 KV write,
-// split-position GQA attention over the Q8_0 KV cache, logit soft-cap and the
+// layers.hip — the per-layer kernels around the GEMVs and GEMMs (gfx950):
+// QK-norm + RoPE + Q8_0 KV write fused into split-position GQA attention over
+// the Q8_0 KV cache, the Gemma post-norm residuals, the row kernels of a
+// prompt batch (embedding, RMSNorm, activation), logit soft-cap and the
 // sampler.  Arithmetic follows llama3pure-c-engine.c (cited per kernel); the
 // library is built with -ffp-contract=off so elementwise expressions round
 // exactly as the reference's scalar C does.
+#include "dequant.h"
 #include "device_common.h"
 #include "model.h"
 
@@ -54,16 +56,63 @@ __device__ float block_sum(float v, float* sh) {
 
 
 // x += rmsnorm(y) (Gemma post-attention / post-FFN norm then residual,
-// c:3364-3371, c:3411-3417).
-__global__ void __launch_bounds__(1024) rmsnorm_add_kernel(const float* __restrict__ y, const float* __restrict__ w,
-                                                           int n, float inv_n, float eps, float* x) {
+// c:3364-3371, c:3411-3417), one row per workgroup (row strides ldy, ldx).
+__global__ void __launch_bounds__(1024) rmsnorm_add_kernel(const float* __restrict__ y, int ldy,
+                                                           const float* __restrict__ w, int n, float inv_n, float eps,
+                                                           float* x, int ldx) {
     __shared__ float sh[16];
     const int t = threadIdx.x, nt = blockDim.x;
+    y += (size_t)blockIdx.x * ldy;
+    x += (size_t)blockIdx.x * ldx;
     float ss = 0.0f;
     for (int j = t; j < n; j += nt) ss += y[j] * y[j];
     ss = block_sum(ss, sh);
     const float r = 1.0f / sqrtf(ss * inv_n + eps);
     for (int j = t; j < n; j += nt) x[j] += w[j] * (r * y[j]);
+}
+
+// ---------------------------------------------------------------------------
+// Rows of a prompt batch (transformer_prefill, c:3439-3680).
+// ---------------------------------------------------------------------------
+// x[b] = embedding row of tokens[b] (dequantize_row, c:3447-3452), times
+// scale when non-zero (Gemma, c:3132-3148), and the step record
+// {token, start + b} that token b's attention reads.
+__global__ void embed_rows_kernel(int type, const uint8_t* __restrict__ emb, size_t rb, int n, float scale,
+                                  const int* __restrict__ tokens, int start, float* __restrict__ x, int ldx,
+                                  int* __restrict__ steps) {
+    const int b = blockIdx.y, i = blockIdx.x * blockDim.x + threadIdx.x;
+    const int tok = tokens[b];
+    if (i < n) {
+        const float v = deq_elem(type, emb + (size_t)tok * rb, i);
+        x[(size_t)b * ldx + i] = scale != 0.0f ? v * scale : v;
+    }
+    if (i == 0) {
+        steps[2 * b] = tok;
+        steps[2 * b + 1] = start + b;
+    }
+}
+
+// o[b] = w * (r * x[b]) with r = 1/sqrt(sum(x[b]^2)/n + eps) (rmsnorm,
+// c:3117-3129), one row per workgroup.
+__global__ void __launch_bounds__(1024) rmsnorm_rows_kernel(const float* __restrict__ x, int ldx,
+                                                            const float* __restrict__ w, int n, float inv_n,
+                                                            float eps, float* __restrict__ o, int ldo) {
+    __shared__ float sh[16];
+    const int t = threadIdx.x, nt = blockDim.x;
+    x += (size_t)blockIdx.x * ldx;
+    o += (size_t)blockIdx.x * ldo;
+    float ss = 0.0f;
+    for (int j = t; j < n; j += nt) ss += x[j] * x[j];
+    ss = block_sum(ss, sh);
+    const float r = 1.0f / sqrtf(ss * inv_n + eps);
+    for (int j = t; j < n; j += nt) o[j] = w[j] * (r * x[j]);
+}
+
+// h = act(h) * h2 elementwise over the batch's FFN rows: SwiGLU
+// (c:3400-3406) or tanh-GeLU (c:3391-3398).
+__global__ void act_rows_kernel(float* __restrict__ h, const float* __restrict__ h2, int64_t n, int gelu) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) h[i] = gelu ? ref_geglu(h[i], h2[i]) : ref_swiglu(h[i], h2[i]);
 }
 
 // ---------------------------------------------------------------------------
@@ -97,7 +146,24 @@ struct AttnCArgs {
     size_t head_seq;
     int n_heads, kv_mul, hs, hq8, window, neox;
     float attn_scale, eps, inv_hs;
+    // Prompt batches: token z (the last grid dimension) uses q + z*q_stride,
+    // k, v + z*kv_stride, step + 2z, part + z*part_stride, out + z*out_stride,
+    // and its K/V rows are already in the cache (kv_ready, kv_rows_kernel).
+    int q_stride, kv_stride, out_stride, kv_ready;
+    size_t part_stride;
 };
+
+// The arguments of token z of a prompt batch (z = 0: a decode step).
+__device__ __forceinline__ AttnCArgs token_args(const AttnCArgs& a0, int z) {
+    AttnCArgs a = a0;
+    a.q += (size_t)z * a.q_stride;
+    a.k += (size_t)z * a.kv_stride;
+    a.v += (size_t)z * a.kv_stride;
+    a.step += 2 * z;
+    a.part += (size_t)z * a.part_stride;
+    a.out += (size_t)z * a.out_stride;
+    return a;
+}
 
 // Positions this step attends to: [t0, pos], in chunks of kTC (c:3316-3322).
 struct Span {
@@ -126,8 +192,9 @@ __device__ __forceinline__ float row_block(const uint32_t* base, uint32_t off, u
     return h2f(odd ? (dw[0] >> 16) : dw[0]);
 }
 
-__global__ void __launch_bounds__(1024) attn_chunk_kernel(AttnCArgs a) {
+__global__ void __launch_bounds__(1024) attn_chunk_kernel(AttnCArgs a0) {
     extern __shared__ __align__(16) float smem[];
+    const AttnCArgs a = token_args(a0, blockIdx.z);
     const int g = blockIdx.x, c = blockIdx.y;
     const Span sp = span_of(a.step, a.window);
     if (c >= sp.n_chunks) return;   // the grid covers the longest context
@@ -135,7 +202,9 @@ __global__ void __launch_bounds__(1024) attn_chunk_kernel(AttnCArgs a) {
     const int hs = a.hs, nb = hs / 32, half = hs / 2, km = a.kv_mul;
     const int h = g * km + w;
     const int jbeg = c * kTC, jend = min(sp.na, jbeg + kTC), cnt = jend - jbeg;
-    const bool has_pos = c == sp.n_chunks - 1;   // the chunk holding the step's position
+    // the chunk holding the step's position forms and writes its K/V row,
+    // unless a prompt batch's kv_rows_kernel already wrote it
+    const bool has_pos = c == sp.n_chunks - 1 && !a.kv_ready;
 
     // LDS: [kv_mul][hs] q rows, [2][hs] k and v rows, [kv_mul][8][kTC] V
     // factors, [kv_mul][hs] int8 q, [kv_mul][8] q scales, then the chunk's K
@@ -377,12 +446,69 @@ __global__ void __launch_bounds__(1024) attn_chunk_kernel(AttnCArgs a) {
     }
 }
 
+// K and V rows of every token of a prompt batch into the cache, before the
+// batch's attention reads them (c:3301-3308): for KV head g = blockIdx.x of
+// token z = blockIdx.y, Gemma's QK-norm of k (c:3232-3236), RoPE of k
+// (c:3254-3296) and the Q8_0 rows of k and v (quantize_to_q8_0_cache,
+// c:1535-1570), with the arithmetic and order of attn_chunk_kernel's own
+// K/V path.  One wave.
+__global__ void __launch_bounds__(64) kv_rows_kernel(AttnCArgs a0) {
+    __shared__ float kvh[2 * 256];
+    const AttnCArgs a = token_args(a0, blockIdx.y);
+    const int g = blockIdx.x, lane = threadIdx.x;
+    const int hs = a.hs, half = hs / 2;
+    const int pos = a.step[1];
+    for (int j = lane; j < 2 * hs; j += 64)
+        kvh[j] = j < hs ? a.k[(size_t)g * hs + j] : a.v[(size_t)g * hs + j - hs];
+    __syncthreads();
+    if (a.k_norm) {
+        float ssk = 0.0f;
+        for (int j = lane; j < hs; j += 64) ssk += kvh[j] * kvh[j];
+        ssk = wave_sum(ssk);
+        const float rk = 1.0f / sqrtf(ssk * a.inv_hs + a.eps);
+        __syncthreads();
+        for (int j = lane; j < hs; j += 64) kvh[j] = a.k_norm[j] * (rk * kvh[j]);
+        __syncthreads();
+    }
+    const float* cosr = a.cos + (size_t)pos * half;
+    const float* sinr = a.sin + (size_t)pos * half;
+    for (int p = lane; p < half; p += 64) {
+        const int i0 = a.neox ? p : 2 * p;
+        const int i1 = a.neox ? p + half : 2 * p + 1;
+        const float k0 = kvh[i0], k1 = kvh[i1], cs = cosr[p], sn = sinr[p];
+        kvh[i0] = k0 * cs - k1 * sn;
+        kvh[i1] = k0 * sn + k1 * cs;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int sel = 0; sel < 2; ++sel) {
+        uint8_t* cd = (sel ? a.vc : a.kc) + (size_t)g * a.head_seq + (size_t)pos * a.hq8;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int j = lane + 64 * k;
+            if (k * 64 < hs) {
+                uint32_t dh;
+                const int8_t q = quant_lane(j < hs ? kvh[sel * hs + j] : 0.0f, dh);   // all lanes take part
+                if (j < hs) {
+                    const int b = j >> 5;
+                    cd[34 * b + 2 + (j & 31)] = (uint8_t)q;
+                    if ((lane & 31) == 0) {
+                        cd[34 * b] = (uint8_t)(dh & 0xff);
+                        cd[34 * b + 1] = (uint8_t)(dh >> 8);
+                    }
+                }
+            }
+        }
+    }
+}
+
 // out = sum_c acc_c * expf(m_c - M) / S with M = max m_c, S = sum l_c expf(m_c - M).
 // Every load is issued before anything waits: the first wave reads the
 // chunk maxima and sums (lane = chunk) while each thread reads its output's
 // chunk partials; the weights expf(m_c - M) / S go through LDS.
-__global__ void __launch_bounds__(256) attn_merge_kernel(AttnCArgs a) {
+__global__ void __launch_bounds__(256) attn_merge_kernel(AttnCArgs a0) {
     __shared__ float wc[256];
+    const AttnCArgs a = token_args(a0, blockIdx.y);
     const Span sp = span_of(a.step, a.window);
     const int h = blockIdx.x, hs = a.hs, nch = sp.n_chunks, t = threadIdx.x;
     const float* part = a.part + (size_t)h * nch * (hs + 2);
@@ -570,27 +696,59 @@ void launch_embed_step(const Mat& emb, int token, int pos, float scale, float* x
 }
 
 void launch_rmsnorm_add(const float* y, const float* w, int n, float inv_n, float eps, float* x, hipStream_t s) {
-    hipLaunchKernelGGL(rmsnorm_add_kernel, dim3(1), dim3(1024), 0, s, y, w, n, inv_n, eps, x);
+    launch_rmsnorm_add_rows(y, 0, w, n, inv_n, eps, x, 0, 1, s);
+}
+
+void launch_rmsnorm_add_rows(const float* y, int ldy, const float* w, int n, float inv_n, float eps, float* x,
+                             int ldx, int rows, hipStream_t s) {
+    if (rows == 0) return;
+    hipLaunchKernelGGL(rmsnorm_add_kernel, dim3(rows), dim3(1024), 0, s, y, ldy, w, n, inv_n, eps, x, ldx);
+    L3P_HIP(hipGetLastError());
+}
+
+void launch_embed_rows(const Mat& emb, const int* tokens, int rows, int start, float scale, float* x, int ldx,
+                       int* steps, hipStream_t s) {
+    if (rows == 0) return;
+    hipLaunchKernelGGL(embed_rows_kernel, dim3((emb.cols + 255) / 256, rows), dim3(256), 0, s, emb.type, emb.w,
+                       emb.rb, emb.cols, scale, tokens, start, x, ldx, steps);
+    L3P_HIP(hipGetLastError());
+}
+
+void launch_rmsnorm_rows(const float* x, int ldx, const float* w, int n, float inv_n, float eps, float* o, int ldo,
+                         int rows, hipStream_t s) {
+    if (rows == 0) return;
+    hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(rows), dim3(1024), 0, s, x, ldx, w, n, inv_n, eps, o, ldo);
+    L3P_HIP(hipGetLastError());
+}
+
+void launch_act_rows(float* h, const float* h2, int64_t n, bool gelu, hipStream_t s) {
+    if (n == 0) return;
+    hipLaunchKernelGGL(act_rows_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, h, h2, n, gelu ? 1 : 0);
     L3P_HIP(hipGetLastError());
 }
 
 void launch_attention(const Model& m, int l, float* out, hipStream_t s) {
+    launch_attention(m, l, AttnIO{m.q, m.k, m.v, m.step, out}, s);
+}
+
+// The attention arguments of layer l for the token whose rows io holds.
+static AttnCArgs attn_args(const Model& m, int l, const AttnIO& io) {
     const Layer& L = m.layers[l];
     const bool swa = m.swa_pattern > 0 && (l % m.swa_pattern < m.swa_pattern - 1);   // c:3247
     const bool use_swa = m.is_gemma && swa;
-    AttnCArgs a;
-    a.q = m.q;
-    a.k = m.k;
-    a.v = m.v;
+    AttnCArgs a{};
+    a.q = io.q;
+    a.k = io.k;
+    a.v = io.v;
     a.q_norm = m.is_gemma ? L.q_norm : nullptr;
     a.k_norm = m.is_gemma ? L.k_norm : nullptr;
     a.cos = use_swa ? m.cos_s : m.cos_d;
     a.sin = use_swa ? m.sin_s : m.sin_d;
     a.kc = m.kc + (size_t)l * m.layer_kv;
     a.vc = m.vc + (size_t)l * m.layer_kv;
-    a.step = m.step;
+    a.step = io.step;
     a.part = m.part_acc;
-    a.out = out;
+    a.out = io.out;
     a.head_seq = m.head_seq;
     a.n_heads = m.n_heads;
     a.kv_mul = m.kv_mul;
@@ -601,10 +759,15 @@ void launch_attention(const Model& m, int l, float* out, hipStream_t s) {
     a.attn_scale = m.attn_scale;
     a.eps = m.eps > 0 ? m.eps : 1e-5f;
     a.inv_hs = m.inv_hs;
+    return a;
+}
+
+// Chunk and merge launches for `tokens` tokens of up to `chunks` chunks each.
+static void launch_chunks(const Model& m, const AttnCArgs& a, int chunks, int tokens, hipStream_t s) {
     const int rowdw = (kTC * m.hq8 + 8 + 3) / 4;
     const size_t lds = (size_t)m.kv_mul * m.hs * 4 + 2 * (size_t)m.hs * 4 + (size_t)m.kv_mul * 8 * kTC * 4 +
                        (size_t)m.kv_mul * m.hs + (size_t)m.kv_mul * 8 * 4 + 2 * (size_t)rowdw * 4 + 16;
-    const dim3 grid(m.n_kv, m.max_chunks), block(64 * m.kv_mul);
+    const dim3 grid(m.n_kv, chunks, tokens), block(64 * m.kv_mul);
     static size_t lds_set = 65536;   // dynamic LDS above 64 KB must be allowed first
     if (lds > lds_set) {
         L3P_HIP(hipFuncSetAttribute((const void*)attn_chunk_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
@@ -612,8 +775,36 @@ void launch_attention(const Model& m, int l, float* out, hipStream_t s) {
     }
     hipLaunchKernelGGL(attn_chunk_kernel, grid, block, lds, s, a);
     L3P_HIP(hipGetLastError());
-    hipLaunchKernelGGL(attn_merge_kernel, dim3(m.n_heads), dim3((m.hs + 63) / 64 * 64), 0, s, a);
+    hipLaunchKernelGGL(attn_merge_kernel, dim3(m.n_heads, tokens), dim3((m.hs + 63) / 64 * 64), 0, s, a);
     L3P_HIP(hipGetLastError());
+}
+
+void launch_attention(const Model& m, int l, const AttnIO& io, hipStream_t s) {
+    launch_chunks(m, attn_args(m, l, io), m.max_chunks, 1, s);
+}
+
+int attention_chunks(const Model& m, int l, int last_pos) {
+    const AttnCArgs a = attn_args(m, l, AttnIO{});
+    const int t0 = a.window > 0 ? std::max(0, last_pos - a.window + 1) : 0;
+    return (last_pos - t0 + 1 + kTC - 1) / kTC;
+}
+
+void launch_attention_rows(const Model& m, int l, const AttnIO& io, int q_stride, int kv_stride, int out_stride,
+                           int tokens, int last_pos, float* part, size_t part_cap, hipStream_t s) {
+    if (tokens == 0) return;
+    AttnCArgs a = attn_args(m, l, io);
+    const int chunks = attention_chunks(m, l, last_pos);   // the most any token of the batch has
+    a.q_stride = q_stride;
+    a.kv_stride = kv_stride;
+    a.out_stride = out_stride;
+    a.kv_ready = 1;
+    a.part = part;
+    a.part_stride = (size_t)m.n_heads * chunks * (m.hs + 2);
+    L3P_REQUIRE(a.part_stride * tokens <= part_cap, L3P_E_INVALID, "attention: %d tokens exceed the partials buffer",
+                tokens);
+    hipLaunchKernelGGL(kv_rows_kernel, dim3(m.n_kv, tokens), dim3(64), 0, s, a);
+    L3P_HIP(hipGetLastError());
+    launch_chunks(m, a, chunks, tokens, s);
 }
 
 void launch_softcap(float* l, int n, float cap, hipStream_t s) {

@@ -584,12 +584,126 @@ static void layers_impl(l3p_ctx* c, bool with_logits) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// batched prefill (transformer_prefill, c:3439-3680)
+// ---------------------------------------------------------------------------
+static constexpr int kPrefillRows = 256;   // prompt tokens per pass over the weights
+
+static void ensure_prefill_rows(Model& m) {
+    if (m.pf_rows) return;
+    const int R = kPrefillRows;
+    auto f = [&](int n) { return (float*)m.dalloc((size_t)R * n * 4 + 64); };
+    m.pf_x = f(m.dim);
+    m.pf_xb = f(m.max_dim);
+    m.pf_xb2 = f(m.dim);
+    m.pf_q = f(m.q_dim);
+    m.pf_k = f(m.kv_dim);
+    m.pf_v = f(m.kv_dim);
+    m.pf_att = f(m.q_dim);
+    m.pf_hb = f(m.hidden);
+    m.pf_hb2 = f(m.hidden);
+    m.pf_tok = (int*)m.dalloc((size_t)R * 4);
+    m.pf_steps = (int*)m.dalloc((size_t)R * 8);
+    // partials for up to R tokens at the longest context, within 128 MB
+    const size_t per_token = (size_t)m.n_heads * m.max_chunks * (m.hs + 2);
+    m.pf_part_cap = std::max(per_token, std::min(per_token * R, (size_t)32 << 20));
+    m.pf_part = (float*)m.dalloc(m.pf_part_cap * 4);
+    m.pf_rows = R;
+}
+
+static std::string gemm_label(const char* what, int type, int rows, int n, int k) {
+    char b[112];
+    snprintf(b, sizeof b, "%s gemm %s %dx%d b%d", type_name(type), what, n, k, rows);
+    return b;
+}
+
+// y rows (=|+=) W . x rows for `rows` prompt tokens: the MFMA GEMM, or for
+// Q4_0 the GEMV per row, which quantizes each row to Q8_0 and takes the
+// reference's integer block dots (matmul_quantized_batch, c:2305-2318).
+static void gemm_rows(l3p_ctx* c, const Mat& W, const float* x, int ldx, int rows, float* y, int ldy, bool add,
+                      const char* what) {
+    hipStream_t s = c->stream;
+    ProfRange r(c->prof, s, gemm_label(what, W.type, rows, W.rows, W.cols),
+                gemv_bytes(W.type, W.rows, W.cols, W.rows) + 4.0 * rows * (W.cols + W.rows));
+    if (gemm_mfma_supported(W.type)) {
+        launch_gemm(W.type, W.w, W.rows, W.cols, x, rows, ldx, y, ldy, add, s);
+        return;
+    }
+    for (int b = 0; b < rows; ++b)
+        launch_gemv(W.type, one(W, y + (size_t)b * ldy, add ? EPI_ADD : EPI_STORE), W.cols, x + (size_t)b * ldx,
+                    nullptr, 0.0f, s);
+}
+
+// Positions [start, start + n) of a prompt, kPrefillRows tokens per pass:
+// the embedding, norm, projection and FFN work of a pass runs on all its rows
+// (GEMMs read every weight once per pass).  Attention follows the reference's
+// per-token order (c:3496-3612) in effect: the K/V rows of all the pass's
+// tokens are written first, then every token attends to the positions up to
+// its own, so each sees exactly the rows written before it.
+static void prefill_batched(l3p_ctx* c, const int32_t* tokens, int n, int start) {
+    Model& m = *c->model;
+    hipStream_t s = c->stream;
+    ensure_prefill_rows(m);
+    const float eps = m.eps > 0 ? m.eps : 1e-5f;   // c:3198
+    const int D = m.dim, QD = m.q_dim, KD = m.kv_dim, H = m.hidden, XB = m.max_dim;
+    for (int b0 = 0; b0 < n; b0 += m.pf_rows) {
+        const int R = std::min(m.pf_rows, n - b0);
+        L3P_HIP(hipMemcpyAsync(m.pf_tok, tokens + b0, (size_t)R * 4, hipMemcpyHostToDevice, s));
+        launch_embed_rows(m.emb, m.pf_tok, R, start + b0, m.is_gemma ? m.embed_scale : 0.0f, m.pf_x, D, m.pf_steps,
+                          s);
+        for (int l = 0; l < m.n_layers; ++l) {
+            const Layer& L = m.layers[l];
+            launch_rmsnorm_rows(m.pf_x, D, L.att_norm, D, m.inv_dim, eps, m.pf_xb, XB, R, s);
+            gemm_rows(c, L.wq, m.pf_xb, XB, R, m.pf_q, QD, false, "q");
+            gemm_rows(c, L.wk, m.pf_xb, XB, R, m.pf_k, KD, false, "k");
+            gemm_rows(c, L.wv, m.pf_xb, XB, R, m.pf_v, KD, false, "v");
+            // attention of the rows, as many tokens per launch as the partials hold
+            const size_t per_token =
+                (size_t)m.n_heads * attention_chunks(m, l, start + b0 + R - 1) * (m.hs + 2);
+            const int T = (int)std::max<size_t>(1, std::min<size_t>(R, m.pf_part_cap / per_token));
+            for (int z0 = 0; z0 < R; z0 += T) {
+                const int nz = std::min(T, R - z0);
+                launch_attention_rows(m, l,
+                                      AttnIO{m.pf_q + (size_t)z0 * QD, m.pf_k + (size_t)z0 * KD,
+                                             m.pf_v + (size_t)z0 * KD, m.pf_steps + 2 * z0, m.pf_att + (size_t)z0 * QD},
+                                      QD, KD, QD, nz, start + b0 + z0 + nz - 1, m.pf_part, m.pf_part_cap, s);
+            }
+            if (m.is_gemma) {
+                gemm_rows(c, L.wo, m.pf_att, QD, R, m.pf_xb2, D, false, "wo");
+                launch_rmsnorm_add_rows(m.pf_xb2, D, L.post_att, D, m.inv_dim, eps, m.pf_x, D, R, s);
+            } else {
+                gemm_rows(c, L.wo, m.pf_att, QD, R, m.pf_x, D, true, "wo");
+            }
+            launch_rmsnorm_rows(m.pf_x, D, L.ffn_norm, D, m.inv_dim, eps, m.pf_xb, XB, R, s);
+            gemm_rows(c, L.w1, m.pf_xb, XB, R, m.pf_hb, H, false, "gate");
+            gemm_rows(c, L.w3, m.pf_xb, XB, R, m.pf_hb2, H, false, "up");
+            launch_act_rows(m.pf_hb, m.pf_hb2, (int64_t)R * H, m.is_gemma, s);
+            if (m.is_gemma) {
+                gemm_rows(c, L.w2, m.pf_hb, H, R, m.pf_xb2, D, false, "down");
+                launch_rmsnorm_add_rows(m.pf_xb2, D, L.post_ffn, D, m.inv_dim, eps, m.pf_x, D, R, s);
+            } else {
+                gemm_rows(c, L.w2, m.pf_hb, H, R, m.pf_x, D, true, "down");
+            }
+        }
+    }
+}
+
 void l3p_ctx::drop_graphs() {
     for (int i = 0; i < 2; ++i) {
         if (graph[i]) hipGraphExecDestroy(graph[i]);
         graph[i] = nullptr;
         graph_runs[i] = 0;
     }
+}
+
+// L3P_PREFILL_BATCH=0 runs prompts token by token through the decode step.
+static bool prefill_batching() {
+    static int on = -1;
+    if (on < 0) {
+        const char* e = getenv("L3P_PREFILL_BATCH");
+        on = e ? atoi(e) != 0 : 1;
+    }
+    return on != 0;
 }
 
 static bool graphs_enabled() {
@@ -726,6 +840,12 @@ static void sample_impl(l3p_ctx* c, const float* logits, int n, const l3p_sample
 // ---------------------------------------------------------------------------
 void run_gemm(l3p_ctx* c, int type, const uint8_t* w, int rows, int cols, const float* x, int batch, int in_stride,
               float* y, int out_stride) {
+    if (gemm_mfma_supported(type)) {
+        launch_gemm(type, w, rows, cols, x, batch, in_stride, y, out_stride, false, c->stream);
+        return;
+    }
+    // Q4_0: the reference quantizes every batch row to Q8_0 and takes integer
+    // block dots (c:2305-2318), which is what the GEMV computes per row
     for (int b = 0; b < batch; ++b) {
         GemvBatch gb{};
         gb.seg[0] = GemvSegment{w, y + (size_t)b * out_stride, rows};
@@ -803,7 +923,9 @@ int l3p_prefill(l3p_ctx* c, const int32_t* tokens, int n, int32_t start) {
         for (int i = 0; i < n; ++i)
             L3P_REQUIRE(tokens[i] >= 0 && tokens[i] < m.vocab, L3P_E_INVALID, "prefill: token %d out of range",
                         tokens[i]);
-        for (int i = 0; i < n; ++i) forward_impl(c, tokens[i], start + i, false);
+        if (prefill_batching()) prefill_batched(c, tokens, n, start);
+        else
+            for (int i = 0; i < n; ++i) forward_impl(c, tokens[i], start + i, false);
         L3P_HIP(hipStreamSynchronize(c->stream));
         c->prof.collect();
     });

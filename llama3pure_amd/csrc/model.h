@@ -39,6 +39,14 @@ struct Model {
     float *hb = nullptr, *hb2 = nullptr, *logits = nullptr;
     float* part_acc = nullptr;     // [n_heads][max_chunks][hs + 2] attention chunk partials
     int* step = nullptr;           // device {token, pos} of the step being computed
+    // prompt-batch rows (transformer_prefill's batch_* arrays, c:326-343),
+    // allocated at the first batched prefill for pf_rows tokens
+    int pf_rows = 0;
+    float *pf_x = nullptr, *pf_xb = nullptr, *pf_xb2 = nullptr, *pf_q = nullptr, *pf_k = nullptr, *pf_v = nullptr;
+    float *pf_att = nullptr, *pf_hb = nullptr, *pf_hb2 = nullptr;
+    int *pf_tok = nullptr, *pf_steps = nullptr;
+    float* pf_part = nullptr;      // attention chunk partials of a batch's tokens
+    size_t pf_part_cap = 0;        // floats
     int max_chunks = 0;
     // sampler scratch
     float* cand_val = nullptr;     // device: group maxima, then top-k slot values
@@ -110,8 +118,31 @@ void gemv_plain(l3p_ctx* c, int type, const GemvBatch& b, int cols, const float*
 void launch_embed_step(const Mat& emb, int token, int pos, float scale, float* x, int* step, hipStream_t s);
 void launch_rmsnorm_add(const float* y, const float* w, int n, float inv_n, float eps, float* x, hipStream_t s);
 // QK-norm, RoPE, the K/V cache write and attention of one layer for the
-// step's position (c:3232-3359); out = [n_heads][head_dim].
+// step's position (c:3232-3359); out = [n_heads][head_dim].  The first form
+// reads the decode step's q, k, v and step record.
+struct AttnIO {
+    const float *q, *k, *v;   // this token's projections
+    const int* step;          // device {token, pos}
+    float* out;
+};
 void launch_attention(const Model& m, int layer, float* out, hipStream_t s);
+void launch_attention(const Model& m, int layer, const AttnIO& io, hipStream_t s);
+// Attention of `tokens` consecutive prompt tokens of a batch in three
+// launches (K/V rows of all of them, then chunks and merge): io holds token
+// 0's rows, token z's are `*_stride` floats further and its step record 2z
+// ints further; last_pos is the last token's position.  part holds
+// part_cap floats of chunk partials.
+int attention_chunks(const Model& m, int layer, int last_pos);
+void launch_attention_rows(const Model& m, int layer, const AttnIO& io, int q_stride, int kv_stride, int out_stride,
+                           int tokens, int last_pos, float* part, size_t part_cap, hipStream_t s);
+// rows of a prompt batch (row strides ld*)
+void launch_rmsnorm_add_rows(const float* y, int ldy, const float* w, int n, float inv_n, float eps, float* x,
+                             int ldx, int rows, hipStream_t s);
+void launch_embed_rows(const Mat& emb, const int* tokens, int rows, int start, float scale, float* x, int ldx,
+                       int* steps, hipStream_t s);
+void launch_rmsnorm_rows(const float* x, int ldx, const float* w, int n, float inv_n, float eps, float* o, int ldo,
+                         int rows, hipStream_t s);
+void launch_act_rows(float* h, const float* h2, int64_t n, bool gelu, hipStream_t s);
 void launch_softcap(float* logits, int n, float cap, hipStream_t s);
 void launch_argmax(const float* logits, int n, int* out, hipStream_t s, float* cv, int* ci);
 void launch_topk_slots(const float* logits, int n, int k, float* gmax, float* out_v, int* out_i, hipStream_t s);

@@ -201,10 +201,10 @@ def test_gemv_deterministic(ctx, torch_gpu):
     assert torch_gpu.equal(y1, y2)
 
 
-@pytest.mark.parametrize("qtype", [l3p.Q8_0, l3p.Q4_0])
-def test_gemm_equals_gemv_rows(ctx, torch_gpu, qtype):
-    """The batched form gives, per batch element, exactly the GEMV result."""
-    rows, cols, batch = 1024, 2048, 7
+def test_gemm_q4_0_equals_gemv_rows(ctx, torch_gpu):
+    """Q4_0 batches run the GEMV per row (the reference's integer Q8_0-activation
+    dot, c:2305-2318): per batch element exactly the GEMV result."""
+    qtype, rows, cols, batch = l3p.Q4_0, 1024, 2048, 7
     w = dev(torch_gpu, synth.random_blocks(qtype, rows, cols, seed=5))
     xb = synth.random_x(cols, seed=6, batch=batch)
     xd = dev(torch_gpu, xb)
@@ -217,3 +217,82 @@ def test_gemm_equals_gemv_rows(ctx, torch_gpu, qtype):
         ys.append(yb)
     ctx.synchronize()
     assert torch_gpu.equal(y.view(batch, rows), torch_gpu.stack(ys))
+
+
+def _dequant_bound(cpuref, qtype, w, rows, cols):
+    """(W, A): the exact dequantized weights in float64 and the per-element
+    magnitudes whose products with |x| bound either side's fp32 sums (module doc)."""
+    W = np.stack([cpuref.dequant(qtype, w[r], cols) for r in range(rows)]).astype(np.float64)
+    if qtype == l3p.Q8_0:
+        return W, np.abs(W)
+    if qtype == l3p.Q6_K:
+        wb = w.reshape(rows, -1, 210)
+        d = wb[:, :, 208:210].copy().view(np.float16).astype(np.float64)[:, :, 0]
+        sc = wb[:, :, 192:208].view(np.int8).astype(np.float64)
+        return W, np.repeat(np.abs(d[:, :, None] * sc), 16, axis=2).reshape(rows, cols) * 95.0
+    # Q4_K: |d1 q| + |m1| (see _bound_terms); the GEMM forms exact w = d1 q - m1, which this also bounds
+    wb = w.reshape(rows, -1, 144)
+    d = wb[:, :, 0:2].copy().view(np.float16).astype(np.float64)[:, :, 0]
+    dmin = wb[:, :, 2:4].copy().view(np.float16).astype(np.float64)[:, :, 0]
+    sb = wb[:, :, 4:16].astype(np.int64)
+    A = np.empty((rows, cols))
+    for j in range(8):
+        if j < 4:
+            sc, m = sb[:, :, j] & 63, sb[:, :, j + 4] & 63
+        else:
+            sc = (sb[:, :, j + 4] & 15) | ((sb[:, :, j - 4] >> 6) << 4)
+            m = (sb[:, :, j + 4] >> 4) | ((sb[:, :, j] >> 6) << 4)
+        q = wb[:, :, 16 + 32 * (j // 2): 48 + 32 * (j // 2)].astype(np.int64)
+        q = (q >> 4) if j % 2 else (q & 15)
+        A.reshape(rows, -1, 8, 32)[:, :, j, :] = np.abs(d * sc)[:, :, None] * q + np.abs(dmin * m)[:, :, None]
+    return W, A
+
+
+@pytest.mark.parametrize("qtype,rows,cols,batch", [
+    (l3p.Q8_0, 1024, 2048, 7),
+    (l3p.Q8_0, 2304, 2304, 130),     # Gemma-2-2B projection, 3 ragged batch tiles
+    (l3p.Q8_0, 300, 96, 65),         # K of one and a half 64-wide steps
+    (l3p.Q8_0, 2048, 1152, 33),      # rows that are not 16-byte multiples
+    (l3p.Q8_0, 77, 14336, 1),
+    (l3p.Q4_K, 1000, 2304, 17),
+    (l3p.Q6_K, 513, 1536, 40),
+])
+def test_gemm_mfma_parity(ctx, torch_gpu, cpuref, qtype, rows, cols, batch):
+    """MFMA GEMM against the float64 value of the reference's dequantize-then-
+    fp32-dot (matmul_deq_batch_4row, c:2179-2273), every output within the
+    fp32 summation bound gamma_(K+4) * S of the module doc."""
+    seed = rows + cols + batch
+    w = synth.random_blocks(qtype, rows, cols, seed=seed)
+    xb = synth.random_x(cols, seed=seed + 1, batch=batch)
+    ld_out = rows + 3                  # strided output rows
+    y = torch_gpu.full((batch * ld_out,), float("nan"), dtype=torch_gpu.float32, device="cuda")
+    ctx.gemm(qtype, dev(torch_gpu, w), rows, cols, dev(torch_gpu, xb), batch, cols, y, ld_out)
+    ctx.synchronize()
+    got = y.cpu().numpy().reshape(batch, ld_out)
+    W, A = _dequant_bound(cpuref, qtype, w, rows, cols)
+    x64 = xb.astype(np.float64)
+    y64 = x64 @ W.T
+    tol = gamma(cols + 4) * (np.abs(x64) @ A.T)
+    err = np.abs(got[:, :rows] - y64)
+    assert np.all(err <= tol), f"max err/tol {np.max(err / np.maximum(tol, 1e-30)):.3g}"
+    assert np.all(np.isnan(got[:, rows:])), "wrote outside the output rows"
+
+
+def test_gemm_mfma_equals_gemv_within_bound(ctx, torch_gpu, cpuref):
+    """The batched and the single-row forms agree within the same bound."""
+    qtype, rows, cols, batch = l3p.Q8_0, 4096, 4096, 5
+    w = synth.random_blocks(qtype, rows, cols, seed=11)
+    xb = synth.random_x(cols, seed=12, batch=batch)
+    wd, xd = dev(torch_gpu, w), dev(torch_gpu, xb)
+    y = empty_f32(torch_gpu, batch * rows)
+    ctx.gemm(qtype, wd, rows, cols, xd, batch, cols, y, rows)
+    ys = []
+    for b in range(batch):
+        yb = empty_f32(torch_gpu, rows)
+        ctx.gemv(qtype, wd, rows, cols, xd[b], yb)
+        ys.append(yb)
+    ctx.synchronize()
+    W, A = _dequant_bound(cpuref, qtype, w, rows, cols)
+    tol = 2 * gamma(cols + 4) * (np.abs(xb.astype(np.float64)) @ A.T)
+    diff = np.abs(y.view(batch, rows).cpu().numpy() - torch_gpu.stack(ys).cpu().numpy())
+    assert np.all(diff <= tol)
