@@ -17,6 +17,8 @@ Printed as one JSON line:
   gemv         standalone GEMV launches at the Llama-3-8B shapes (Q8_0, Q4_0,
                Q4_K, Q6_K), weight copies rotated through >= 1 GiB so the
                256 MB last-level cache does not serve them;
+  prefill      the 1024-position prompt before the decode: positions/s and
+               the fp32-MFMA roofline of the dominant prefill GEMM class;
   cpu_baseline the reference C engine (oracle/_ref/libref_omp.so: its own
                source built with its Makefile's -Ofast -fopenmp line) decoding
                the same GGUF on the host cores for a bounded sample; the
@@ -38,6 +40,8 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0   # MI355X HBM3E, 8 TB/s
+MFMA_F32_PEAK_TFLOPS = 157.3   # MI355X dense fp32 matrix peak
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "hbm_traffic_decode_gemv.md")
 
 LLAMA3_8B = dict(arch="llama", dim=4096, hidden=14336, n_layers=32, n_heads=32, n_kv=8, vocab=128256, ctx=2048,
                  rope_theta=500000.0, eps=1e-5, std=0.02, seed=1234)
@@ -100,6 +104,52 @@ def time_gemv_shapes(ctx, torch, l3p, synth):
         del ws, base
         torch.cuda.empty_cache()
     return out
+
+
+def prefill_summary(positions: int, seconds: float, stats: dict) -> dict:
+    """Prompt throughput and the fp32-MFMA roofline of the dominant GEMM class
+    (labels "<type> gemm <what> <N>x<K> b<rows>", 2*N*K*rows flops a launch)."""
+    gemms = {k: v for k, v in stats.items() if " gemm " in k}
+    out = {"positions": positions, "ms": round(seconds * 1e3, 2), "tok_s": round(positions / seconds, 1)}
+    if not gemms:
+        return out
+    name, (launches, ms, _) = max(gemms.items(), key=lambda kv: kv[1][1])
+    n, k = (int(v) for v in name.split()[3].split("x"))
+    rows = int(name.split()[4][1:])
+    flops = 2.0 * n * k * rows
+    avg_us = ms * 1e3 / launches
+    tf = flops / (avg_us * 1e-6) / 1e12
+    out["gemm_ms"] = round(sum(v[1] for v in gemms.values()), 2)
+    out["roofline"] = {"bound": "mfma", "kernel": name, "achieved": round(tf, 1), "peak": MFMA_F32_PEAK_TFLOPS,
+                       "unit": "TFLOP/s", "frac": round(tf / MFMA_F32_PEAK_TFLOPS, 4), "flops_per_launch": flops,
+                       "avg_launch_us": round(avg_us, 2), "launches": launches}
+    return out
+
+
+def measured_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE +
+    WRITE_SIZE summary (a line "traffic <kernel>: <bytes>"), else None."""
+    try:
+        with open(TRAFFIC_PROFILE) as f:
+            for line in f:
+                if line.startswith(f"traffic {kernel}:"):
+                    return int(float(line.split(":")[1]))
+    except OSError:
+        pass
+    return None
+
+
+def calibrate_copy():
+    """512 MiB device-to-device copies: FETCH_SIZE and WRITE_SIZE per copy
+    dispatch should each read 524288 KiB; the ratio scales the GEMV counts."""
+    import torch
+    a = torch.empty(1 << 27, dtype=torch.float32, device="cuda")
+    b = torch.empty_like(a)
+    a.fill_(1.0)
+    for _ in range(5):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibrate_copy_bytes": a.numel() * 4, "copies": 5}), flush=True)
 
 
 def cpu_leg(path: str, seconds: float, max_tokens: int, use_ref: bool) -> dict:
@@ -177,12 +227,19 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-gemv", action="store_true", help="skip the standalone GEMV shapes")
+    ap.add_argument("--layers", type=int, default=32,
+                    help="layers of the model (32 = Llama-3-8B; fewer only for short counter-collection runs)")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only copy 512 MiB device-to-device 5 times (scale for rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     ap.add_argument("--cpu-leg", help=argparse.SUPPRESS)
     ap.add_argument("--cpu-ref", type=int, default=1, help=argparse.SUPPRESS)
     a = ap.parse_args()
 
     if a.cpu_leg:
         print(json.dumps(cpu_leg(a.cpu_leg, a.cpu_seconds, 64, bool(a.cpu_ref))))
+        return
+    if a.calibrate_copy:
+        calibrate_copy()
         return
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the decode path runs on a single MI355X and has no multi-GPU "
@@ -197,7 +254,8 @@ def main():
 
     ctx = l3p.Context(0)
     t0 = time.perf_counter()
-    img = synth.synthetic_model(qtype=synth.Q8_0, make_mat=gpu_q8_0_maker(ctx, torch, 99), **LLAMA3_8B)
+    cfg = dict(LLAMA3_8B, n_layers=a.layers)
+    img = synth.synthetic_model(qtype=synth.Q8_0, make_mat=gpu_q8_0_maker(ctx, torch, 99), **cfg)
     t_gen = time.perf_counter() - t0
     mi = ctx.load_gguf(img)
     print(f"[bench] model {img.nbytes / 1e9:.2f} GB generated in {t_gen:.1f} s, "
@@ -207,7 +265,19 @@ def main():
     prompt = rng.integers(0, mi.vocab_size, a.prefill + 1).astype(np.int32)
     t0 = time.perf_counter()
     ctx.prefill(prompt[:-1], 0)
-    print(f"[bench] prefill {a.prefill} positions in {time.perf_counter() - t0:.1f} s", file=sys.stderr, flush=True)
+    t_pre = time.perf_counter() - t0
+    print(f"[bench] prefill {a.prefill} positions in {t_pre * 1e3:.1f} ms", file=sys.stderr, flush=True)
+    # the same prompt again (it rewrites the same cache rows): timed, then per launch
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ctx.prefill(prompt[:-1], 0)
+    t_pre = time.perf_counter() - t0
+    ctx.profile(True)
+    ctx.prefill(prompt[:-1], 0)
+    pstats = ctx.profile_read()
+    ctx.profile(False)
+    prefill = prefill_summary(a.prefill, t_pre, pstats)
+    print(f"[bench] prefill: {json.dumps(prefill)}", file=sys.stderr, flush=True)
 
     def run(n, tok, pos):
         for _ in range(n):
@@ -257,15 +327,16 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "q8_0 weights, int8-digit dot, fp32 accumulate",
+        "dtype": "q8_0 weights (int8 quants, fp16 block scales); fp32 activations and accumulation",
         "data": "synthetic: random-init weights N(0,0.02) quantized to Q8_0, uniform random token ids",
         "config": {"workload": "greedy decode, Llama-3-8B architecture, all matrices Q8_0, KV prefilled to "
-                               f"{a.prefill} of 2048", "layers": 32, "dim": 4096, "heads": 32, "kv_heads": 8,
+                               f"{a.prefill} of 2048", "layers": a.layers, "dim": 4096, "heads": 32, "kv_heads": 8,
                    "ffn": 14336, "vocab": 128256, "start_pos": a.prefill, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "kernel": name, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(name),
                      "bytes_per_launch": int(bpl), "avg_launch_us": round(avg_us, 2), "launches": launches},
         "gemv_classes": kernels,
+        "prefill": prefill,
         "gemv": gemv,
         "cpu_baseline": base,
     }

@@ -69,17 +69,22 @@ int l3p_dequant(l3p_ctx* ctx, int type, const void* src_dev, int64_t n, float* d
 int l3p_quantize_q8_0(l3p_ctx* ctx, const float* x_dev, int64_t n, void* dst_dev);
 
 /* y[rows] = W[rows x cols] . x[cols] with W in its native block layout.
- * Replaces matmul_quantized (c:2091-2133; js:3107-3142).  Semantics per type
- * follow the reference: Q8_0/Q4_K/Q6_K use fp32 x (matmul_deq_4row,
+ * Replaces matmul_quantized (c:2091-2133; js:3107-3142) for Q8_0, Q4_0, Q4_K
+ * and Q6_K with cols <= 32768 (other types: L3P_E_UNSUPPORTED).  Semantics
+ * per type follow the reference: Q8_0/Q4_K/Q6_K use fp32 x (matmul_deq_4row,
  * c:2136-2176); Q4_0 quantizes x to Q8_0 first and uses integer block dots
- * (c:2105-2116, c:1625-1643).  Results match the reference within the
- * summation-order tolerance documented in DESIGN.md. */
+ * (c:2105-2116, c:1625-1643).  Results differ from the reference's only by
+ * fp32 summation order.  w_dev and x_dev must be 16-byte aligned (l3p_malloc
+ * memory is). */
 int l3p_gemv(l3p_ctx* ctx, int type, const void* w_dev, int rows, int cols, const float* x_dev,
              float* y_dev);
 
 /* Batched form for prefill: y[b*out_stride + r] = W[r,:] . x[b*in_stride + :]
  * for b < batch.  Replaces matmul_quantized_batch (c:2291-2331; js:3159-3845).
- * Q8_0 runs on an MFMA-tiled GEMM; other types loop the GEMV kernels. */
+ * Q8_0, Q4_K and Q6_K run on the fp32-MFMA GEMM (weights dequantized exactly,
+ * as matmul_deq_batch_4row, c:2179-2273); Q4_0 runs the GEMV per batch row
+ * (the reference's Q8_0-activation integer dot, c:2305-2318).  in_stride
+ * must be a multiple of 4 and x_dev 16-byte aligned. */
 int l3p_gemm(l3p_ctx* ctx, int type, const void* w_dev, int rows, int cols, const float* x_dev,
              int batch, int in_stride, float* y_dev, int out_stride);
 

@@ -158,6 +158,7 @@ int l3p_gemm(l3p_ctx* c, int type, const void* w, int rows, int cols, const floa
     return guard(c, [&] {
         L3P_REQUIRE(batch >= 0 && in_stride >= cols && out_stride >= rows, L3P_E_INVALID,
                     "gemm: bad batch/strides");
+        L3P_REQUIRE(in_stride % 4 == 0, L3P_E_INVALID, "gemm: in_stride %d is not a multiple of 4", in_stride);
         L3P_REQUIRE(gemv_supported(type, cols), L3P_E_UNSUPPORTED,
                     "gemm: type %d with %d columns not supported", type, cols);
         if (rows == 0 || batch == 0) return;
