@@ -94,4 +94,92 @@ __device__ __forceinline__ void quantize32(const float* v, QBlock& o) {
     o.sum = s;
 }
 
+// Barrier for LDS traffic only: lgkmcnt(0) and s_barrier, with no wait on
+// outstanding vector memory (which __syncthreads' release fence adds, LDS
+// copies in flight included).  Callers wait for their own copies explicitly.
+__device__ __forceinline__ void lds_sync() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // vmcnt(63) expcnt(7) lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+__device__ __forceinline__ void wait_lgkm() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// Cross-lane exchanges in registers (gfx950), instead of ds_bpermute round
+// trips through the LDS unit: the value of the partner lane in butterfly step
+// M = 32, 16, 8, 4, 2, 1.  M = 32 and 16 use the permlane swaps (partner lane
+// ^ 32, lane ^ 16: swap(x, x) returns the lower and the upper lane's value);
+// within a row of 16 lanes, M = 8 pairs lane i with 15 - i and M = 4 pairs i
+// with 7 - i (DPP row mirrors), M = 2 and 1 are the quad exchanges i ^ 2 and
+// i ^ 1.  Every step pairs lanes that differ in bit log2(M) and agree in all
+// higher bits, which is all a butterfly reduction or transpose needs.  Call
+// with every lane of the wave active.
+template <int M>
+__device__ __forceinline__ float lane_partner(float v) {
+    const int x = __float_as_int(v);
+    if constexpr (M == 32) {
+        const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+        return __int_as_float((__lane_id() & 32) ? r[0] : r[1]);
+    } else if constexpr (M == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+        return __int_as_float((__lane_id() & 16) ? r[0] : r[1]);
+    } else if constexpr (M == 8) {
+        return __int_as_float(__builtin_amdgcn_mov_dpp(x, 0x140, 0xF, 0xF, false));   // row_mirror
+    } else if constexpr (M == 4) {
+        return __int_as_float(__builtin_amdgcn_mov_dpp(x, 0x141, 0xF, 0xF, false));   // row_half_mirror
+    } else if constexpr (M == 2) {
+        return __int_as_float(__builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, false));    // quad_perm [2,3,0,1]
+    } else {
+        static_assert(M == 1, "butterfly step");
+        return __int_as_float(__builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, false));    // quad_perm [1,0,3,2]
+    }
+}
+
+// lane_partner with a step known once loops are unrolled
+__device__ __forceinline__ float lane_partner_m(float v, int m) {
+    switch (m) {
+    case 32: return lane_partner<32>(v);
+    case 16: return lane_partner<16>(v);
+    case 8: return lane_partner<8>(v);
+    case 4: return lane_partner<4>(v);
+    case 2: return lane_partner<2>(v);
+    default: return lane_partner<1>(v);
+    }
+}
+
+// Sum / maximum over the wave (every lane gets the same value: each step adds
+// a lane's and its partner's values, a + b in one and b + a in the other).
+__device__ __forceinline__ float wave_sum(float v) {
+    v += lane_partner<32>(v);
+    v += lane_partner<16>(v);
+    v += lane_partner<8>(v);
+    v += lane_partner<4>(v);
+    v += lane_partner<2>(v);
+    v += lane_partner<1>(v);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, lane_partner<32>(v));
+    v = fmaxf(v, lane_partner<16>(v));
+    v = fmaxf(v, lane_partner<8>(v));
+    v = fmaxf(v, lane_partner<4>(v));
+    v = fmaxf(v, lane_partner<2>(v));
+    v = fmaxf(v, lane_partner<1>(v));
+    return v;
+}
+// Maximum over each 32-lane half of the wave.
+__device__ __forceinline__ float half_max(float v) {
+    v = fmaxf(v, lane_partner<16>(v));
+    v = fmaxf(v, lane_partner<8>(v));
+    v = fmaxf(v, lane_partner<4>(v));
+    v = fmaxf(v, lane_partner<2>(v));
+    v = fmaxf(v, lane_partner<1>(v));
+    return v;
+}
+
 }  // namespace l3pd

@@ -95,20 +95,6 @@ __host__ __device__ __forceinline__ uint32_t row_bytes(int cols) {
     return (uint32_t)(cols / Fmt<QT>::kUnitElems) * Fmt<QT>::kUnitBytes;
 }
 
-// Barrier for LDS traffic only (no wait on outstanding vector memory, which
-// __syncthreads' release fence would add).
-__device__ __forceinline__ void lds_sync() {
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
-    __builtin_amdgcn_s_barrier();
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
-
-__device__ __forceinline__ void wait_lgkm() {
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_waitcnt(0xC07F);
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
 
 // Wait until at most N of this wave's vector-memory operations are outstanding
 // (s_waitcnt on gfx9: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] << 14).
@@ -195,13 +181,13 @@ __device__ __forceinline__ float xreduce(float (&v)[N], int lane) {
                 asm volatile("" : "+v"(lo), "+v"(hi));
                 const float send = up ? lo : hi;
                 const float keep = up ? hi : lo;
-                v[i] = keep + __shfl_xor(send, m, 64);
+                v[i] = keep + lane_partner_m(send, m);
             }
         }
     }
     float r = v[0];
 #pragma unroll
-    for (int m = 32 >> L; m > 0; m >>= 1) r += __shfl_xor(r, m, 64);
+    for (int m = 32 >> L; m > 0; m >>= 1) r += lane_partner_m(r, m);
     return r;
 }
 
@@ -575,8 +561,7 @@ __global__ void __launch_bounds__(1024) gemv_kernel(GemvArgs a) {
         float ss = 0.0f;
 #pragma unroll
         for (int j = 0; j < 32; ++j) ss += v[j] * v[j];
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+        ss = wave_sum(ss);
         if (lane == 0) ssred[w] = ss;
         float r = 1.0f;
         if (!kLateScale) {

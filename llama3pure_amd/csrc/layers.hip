@@ -16,24 +16,11 @@ typedef __attribute__((address_space(3))) void lds_void;
 
 using namespace l3pd;
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
-}
-
 // Q8_0 quantization with one value per lane, 32 lanes per block: the
 // reference's quantize_row_q8_0 (c:1508-1528) per element.  Returns the
 // quant; dh is the block's truncated fp16 scale (the same in its 32 lanes).
 __device__ __forceinline__ int8_t quant_lane(float v, uint32_t& dh) {
-    float amax = fabsf(v);
-#pragma unroll
-    for (int o = 16; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+    const float amax = half_max(fabsf(v));
     const float d = amax / 127.0f;
     const float id = d > 0.0f ? 127.0f / amax : 0.0f;
     dh = f2h_trunc(d);
@@ -141,7 +128,8 @@ struct AttnCArgs {
     const float *cos, *sin;          // RoPE tables [seq][hs/2]; the step's row is used
     uint8_t *kc, *vc;                // this layer's caches [n_kv][seq][hq8]
     const int* step;                 // device {token, pos}
-    float* part;                     // [n_heads][n_chunks][hs + 2]: chunk output, max, sum
+    float* part;                     // [n_heads][part_chunks][hs + 2]: chunk output, max, sum
+    int part_chunks;                 // chunk slots per head in part
     float* out;                      // [n_heads][hs]
     size_t head_seq;
     int n_heads, kv_mul, hs, hq8, window, neox;
@@ -192,15 +180,54 @@ __device__ __forceinline__ float row_block(const uint32_t* base, uint32_t off, u
     return h2f(odd ? (dw[0] >> 16) : dw[0]);
 }
 
+// V values of one cache row for the lane's PER outputs (PER consecutive bytes
+// inside one 32-block, 2-byte aligned for PER >= 2)
+template <int PER>
+__device__ __forceinline__ uint32_t v_quants(const uint8_t* p) {
+    if (PER == 1) return *p;
+    if (PER == 2) return *reinterpret_cast<const uint16_t*>(p);
+    return (uint32_t)reinterpret_cast<const uint16_t*>(p)[0] | ((uint32_t)reinterpret_cast<const uint16_t*>(p)[1] << 16);
+}
+
+// acc += q * (d * e) for the lane's PER outputs, the position skipped when
+// e < 1e-8 (accum_q8_0_cache, c:1600-1622)
+template <int PER>
+__device__ __forceinline__ void v_accum(uint32_t dh, uint32_t q, float e, float (&acc)[4]) {
+    const float f = e < 1e-8f ? 0.0f : h2f(dh) * e;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) acc[i] = fmaf((float)(int8_t)((q >> (8 * i)) & 0xffu), f, acc[i]);
+}
+
+template <int NB>
 __global__ void __launch_bounds__(1024) attn_chunk_kernel(AttnCArgs a0) {
     extern __shared__ __align__(16) float smem[];
     const AttnCArgs a = token_args(a0, blockIdx.z);
     const int g = blockIdx.x, c = blockIdx.y;
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, nt = blockDim.x;
+    constexpr int hs = 32 * NB, half = hs / 2, hq8 = 34 * NB;
+    constexpr int PER = NB <= 2 ? 1 : (NB <= 4 ? 2 : 4);   // V outputs per lane, inside one 32-block
+    const int km = a.kv_mul;
+    const int h = g * km + w;
+
+    // this step's q, k and v rows and the norm weights go to registers first:
+    // they do not depend on the step record, so they are issued before it
+    // arrives, and before the row copies below, so waiting for these loads
+    // never waits for the copies (hs <= 256)
+    float qv[4], kv2[8], cs[2], sn[2], qn[4], kn[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int j = lane + 64 * k;
+        qv[k] = j < hs ? a.q[(size_t)h * hs + j] : 0.0f;
+        qn[k] = (a.q_norm && j < hs) ? a.q_norm[j] : 0.0f;
+        kn[k] = (a.k_norm && j < hs) ? a.k_norm[j] : 0.0f;
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {   // k then v over the workgroup (2*hs <= 8*64)
+        const int j = threadIdx.x + nt * k;
+        kv2[k] = j < 2 * hs ? (j < hs ? a.k[(size_t)g * hs + j] : a.v[(size_t)g * hs + j - hs]) : 0.0f;
+    }
     const Span sp = span_of(a.step, a.window);
     if (c >= sp.n_chunks) return;   // the grid covers the longest context
-    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, nt = blockDim.x;
-    const int hs = a.hs, nb = hs / 32, half = hs / 2, km = a.kv_mul;
-    const int h = g * km + w;
     const int jbeg = c * kTC, jend = min(sp.na, jbeg + kTC), cnt = jend - jbeg;
     // the chunk holding the step's position forms and writes its K/V row,
     // unless a prompt batch's kv_rows_kernel already wrote it
@@ -214,40 +241,25 @@ __global__ void __launch_bounds__(1024) attn_chunk_kernel(AttnCArgs a0) {
     float* f = kvh + 2 * hs;
     int8_t* qq = reinterpret_cast<int8_t*>(f + km * 8 * kTC);
     float* qd = reinterpret_cast<float*>(qq + km * hs);
-    const int rowdw = (kTC * a.hq8 + 8 + 3) / 4;
+    const int rowdw = (kTC * hq8 + 8 + 3) / 4;
     uint32_t* krows = reinterpret_cast<uint32_t*>(qd + km * 8);
     uint32_t* vrows = krows + rowdw;
 
-    // this step's q (and k, v) rows, RoPE factors and norm weights go to
-    // registers first: everything is issued before the row copies below, so
-    // waiting for these loads never waits for the copies (hs <= 256)
+    // the RoPE factors of the step's position
     const float* cosr = a.cos + (size_t)sp.pos * half;
     const float* sinr = a.sin + (size_t)sp.pos * half;
-    float qv[4], kv2[8], cs[2], sn[2], qn[4], kn[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const int j = lane + 64 * k;
-        qv[k] = j < hs ? a.q[(size_t)h * hs + j] : 0.0f;
-        qn[k] = (a.q_norm && j < hs) ? a.q_norm[j] : 0.0f;
-        kn[k] = (a.k_norm && j < hs) ? a.k_norm[j] : 0.0f;
-    }
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
         const int p = lane + 64 * k;
         cs[k] = p < half ? cosr[p] : 0.0f;
         sn[k] = p < half ? sinr[p] : 0.0f;
     }
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {   // k then v over the workgroup (2*hs <= 8*64)
-        const int j = threadIdx.x + nt * k;
-        kv2[k] = (has_pos && j < 2 * hs) ? (j < hs ? a.k[(size_t)g * hs + j] : a.v[(size_t)g * hs + j - hs]) : 0.0f;
-    }
 
     // the chunk's K and V rows, HBM -> LDS (dword copies from the 4-byte
     // aligned start; the row at the step's position is replaced below)
-    const size_t start = (size_t)g * a.head_seq + (size_t)(sp.t0 + jbeg) * a.hq8;
+    const size_t start = (size_t)g * a.head_seq + (size_t)(sp.t0 + jbeg) * hq8;
     const size_t s4 = start & ~(size_t)3;
-    const int nd = (int)((start + (size_t)cnt * a.hq8 - s4 + 3) >> 2);
+    const int nd = (int)((start + (size_t)cnt * hq8 - s4 + 3) >> 2);
     {
         const uint32_t* ks = reinterpret_cast<const uint32_t*>(a.kc) + (s4 >> 2);
         const uint32_t* vs = reinterpret_cast<const uint32_t*>(a.vc) + (s4 >> 2);
@@ -344,7 +356,7 @@ __global__ void __launch_bounds__(1024) attn_chunk_kernel(AttnCArgs a0) {
 #pragma unroll
         for (int sel = 0; sel < 2; ++sel) {
             if (km > 1 && sel != kvsel) continue;
-            uint8_t* rb = reinterpret_cast<uint8_t*>(sel ? vrows : krows) + roff + (size_t)(cnt - 1) * a.hq8;
+            uint8_t* rb = reinterpret_cast<uint8_t*>(sel ? vrows : krows) + roff + (size_t)(cnt - 1) * hq8;
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
                 const int j = lane + 64 * k;
@@ -361,19 +373,21 @@ __global__ void __launch_bounds__(1024) attn_chunk_kernel(AttnCArgs a0) {
     }
     __syncthreads();
 
-    // scores of head h: lane = position
+    // scores of head h: lane = position (all of a row's blocks read first)
     float sc = -INFINITY;
     if (lane < cnt) {
+        const int* qw = reinterpret_cast<const int*>(qq + w * hs);
+        uint32_t kq[NB][8];
+        float db[NB];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) db[b] = row_block(krows, roff + (uint32_t)lane * hq8 + 34u * b, kq[b]);
         float sum = 0.0f;
-        const int8_t* qw = qq + w * hs;
-        for (int b = 0; b < nb; ++b) {
-            uint32_t kq[8];
-            const float db = row_block(krows, roff + (uint32_t)lane * a.hq8 + 34u * b, kq);
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
             int isum = 0;
 #pragma unroll
-            for (int k = 0; k < 8; ++k)
-                isum = __builtin_amdgcn_sdot4(*reinterpret_cast<const int*>(qw + 32 * b + 4 * k), (int)kq[k], isum, false);
-            sum += qd[w * 8 + b] * db * (float)isum;
+            for (int k = 0; k < 8; ++k) isum = __builtin_amdgcn_sdot4(qw[8 * b + k], (int)kq[b][k], isum, false);
+            sum += qd[w * 8 + b] * db[b] * (float)isum;
         }
         sc = sum;
     }
@@ -386,41 +400,45 @@ __global__ void __launch_bounds__(1024) attn_chunk_kernel(AttnCArgs a0) {
     float* fw = f + (size_t)w * 8 * kTC;
     if (lane < cnt) {
         const bool skip = e < 1e-8f;
-        for (int bb = 0; bb < nb; ++bb) {
-            const uint8_t* s2 = vbytes + (size_t)lane * a.hq8 + 34 * bb;
-            const float d = h2f((uint32_t)s2[0] | ((uint32_t)s2[1] << 8));
-            fw[bb * kTC + lane] = skip ? 0.0f : d * e;
-        }
+        uint32_t dv[NB];
+#pragma unroll
+        for (int bb = 0; bb < NB; ++bb) dv[bb] = *reinterpret_cast<const uint16_t*>(vbytes + (size_t)lane * hq8 + 34 * bb);
+#pragma unroll
+        for (int bb = 0; bb < NB; ++bb) fw[bb * kTC + lane] = skip ? 0.0f : h2f(dv[bb]) * e;
     }
     __syncthreads();
-    const int per = (hs + 63) / 64;            // outputs per lane (1, 2 or 4)
-    const int i0 = lane * per;
+    // V: acc_i += q_ji * f_j over the chunk's rows, eight rows' loads at a time
+    const int i0 = lane * PER;
     const bool act = i0 < hs;
     const int b = act ? i0 >> 5 : 0;
     const uint8_t* qrow = vbytes + 34 * b + 2 + (i0 & 31);
     const float* fb = fw + b * kTC;
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     if (act) {
-        if (per == 2) {
-#pragma unroll 8
-            for (int j = 0; j < cnt; ++j) {
-                const uint32_t q = *reinterpret_cast<const uint16_t*>(qrow + (size_t)j * a.hq8);
-                const float fj = fb[j];
-                acc[0] += (float)(int8_t)(q & 0xffu) * fj;
-                acc[1] += (float)(int8_t)(q >> 8) * fj;
+        int j = 0;
+        for (; j + 8 <= cnt; j += 8) {
+            uint32_t qv[8];
+            float fv[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                qv[u] = v_quants<PER>(qrow + (size_t)(j + u) * hq8);
+                fv[u] = fb[j + u];
             }
-        } else {
-#pragma unroll 4
-            for (int j = 0; j < cnt; ++j) {
-                const int8_t* qs = reinterpret_cast<const int8_t*>(qrow + (size_t)j * a.hq8);
-                const float fj = fb[j];
-                for (int e2 = 0; e2 < per; ++e2) acc[e2] += (float)qs[e2] * fj;
-            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+#pragma unroll
+                for (int e2 = 0; e2 < PER; ++e2) acc[e2] = fmaf((float)(int8_t)((qv[u] >> (8 * e2)) & 0xffu), fv[u], acc[e2]);
+        }
+        for (; j < cnt; ++j) {
+            const uint32_t q = v_quants<PER>(qrow + (size_t)j * hq8);
+#pragma unroll
+            for (int e2 = 0; e2 < PER; ++e2) acc[e2] = fmaf((float)(int8_t)((q >> (8 * e2)) & 0xffu), fb[j], acc[e2]);
         }
     }
-    float* dst = a.part + ((size_t)h * sp.n_chunks + c) * (hs + 2);
+    float* dst = a.part + ((size_t)h * a.part_chunks + c) * (hs + 2);
     if (act)
-        for (int e2 = 0; e2 < per; ++e2) dst[i0 + e2] = acc[e2];
+#pragma unroll
+        for (int e2 = 0; e2 < PER; ++e2) dst[i0 + e2] = acc[e2];
     if (lane == 0) {
         dst[hs] = m;
         dst[hs + 1] = l;
@@ -429,7 +447,7 @@ __global__ void __launch_bounds__(1024) attn_chunk_kernel(AttnCArgs a0) {
 #pragma unroll
         for (int sel = 0; sel < 2; ++sel) {
             if (km > 1 && sel != kvsel) continue;
-            uint8_t* cd = (sel ? a.vc : a.kc) + (size_t)g * a.head_seq + (size_t)sp.pos * a.hq8;
+            uint8_t* cd = (sel ? a.vc : a.kc) + (size_t)g * a.head_seq + (size_t)sp.pos * hq8;
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
                 const int j = lane + 64 * k;
@@ -503,36 +521,41 @@ __global__ void __launch_bounds__(64) kv_rows_kernel(AttnCArgs a0) {
 }
 
 // out = sum_c acc_c * expf(m_c - M) / S with M = max m_c, S = sum l_c expf(m_c - M).
-// Every load is issued before anything waits: the first wave reads the
-// chunk maxima and sums (lane = chunk) while each thread reads its output's
-// chunk partials; the weights expf(m_c - M) / S go through LDS.
+// One round trip for up to 64 chunks (4096 positions): every load is issued
+// before anything waits; the first wave holds the chunk maxima and sums
+// (lane = chunk, with a running rescale for more than 64 chunks), each thread
+// its output's chunk partials, and the weights expf(m_c - M) / S go through
+// LDS.  (Reading all chunk slots before the step record arrives was measured
+// slower: the extra loads cost more than the wait they save.)
 __global__ void __launch_bounds__(256) attn_merge_kernel(AttnCArgs a0) {
-    __shared__ float wc[256];
+    __shared__ float wc[64];
     const AttnCArgs a = token_args(a0, blockIdx.y);
     const Span sp = span_of(a.step, a.window);
     const int h = blockIdx.x, hs = a.hs, nch = sp.n_chunks, t = threadIdx.x;
-    const float* part = a.part + (size_t)h * nch * (hs + 2);
-    for (int c0 = 0; c0 < nch; c0 += 64) {   // 64 chunks (4096 positions) per round
+    const int ps = hs + 2;
+    const float* part = a.part + (size_t)h * a.part_chunks * ps;
+    float mx = -INFINITY, ssum = 0.0f, m0 = -INFINITY;
+    for (int c0 = 0; c0 < nch; c0 += 64) {   // 64 chunks per round
         const int nc = min(64, nch - c0);
         float pv[64];
         const int i = t;   // this thread's output element (hs <= 256 = blockDim)
 #pragma unroll
-        for (int k = 0; k < 64; ++k) pv[k] = (k < nc && i < hs) ? part[(size_t)(c0 + k) * (hs + 2) + i] : 0.0f;
+        for (int k = 0; k < 64; ++k) pv[k] = (k < nc && i < hs) ? part[(size_t)(c0 + k) * ps + i] : 0.0f;
         if (t < 64) {
-            const bool ok = t < nch;
-            // the statistics of every chunk (not only this round's), for M and S
-            float mx = -INFINITY;
-            for (int c = t; c < nch; c += 64) mx = fmaxf(mx, part[(size_t)c * (hs + 2) + hs]);
-            mx = wave_max(mx);
-            float ssum = 0.0f;
-            for (int c = t; c < nch; c += 64) {
-                const float* pc = part + (size_t)c * (hs + 2);
-                ssum += pc[hs + 1] * expf(pc[hs] - mx);
+            if (c0 == 0) {   // the statistics of every chunk, for M and S
+                for (int c = t; c < nch; c += 64) {
+                    const float mc = part[(size_t)c * ps + hs], lc = part[(size_t)c * ps + hs + 1];
+                    if (c == t) m0 = mc;
+                    const float mn = fmaxf(mx, mc);
+                    ssum = ssum * expf(mx - mn) + lc * expf(mc - mn);
+                    mx = mn;
+                }
+                const float M = wave_max(mx);
+                ssum = wave_sum(t < nch ? ssum * expf(mx - M) : 0.0f);
+                mx = M;
             }
-            ssum = wave_sum(ssum);
-            const float inv = 1.0f / ssum;
-            if (t < nc) wc[t] = expf(part[(size_t)(c0 + t) * (hs + 2) + hs] - mx) * inv;
-            (void)ok;
+            const float mc = c0 == 0 ? m0 : (t < nc ? part[(size_t)(c0 + t) * ps + hs] : -INFINITY);
+            if (t < nc) wc[t] = expf(mc - mx) * (1.0f / ssum);
         }
         __syncthreads();
         if (i < hs) {
@@ -543,6 +566,330 @@ __global__ void __launch_bounds__(256) attn_merge_kernel(AttnCArgs a0) {
             a.out[(size_t)h * hs + i] = tot;
         }
         __syncthreads();
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Attention of one decode step (c:3232-3359) with one workgroup per query
+// head (any context; the faster choice for short ones).  The position loop is split
+// over kHW waves: wave w takes chunks w, w + kHW, ... of cp positions and
+// streams each chunk's K rows and V rows HBM -> LDS (dwordx4 copies into two
+// slots of its own: the V rows land while the scores are formed, the next K
+// rows while V is accumulated).  Per chunk, as in attn_chunk_kernel: the
+// exact Q8_0 score of each position (lane = position), e = expf(s - m) with
+// m the wave's running maximum (earlier chunks rescaled by expf(m_old - m)),
+// and the unnormalized V accumulation sum_t q_t * (d_t * e_t), a position
+// skipped when e < 1e-8.  The waves' (m, l, acc) are merged at the end into
+// sum_w acc_w * expf(m_w - M) / S.
+//   The step's own K and V rows (QK-norm, RoPE, Q8_0, the arithmetic of
+// attn_chunk_kernel) are formed by every workgroup of the KV group, used
+// from LDS, and written to the cache by the group's first head.
+// blockIdx.x = head-in-group * n_kv + group: with n_kv a multiple of 8 the
+// heads of a group run on one XCD and share its L2.
+// ---------------------------------------------------------------------------
+constexpr int kHeadAutoPositions = 512;           // default: longer contexts use attn_chunk_kernel
+constexpr int kHW = 16;                           // waves per workgroup
+constexpr int kHCopies = 4;                       // dwordx4 copy instructions per slot
+constexpr int kHSlot = kHCopies * 1024;           // bytes per K or V slot
+constexpr int kHRows = kHSlot - 16;               // bytes of rows per chunk (room for 15 B of alignment slack)
+
+__host__ __device__ constexpr int head_chunk_positions(int hq8) { return kHRows / hq8 < 64 ? kHRows / hq8 : 64; }
+
+// vmcnt(N) (expcnt and lgkmcnt not waited for)
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// cnt rows of one KV head's cache into an LDS slot, from the 16-byte aligned
+// address at or below the first row: kHCopies instructions, lane l of
+// instruction i copying 16-byte piece 64 i + l (pieces past the rows repeat
+// the last one).  Every lane of every instruction copies, so the code has no
+// branch and the waits that follow can count the copies.  Returns the first
+// row's offset in the slot.
+__device__ __forceinline__ uint32_t head_copy(uint32_t* slot, const uint8_t* rows, int cnt, int hq8, int lane) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(rows);
+    const uint8_t* a16 = reinterpret_cast<const uint8_t*>(a & ~(uintptr_t)15);
+    const uint32_t roff = (uint32_t)(a & 15);
+    const int np = (int)((roff + (uint32_t)cnt * hq8 + 15) >> 4);   // pieces, <= kHSlot / 16 (cnt * hq8 <= kHRows)
+    __builtin_amdgcn_s_waitcnt(0xc07f);                             // lgkmcnt(0): earlier reads of the slot done
+#pragma unroll
+    for (int i = 0; i < kHCopies; ++i) {
+        const int pc = min(64 * i + lane, np - 1);
+        __builtin_amdgcn_global_load_lds(a16 + 16 * pc, (lds_void*)(slot + 256 * i), 16, 0, 0);
+    }
+    return roff;
+}
+
+template <int NB>
+__global__ void __launch_bounds__(1024) attn_head_kernel(AttnCArgs a) {
+    constexpr int hs = 32 * NB, nb = NB, half = hs / 2;
+    constexpr int PER = NB <= 2 ? 1 : (NB <= 4 ? 2 : 4);   // V outputs per lane, inside one 32-block
+    extern __shared__ __align__(16) uint32_t hl[];
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int hq8 = 34 * NB;
+    const int n_kv = a.n_heads / a.kv_mul;
+    const int g = blockIdx.x % n_kv, hg = blockIdx.x / n_kv, h = g * a.kv_mul + hg;
+    const Span sp = span_of(a.step, a.window);
+    const int cp = head_chunk_positions(hq8);
+    const int nch = (sp.na + cp - 1) / cp;
+    const int nk = w < nch ? (nch - 1 - w) / kHW + 1 : 0;   // chunks of this wave
+
+    // LDS: [kHW][K slot, V slot], [kHW][hs + 2] wave results (the prologue's
+    // staging rows alias them), hs int8 q, 8 q scales, the step's K and V rows
+    uint32_t* kslot = hl + (size_t)w * 2 * (kHSlot / 4);
+    uint32_t* vslot = kslot + kHSlot / 4;
+    float* red = reinterpret_cast<float*>(hl + (size_t)kHW * 2 * (kHSlot / 4));
+    int8_t* qq = reinterpret_cast<int8_t*>(red + kHW * (hs + 2));
+    float* qd = reinterpret_cast<float*>(qq + 256);
+    uint8_t* kvrow = reinterpret_cast<uint8_t*>(qd + 8);   // [2][hq8 rounded up to 4]
+    const int rowst = (hq8 + 3) & ~3;
+
+    // ---- the step's rows (wave 0: q of head h, the RoPE row and q_norm;
+    // 1: k of group g and k_norm; 2: v) and this wave's first K and V rows,
+    // all as LDS copies: explicit waits count them, so waiting for the step's
+    // rows never waits for the cache rows
+    const int role = w < 3 ? w : -1;
+    float* stg = red;   // [q, q_norm, k, k_norm, v][hs], cos, sin [half]: aliases the wave results
+    auto copy_vec = [&](float* dst, const float* src, int n) {   // n floats, dword pieces
+        for (int i = 0; 64 * i < n; ++i)
+            if (64 * i + lane < n) __builtin_amdgcn_global_load_lds(src + 64 * i + lane, (lds_void*)(dst + 64 * i), 4, 0, 0);
+    };
+    if (role == 0) {
+        copy_vec(stg, a.q + (size_t)h * hs, hs);
+        if (a.q_norm) copy_vec(stg + hs, a.q_norm, hs);
+        copy_vec(stg + 5 * hs, a.cos + (size_t)sp.pos * half, half);
+        copy_vec(stg + 5 * hs + half, a.sin + (size_t)sp.pos * half, half);
+    } else if (role == 1) {
+        copy_vec(stg + 2 * hs, a.k + (size_t)g * hs, hs);
+        if (a.k_norm) copy_vec(stg + 3 * hs, a.k_norm, hs);
+    } else if (role == 2) {
+        copy_vec(stg + 4 * hs, a.v + (size_t)g * hs, hs);
+    }
+    const size_t head_base = (size_t)g * a.head_seq;
+    auto chunk_rows = [&](int c, int& cnt) {
+        const int j0 = c * cp;
+        cnt = min(cp, sp.na - j0);
+        return head_base + (size_t)(sp.t0 + j0) * hq8;
+    };
+    uint32_t roff;
+    {   // waves past the last chunk copy it too (unused), so the copies are unconditional
+        int cnt;
+        const size_t off = chunk_rows(min(w, nch - 1), cnt);
+        roff = head_copy(kslot, a.kc + off, cnt, hq8, lane);
+        head_copy(vslot, a.vc + off, cnt, hq8, lane);
+    }
+    wait_vm<2 * kHCopies>();   // the step's rows have landed
+    lds_sync();
+
+    // ---- QK-norm (c:3151-3165), RoPE (c:3240-3296) and Q8_0 of q (c:3311-3312),
+    // k and v (c:3301-3308), with the arithmetic of attn_chunk_kernel
+    if (role == 0 || role == 1) {
+        float* row = stg + 2 * role * hs;
+        const bool normed = role == 0 ? a.q_norm != nullptr : a.k_norm != nullptr;
+        if (normed) {
+            float xv[4];
+            float ss = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int j = lane + 64 * k;
+                xv[k] = j < hs ? row[j] : 0.0f;
+                ss += xv[k] * xv[k];
+            }
+            ss = wave_sum(ss);
+            const float r = 1.0f / sqrtf(ss * a.inv_hs + a.eps);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int j = lane + 64 * k;
+                if (j < hs) row[j] = row[hs + j] * (r * xv[k]);
+            }
+        }
+    }
+    lds_sync();
+    if (role == 0 || role == 1) {
+        float* row = stg + 2 * role * hs;
+        const float* cosr = stg + 5 * hs;
+        const float* sinr = cosr + half;
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int p = lane + 64 * k;
+            if (p < half) {
+                const int i0 = a.neox ? p : 2 * p;
+                const int i1 = a.neox ? p + half : 2 * p + 1;
+                const float v0 = row[i0], v1 = row[i1], cs = cosr[p], sn = sinr[p];
+                if (role == 0) {
+                    row[i0] = (v0 * cs - v1 * sn) * a.attn_scale;
+                    row[i1] = (v0 * sn + v1 * cs) * a.attn_scale;
+                } else {
+                    row[i0] = v0 * cs - v1 * sn;
+                    row[i1] = v0 * sn + v1 * cs;
+                }
+            }
+        }
+    }
+    lds_sync();
+    uint32_t kvq[4], kvdh[4];
+    if (role >= 0) {
+        const float* row = stg + 2 * role * hs;
+        uint8_t* rb = kvrow + (role == 2 ? rowst : 0);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int j = lane + 64 * k;
+            if (k * 64 < hs) {
+                uint32_t dh;
+                const int8_t q8 = quant_lane(j < hs ? row[j] : 0.0f, dh);   // all lanes take part
+                kvq[k] = (uint8_t)q8;
+                kvdh[k] = dh;
+                if (j < hs) {
+                    const int b = j >> 5;
+                    if (role == 0) {
+                        qq[j] = q8;
+                        if ((lane & 31) == 0) qd[b] = h2f_exact(dh);
+                    } else {
+                        rb[34 * b + 2 + (j & 31)] = (uint8_t)q8;
+                        if ((lane & 31) == 0) {
+                            rb[34 * b] = (uint8_t)(dh & 0xff);
+                            rb[34 * b + 1] = (uint8_t)(dh >> 8);
+                        }
+                    }
+                }
+            }
+        }
+    }
+    lds_sync();   // q and the step's rows ready; the staging rows are free again
+
+    // ---- this wave's chunks
+    const int i0 = lane * PER;
+    const bool act = i0 < hs;
+    const int vb = act ? i0 >> 5 : 0;
+    const uint32_t doff = 34u * vb, qoff = 34u * vb + 2u + (uint32_t)(i0 & 31);
+    // q of the head: the same in every lane
+    int qw[8 * NB];
+    float qs[NB];
+#pragma unroll
+    for (int i = 0; i < 8 * NB; ++i) qw[i] = __builtin_amdgcn_readfirstlane(reinterpret_cast<const int*>(qq)[i]);
+#pragma unroll
+    for (int b = 0; b < NB; ++b) qs[b] = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(qd[b])));
+    float m_run = -INFINITY, l_run = 0.0f;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    const uint32_t* kpos = reinterpret_cast<const uint32_t*>(kvrow);
+    const uint8_t* vpos = kvrow + rowst;
+    for (int k = 0; k < nk; ++k) {
+        const int c = w + k * kHW;
+        int cnt;
+        (void)chunk_rows(c, cnt);
+        const bool last = c == nch - 1;   // holds the step's position, at row cnt - 1
+        const uint32_t ro_c = roff;       // this chunk's first-row offset in both slots
+        wait_vm<kHCopies>();              // the K rows have landed (the V copy may be in flight)
+        float sc = -INFINITY;
+        if (lane < cnt) {   // dot_q8_0_q8_0_cache (c:1574-1597): exact block dots in block order
+            const bool mine = last && lane == cnt - 1;
+            const uint32_t* kb = mine ? kpos : kslot;
+            const uint32_t ro = mine ? 0u : ro_c + (uint32_t)lane * hq8;
+            uint32_t kq[NB][8];
+            float db[NB];
+#pragma unroll
+            for (int b = 0; b < NB; ++b) db[b] = row_block(kb, ro + 34u * b, kq[b]);
+            float sum = 0.0f;
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                int isum = 0;
+#pragma unroll
+                for (int e2 = 0; e2 < 8; ++e2) isum = __builtin_amdgcn_sdot4(qw[8 * b + e2], (int)kq[b][e2], isum, false);
+                sum += qs[b] * db[b] * (float)isum;
+            }
+            sc = sum;
+        }
+        const float mn = fmaxf(m_run, wave_max(sc));
+        const float alpha = expf(m_run - mn);   // 0 for the first chunk
+        const float e = lane < cnt ? expf(sc - mn) : 0.0f;
+        l_run = l_run * alpha + wave_sum(e);
+#pragma unroll
+        for (int e2 = 0; e2 < 4; ++e2) acc[e2] *= alpha;
+        m_run = mn;
+        // the next chunk's K rows go into the K slot (its reads are done)
+        // while this chunk's V rows are accumulated
+        const bool more = k + 1 < nk;
+        size_t off2 = 0;
+        int cnt2 = 0;
+        if (more) {
+            off2 = chunk_rows(c + kHW, cnt2);
+            roff = head_copy(kslot, a.kc + off2, cnt2, hq8, lane);
+            wait_vm<kHCopies>();   // this chunk's V rows have landed
+        } else {
+            wait_vm<0>();
+        }
+        if (act) {
+            const uint8_t* vrows = reinterpret_cast<const uint8_t*>(vslot) + ro_c;
+            const int nrow = last ? cnt - 1 : cnt;   // the step's own row comes from vpos
+            int j = 0;
+            for (; j + 8 <= nrow; j += 8) {
+                uint32_t dv[8], qv[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    const uint8_t* row = vrows + (size_t)(j + u) * hq8;
+                    dv[u] = *reinterpret_cast<const uint16_t*>(row + doff);
+                    qv[u] = v_quants<PER>(row + qoff);
+                }
+#pragma unroll
+                for (int u = 0; u < 8; ++u)
+                    v_accum<PER>(dv[u], qv[u], __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), j + u)), acc);
+            }
+            for (; j < nrow; ++j) {
+                const uint8_t* row = vrows + (size_t)j * hq8;
+                v_accum<PER>(*reinterpret_cast<const uint16_t*>(row + doff), v_quants<PER>(row + qoff),
+                             __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), j)), acc);
+            }
+            if (last)
+                v_accum<PER>(*reinterpret_cast<const uint16_t*>(vpos + doff), v_quants<PER>(vpos + qoff),
+                             __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), cnt - 1)), acc);
+        }
+        if (more) head_copy(vslot, a.vc + off2, cnt2, hq8, lane);
+    }
+    wait_vm<0>();   // waves without chunks: their unused copies
+
+    // ---- merge the waves: out = sum_w acc_w * expf(m_w - M) / S
+    float* rw = red + w * (hs + 2);
+    if (act)
+        for (int e2 = 0; e2 < PER; ++e2) rw[i0 + e2] = acc[e2];
+    if (lane == 0) {
+        rw[hs] = m_run;
+        rw[hs + 1] = l_run;
+    }
+    lds_sync();
+    if (w == 0) {
+        const float mw = lane < kHW ? red[lane * (hs + 2) + hs] : -INFINITY;
+        const float lw = lane < kHW ? red[lane * (hs + 2) + hs + 1] : 0.0f;
+        const float M = wave_max(mw);
+        const float ex = lane < kHW ? expf(mw - M) : 0.0f;   // 0 for waves without chunks
+        const float S = wave_sum(lw * ex);
+        const float wt = ex * (1.0f / S);
+        if (act) {
+            float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int q = 0; q < kHW; ++q) {
+                const float wq = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wt), q));
+                for (int e2 = 0; e2 < PER; ++e2) o[e2] += red[q * (hs + 2) + i0 + e2] * wq;
+            }
+            for (int e2 = 0; e2 < PER; ++e2) a.out[(size_t)h * hs + i0 + e2] = o[e2];
+        }
+    }
+    // the step's K and V rows into the cache (c:3301-3308), by the group's first head
+    if (hg == 0 && (role == 1 || role == 2)) {
+        uint8_t* cd = (role == 2 ? a.vc : a.kc) + head_base + (size_t)sp.pos * hq8;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int j = lane + 64 * k;
+            if (j < hs) {
+                const int b = j >> 5;
+                cd[34 * b + 2 + (j & 31)] = (uint8_t)kvq[k];
+                if ((lane & 31) == 0) {
+                    cd[34 * b] = (uint8_t)(kvdh[k] & 0xff);
+                    cd[34 * b + 1] = (uint8_t)(kvdh[k] >> 8);
+                }
+            }
+        }
     }
 }
 
@@ -727,8 +1074,18 @@ void launch_act_rows(float* h, const float* h2, int64_t n, bool gelu, hipStream_
     L3P_HIP(hipGetLastError());
 }
 
-void launch_attention(const Model& m, int l, float* out, hipStream_t s) {
-    launch_attention(m, l, AttnIO{m.q, m.k, m.v, m.step, out}, s);
+void launch_attention(const Model& m, int l, float* out, bool per_head, hipStream_t s) {
+    launch_attention(m, l, AttnIO{m.q, m.k, m.v, m.step, out}, per_head, s);
+}
+
+// L3P_ATTN_HEAD=1 / 0 forces one attention or the other; by default the
+// per-head kernel takes steps attending to fewer than kHeadAutoPositions
+// positions (at Llama-3-8B shapes on MI355X it is faster there: 6.5 us
+// against 11.1 us for chunks + merge at 64 positions, even at ~600).
+bool attention_per_head(const Model&, int pos) {
+    const char* e = getenv("L3P_ATTN_HEAD");
+    if (e && *e) return atoi(e) != 0;
+    return pos < kHeadAutoPositions;
 }
 
 // The attention arguments of layer l for the token whose rows io holds.
@@ -748,6 +1105,7 @@ static AttnCArgs attn_args(const Model& m, int l, const AttnIO& io) {
     a.vc = m.vc + (size_t)l * m.layer_kv;
     a.step = io.step;
     a.part = m.part_acc;
+    a.part_chunks = m.max_chunks;
     a.out = io.out;
     a.head_seq = m.head_seq;
     a.n_heads = m.n_heads;
@@ -762,25 +1120,65 @@ static AttnCArgs attn_args(const Model& m, int l, const AttnIO& io) {
     return a;
 }
 
+template <int NB>
+static void launch_chunk_kernel(dim3 grid, dim3 block, size_t lds, const AttnCArgs& a, hipStream_t s) {
+    static size_t lds_set = 65536;   // dynamic LDS above 64 KB must be allowed first
+    if (lds > lds_set) {
+        L3P_HIP(hipFuncSetAttribute((const void*)attn_chunk_kernel<NB>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+        lds_set = lds;
+    }
+    hipLaunchKernelGGL(attn_chunk_kernel<NB>, grid, block, lds, s, a);
+    L3P_HIP(hipGetLastError());
+}
+
 // Chunk and merge launches for `tokens` tokens of up to `chunks` chunks each.
 static void launch_chunks(const Model& m, const AttnCArgs& a, int chunks, int tokens, hipStream_t s) {
     const int rowdw = (kTC * m.hq8 + 8 + 3) / 4;
     const size_t lds = (size_t)m.kv_mul * m.hs * 4 + 2 * (size_t)m.hs * 4 + (size_t)m.kv_mul * 8 * kTC * 4 +
                        (size_t)m.kv_mul * m.hs + (size_t)m.kv_mul * 8 * 4 + 2 * (size_t)rowdw * 4 + 16;
     const dim3 grid(m.n_kv, chunks, tokens), block(64 * m.kv_mul);
-    static size_t lds_set = 65536;   // dynamic LDS above 64 KB must be allowed first
-    if (lds > lds_set) {
-        L3P_HIP(hipFuncSetAttribute((const void*)attn_chunk_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-        lds_set = lds;
+    switch (m.hs / 32) {
+    case 1: launch_chunk_kernel<1>(grid, block, lds, a, s); break;
+    case 2: launch_chunk_kernel<2>(grid, block, lds, a, s); break;
+    case 3: launch_chunk_kernel<3>(grid, block, lds, a, s); break;
+    case 4: launch_chunk_kernel<4>(grid, block, lds, a, s); break;
+    case 5: launch_chunk_kernel<5>(grid, block, lds, a, s); break;
+    case 6: launch_chunk_kernel<6>(grid, block, lds, a, s); break;
+    case 7: launch_chunk_kernel<7>(grid, block, lds, a, s); break;
+    default: launch_chunk_kernel<8>(grid, block, lds, a, s); break;
     }
-    hipLaunchKernelGGL(attn_chunk_kernel, grid, block, lds, s, a);
-    L3P_HIP(hipGetLastError());
     hipLaunchKernelGGL(attn_merge_kernel, dim3(m.n_heads, tokens), dim3((m.hs + 63) / 64 * 64), 0, s, a);
     L3P_HIP(hipGetLastError());
 }
 
-void launch_attention(const Model& m, int l, const AttnIO& io, hipStream_t s) {
-    launch_chunks(m, attn_args(m, l, io), m.max_chunks, 1, s);
+template <int NB>
+static void launch_head(const Model& m, const AttnCArgs& a, hipStream_t s) {
+    const size_t lds = (size_t)kHW * 2 * kHSlot + (size_t)kHW * (32 * NB + 2) * 4 + 256 + 32 + 2 * (size_t)((34 * NB + 3) & ~3);
+    static size_t lds_set = 65536;   // dynamic LDS above 64 KB must be allowed first
+    if (lds > lds_set) {
+        L3P_HIP(hipFuncSetAttribute((const void*)attn_head_kernel<NB>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+        lds_set = lds;
+    }
+    hipLaunchKernelGGL(attn_head_kernel<NB>, dim3(m.n_heads), dim3(64 * kHW), lds, s, a);
+    L3P_HIP(hipGetLastError());
+}
+
+void launch_attention(const Model& m, int l, const AttnIO& io, bool per_head, hipStream_t s) {
+    const AttnCArgs a = attn_args(m, l, io);
+    if (!per_head) {
+        launch_chunks(m, a, m.max_chunks, 1, s);
+        return;
+    }
+    switch (m.hs / 32) {
+    case 1: launch_head<1>(m, a, s); break;
+    case 2: launch_head<2>(m, a, s); break;
+    case 3: launch_head<3>(m, a, s); break;
+    case 4: launch_head<4>(m, a, s); break;
+    case 5: launch_head<5>(m, a, s); break;
+    case 6: launch_head<6>(m, a, s); break;
+    case 7: launch_head<7>(m, a, s); break;
+    default: launch_head<8>(m, a, s); break;
+    }
 }
 
 int attention_chunks(const Model& m, int l, int last_pos) {
@@ -799,6 +1197,7 @@ void launch_attention_rows(const Model& m, int l, const AttnIO& io, int q_stride
     a.out_stride = out_stride;
     a.kv_ready = 1;
     a.part = part;
+    a.part_chunks = chunks;
     a.part_stride = (size_t)m.n_heads * chunks * (m.hs + 2);
     L3P_REQUIRE(a.part_stride * tokens <= part_cap, L3P_E_INVALID, "attention: %d tokens exceed the partials buffer",
                 tokens);

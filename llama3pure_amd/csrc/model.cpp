@@ -552,7 +552,7 @@ static void layers_impl(l3p_ctx* c, bool with_logits) {
             gemv_batch(c, L.wv.type, one(L.wv, m.v, EPI_STORE), m.dim, m.x, L.att_norm, "v");
         }
         // QK-norm, RoPE, KV write, Q quantization and attention (c:3232-3359)
-        launch_attention(m, l, m.xb, s);
+        launch_attention(m, l, m.xb, c->attn_per_head, s);
         // output projection + residual (c:3362-3371)
         if (m.is_gemma) {
             gemv_batch(c, L.wo.type, one(L.wo, m.xb2, EPI_STORE), m.q_dim, m.xb, nullptr, "wo");
@@ -689,7 +689,7 @@ static void prefill_batched(l3p_ctx* c, const int32_t* tokens, int n, int start)
 }
 
 void l3p_ctx::drop_graphs() {
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < 4; ++i) {
         if (graph[i]) hipGraphExecDestroy(graph[i]);
         graph[i] = nullptr;
         graph_runs[i] = 0;
@@ -723,7 +723,8 @@ static void forward_impl(l3p_ctx* c, int token, int pos, bool with_logits) {
     Model& m = *c->model;
     hipStream_t s = c->stream;
     launch_embed_step(m.emb, token, pos, m.is_gemma ? m.embed_scale : 0.0f, m.x, m.step, s);
-    const int v = with_logits ? 1 : 0;
+    c->attn_per_head = attention_per_head(m, pos);
+    const int v = (with_logits ? 1 : 0) | (c->attn_per_head ? 2 : 0);
     if (c->prof.on || !graphs_enabled() || c->graph_runs[v]++ == 0) {
         layers_impl(c, with_logits);
         return;

@@ -104,8 +104,10 @@ struct l3p_ctx {
     Profiler prof;
     // the layer stack of one forward step, captured once per variant
     // (index: with logits) and replayed; dropped when the model changes
-    hipGraphExec_t graph[2] = {nullptr, nullptr};
-    int graph_runs[2] = {0, 0};
+    // decode graphs by variant: bit 0 logits, bit 1 per-head attention
+    hipGraphExec_t graph[4] = {nullptr, nullptr, nullptr, nullptr};
+    int graph_runs[4] = {0, 0, 0, 0};
+    bool attn_per_head = false;   // the attention of the step being recorded
     void drop_graphs();
 };
 
@@ -125,8 +127,11 @@ struct AttnIO {
     const int* step;          // device {token, pos}
     float* out;
 };
-void launch_attention(const Model& m, int layer, float* out, hipStream_t s);
-void launch_attention(const Model& m, int layer, const AttnIO& io, hipStream_t s);
+// per_head: one workgroup per query head (attention_per_head(m, pos) says
+// whether the step at pos may take it); else split-position chunks + merge.
+bool attention_per_head(const Model& m, int pos);
+void launch_attention(const Model& m, int layer, float* out, bool per_head, hipStream_t s);
+void launch_attention(const Model& m, int layer, const AttnIO& io, bool per_head, hipStream_t s);
 // Attention of `tokens` consecutive prompt tokens of a batch in three
 // launches (K/V rows of all of them, then chunks and merge): io holds token
 // 0's rows, token z's are `*_stride` floats further and its step record 2z

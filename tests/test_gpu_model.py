@@ -226,3 +226,59 @@ def test_head_shapes(torch_gpu, cpuref, dim, heads, kv):
             d = kv_quant_diff(c2.copy_kv(0, wv), m.kv(0, wv), m, 75)
             assert d.max() <= 1 and d.mean() < 0.01, (dim, heads, kv, wv, int(d.max()), float(d.mean()))
         m.close()
+
+
+PATH_CASES = {
+    # head size 64 (60-position chunks), 1400 positions: 24 chunks, 2 per wave for most waves
+    "llama_hs64": (dict(arch="llama", dim=512, hidden=512, n_layers=3, n_heads=8, n_kv=2, vocab=512, ctx=2048,
+                        qtype=synth.Q8_0, seed=31, norm_jitter=0.1), 1400),
+    # head size 96 (40-position chunks, three blocks per row), odd group size
+    "llama_hs96": (dict(arch="llama", dim=768, hidden=512, n_layers=2, n_heads=8, n_kv=4, vocab=512, ctx=1024,
+                        qtype=synth.Q8_0, seed=32, norm_jitter=0.1), 700),
+    # head size 256 (15-position chunks), QK-norm, NEOX RoPE, a sliding window
+    # of 101 positions on five of six layers
+    "gemma_hs256": (dict(arch="gemma3", dim=512, hidden=512, n_layers=6, n_heads=4, n_kv=2, head_dim=256, vocab=512,
+                         ctx=1024, qtype=synth.Q8_0, seed=33, softcap=30.0, swa_window=101, norm_jitter=0.1,
+                         tied=True), 600),
+    # head size 128 (136-byte rows): windows starting at odd positions put the
+    # first row 8 bytes into a 16-byte piece
+    "gemma_hs128": (dict(arch="gemma3", dim=512, hidden=512, n_layers=6, n_heads=8, n_kv=2, head_dim=128, vocab=512,
+                         ctx=1024, qtype=synth.Q8_0, seed=34, softcap=30.0, swa_window=101, norm_jitter=0.1,
+                         tied=True), 600),
+}
+
+
+@pytest.mark.parametrize("case", list(PATH_CASES))
+def test_attention_paths_agree(torch_gpu, monkeypatch, case):
+    """The two decode attentions give the same steps: one workgroup per query
+    head (L3P_ATTN_HEAD=1; by default for steps attending to fewer than 512
+    positions) and split position chunks with a merge kernel
+    (L3P_ATTN_HEAD=0; by default from 512 positions on).  Both form the
+    step's K/V rows with the same arithmetic, so the layer-0 cache (whose
+    inputs are the embeddings) is bit-identical and deeper layers differ by
+    at most one-step quant flips; the attention outputs differ only in fp32
+    summation order, so logits agree to 1e-3 * rms.  Every wave of the
+    per-head kernel takes one or more chunks at these lengths."""
+    kw, n_prompt = PATH_CASES[case]
+    g = synth.synthetic_model(**kw)
+    rng = np.random.default_rng(kw["seed"])
+    toks = rng.integers(0, kw["vocab"], n_prompt + 6).astype(np.int32)
+    with l3p.Context(0) as ch, l3p.Context(0) as cc:
+        for c in (ch, cc):
+            c.load_gguf(g)
+            c.prefill(toks[:n_prompt], 0)
+        for i in range(n_prompt, n_prompt + 6):
+            monkeypatch.setenv("L3P_ATTN_HEAD", "1")
+            a = ch.forward(int(toks[i]), i)
+            monkeypatch.setenv("L3P_ATTN_HEAD", "0")
+            b = cc.forward(int(toks[i]), i)
+            assert float(np.max(np.abs(a - b))) <= 1e-3 * rms(b), (case, i)
+        mi = ch.model_info()
+        for wv in (False, True):
+            ka, kb = ch.copy_kv(0, wv), cc.copy_kv(0, wv)
+            assert np.array_equal(ka, kb), (case, wv)
+            for layer in range(1, mi.n_layers):
+                qa = ch.copy_kv(layer, wv).reshape(mi.n_kv_heads, mi.seq_len, -1, 34)[:, :n_prompt + 6, :, 2:]
+                qb = cc.copy_kv(layer, wv).reshape(mi.n_kv_heads, mi.seq_len, -1, 34)[:, :n_prompt + 6, :, 2:]
+                d = np.abs(qa.view(np.int8).astype(np.int32) - qb.view(np.int8).astype(np.int32))
+                assert d.max() <= 1, (case, layer, wv, int(d.max()))
