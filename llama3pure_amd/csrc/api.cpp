@@ -116,8 +116,7 @@ int l3p_dequant(l3p_ctx* c, int type, const void* src, int64_t n, float* dst) {
     CHECK_CTX(c);
     return guard(c, [&] {
         const int e = type_block_elems(type);
-        L3P_REQUIRE(e > 0 && type != L3P_Q2_K && type != L3P_Q3_K && type != L3P_Q5_K, L3P_E_UNSUPPORTED,
-                    "dequant: unsupported type %d", type);
+        L3P_REQUIRE(e > 0, L3P_E_UNSUPPORTED, "dequant: unsupported type %d", type);
         L3P_REQUIRE(n >= 0 && n % e == 0, L3P_E_INVALID, "dequant: n=%lld not a multiple of %d", (long long)n, e);
         L3P_REQUIRE(n == 0 || (src && dst), L3P_E_INVALID, "dequant: null pointer");
         launch_dequant(type, (const uint8_t*)src, n, dst, c->stream);

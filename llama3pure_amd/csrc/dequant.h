@@ -72,6 +72,41 @@ __device__ __forceinline__ float deq_elem(int type, const uint8_t* __restrict__ 
         const int q = hi ? (b[16 + 32 * g + l] >> 4) : (b[16 + 32 * g + l] & 0x0f);
         return d1 * (float)q - m1;
     }
+    case L3P_Q2_K: {   // dequantize_row_q2_K (c:748-784): group g = e / 16
+        const uint8_t* b = s + (i >> 8) * 84;
+        const int e = (int)(i & 255), g = e >> 4, l = e & 15;
+        const int half = g >> 3, j = (g >> 1) & 3, second = g & 1;
+        const int u = (b[16 + 32 * half + 16 * second + l] >> (2 * j)) & 3;
+        const float dl = ldh(b + 80) * (float)(b[g] & 0x0f), ml = ldh(b + 82) * (float)(b[g] >> 4);
+        return dl * (float)u - ml;
+    }
+    case L3P_Q3_K: {   // dequantize_row_q3_K (c:786-832)
+        const uint8_t* b = s + (i >> 8) * 110;
+        const int e = (int)(i & 255), g = e >> 4, l = e & 15;
+        const int half = g >> 3, j = (g >> 1) & 3, second = g & 1;
+        const uint8_t* sb = b + 96;
+        const int lo = g < 8 ? (sb[g] & 0x0f) : (sb[g - 8] >> 4);
+        const int sg = (lo | (((sb[8 + (g & 3)] >> (2 * (g >> 2))) & 3) << 4)) - 32;
+        const int u = (b[32 + 32 * half + 16 * second + l] >> (2 * j)) & 3;
+        const int h = (b[16 * second + l] >> (4 * half + j)) & 1;
+        return (ldh(b + 108) * (float)sg) * (float)(u - (h ? 0 : 4));
+    }
+    case L3P_Q5_K: {   // dequantize_row_q5_K (c:834-871): sub-block k = e / 32
+        const uint8_t* b = s + (i >> 8) * 176;
+        const int e = (int)(i & 255), k = e >> 5, l = e & 31;
+        const uint8_t* sc = b + 4;
+        int scv, mnv;
+        if (k < 4) {
+            scv = sc[k] & 63;
+            mnv = sc[k + 4] & 63;
+        } else {
+            scv = (sc[k + 4] & 0x0f) | ((sc[k - 4] >> 6) << 4);
+            mnv = (sc[k + 4] >> 4) | ((sc[k] >> 6) << 4);
+        }
+        const uint8_t byte = b[48 + 32 * (k >> 1) + l];
+        const int q = ((k & 1) ? (byte >> 4) : (byte & 0x0f)) + (((b[16 + l] >> k) & 1) ? 16 : 0);
+        return (ldh(b) * (float)scv) * (float)q - ldh(b + 2) * (float)mnv;
+    }
     case L3P_Q6_K: {
         const uint8_t* b = s + (i >> 8) * 210;
         const int e = (int)(i & 255), half = e >> 7, r = e & 127, g = r >> 5, l = r & 31;

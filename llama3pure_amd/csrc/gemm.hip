@@ -158,8 +158,15 @@ void launch_typed(const GemmArgs& a, hipStream_t st) {
 
 }  // namespace
 
+// The types the reference multiplies as fp32 (a row dequantizer or a float
+// dot, c:2291-2331); Q4_0, Q4_1, Q5_0, Q5_1 and IQ4_NL take the Q8_0
+// activation path instead.
 bool gemm_mfma_supported(int type) {
-    return type == L3P_Q8_0 || type == L3P_Q4_K || type == L3P_Q6_K;
+    switch (type) {
+    case L3P_Q8_0: case L3P_Q2_K: case L3P_Q3_K: case L3P_Q4_K: case L3P_Q5_K: case L3P_Q6_K:
+    case L3P_F16: case L3P_BF16: return true;
+    default: return false;
+    }
 }
 
 void launch_gemm(int type, const uint8_t* w, int n, int k, const float* x, int m, int ldx, float* y, int ldy,
@@ -172,7 +179,12 @@ void launch_gemm(int type, const uint8_t* w, int n, int k, const float* x, int m
     GemmArgs a{w, type_row_bytes(type, k), n, k, m, x, ldx, y, ldy, add ? 1 : 0};
     switch (type) {
     case L3P_Q8_0: launch_typed<L3P_Q8_0>(a, st); break;
+    case L3P_Q2_K: launch_typed<L3P_Q2_K>(a, st); break;
+    case L3P_Q3_K: launch_typed<L3P_Q3_K>(a, st); break;
     case L3P_Q4_K: launch_typed<L3P_Q4_K>(a, st); break;
-    default: launch_typed<L3P_Q6_K>(a, st); break;
+    case L3P_Q5_K: launch_typed<L3P_Q5_K>(a, st); break;
+    case L3P_Q6_K: launch_typed<L3P_Q6_K>(a, st); break;
+    case L3P_F16: launch_typed<L3P_F16>(a, st); break;
+    default: launch_typed<L3P_BF16>(a, st); break;
     }
 }

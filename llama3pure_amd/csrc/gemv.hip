@@ -72,7 +72,8 @@ constexpr int kMaxOut = 4096;       // per-workgroup result slots kept in LDS
 // instruction (256 B).  The pieces cover kChunkBytes + 14 (the largest start
 // offset of an unaligned chunk); clamped lanes write past the data, so a
 // buffer is kBufBytes long.
-template <int UE, int UB, int X4, int TAIL>
+// ALIGNED: the type's rows are always 16-byte multiples (no UA kernel).
+template <int UE, int UB, int X4, int TAIL, bool ALIGNED = false>
 struct FmtBase {
     static constexpr int kUnitElems = UE;
     static constexpr int kUnitBytes = UB;
@@ -81,14 +82,31 @@ struct FmtBase {
     static constexpr int kTail = TAIL;
     static constexpr int kCI = X4 + TAIL;   // copy instructions per chunk
     static constexpr int kBufBytes = X4 * 1024 + TAIL * 256;
-    static_assert(kChunkBytes + 14 <= kBufBytes, "copy pieces must cover an unaligned chunk");
+    static constexpr bool kAligned = ALIGNED;
+    static_assert(kChunkBytes + (ALIGNED ? 0 : 14) <= kBufBytes, "copy pieces must cover an unaligned chunk");
 };
 template <int QT>
 struct Fmt;
-template <> struct Fmt<L3P_Q8_0> : FmtBase<32, 34, 2, 1> {};    // 2176 B chunks
-template <> struct Fmt<L3P_Q4_0> : FmtBase<32, 18, 1, 1> {};    // 1152 B
-template <> struct Fmt<L3P_Q4_K> : FmtBase<256, 144, 1, 1> {};  // 1152 B, always aligned
-template <> struct Fmt<L3P_Q6_K> : FmtBase<256, 210, 2, 0> {};  // 1680 B
+template <> struct Fmt<L3P_Q8_0> : FmtBase<32, 34, 2, 1> {};            // 2176 B chunks
+template <> struct Fmt<L3P_Q4_0> : FmtBase<32, 18, 1, 1> {};            // 1152 B
+template <> struct Fmt<L3P_Q4_1> : FmtBase<32, 20, 2, 0> {};            // 1280 B
+template <> struct Fmt<L3P_Q5_0> : FmtBase<32, 22, 2, 0> {};            // 1408 B
+template <> struct Fmt<L3P_Q5_1> : FmtBase<32, 24, 2, 0> {};            // 1536 B
+template <> struct Fmt<L3P_IQ4_NL> : FmtBase<32, 18, 1, 1> {};          // 1152 B
+template <> struct Fmt<L3P_Q2_K> : FmtBase<256, 84, 1, 0> {};           // 672 B
+template <> struct Fmt<L3P_Q3_K> : FmtBase<256, 110, 1, 0> {};          // 880 B
+template <> struct Fmt<L3P_Q4_K> : FmtBase<256, 144, 1, 1, true> {};    // 1152 B
+template <> struct Fmt<L3P_Q5_K> : FmtBase<256, 176, 2, 0, true> {};    // 1408 B
+template <> struct Fmt<L3P_Q6_K> : FmtBase<256, 210, 2, 0> {};          // 1680 B
+template <> struct Fmt<L3P_F16> : FmtBase<32, 64, 4, 0, true> {};       // 4096 B
+template <> struct Fmt<L3P_BF16> : FmtBase<32, 64, 4, 0, true> {};      // 4096 B
+
+// Types whose reference dot takes the activation as Q8_0 (vec_dot_*_q8_0:
+// q8_func without a row dequantizer, c:2091-2133); the others dot fp32.
+template <int QT>
+__host__ __device__ constexpr bool q8_act() {
+    return QT == L3P_Q4_0 || QT == L3P_Q4_1 || QT == L3P_Q5_0 || QT == L3P_Q5_1 || QT == L3P_IQ4_NL;
+}
 
 template <int QT>
 __host__ __device__ __forceinline__ uint32_t row_bytes(int cols) {
@@ -127,15 +145,16 @@ __device__ __forceinline__ void wait_chunk(int younger) {
 // Every chunk is therefore exactly kCI instructions with all lanes active, a
 // constant the waits count on.
 struct DmaLane {
-    int o0, o1;   // the dwordx4 pieces (o1 unused when kX4 == 1)
-    int ot;       // the dword piece (unused without a tail)
+    int o[4];   // the dwordx4 pieces (kX4 <= 4 of them)
+    int ot;     // the dword piece (unused without a tail)
 };
 template <int QT>
 __device__ __forceinline__ DmaLane dma_lane(int lane, int span) {
+    static_assert(Fmt<QT>::kX4 <= 4, "at most four dwordx4 pieces");
     const int e16 = ((span + 15) & ~15) - 16, e4 = ((span + 3) & ~3) - 4;
     DmaLane d;
-    d.o0 = min(lane * 16, e16);
-    d.o1 = min(1024 + lane * 16, e16);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) d.o[i] = min(1024 * i + lane * 16, e16);
     d.ot = min(Fmt<QT>::kX4 * 1024 + lane * 4, e4);
     return d;
 }
@@ -143,8 +162,9 @@ __device__ __forceinline__ DmaLane dma_lane(int lane, int span) {
 // instruction writes the instruction's LDS base + 16 i, or + 4 i for the dword piece).
 template <int QT>
 __device__ __forceinline__ void chunk_dma(uint32_t* dst, const uint8_t* src, DmaLane d) {
-    __builtin_amdgcn_global_load_lds(src + d.o0, (lds_void*)dst, 16, 0, 2);
-    if (Fmt<QT>::kX4 > 1) __builtin_amdgcn_global_load_lds(src + d.o1, (lds_void*)(dst + 256), 16, 0, 2);
+#pragma unroll
+    for (int i = 0; i < Fmt<QT>::kX4; ++i)
+        __builtin_amdgcn_global_load_lds(src + d.o[i], (lds_void*)(dst + 256 * i), 16, 0, 2);
     if (Fmt<QT>::kTail)
         __builtin_amdgcn_global_load_lds(src + d.ot, (lds_void*)(dst + Fmt<QT>::kX4 * 256), 4, 0, 2);
 }
@@ -265,17 +285,17 @@ __device__ __forceinline__ bool chunk_src(const Cursor& cc, int k, const uint8_t
 
 // Activation of one lane's 32 elements in the form the weight type consumes.
 struct XBlock {
-    float x[32];    // Q8_0, Q4_K, Q6_K: the fp32 values
-    int q[8];       // Q4_0: the Q8_0 quants, four per dword
-    float s;        // Q4_0: fp32 value of the Q8_0 scale
-    int sum8;       // Q4_0: 8 * sum of quants
-    float xs;       // Q4_K: sum of the 32 values
-    float xs0, xs1; // Q6_K: sums of values 0..15 and 16..31
+    float x[32];    // fp32-activation types: the values
+    int q[8];       // Q8_0-activation types: the Q8_0 quants, four per dword
+    float s;        //   fp32 value of the Q8_0 scale
+    int sum8;       //   8 * sum of quants
+    float xs;       // sum of the 32 values (Q4_K, Q5_K)
+    float xs0, xs1; // sums of values 0..15 and 16..31 (Q2_K, Q3_K, Q6_K)
 };
 
 template <int QT>
 __device__ __forceinline__ void prepare_block(const float* v, XBlock& xb) {
-    if (QT == L3P_Q4_0) {
+    if (q8_act<QT>()) {
         QBlock qb;
         quantize32(v, qb);
 #pragma unroll
@@ -477,6 +497,309 @@ struct Lane<L3P_Q6_K> {
     }
 };
 
+// Eight dwords of a byte stream starting at bit `pos` of buf: nine aligned
+// dword reads and a funnel shift each (any byte or bit alignment).
+__device__ __forceinline__ void bit_window8(const uint32_t* buf, uint32_t pos, uint32_t (&w)[8]) {
+    const uint32_t f = pos >> 5, n = pos & 31u;
+    uint32_t d[9];
+#pragma unroll
+    for (int k = 0; k < 9; ++k) d[k] = buf[f + k];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) w[k] = __builtin_amdgcn_alignbit(d[k + 1], d[k], n);
+}
+
+// Four bits b0..b3 of n -> 0x10 in the bytes whose bit is set: the fifth
+// bit of four Q5 codes (n * 0x204081 puts bit i at bit 8i, masked).
+__device__ __forceinline__ uint32_t spread4(uint32_t n) {
+    return (((n & 15u) * 0x00204081u) & 0x01010101u) << 4;
+}
+
+// exact isum of the four low / four high nibble dwords of a 32-block
+// against the Q8_0 activation quants
+__device__ __forceinline__ int nib_dot(const uint32_t (&lo)[4], const uint32_t (&hi)[4], const XBlock& xb, int isum) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        isum = __builtin_amdgcn_sdot4((int)lo[k], xb.q[k], isum, false);
+        isum = __builtin_amdgcn_sdot4((int)hi[k], xb.q[4 + k], isum, false);
+    }
+    return isum;
+}
+
+// Q4_1 {fp16 d, m; u8 qs[16]} (c:140-145): the lane's block at byte
+// b = sh + 20*lane (4-aligned: rows and chunks start 4-aligned).  Per block
+// the reference's dw*dx*isum + mw*dx*xsum with isum = sum xq*u, xsum = sum xq
+// (vec_dot_q4_1_q8_0, c:1646-1665).
+template <>
+struct Lane<L3P_Q4_1> {
+    uint32_t hdr;
+    __device__ __forceinline__ void at(int lane, uint32_t sh) { hdr = (sh + 20u * (uint32_t)lane) >> 2; }
+    __device__ __forceinline__ float dot(const uint32_t* buf, const XBlock& xb) const {
+        const uint32_t dm = buf[hdr];
+        uint32_t lo[4], hi[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t q = buf[hdr + 1 + k];
+            lo[k] = q & 0x0f0f0f0fu;
+            hi[k] = (q >> 4) & 0x0f0f0f0fu;
+        }
+        const int isum = nib_dot(lo, hi, xb, 0);
+        return h2f(dm) * xb.s * (float)isum + h2f(dm >> 16) * xb.s * (float)(xb.sum8 / 8);
+    }
+};
+
+// Q5_0 {fp16 d; u8 qh[4]; u8 qs[16]} (c:147-151): block at byte
+// b = sh + 22*lane (even).  Code u_j = nibble | bit j of qh << 4; per block
+// dw*dx*isum with isum = sum xq*(u - 16) (vec_dot_q5_0_q8_0, c:1668-1690).
+template <>
+struct Lane<L3P_Q5_0> {
+    uint32_t half, pos;   // halfword of d; bit position of qh (qs follows)
+    __device__ __forceinline__ void at(int lane, uint32_t sh) {
+        const uint32_t b = sh + 22u * (uint32_t)lane;
+        half = b >> 1;
+        pos = 8u * (b + 2u);
+    }
+    __device__ __forceinline__ float dot(const uint32_t* buf, const XBlock& xb) const {
+        const uint32_t f = pos >> 5, n = pos & 31u;
+        uint32_t d[6];
+#pragma unroll
+        for (int k = 0; k < 6; ++k) d[k] = buf[f + k];
+        const uint32_t qh = __builtin_amdgcn_alignbit(d[1], d[0], n);
+        uint32_t lo[4], hi[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t q = __builtin_amdgcn_alignbit(d[k + 2], d[k + 1], n);
+            lo[k] = (q & 0x0f0f0f0fu) | spread4(qh >> (4 * k));
+            hi[k] = ((q >> 4) & 0x0f0f0f0fu) | spread4(qh >> (16 + 4 * k));
+        }
+        const int isum = nib_dot(lo, hi, xb, -2 * xb.sum8);
+        return h2f(reinterpret_cast<const uint16_t*>(buf)[half]) * xb.s * (float)isum;
+    }
+};
+
+// Q5_1 {fp16 d, m; u8 qh[4]; u8 qs[16]} (c:153-158): block at byte
+// b = sh + 24*lane (8-aligned).  dw*dx*isum + mw*dx*xsum with isum = sum xq*u
+// (vec_dot_q5_1_q8_0, c:1693-1717).
+template <>
+struct Lane<L3P_Q5_1> {
+    uint32_t hdr;
+    __device__ __forceinline__ void at(int lane, uint32_t sh) { hdr = (sh + 24u * (uint32_t)lane) >> 2; }
+    __device__ __forceinline__ float dot(const uint32_t* buf, const XBlock& xb) const {
+        const uint32_t dm = buf[hdr], qh = buf[hdr + 1];
+        uint32_t lo[4], hi[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t q = buf[hdr + 2 + k];
+            lo[k] = (q & 0x0f0f0f0fu) | spread4(qh >> (4 * k));
+            hi[k] = ((q >> 4) & 0x0f0f0f0fu) | spread4(qh >> (16 + 4 * k));
+        }
+        const int isum = nib_dot(lo, hi, xb, 0);
+        return h2f(dm) * xb.s * (float)isum + h2f(dm >> 16) * xb.s * (float)(xb.sum8 / 8);
+    }
+};
+
+// IQ4_NL {fp16 d; u8 qs[16]} (c:197-201): the Q4_0 layout, nibbles indexing
+// the 16-entry code book (c:204-206); dw*dx*isum with isum = sum xq*table[u]
+// (vec_dot_iq4_nl_q8_0, c:1994-2011).  Four nibble bytes map through the
+// table with two byte permutes (entries 0..7 and 8..15) and a select on
+// bit 3.
+template <>
+struct Lane<L3P_IQ4_NL> : Lane<L3P_Q4_0> {
+    static __device__ __forceinline__ uint32_t lookup(uint32_t nib) {
+        const uint32_t sel = nib & 0x07070707u;
+        const uint32_t a = __builtin_amdgcn_perm(0xF6EADDCFu, 0xBFAD9881u, sel);   // -127 -104 -83 -65 | -49 -35 -22 -10
+        const uint32_t b = __builtin_amdgcn_perm(0x71594535u, 0x26190D01u, sel);   //    1   13  25  38 |  53  69  89 113
+        const uint32_t m = ((nib >> 3) & 0x01010101u) * 0xffu;
+        return (a & ~m) | (b & m);
+    }
+    __device__ __forceinline__ float dot(const uint32_t* buf, const XBlock& xb) const {
+        const float d = h2f(reinterpret_cast<const uint16_t*>(buf)[half]);
+        const uint32_t* p = buf + first;
+        uint32_t dw[5];
+#pragma unroll
+        for (int k = 0; k < 5; ++k) dw[k] = p[k];
+        uint32_t lo[4], hi[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t q = __builtin_amdgcn_alignbyte(dw[k + 1], dw[k], shift);
+            lo[k] = lookup(q & 0x0f0f0f0fu);
+            hi[k] = lookup((q >> 4) & 0x0f0f0f0fu);
+        }
+        return d * xb.s * (float)nib_dot(lo, hi, xb, 0);
+    }
+};
+
+// fp32 dot of four packed unsigned byte codes with four activations
+__device__ __forceinline__ void ubyte_fma(uint32_t u, const float* x, float& s0, float& s1) {
+    s0 = fmaf((float)(u & 0xffu), x[0], s0);
+    s1 = fmaf((float)((u >> 8) & 0xffu), x[1], s1);
+    s0 = fmaf((float)((u >> 16) & 0xffu), x[2], s0);
+    s1 = fmaf((float)(u >> 24), x[3], s1);
+}
+
+// Q2_K super-block {u8 scales[16]; u8 qs[64]; fp16 d, dmin} (c:165-170), 84 B
+// at byte base = sh + 84*sb of the buffer (4-aligned).  Lane = 32-element
+// slice k = lane % 8 of super-block sb = lane / 8: groups 2k and 2k+1 of 16,
+// 2-bit codes at shift 2j of qs[32*half + l] (half = k / 4, j = k % 4), scale
+// byte scales[g] = (min << 4) | scale (dequantize_row_q2_K, c:748-784):
+//   (d*sc_a)*sum_a u x - (dmin*m_a)*sum_a x  +  the same for group b.
+template <>
+struct Lane<L3P_Q2_K> {
+    uint32_t qs, sch, dd, sj;   // dword of the codes, halfword of the two scale bytes, dword of {d, dmin}, 2j
+    __device__ __forceinline__ void at(int lane, uint32_t sh) {
+        const uint32_t sb = (uint32_t)lane >> 3, k = (uint32_t)lane & 7u;
+        const uint32_t base = sh + 84u * sb;
+        qs = (base + 16u + 32u * (k >> 2)) >> 2;
+        sch = (base + 2u * k) >> 1;
+        dd = (base + 80u) >> 2;
+        sj = 2u * (k & 3u);
+    }
+    __device__ __forceinline__ float dot(const uint32_t* buf, const XBlock& xb) const {
+        uint32_t w[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) w[i] = buf[qs + i];
+        const uint32_t scw = reinterpret_cast<const uint16_t*>(buf)[sch];
+        const uint32_t dm = buf[dd];
+        float a0 = 0.0f, a1 = 0.0f, b0 = 0.0f, b1 = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t u = (w[i] >> sj) & 0x03030303u;
+            if (i < 4) ubyte_fma(u, xb.x + 4 * i, a0, a1);
+            else ubyte_fma(u, xb.x + 4 * i, b0, b1);
+        }
+        const float d = h2f(dm), dmin = h2f(dm >> 16);
+        return (d * (float)(scw & 15u)) * (a0 + a1) - (dmin * (float)((scw >> 4) & 15u)) * xb.xs0 +
+               ((d * (float)((scw >> 8) & 15u)) * (b0 + b1) - (dmin * (float)((scw >> 12) & 15u)) * xb.xs1);
+    }
+};
+
+// Q3_K super-block {u8 hmask[32]; u8 qs[64]; u8 scales[12]; fp16 d}
+// (c:172-178), 110 B at byte base = sh + 110*sb (even).  Lane slice k as in
+// Q2_K; element l of group 2k + (l >= 16) has code v = u | h << 2 with u the
+// 2 bits at shift 2j of qs[32*half + l] and h bit 4*half + j of hmask[l],
+// value v - 4, and the 6-bit scale s_g (low 4 bits from byte g or the high
+// nibble of byte g - 8, high 2 bits from byte 8 + g%4 at bit 2*(g/4)):
+//   (d*(s_a - 32))*(sum_a v x - 4 sum_a x) + the same for group b
+// (dequantize_row_q3_K, c:786-832).
+template <>
+struct Lane<L3P_Q3_K> {
+    uint32_t qpos, hpos, spos, dh;   // bit positions of qs, hmask, scales; halfword of d
+    uint32_t sj, hr, hl;             // 2j; hmask bit 4*half + j moved to bit 2 by >> hr << hl
+    uint32_t olo, ohi;               // bit offsets of group a's low nibble and high bits in the scale bytes
+    __device__ __forceinline__ void at(int lane, uint32_t sh) {
+        const uint32_t sb = (uint32_t)lane >> 3, k = (uint32_t)lane & 7u;
+        const uint32_t base = sh + 110u * sb, half = k >> 2, j = k & 3u, hb = 4u * half + j;
+        qpos = 8u * (base + 32u + 32u * half);
+        hpos = 8u * base;
+        spos = 8u * (base + 96u);
+        dh = (base + 108u) >> 1;
+        sj = 2u * j;
+        hr = hb >= 2u ? hb - 2u : 0u;
+        hl = hb >= 2u ? 0u : 2u - hb;
+        olo = k < 4u ? 16u * k : 16u * (k - 4u) + 4u;
+        ohi = 64u + 16u * (k & 1u) + 2u * (k >> 1);
+    }
+    __device__ __forceinline__ float dot(const uint32_t* buf, const XBlock& xb) const {
+        uint32_t q[8], h[8];
+        bit_window8(buf, qpos, q);
+        bit_window8(buf, hpos, h);
+        const uint32_t f = spos >> 5, n = spos & 31u;
+        const uint32_t s0 = __builtin_amdgcn_alignbit(buf[f + 1], buf[f], n);
+        const uint32_t s1 = __builtin_amdgcn_alignbit(buf[f + 2], buf[f + 1], n);
+        const uint32_t s2 = __builtin_amdgcn_alignbit(buf[f + 3], buf[f + 2], n);
+        const float d = h2f(reinterpret_cast<const uint16_t*>(buf)[dh]);
+        const uint32_t sl = olo < 32u ? s0 : s1;
+        const uint32_t ol = olo & 31u, oh = ohi - 64u;
+        const int sa = (int)(__builtin_amdgcn_ubfe(sl, ol, 4u) | (__builtin_amdgcn_ubfe(s2, oh, 2u) << 4)) - 32;
+        const int sb = (int)(__builtin_amdgcn_ubfe(sl, ol + 8u, 4u) | (__builtin_amdgcn_ubfe(s2, oh + 8u, 2u) << 4)) - 32;
+        float a0 = 0.0f, a1 = 0.0f, b0 = 0.0f, b1 = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t v = ((q[i] >> sj) & 0x03030303u) | (((h[i] >> hr) << hl) & 0x04040404u);
+            if (i < 4) ubyte_fma(v, xb.x + 4 * i, a0, a1);
+            else ubyte_fma(v, xb.x + 4 * i, b0, b1);
+        }
+        return (d * (float)sa) * ((a0 + a1) - 4.0f * xb.xs0) + (d * (float)sb) * ((b0 + b1) - 4.0f * xb.xs1);
+    }
+};
+
+// Q5_K super-block {fp16 d, dmin; u8 scales[12]; u8 qh[32]; u8 qs[128]}
+// (c:180-187), 176 B at byte 176*sb (16-byte aligned).  Lane = sub-block
+// k = lane % 8: code = nibble of qs[32*(k/2) + l] (low for even k) + 16 * bit
+// k of qh[l], with the Q4_K 6-bit scale and min k:
+//   (d*sc)*sum q x - (dmin*m)*sum x   (dequantize_row_q5_K, c:834-871).
+template <>
+struct Lane<L3P_Q5_K> {
+    uint32_t hdr, qh, qs, ns, kb, bs;
+    bool hi;
+    __device__ __forceinline__ void at(int lane, uint32_t /*sh: always 0*/) {
+        const uint32_t sb = (uint32_t)lane >> 3, k = (uint32_t)lane & 7u;
+        hdr = 44u * sb;
+        qh = hdr + 4u;
+        qs = hdr + 12u + 8u * (k >> 1);
+        ns = 4u * (k & 1u);
+        kb = k;
+        bs = 8u * (k & 3u);
+        hi = k >= 4u;
+    }
+    __device__ __forceinline__ float dot(const uint32_t* buf, const XBlock& xb) const {
+        uint4 h;   // dword reads (merged by the compiler), as in Lane<Q4_K>
+        h.x = buf[hdr];
+        h.y = buf[hdr + 1];
+        h.z = buf[hdr + 2];
+        h.w = buf[hdr + 3];
+        const float d = h2f(h.x), dmin = h2f(h.x >> 16);
+        const uint32_t sc = __builtin_amdgcn_ubfe(hi ? h.w : h.y, bs, hi ? 4u : 6u) |
+                            (hi ? __builtin_amdgcn_ubfe(h.y, bs + 6u, 2u) << 4 : 0u);
+        const uint32_t mn = __builtin_amdgcn_ubfe(hi ? h.w : h.z, hi ? bs + 4u : bs, hi ? 4u : 6u) |
+                            (hi ? __builtin_amdgcn_ubfe(h.z, bs + 6u, 2u) << 4 : 0u);
+        uint32_t qw[8], hw[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            qw[i] = buf[qs + i];
+            hw[i] = buf[qh + i];
+        }
+        float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t q = ((qw[i] >> ns) & 0x0f0f0f0fu) | (((hw[i] >> kb) & 0x01010101u) << 4);
+            ubyte_fma(q, xb.x + 4 * i, s0, s1);
+        }
+        return (d * (float)sc) * (s0 + s1) - (dmin * (float)mn) * xb.xs;
+    }
+};
+
+// F16 / BF16 rows: the lane's 32 values are the 64 bytes at 64*lane, two per
+// dword, converted exactly and summed as fp32 products (vec_dot_f16 /
+// vec_dot_bf16, c:1467-1485, sum in another order).
+template <int QT>
+struct LaneHalf {
+    uint32_t first;
+    __device__ __forceinline__ void at(int lane, uint32_t /*sh: always 0*/) { first = 16u * (uint32_t)lane; }
+    __device__ __forceinline__ float dot(const uint32_t* buf, const XBlock& xb) const {
+        uint32_t w[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) w[i] = buf[first + i];
+        float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; i += 2) {
+            float v[4];
+            if (QT == L3P_F16) {
+                v[0] = h2f(w[i]); v[1] = h2f(w[i] >> 16); v[2] = h2f(w[i + 1]); v[3] = h2f(w[i + 1] >> 16);
+            } else {
+                v[0] = __uint_as_float(w[i] << 16); v[1] = __uint_as_float(w[i] & 0xffff0000u);
+                v[2] = __uint_as_float(w[i + 1] << 16); v[3] = __uint_as_float(w[i + 1] & 0xffff0000u);
+            }
+            s0 = fmaf(v[0], xb.x[2 * i], s0);
+            s1 = fmaf(v[1], xb.x[2 * i + 1], s1);
+            s2 = fmaf(v[2], xb.x[2 * i + 2], s2);
+            s3 = fmaf(v[3], xb.x[2 * i + 3], s3);
+        }
+        return (s0 + s1) + (s2 + s3);
+    }
+};
+template <> struct Lane<L3P_F16> : LaneHalf<L3P_F16> {};
+template <> struct Lane<L3P_BF16> : LaneHalf<L3P_BF16> {};
+
 template <int QT, int G, int NB, bool PAIR, bool UA>
 __global__ void __launch_bounds__(1024) gemv_kernel(GemvArgs a) {
     constexpr int CB = Fmt<QT>::kChunkBytes;
@@ -556,7 +879,7 @@ __global__ void __launch_bounds__(1024) gemv_kernel(GemvArgs a) {
     // the row totals are scaled by r after the first group's cross-wave sum:
     // nothing here waits for the other waves.  Q4_0 quantizes w[j] * (r *
     // x[j]) exactly as the reference does, so it forms r first.
-    constexpr bool kLateScale = QT != L3P_Q4_0;
+    constexpr bool kLateScale = !q8_act<QT>();
     if (a.norm) {
         float ss = 0.0f;
 #pragma unroll
@@ -731,13 +1054,17 @@ void launch_rows(GemvArgs a, hipStream_t st) {
     L3P_HIP(hipGetLastError());
 }
 
+// Ring depth: 3 buffers per wave (deeper rings measured no faster on
+// MI355X); 2 for the 4 KB F16/BF16 chunks of rows too wide for 3.
 template <int QT, int G, bool PAIR, bool UA>
 void launch_nb(GemvArgs a, int nbuf, hipStream_t st) {
-    switch (nbuf) {
-    case 3: launch_rows<QT, G, 3, PAIR, UA>(a, st); break;
-    case 6: launch_rows<QT, G, 6, PAIR, UA>(a, st); break;
-    default: launch_rows<QT, G, 4, PAIR, UA>(a, st); break;
+    if constexpr (Fmt<QT>::kBufBytes >= 4096) {
+        if (nbuf == 2) {
+            launch_rows<QT, G, 2, PAIR, UA>(a, st);
+            return;
+        }
     }
+    launch_rows<QT, G, 3, PAIR, UA>(a, st);
 }
 
 template <int QT, bool UA>
@@ -761,21 +1088,16 @@ void launch_type(GemvArgs a, bool pair, int G, int nbuf, hipStream_t st) {
     const int units = pair ? a.rows[0] : a.rows_total;
     const int per = pair ? G / 2 : G;
     a.ngroups = (units + per - 1) / per;
-    // the deepest ring (3, 4 or 6 buffers per wave) not above nbuf whose
-    // buffers fit the 160 KB of LDS with room for the result slots
+    // three buffers per wave when they fit the 160 KB of LDS with room for
+    // the result slots, else two
     const int nw = (a.cols / 32 + 63) / 64;
-    static const int depths[] = {6, 4, 3};
-    int nb = 3;
-    for (int d : depths)
-        if (d <= nbuf && (size_t)nw * d * Fmt<QT>::kBufBytes + 16384 <= 160 * 1024) {
-            nb = d;
-            break;
-        }
+    const int nb = (size_t)nw * 3 * Fmt<QT>::kBufBytes + 16384 <= 160 * 1024 ? 3 : 2;
+    (void)nbuf;
     if (row_bytes<QT>(a.cols) % 16 == 0) {
         launch_g<QT, false>(a, pair, G, nb, st);
     } else {
-        // Q4_K rows (144 B super-blocks, cols % 256 == 0) are always 16-byte multiples
-        if constexpr (QT != L3P_Q4_K) launch_g<QT, true>(a, pair, G, nb, st);
+        // Q4_K, Q5_K and F16/BF16 rows are always 16-byte multiples
+        if constexpr (!Fmt<QT>::kAligned) launch_g<QT, true>(a, pair, G, nb, st);
     }
 }
 
@@ -784,8 +1106,9 @@ void launch_type(GemvArgs a, bool pair, int G, int nbuf, hipStream_t st) {
 bool gemv_supported(int type, int cols) {
     int unit;
     switch (type) {
-    case L3P_Q8_0: case L3P_Q4_0: unit = 32; break;
-    case L3P_Q4_K: case L3P_Q6_K: unit = 256; break;
+    case L3P_Q8_0: case L3P_Q4_0: case L3P_Q4_1: case L3P_Q5_0: case L3P_Q5_1: case L3P_IQ4_NL:
+    case L3P_F16: case L3P_BF16: unit = 32; break;
+    case L3P_Q2_K: case L3P_Q3_K: case L3P_Q4_K: case L3P_Q5_K: case L3P_Q6_K: unit = 256; break;
     default: return false;
     }
     return cols > 0 && cols % unit == 0 && cols <= kMaxWaves * kChunkElems;
@@ -833,11 +1156,20 @@ void launch_gemv(int type, const GemvBatch& b, int cols, const float* x, const f
                 break;
             }
     }
-    const int nbuf = env_int("L3P_GEMV_NB", 3);
+    const bool pr = b.pair != 0;
     switch (type) {
-    case L3P_Q8_0: launch_type<L3P_Q8_0>(a, b.pair != 0, G, nbuf, st); break;
-    case L3P_Q4_0: launch_type<L3P_Q4_0>(a, b.pair != 0, G, nbuf, st); break;
-    case L3P_Q4_K: launch_type<L3P_Q4_K>(a, b.pair != 0, G, nbuf, st); break;
-    default: launch_type<L3P_Q6_K>(a, b.pair != 0, G, nbuf, st); break;
+    case L3P_Q8_0: launch_type<L3P_Q8_0>(a, pr, G, 3, st); break;
+    case L3P_Q4_0: launch_type<L3P_Q4_0>(a, pr, G, 3, st); break;
+    case L3P_Q4_1: launch_type<L3P_Q4_1>(a, pr, G, 3, st); break;
+    case L3P_Q5_0: launch_type<L3P_Q5_0>(a, pr, G, 3, st); break;
+    case L3P_Q5_1: launch_type<L3P_Q5_1>(a, pr, G, 3, st); break;
+    case L3P_IQ4_NL: launch_type<L3P_IQ4_NL>(a, pr, G, 3, st); break;
+    case L3P_Q2_K: launch_type<L3P_Q2_K>(a, pr, G, 3, st); break;
+    case L3P_Q3_K: launch_type<L3P_Q3_K>(a, pr, G, 3, st); break;
+    case L3P_Q4_K: launch_type<L3P_Q4_K>(a, pr, G, 3, st); break;
+    case L3P_Q5_K: launch_type<L3P_Q5_K>(a, pr, G, 3, st); break;
+    case L3P_Q6_K: launch_type<L3P_Q6_K>(a, pr, G, 3, st); break;
+    case L3P_F16: launch_type<L3P_F16>(a, pr, G, 3, st); break;
+    default: launch_type<L3P_BF16>(a, pr, G, 3, st); break;
     }
 }

@@ -220,7 +220,10 @@ void rope_tables(int seq, int hs, float theta, std::vector<float>& c, std::vecto
         }
 }
 
-bool q8_class(int t) { return t == L3P_Q4_0; }   // q8_func && !deq_func (c:3221)
+// q8_func && !deq_func (c:2091-2133, c:3221): the activation goes to Q8_0
+bool q8_class(int t) {
+    return t == L3P_Q4_0 || t == L3P_Q4_1 || t == L3P_Q5_0 || t == L3P_Q5_1 || t == L3P_IQ4_NL;
+}
 
 }  // namespace
 
@@ -481,9 +484,16 @@ ProfRange::~ProfRange() {
 static const char* type_name(int t) {
     switch (t) {
     case L3P_Q4_0: return "q4_0";
+    case L3P_Q4_1: return "q4_1";
+    case L3P_Q5_0: return "q5_0";
+    case L3P_Q5_1: return "q5_1";
     case L3P_Q8_0: return "q8_0";
+    case L3P_Q2_K: return "q2_k";
+    case L3P_Q3_K: return "q3_k";
     case L3P_Q4_K: return "q4_k";
+    case L3P_Q5_K: return "q5_k";
     case L3P_Q6_K: return "q6_k";
+    case L3P_IQ4_NL: return "iq4_nl";
     case L3P_F16: return "f16";
     case L3P_BF16: return "bf16";
     case L3P_F32: return "f32";

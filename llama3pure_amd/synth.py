@@ -9,6 +9,9 @@ configurations':
 * Q4_0: nibbles uniform in [0, 15], fp16 scale |N(0, 0.02)| / 8;
 * Q4_K: every scale and quant byte uniform, d and dmin |N(0, 0.02)| / (15*63);
 * Q6_K: ql, qh uniform, int8 sub-scales uniform, d |N(0, 0.02)| / (32*127);
+* the other types likewise: every code and sub-scale byte uniform, fp16
+  scales |N(0, 0.02)| over the code range (offsets N(0, 0.02)), F16 / BF16
+  values N(0, 0.02);
 * activations N(0, 1) fp32.
 
 Model weights are drawn N(0, std) in fp32 and block-quantized with the
@@ -20,8 +23,13 @@ import struct
 
 import numpy as np
 
-F32, F16, Q4_0, Q8_0, Q4_K, Q6_K = 0, 1, 2, 8, 12, 14
-BLOCK = {F32: (1, 4), F16: (1, 2), Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210)}
+F32, F16, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0 = 0, 1, 2, 3, 6, 7, 8
+Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, IQ4_NL, BF16 = 10, 11, 12, 13, 14, 20, 29
+BLOCK = {F32: (1, 4), F16: (1, 2), BF16: (1, 2), Q4_0: (32, 18), Q4_1: (32, 20), Q5_0: (32, 22),
+         Q5_1: (32, 24), Q8_0: (32, 34), Q2_K: (256, 84), Q3_K: (256, 110), Q4_K: (256, 144),
+         Q5_K: (256, 176), Q6_K: (256, 210), IQ4_NL: (32, 18)}
+# IQ4_NL code book (llama3pure-c-engine.c:204-206)
+IQ4_NL_VALUES = np.array([-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113], np.int8)
 
 
 def row_bytes(qtype: int, cols: int) -> int:
@@ -31,6 +39,13 @@ def row_bytes(qtype: int, cols: int) -> int:
 
 def _f16_bytes(v: np.ndarray) -> np.ndarray:
     return np.ascontiguousarray(v.astype(np.float16)).view(np.uint8).reshape(v.shape + (2,))
+
+
+def _bf16_bytes(v: np.ndarray) -> np.ndarray:
+    """float32 -> bfloat16 bytes, rounded to nearest even (finite inputs)."""
+    u = np.ascontiguousarray(v, np.float32).view(np.uint32).astype(np.uint64)
+    h = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    return np.ascontiguousarray(h).view(np.uint8).reshape(v.shape + (2,))
 
 
 def random_blocks(qtype: int, rows: int, cols: int, seed: int) -> np.ndarray:
@@ -52,6 +67,31 @@ def random_blocks(qtype: int, rows: int, cols: int, seed: int) -> np.ndarray:
     elif qtype == Q6_K:
         out[:, :, 0:208] = rng.integers(0, 256, (rows, nb, 208), dtype=np.uint8)
         out[:, :, 208:210] = _f16_bytes(np.abs(rng.normal(0, 0.02, (rows, nb))) / (32 * 127))
+    elif qtype in (Q4_1, Q5_1):
+        out[:, :, 0:2] = _f16_bytes(np.abs(rng.normal(0, 0.02, (rows, nb))) / (8 if qtype == Q4_1 else 16))
+        out[:, :, 2:4] = _f16_bytes(rng.normal(0, 0.02, (rows, nb)))
+        out[:, :, 4:] = rng.integers(0, 256, (rows, nb, bb - 4), dtype=np.uint8)
+    elif qtype == Q5_0:
+        out[:, :, 0:2] = _f16_bytes(np.abs(rng.normal(0, 0.02, (rows, nb))) / 16)
+        out[:, :, 2:] = rng.integers(0, 256, (rows, nb, 20), dtype=np.uint8)
+    elif qtype == IQ4_NL:
+        out[:, :, 0:2] = _f16_bytes(np.abs(rng.normal(0, 0.02, (rows, nb))) / 127)
+        out[:, :, 2:] = rng.integers(0, 256, (rows, nb, 16), dtype=np.uint8)
+    elif qtype == Q2_K:
+        out[:, :, 0:80] = rng.integers(0, 256, (rows, nb, 80), dtype=np.uint8)
+        out[:, :, 80:82] = _f16_bytes(np.abs(rng.normal(0, 0.02, (rows, nb))) / (3 * 15))
+        out[:, :, 82:84] = _f16_bytes(np.abs(rng.normal(0, 0.02, (rows, nb))) / (3 * 15))
+    elif qtype == Q3_K:
+        out[:, :, 0:108] = rng.integers(0, 256, (rows, nb, 108), dtype=np.uint8)
+        out[:, :, 108:110] = _f16_bytes(np.abs(rng.normal(0, 0.02, (rows, nb))) / (4 * 32))
+    elif qtype == Q5_K:
+        out[:, :, 0:2] = _f16_bytes(np.abs(rng.normal(0, 0.02, (rows, nb))) / (31 * 63))
+        out[:, :, 2:4] = _f16_bytes(np.abs(rng.normal(0, 0.02, (rows, nb))) / (31 * 63))
+        out[:, :, 4:] = rng.integers(0, 256, (rows, nb, 172), dtype=np.uint8)
+    elif qtype == F16:
+        out[:, :, :] = _f16_bytes(rng.normal(0, 0.02, (rows, nb)))
+    elif qtype == BF16:
+        out[:, :, :] = _bf16_bytes(rng.normal(0, 0.02, (rows, nb)).astype(np.float32))
     else:
         raise ValueError(f"no synthetic generator for type {qtype}")
     return out.reshape(rows, nb * bb)
@@ -129,11 +169,7 @@ def quantize_q4_k(w: np.ndarray) -> np.ndarray:
     out = np.empty((rows, nsb, 144), np.uint8)
     out[:, :, 0:2] = np.ascontiguousarray(d).view(np.uint8).reshape(rows, nsb, 2)
     out[:, :, 2:4] = np.ascontiguousarray(dmin).view(np.uint8).reshape(rows, nsb, 2)
-    s = np.empty((rows, nsb, 12), np.int64)
-    s[:, :, 0:4] = (sc[:, :, 0:4] & 63) | ((sc[:, :, 4:8] >> 4) << 6)
-    s[:, :, 4:8] = (m[:, :, 0:4] & 63) | ((m[:, :, 4:8] >> 4) << 6)
-    s[:, :, 8:12] = (sc[:, :, 4:8] & 15) | ((m[:, :, 4:8] & 15) << 4)
-    out[:, :, 4:16] = s.astype(np.uint8)
+    out[:, :, 4:16] = _pack_k4_scales(sc, m)
     qs = q[:, :, 0::2, :] | (q[:, :, 1::2, :] << 4)          # [rows, nsb, 4, 32]
     out[:, :, 16:] = qs.reshape(rows, nsb, 128).astype(np.uint8)
     return out.reshape(rows, -1)
@@ -165,6 +201,173 @@ def quantize_q6_k(w: np.ndarray) -> np.ndarray:
     return out.reshape(rows, -1)
 
 
+def _h16(v: np.ndarray) -> np.ndarray:
+    """fp32 -> fp16 values (RNE) and their bytes."""
+    h = v.astype(np.float16)
+    return h, np.ascontiguousarray(h).view(np.uint8).reshape(v.shape + (2,))
+
+
+def _pack_k4_scales(sc: np.ndarray, m: np.ndarray) -> np.ndarray:
+    """Eight 6-bit scales and mins [.., 8] -> the 12 bytes get_scale_min_k4
+    reads (llama3pure-c-engine.c:705-714)."""
+    s = np.empty(sc.shape[:-1] + (12,), np.int64)
+    s[..., 0:4] = (sc[..., 0:4] & 63) | ((sc[..., 4:8] >> 4) << 6)
+    s[..., 4:8] = (m[..., 0:4] & 63) | ((m[..., 4:8] >> 4) << 6)
+    s[..., 8:12] = (sc[..., 4:8] & 15) | ((m[..., 4:8] & 15) << 4)
+    return s.astype(np.uint8)
+
+
+def _minmax_32(w: np.ndarray, levels: int):
+    """Per 32-block min/max quantization to 0..levels: fp16 d, m, codes."""
+    rows, cols = w.shape
+    b = w.reshape(rows, cols // 32, 32).astype(np.float32)
+    mn, mx = b.min(axis=2), b.max(axis=2)
+    d, db = _h16((mx - mn) / np.float32(levels))
+    m, mb = _h16(mn)
+    q = _round_div(b - m.astype(np.float32)[..., None], d.astype(np.float32)[..., None], 0, levels)
+    return db, mb, q
+
+
+def _qh_bits(q: np.ndarray) -> np.ndarray:
+    """Bit 4 of each of the 32 codes of a block -> the 4 qh bytes (bit j = code j)."""
+    bits = ((q >> 4) & 1) << np.arange(32, dtype=np.int64)
+    v = bits.sum(axis=-1)
+    return np.stack([(v >> (8 * k)) & 0xFF for k in range(4)], axis=-1).astype(np.uint8)
+
+
+def quantize_q4_1(w: np.ndarray) -> np.ndarray:
+    """fp32 -> Q4_1 {fp16 d, m; nibbles}: per block d = (max-min)/15, m = min."""
+    db, mb, q = _minmax_32(w, 15)
+    out = np.empty(q.shape[:2] + (20,), np.uint8)
+    out[..., 0:2], out[..., 2:4] = db, mb
+    out[..., 4:] = (q[..., :16] | (q[..., 16:] << 4)).astype(np.uint8)
+    return out.reshape(w.shape[0], -1)
+
+
+def quantize_q5_1(w: np.ndarray) -> np.ndarray:
+    """fp32 -> Q5_1 {fp16 d, m; qh[4]; nibbles}: per block d = (max-min)/31."""
+    db, mb, q = _minmax_32(w, 31)
+    out = np.empty(q.shape[:2] + (24,), np.uint8)
+    out[..., 0:2], out[..., 2:4] = db, mb
+    out[..., 4:8] = _qh_bits(q)
+    out[..., 8:] = ((q[..., :16] & 15) | ((q[..., 16:] & 15) << 4)).astype(np.uint8)
+    return out.reshape(w.shape[0], -1)
+
+
+def quantize_q5_0(w: np.ndarray) -> np.ndarray:
+    """fp32 -> Q5_0 {fp16 d; qh[4]; nibbles}: d = (signed max)/-16, code
+    min(31, trunc(w/d + 16.5)) as in llama.cpp's quantize_row_q5_0_ref."""
+    rows, cols = w.shape
+    b = w.reshape(rows, cols // 32, 32).astype(np.float32)
+    idx = np.abs(b).argmax(axis=2)
+    mx = np.take_along_axis(b, idx[:, :, None], axis=2)[:, :, 0]
+    d, db = _h16(mx / np.float32(-16))
+    dd = d.astype(np.float32)
+    with np.errstate(divide="ignore"):
+        inv = np.where(dd != 0, np.float32(1) / dd, np.float32(0)).astype(np.float32)
+    q = np.clip(np.trunc(b * inv[:, :, None] + np.float32(16.5)), 0, 31).astype(np.int64)
+    out = np.empty((rows, cols // 32, 22), np.uint8)
+    out[..., 0:2] = db
+    out[..., 2:6] = _qh_bits(q)
+    out[..., 6:] = ((q[..., :16] & 15) | ((q[..., 16:] & 15) << 4)).astype(np.uint8)
+    return out.reshape(rows, -1)
+
+
+def quantize_iq4_nl(w: np.ndarray) -> np.ndarray:
+    """fp32 -> IQ4_NL {fp16 d; nibbles}: d = max|w|/127, each value the
+    nearest code-book entry."""
+    rows, cols = w.shape
+    b = w.reshape(rows, cols // 32, 32).astype(np.float32)
+    d, db = _h16(np.abs(b).max(axis=2) / np.float32(127))
+    dd = d.astype(np.float32)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        t = np.where(dd[..., None] > 0, b / np.where(dd > 0, dd, 1)[..., None], 0)
+    q = np.abs(t[..., None] - IQ4_NL_VALUES.astype(np.float32)).argmin(axis=-1)
+    out = np.empty((rows, cols // 32, 18), np.uint8)
+    out[..., 0:2] = db
+    out[..., 2:] = (q[..., :16] | (q[..., 16:] << 4)).astype(np.uint8)
+    return out.reshape(rows, -1)
+
+
+def quantize_q2_k(w: np.ndarray) -> np.ndarray:
+    """fp32 -> Q2_K {scales[16]; qs[64]; fp16 d, dmin}: per 16-element group
+    scale (max-min)/3 and offset -min as 4-bit multiples of d and dmin,
+    2-bit codes at the byte and shift dequantize_row_q2_K reads
+    (llama3pure-c-engine.c:748-784)."""
+    rows, cols = w.shape
+    nsb = cols // 256
+    b = w.reshape(rows, nsb, 16, 16).astype(np.float32)
+    mn = np.minimum(b.min(axis=3), 0)
+    scale, off = (b.max(axis=3) - mn) / np.float32(3), -mn
+    d, db = _h16(scale.max(axis=2) / np.float32(15))
+    dmin, dmb = _h16(off.max(axis=2) / np.float32(15))
+    dd, dm = d.astype(np.float32), dmin.astype(np.float32)
+    sc = _round_div(scale, dd[..., None], 0, 15)
+    m = _round_div(off, dm[..., None], 0, 15)
+    u = _round_div(b + (dm[..., None] * m)[..., None], (dd[..., None] * sc)[..., None], 0, 3)
+    u = u.reshape(rows, nsb, 2, 4, 2, 16)          # group g = 8*half + 2*j + second
+    qs = sum(u[:, :, :, j] << (2 * j) for j in range(4))   # [rows, nsb, half, second, l]
+    out = np.empty((rows, nsb, 84), np.uint8)
+    out[..., 0:16] = (sc | (m << 4)).astype(np.uint8)
+    out[..., 16:80] = qs.reshape(rows, nsb, 64).astype(np.uint8)
+    out[..., 80:82], out[..., 82:84] = db, dmb
+    return out.reshape(rows, -1)
+
+
+def quantize_q3_k(w: np.ndarray) -> np.ndarray:
+    """fp32 -> Q3_K {hmask[32]; qs[64]; scales[12]; fp16 d}: per 16-element
+    group scale max|w|/4 stored as 32 + a 5-bit multiple of d, values in
+    [-4, 3] as 2 low bits in qs and a high bit (set for v >= 0) in hmask
+    (llama3pure-c-engine.c:786-832)."""
+    rows, cols = w.shape
+    nsb = cols // 256
+    b = w.reshape(rows, nsb, 16, 16).astype(np.float32)
+    s = np.abs(b).max(axis=3) / np.float32(4)
+    d, db = _h16(s.max(axis=2) / np.float32(31))
+    dd = d.astype(np.float32)
+    sv = _round_div(s, dd[..., None], 0, 31) + 32                 # 6-bit scale codes
+    ds = dd[..., None] * (sv - 32)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        v = np.where(ds[..., None] > 0, np.rint(b / np.where(ds > 0, ds, 1)[..., None]), 0)
+    v = np.clip(v, -4, 3).astype(np.int64)
+    q2 = np.where(v >= 0, v, v + 4).reshape(rows, nsb, 2, 4, 2, 16)
+    h = (v >= 0).astype(np.int64).reshape(rows, nsb, 2, 4, 2, 16)
+    qs = sum(q2[:, :, :, j] << (2 * j) for j in range(4))                       # [.., half, second, l]
+    hm = sum(h[:, :, half, j] << (4 * half + j) for half in range(2) for j in range(4))   # [.., second, l]
+    sc = np.empty((rows, nsb, 12), np.int64)
+    sc[..., 0:8] = (sv[..., 0:8] & 15) | ((sv[..., 8:16] & 15) << 4)
+    sc[..., 8:12] = sum(((sv[..., 4 * k:4 * k + 4] >> 4) & 3) << (2 * k) for k in range(4))
+    out = np.empty((rows, nsb, 110), np.uint8)
+    out[..., 0:32] = hm.reshape(rows, nsb, 32).astype(np.uint8)
+    out[..., 32:96] = qs.reshape(rows, nsb, 64).astype(np.uint8)
+    out[..., 96:108] = sc.astype(np.uint8)
+    out[..., 108:110] = db
+    return out.reshape(rows, -1)
+
+
+def quantize_q5_k(w: np.ndarray) -> np.ndarray:
+    """fp32 -> Q5_K {fp16 d, dmin; scales[12]; qh[32]; qs[128]}: the Q4_K
+    min/max quantizer with 32 levels, bit 4 of sub-block k's codes in bit k
+    of qh (llama3pure-c-engine.c:834-871)."""
+    rows, cols = w.shape
+    nsb = cols // 256
+    b = w.reshape(rows, nsb, 8, 32).astype(np.float32)
+    mn = np.minimum(b.min(axis=3), 0)
+    scale, off = (b.max(axis=3) - mn) / np.float32(31), -mn
+    d, db = _h16(scale.max(axis=2) / np.float32(63))
+    dmin, dmb = _h16(off.max(axis=2) / np.float32(63))
+    dd, dm = d.astype(np.float32), dmin.astype(np.float32)
+    sc = _round_div(scale, dd[..., None], 0, 63)
+    m = _round_div(off, dm[..., None], 0, 63)
+    q = _round_div(b + (dm[..., None] * m)[..., None], (dd[..., None] * sc)[..., None], 0, 31)
+    out = np.empty((rows, nsb, 176), np.uint8)
+    out[..., 0:2], out[..., 2:4] = db, dmb
+    out[..., 4:16] = _pack_k4_scales(sc, m)
+    out[..., 16:48] = sum(((q[:, :, k] >> 4) & 1) << k for k in range(8)).astype(np.uint8)
+    out[..., 48:] = ((q[:, :, 0::2] & 15) | ((q[:, :, 1::2] & 15) << 4)).reshape(rows, nsb, 128).astype(np.uint8)
+    return out.reshape(rows, -1)
+
+
 def quantize(w: np.ndarray, qtype: int) -> np.ndarray:
     if qtype == Q8_0:
         return quantize_q8_0(w)
@@ -176,6 +379,14 @@ def quantize(w: np.ndarray, qtype: int) -> np.ndarray:
         return quantize_q6_k(w)
     if qtype == F32:
         return np.ascontiguousarray(w, np.float32).view(np.uint8).reshape(w.shape[0], -1)
+    if qtype == F16:
+        return _f16_bytes(np.asarray(w, np.float32)).reshape(w.shape[0], -1)
+    if qtype == BF16:
+        return _bf16_bytes(np.asarray(w, np.float32)).reshape(w.shape[0], -1)
+    other = {Q4_1: quantize_q4_1, Q5_0: quantize_q5_0, Q5_1: quantize_q5_1, IQ4_NL: quantize_iq4_nl,
+             Q2_K: quantize_q2_k, Q3_K: quantize_q3_k, Q5_K: quantize_q5_k}
+    if qtype in other:
+        return other[qtype](w)
     raise ValueError(f"no weight quantizer for type {qtype}")
 
 

@@ -243,6 +243,82 @@ static void dq_q6_k(const uint8_t* s, float* y, int n) {          /* c:873-904 *
     }
 }
 
+/* Q2_K super-block {u8 scales[16]; u8 qs[64]; fp16 d, dmin} (c:165-170):
+ * 16 groups of 16 elements; group g has scale byte scales[g] (low nibble the
+ * scale, high nibble the min) and 2-bit codes from qs[32*(g/8) + 16*(g%2) + l]
+ * at bit shift 2*((g/2)%4).  y = (d*sc)*u - (dmin*m)  (c:748-784). */
+static void dq_q2_k(const uint8_t* s, float* y, int n) {
+    for (int b = 0; b < n / 256; b++, s += 84) {
+        const uint8_t* sc = s;
+        const uint8_t* qs = s + 16;
+        float d = h2f(s + 80), dmin = h2f(s + 82);
+        for (int g = 0; g < 16; g++) {
+            int half = g / 8, shift = 2 * ((g / 2) % 4), second = g % 2;
+            float dl = d * (float)(sc[g] & 0x0f), ml = dmin * (float)(sc[g] >> 4);
+            for (int l = 0; l < 16; l++) {
+                int u = (qs[32 * half + 16 * second + l] >> shift) & 3;
+                y[256 * b + 16 * g + l] = dl * (float)u - ml;
+            }
+        }
+    }
+}
+
+/* The 16 six-bit scales of a Q3_K super-block from its 12 packed bytes
+ * (c:802-806): scale i has its low 4 bits in byte i (low nibble) for i < 8
+ * or byte i - 8 (high nibble) for i >= 8, and its high 2 bits in byte
+ * 8 + i%4 at bit 2*(i/4). */
+static int q3k_scale(const uint8_t* p, int i) {
+    int lo = i < 8 ? (p[i] & 0x0f) : (p[i - 8] >> 4);
+    int hi = (p[8 + (i % 4)] >> (2 * (i / 4))) & 3;
+    return lo | (hi << 4);
+}
+
+/* Q3_K super-block {u8 hmask[32]; u8 qs[64]; u8 scales[12]; fp16 d}
+ * (c:172-178): group g of 16 elements uses qs and the shift as in Q2_K, the
+ * high bit hmask[16*(g%2) + l] bit (4*(g/8) + (g/2)%4), value
+ * u - (bit ? 0 : 4), scale d*(s_g - 32)  (c:786-832). */
+static void dq_q3_k(const uint8_t* s, float* y, int n) {
+    for (int b = 0; b < n / 256; b++, s += 110) {
+        const uint8_t* hm = s;
+        const uint8_t* qs = s + 32;
+        const uint8_t* scp = s + 96;
+        float d = h2f(s + 108);
+        for (int g = 0; g < 16; g++) {
+            int half = g / 8, j = (g / 2) % 4, second = g % 2;
+            float dl = d * (float)(q3k_scale(scp, g) - 32);
+            int bit = 4 * half + j;
+            for (int l = 0; l < 16; l++) {
+                int u = (qs[32 * half + 16 * second + l] >> (2 * j)) & 3;
+                int h = (hm[16 * second + l] >> bit) & 1;
+                y[256 * b + 16 * g + l] = dl * (float)(u - (h ? 0 : 4));
+            }
+        }
+    }
+}
+
+/* Q5_K super-block {fp16 d, dmin; u8 scales[12]; u8 qh[32]; u8 qs[128]}
+ * (c:180-187): sub-block k (32 elements) is the low (k even) or high nibble
+ * of qs[32*(k/2) + l] plus 16 * bit k of qh[l], with the Q4_K 6-bit scale and
+ * min k: y = (d*sc)*q - (dmin*m)  (c:834-871). */
+static void dq_q5_k(const uint8_t* s, float* y, int n) {
+    for (int b = 0; b < n / 256; b++, s += 176) {
+        float d = h2f(s), dmin = h2f(s + 2);
+        const uint8_t* sc = s + 4;
+        const uint8_t* qh = s + 16;
+        const uint8_t* qs = s + 48;
+        for (int k = 0; k < 8; k++) {
+            int scv, mnv;
+            k4_scale_min(k, sc, &scv, &mnv);
+            float dk = d * (float)scv, mk = dmin * (float)mnv;
+            for (int l = 0; l < 32; l++) {
+                int nib = (k & 1) ? (qs[32 * (k / 2) + l] >> 4) : (qs[32 * (k / 2) + l] & 0x0f);
+                int q = nib + (((qh[l] >> k) & 1) ? 16 : 0);
+                y[256 * b + 32 * k + l] = dk * (float)q - mk;
+            }
+        }
+    }
+}
+
 static const int8_t k_iq4nl[16] = {-127, -104, -83, -65, -49, -35, -22, -10,
                                    1,    13,   25,  38,  53,  69,  89,  113};   /* c:204-206 */
 
@@ -270,7 +346,10 @@ int l3o_dequant_row(int type, const void* src, float* dst, int n) {   /* c:1003-
     case L3O_Q5_0: dq_q5_0(s, dst, n); return 0;
     case L3O_Q5_1: dq_q5_1(s, dst, n); return 0;
     case L3O_Q8_0: dq_q8_0(s, dst, n); return 0;
+    case L3O_Q2_K: dq_q2_k(s, dst, n); return 0;
+    case L3O_Q3_K: dq_q3_k(s, dst, n); return 0;
     case L3O_Q4_K: dq_q4_k(s, dst, n); return 0;
+    case L3O_Q5_K: dq_q5_k(s, dst, n); return 0;
     case L3O_Q6_K: dq_q6_k(s, dst, n); return 0;
     case L3O_IQ4_NL: dq_iq4_nl(s, dst, n); return 0;
     default: return -1;
@@ -326,6 +405,78 @@ static float dot_q4_0_q8_0(const uint8_t* xq, const uint8_t* w, int n) {
     return sum;
 }
 
+/* Q8_0 activation against one Q4_1 row (c:1646-1665): per block the exact
+ * integer dots isum = sum xq*u and xsum = sum xq, then
+ * sum += dw*dx*isum + mw*dx*xsum. */
+static float dot_q4_1_q8_0(const uint8_t* xq, const uint8_t* w, int n) {
+    float sum = 0.0f;
+    for (int b = 0; b < n / 32; b++, w += 20, xq += 34) {
+        float dw = h2f(w), mw = h2f(w + 2), dx = h2f(xq);
+        const int8_t* xs = (const int8_t*)(xq + 2);
+        int isum = 0, xsum = 0;
+        for (int j = 0; j < 16; j++) {
+            isum += xs[j] * (w[4 + j] & 0x0f) + xs[j + 16] * (w[4 + j] >> 4);
+            xsum += xs[j] + xs[j + 16];
+        }
+        sum += dw * dx * (float)isum + mw * dx * (float)xsum;
+    }
+    return sum;
+}
+
+/* The 5-bit code of element j (< 32) of a Q5_0 / Q5_1 block: nibble of
+ * qs[j % 16] (low for j < 16) and bit j of the 32-bit qh. */
+static int q5_code(const uint8_t* qh4, const uint8_t* qs, int j) {
+    uint32_t qh = (uint32_t)qh4[0] | ((uint32_t)qh4[1] << 8) | ((uint32_t)qh4[2] << 16) | ((uint32_t)qh4[3] << 24);
+    int nib = j < 16 ? (qs[j] & 0x0f) : (qs[j - 16] >> 4);
+    return nib | (int)(((qh >> j) & 1u) << 4);
+}
+
+/* Q8_0 activation against one Q5_0 row (c:1668-1690): isum = sum xq*(u-16),
+ * sum += dw*dx*isum. */
+static float dot_q5_0_q8_0(const uint8_t* xq, const uint8_t* w, int n) {
+    float sum = 0.0f;
+    for (int b = 0; b < n / 32; b++, w += 22, xq += 34) {
+        float dw = h2f(w), dx = h2f(xq);
+        const int8_t* xs = (const int8_t*)(xq + 2);
+        int isum = 0;
+        for (int j = 0; j < 32; j++) isum += xs[j] * (q5_code(w + 2, w + 6, j) - 16);
+        sum += dw * dx * (float)isum;
+    }
+    return sum;
+}
+
+/* Q8_0 activation against one Q5_1 row (c:1693-1717): isum = sum xq*u,
+ * xsum = sum xq, sum += dw*dx*isum + mw*dx*xsum. */
+static float dot_q5_1_q8_0(const uint8_t* xq, const uint8_t* w, int n) {
+    float sum = 0.0f;
+    for (int b = 0; b < n / 32; b++, w += 24, xq += 34) {
+        float dw = h2f(w), mw = h2f(w + 2), dx = h2f(xq);
+        const int8_t* xs = (const int8_t*)(xq + 2);
+        int isum = 0, xsum = 0;
+        for (int j = 0; j < 32; j++) {
+            isum += xs[j] * q5_code(w + 4, w + 8, j);
+            xsum += xs[j];
+        }
+        sum += dw * dx * (float)isum + mw * dx * (float)xsum;
+    }
+    return sum;
+}
+
+/* Q8_0 activation against one IQ4_NL row (c:1994-2011): the nibbles index
+ * the 16-value table, isum = sum xq*table[u], sum += dw*dx*isum. */
+static float dot_iq4_nl_q8_0(const uint8_t* xq, const uint8_t* w, int n) {
+    float sum = 0.0f;
+    for (int b = 0; b < n / 32; b++, w += 18, xq += 34) {
+        float dw = h2f(w), dx = h2f(xq);
+        const int8_t* xs = (const int8_t*)(xq + 2);
+        int isum = 0;
+        for (int j = 0; j < 16; j++)
+            isum += xs[j] * k_iq4nl[w[2 + j] & 0x0f] + xs[j + 16] * k_iq4nl[w[2 + j] >> 4];
+        sum += dw * dx * (float)isum;
+    }
+    return sum;
+}
+
 /* Integer dot of a Q8_0 activation against one Q8_0 row (c:1720-1736). */
 static float dot_q8_0_q8_0(const uint8_t* xq, const uint8_t* w, int n) {
     float sum = 0.0f;
@@ -340,10 +491,11 @@ static float dot_q8_0_q8_0(const uint8_t* xq, const uint8_t* w, int n) {
     return sum;
 }
 
-/* matmul_quantized (c:2091-2133): rows with a row dequantizer go through
- * matmul_deq_4row (c:2136-2176): dequantize to fp32 then a sequential fp32
- * dot `s += w[j]*x[j]`.  Q4_0 quantizes x to Q8_0 once and uses the integer
- * dot.  F32/F16/BF16 take the float dot (sequential, c:1470-1494). */
+/* matmul_quantized (c:2091-2133): rows with a row dequantizer (Q8_0, Q2_K
+ * .. Q6_K) go through matmul_deq_4row (c:2136-2176): dequantize to fp32 then
+ * a sequential fp32 dot `s += w[j]*x[j]`.  Q4_0, Q4_1, Q5_0, Q5_1 and IQ4_NL
+ * quantize x to Q8_0 once and use their integer block dots.  F32/F16/BF16
+ * take the float dot (sequential, c:1467-1494). */
 int l3o_matmul(int type, const void* w, int rows, int cols, const float* x, float* y) {
     const uint8_t* wb = (const uint8_t*)w;
     size_t rb = l3o_row_bytes(type, cols);
@@ -360,11 +512,14 @@ int l3o_matmul(int type, const void* w, int rows, int cols, const float* x, floa
         free(buf);
         return 0;
     }
-    if (type == L3O_Q4_0) {
+    if (type == L3O_Q4_0 || type == L3O_Q4_1 || type == L3O_Q5_0 || type == L3O_Q5_1 || type == L3O_IQ4_NL) {
+        float (*dot)(const uint8_t*, const uint8_t*, int) =
+            type == L3O_Q4_0 ? dot_q4_0_q8_0 : type == L3O_Q4_1 ? dot_q4_1_q8_0 :
+            type == L3O_Q5_0 ? dot_q5_0_q8_0 : type == L3O_Q5_1 ? dot_q5_1_q8_0 : dot_iq4_nl_q8_0;
         uint8_t* xq = (uint8_t*)malloc((size_t)(cols / 32) * 34);
         if (!xq) return -1;
         l3o_quantize_q8_0(x, xq, cols);
-        for (int r = 0; r < rows; r++) y[r] = dot_q4_0_q8_0(xq, wb + (size_t)r * rb, cols);
+        for (int r = 0; r < rows; r++) y[r] = dot(xq, wb + (size_t)r * rb, cols);
         free(xq);
         return 0;
     }
@@ -868,7 +1023,25 @@ void l3o_model_info(const l3o_model* m, int* o) {
     o[9] = m->swa_window; o[10] = m->swa_pattern;
 }
 
-static int is_q8_class(int type) { return type == L3O_Q4_0; }   /* q8_func && !deq_func, c:3221 */
+/* The Q8_0-activation dot the reference's matmul_quantized_preq8 (c:2275-2288)
+ * calls through a matrix's q8_func when the first matrix of its group (wq,
+ * or w1) takes the Q8_0 path; null for a type this restatement lacks. */
+typedef float (*q8dot_t)(const uint8_t*, const uint8_t*, int);
+static q8dot_t q8_dot_of(int type) {
+    switch (type) {
+    case L3O_Q4_0: return dot_q4_0_q8_0;
+    case L3O_Q4_1: return dot_q4_1_q8_0;
+    case L3O_Q5_0: return dot_q5_0_q8_0;
+    case L3O_Q5_1: return dot_q5_1_q8_0;
+    case L3O_Q8_0: return dot_q8_0_q8_0;
+    case L3O_IQ4_NL: return dot_iq4_nl_q8_0;
+    default: return 0;
+    }
+}
+
+static int is_q8_class(int type) {   /* q8_func && !deq_func, c:3221 */
+    return type == L3O_Q4_0 || type == L3O_Q4_1 || type == L3O_Q5_0 || type == L3O_Q5_1 || type == L3O_IQ4_NL;
+}
 
 static int mm(const qt_t* q, const float* x, float* y) {
     return l3o_matmul(q->type, q->data, q->rows, q->cols, x, y);
@@ -1004,9 +1177,9 @@ int l3o_forward(l3o_model* m, int token, int pos, int compute_logits, float* log
                 const qt_t* w = ws[i];
                 for (int r = 0; r < w->rows; r++) {
                     const uint8_t* row = w->data + (size_t)r * w->rb;
-                    if (w->type == L3O_Q4_0) outs[i][r] = dot_q4_0_q8_0(m->xq8, row, w->cols);
-                    else if (w->type == L3O_Q8_0) outs[i][r] = dot_q8_0_q8_0(m->xq8, row, w->cols);
-                    else return -2;
+                    q8dot_t dot = q8_dot_of(w->type);
+                    if (!dot) return -2;
+                    outs[i][r] = dot(m->xq8, row, w->cols);
                 }
             }
         } else {
@@ -1025,9 +1198,9 @@ int l3o_forward(l3o_model* m, int token, int pos, int compute_logits, float* log
                 const qt_t* w = ws[i];
                 for (int r = 0; r < w->rows; r++) {
                     const uint8_t* row = w->data + (size_t)r * w->rb;
-                    if (w->type == L3O_Q4_0) outs[i][r] = dot_q4_0_q8_0(m->xq8, row, w->cols);
-                    else if (w->type == L3O_Q8_0) outs[i][r] = dot_q8_0_q8_0(m->xq8, row, w->cols);
-                    else return -2;
+                    q8dot_t dot = q8_dot_of(w->type);
+                    if (!dot) return -2;
+                    outs[i][r] = dot(m->xq8, row, w->cols);
                 }
             }
         } else {

@@ -18,6 +18,26 @@ MODELS = {
     "llama_q4_k_m": dict(arch="llama", dim=512, hidden=1024, n_layers=4, n_heads=8, n_kv=2, vocab=2048, ctx=256,
                          qtype=synth.Q4_K, seed=4, norm_jitter=0.1,
                          qtypes={"ffn_down": synth.Q6_K, "attn_v": synth.Q6_K, "output": synth.Q6_K}),
+    # Q5_K_M-, Q3_K_M- and Q2_K-style mixes
+    "llama_q5_k_m": dict(arch="llama", dim=512, hidden=1024, n_layers=4, n_heads=8, n_kv=2, vocab=2048, ctx=256,
+                         qtype=synth.Q5_K, seed=5, norm_jitter=0.1,
+                         qtypes={"ffn_down": synth.Q6_K, "attn_v": synth.Q6_K, "output": synth.Q6_K}),
+    "llama_q3_k_m": dict(arch="llama", dim=512, hidden=1024, n_layers=4, n_heads=8, n_kv=2, vocab=2048, ctx=256,
+                         qtype=synth.Q3_K, seed=6, norm_jitter=0.1,
+                         qtypes={"ffn_down": synth.Q4_K, "attn_v": synth.Q5_K, "output": synth.Q6_K}),
+    "llama_q2_k": dict(arch="llama", dim=512, hidden=1024, n_layers=4, n_heads=8, n_kv=2, vocab=2048, ctx=256,
+                       qtype=synth.Q2_K, seed=7, norm_jitter=0.1,
+                       qtypes={"ffn_down": synth.Q3_K, "attn_v": synth.Q3_K, "output": synth.Q6_K}),
+    # the Q8_0-activation types: Q5_0 with Q5_1 V, Q4_1 down, IQ4_NL output
+    # projection (later keys win: "output" is also in "attn_output")
+    "llama_q5_0_mix": dict(arch="llama", dim=512, hidden=1024, n_layers=4, n_heads=8, n_kv=2, vocab=2048, ctx=256,
+                           qtype=synth.Q5_0, seed=8, norm_jitter=0.1,
+                           qtypes={"output": synth.Q8_0, "attn_v": synth.Q5_1, "ffn_down": synth.Q4_1,
+                                   "attn_output": synth.IQ4_NL}),
+    # half-precision weights: F16 with BF16 down and output projections
+    "llama_f16_bf16": dict(arch="llama", dim=512, hidden=1024, n_layers=4, n_heads=8, n_kv=2, vocab=2048, ctx=256,
+                           qtype=synth.F16, seed=9, norm_jitter=0.1,
+                           qtypes={"ffn_down": synth.BF16, "attn_output": synth.BF16}),
 }
 
 
@@ -37,6 +57,18 @@ SINGLE_LAYER = {
     "gemma_q8_0_1152": dict(qtype=synth.Q8_0, dim=1152, hidden=1536, n_heads=4, n_kv=1, **_GEMMA),
     "llama_q4_0_640": dict(qtype=synth.Q4_0, dim=640, hidden=2048, n_heads=5, n_kv=1),
     "llama_q6_k_768": dict(qtype=synth.Q6_K, dim=768, hidden=1280, n_heads=6, n_kv=2),
+    # every other weight type on its own, at widths that are not multiples of
+    # a 2048-element chunk (and for Q4_1 / Q5_0 / Q5_1 / IQ4_NL / Q2_K / Q3_K,
+    # rows that are not 16-byte multiples)
+    "llama_q4_1_1120": dict(qtype=synth.Q4_1, dim=1120, hidden=1440, n_heads=5, n_kv=1),     # head size 224
+    "llama_q5_0_1152": dict(qtype=synth.Q5_0, dim=1152, hidden=1536, n_heads=9, n_kv=3),
+    "llama_q5_1_1120": dict(qtype=synth.Q5_1, dim=1120, hidden=1440, n_heads=5, n_kv=5),
+    "llama_iq4_nl_640": dict(qtype=synth.IQ4_NL, dim=640, hidden=2048, n_heads=5, n_kv=1),
+    "llama_q2_k_2304": dict(qtype=synth.Q2_K, dim=2304, hidden=1280, n_heads=18, n_kv=6),
+    "llama_q3_k_2304": dict(qtype=synth.Q3_K, dim=2304, hidden=1280, n_heads=18, n_kv=6),
+    "llama_q5_k_768": dict(qtype=synth.Q5_K, dim=768, hidden=1280, n_heads=6, n_kv=2),
+    "llama_f16_640": dict(qtype=synth.F16, dim=640, hidden=1536, n_heads=5, n_kv=1),
+    "llama_bf16_640": dict(qtype=synth.BF16, dim=640, hidden=1536, n_heads=5, n_kv=1),
 }
 SINGLE_TOKENS = (0, 7, 1234, 42, 555, 1000, 1999, 2047)
 

@@ -6,10 +6,13 @@ fp32 summation tolerance of the float64 value of the reference arithmetic:
     |y_gpu - y64| <= gamma_(K+4) * S,   gamma_n = n u / (1 - n u), u = 2^-24
 
 where S bounds the magnitudes summed by either side:
-    Q8_0:  S = sum_j |w_j x_j|
-    Q4_0:  S = sum_blocks |dw dx isum|           (integer block dots are exact)
-    Q4_K:  S = sum_j (|d1 q_j| + |m1|) |x_j|     (kernel factors d1, m1 out of a sub-block)
-    Q6_K:  S = sum_j |d sc| (|q_j| + 32) |x_j|   (kernel factors d sc, offset 32)
+    Q8_0, F16, BF16:  S = sum_j |w_j x_j|
+    Q4_0, Q4_1, Q5_0, Q5_1, IQ4_NL:
+           S = sum_blocks |dw dx isum| (+ |mw dx xsum|)   (integer block dots are exact)
+    Q2_K, Q4_K, Q5_K:
+           S = sum_j (|d1 q_j| + |m1|) |x_j|   (kernel factors scale and min out of a group)
+    Q3_K:  S = sum_j |d s| (v_j + 4) |x_j|     (code v in 0..7, offset 4)
+    Q6_K:  S = sum_j |d sc| (|q_j| + 32) |x_j| (kernel factors d sc, offset 32)
 and the oracle itself must satisfy the same bound.
 """
 import numpy as np
@@ -17,6 +20,7 @@ import pytest
 
 import llama3pure_amd as l3p
 import oracle
+from block_math import kquant_magnitudes, q8_block_terms
 from llama3pure_amd import synth
 
 pytestmark = pytest.mark.gpu
@@ -36,8 +40,8 @@ def empty_f32(torch, n):
 
 
 # --------------------------------------------------------------------------- dequant / quantize
-@pytest.mark.parametrize("qtype", [l3p.Q8_0, l3p.Q4_0, l3p.Q4_1, l3p.Q5_0, l3p.Q5_1, l3p.Q4_K, l3p.Q6_K,
-                                   l3p.IQ4_NL, l3p.F16, l3p.BF16, l3p.F32])
+@pytest.mark.parametrize("qtype", [l3p.Q8_0, l3p.Q4_0, l3p.Q4_1, l3p.Q5_0, l3p.Q5_1, l3p.Q2_K, l3p.Q3_K, l3p.Q4_K,
+                                   l3p.Q5_K, l3p.Q6_K, l3p.IQ4_NL, l3p.F16, l3p.BF16, l3p.F32])
 def test_dequant_bit_exact(ctx, torch_gpu, cpuref, qtype):
     e, bb = oracle.BLOCK[qtype]
     n = 256 * 40
@@ -49,7 +53,13 @@ def test_dequant_bit_exact(ctx, torch_gpu, cpuref, qtype):
     ctx.dequant(qtype, d, n, out)
     ctx.synchronize()
     want = cpuref.dequant(qtype, raw, n)
-    assert np.array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32))
+    got = out.cpu().numpy()
+    # random bytes include NaN fp16 scales: NaN outputs must match in place;
+    # their payload and sign (which the CPU and GPU propagate differently
+    # through a - b) are not compared
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
 
 
 def test_quantize_q8_0_bit_exact(ctx, torch_gpu, cpuref):
@@ -67,48 +77,21 @@ def test_quantize_q8_0_bit_exact(ctx, torch_gpu, cpuref):
 
 
 # --------------------------------------------------------------------------- GEMV
+Q8_ACT = (l3p.Q4_0, l3p.Q4_1, l3p.Q5_0, l3p.Q5_1, l3p.IQ4_NL)
+K_QUANTS = (l3p.Q2_K, l3p.Q3_K, l3p.Q4_K, l3p.Q5_K, l3p.Q6_K)
+
+
 def _bound_terms(cpuref, qtype, w, rows, cols, x):
     """(y64, S) of the reference arithmetic in float64, per the module doc."""
     x64 = x.astype(np.float64)
-    if qtype == l3p.Q4_0:
-        xq = cpuref.quantize_q8_0(x).reshape(-1, 34)
-        dx = xq[:, 0:2].copy().view(np.float16).astype(np.float64)[:, 0]
-        qx = xq[:, 2:].view(np.int8).astype(np.int64)
-        wb = w.reshape(rows, -1, 18)
-        dw = wb[:, :, 0:2].copy().view(np.float16).astype(np.float64)[:, :, 0]
-        nib = np.concatenate([(wb[:, :, 2:] & 15), (wb[:, :, 2:] >> 4)], axis=2).astype(np.int64) - 8
-        terms = dw * dx[None] * np.einsum("rbj,bj->rb", nib, qx)
+    if qtype in Q8_ACT:
+        terms = q8_block_terms(cpuref, qtype, w, rows, cols, x)
         return terms.sum(1), np.abs(terms).sum(1)
     W = np.stack([cpuref.dequant(qtype, w[r], cols) for r in range(rows)]).astype(np.float64)
     y64 = W @ x64
-    if qtype == l3p.Q8_0:
-        return y64, np.abs(W) @ np.abs(x64)
-    if qtype == l3p.Q4_K:
-        # |d1 q| + |m1| per element, from the block fields
-        wb = w.reshape(rows, -1, 144)
-        d = wb[:, :, 0:2].copy().view(np.float16).astype(np.float64)[:, :, 0]
-        dmin = wb[:, :, 2:4].copy().view(np.float16).astype(np.float64)[:, :, 0]
-        s = wb[:, :, 4:16].astype(np.int64)
-        A = np.empty((rows, cols))
-        for j in range(8):
-            if j < 4:
-                sc, m = s[:, :, j] & 63, s[:, :, j + 4] & 63
-            else:
-                sc = (s[:, :, j + 4] & 15) | ((s[:, :, j - 4] >> 6) << 4)
-                m = (s[:, :, j + 4] >> 4) | ((s[:, :, j] >> 6) << 4)
-            q = wb[:, :, 16 + 32 * (j // 2): 48 + 32 * (j // 2)].astype(np.int64)
-            q = (q >> 4) if j % 2 else (q & 15)
-            a = np.abs(d * sc)[:, :, None] * q + np.abs(dmin * m)[:, :, None]
-            A.reshape(rows, -1, 8, 32)[:, :, j, :] = a
-        return y64, A @ np.abs(x64)
-    if qtype == l3p.Q6_K:
-        wb = w.reshape(rows, -1, 210)
-        d = wb[:, :, 208:210].copy().view(np.float16).astype(np.float64)[:, :, 0]
-        sc = wb[:, :, 192:208].view(np.int8).astype(np.float64)
-        # |d sc| (|q| + 32) <= |d sc| * 95
-        A = np.repeat(np.abs(d[:, :, None] * sc), 16, axis=2).reshape(rows, cols) * 95.0
-        return y64, A @ np.abs(x64)
-    raise ValueError(qtype)
+    if qtype in K_QUANTS:
+        return y64, kquant_magnitudes(qtype, w, rows, cols) @ np.abs(x64)
+    return y64, np.abs(W) @ np.abs(x64)
 
 
 def _check_gemv(ctx, torch, cpuref, qtype, rows, cols, seed=0, sample_rows=None):
@@ -158,6 +141,29 @@ def _check_gemv(ctx, torch, cpuref, qtype, rows, cols, seed=0, sample_rows=None)
     (l3p.Q4_K, 2304, 2304),
     (l3p.Q4_K, 100, 256),
     (l3p.Q4_K, 4096, 14336),
+    # the other types: a full-width shape, a partial last chunk, and rows
+    # that are not 16-byte multiples where the type allows them
+    (l3p.Q4_1, 2048, 4096),
+    (l3p.Q4_1, 700, 1120),         # 700 B rows
+    (l3p.Q5_0, 2048, 4096),
+    (l3p.Q5_0, 999, 1152),         # 792 B rows
+    (l3p.Q5_1, 1024, 14336),
+    (l3p.Q5_1, 515, 1120),         # 840 B rows
+    (l3p.IQ4_NL, 2048, 4096),
+    (l3p.IQ4_NL, 333, 160),
+    (l3p.Q2_K, 2048, 4096),
+    (l3p.Q2_K, 1000, 2304),        # 756 B rows
+    (l3p.Q3_K, 2048, 4096),
+    (l3p.Q3_K, 1000, 2304),        # 990 B rows
+    (l3p.Q3_K, 301, 256),
+    (l3p.Q5_K, 2048, 4096),
+    (l3p.Q5_K, 777, 2304),
+    (l3p.F16, 1024, 4096),
+    (l3p.F16, 200, 9216),
+    (l3p.F16, 64, 32768),          # 16 chunk columns: two buffers per wave
+    (l3p.BF16, 1024, 4096),
+    (l3p.BF16, 99, 288),
+    (l3p.BF16, 65, 30720),
 ])
 def test_gemv_parity(ctx, torch_gpu, cpuref, qtype, rows, cols):
     _check_gemv(ctx, torch_gpu, cpuref, qtype, rows, cols, seed=rows + cols, sample_rows=min(rows, 768))
@@ -168,7 +174,8 @@ def test_gemv_q6_k_lm_head_shape(ctx, torch_gpu, cpuref):
     _check_gemv(ctx, torch_gpu, cpuref, l3p.Q6_K, 128256, 4096, seed=9, sample_rows=512)
 
 
-@pytest.mark.parametrize("qtype", [l3p.Q8_0, l3p.Q4_0, l3p.Q4_K, l3p.Q6_K])
+@pytest.mark.parametrize("qtype", [l3p.Q8_0, l3p.Q4_0, l3p.Q5_1, l3p.IQ4_NL, l3p.Q3_K, l3p.Q4_K, l3p.Q6_K,
+                                   l3p.BF16])
 @pytest.mark.parametrize("rows", [1, 3, 5, 7, 9, 4097])
 def test_gemv_ragged_rows(ctx, torch_gpu, cpuref, qtype, rows):
     cols = 2048 if qtype == l3p.Q6_K else 512
@@ -183,7 +190,7 @@ def test_gemv_zero_rows_and_errors(ctx, torch_gpu):
         ctx.gemv(l3p.Q8_0, 0, 8, 500, x, y)          # cols not a block multiple
     assert e.value.code == l3p.E_INVALID
     with pytest.raises(l3p.L3PError) as e:
-        ctx.gemv(l3p.Q4_1, 0, 8, 512, x, y)          # type without a GEMV kernel
+        ctx.gemv(l3p.F32, 0, 8, 512, x, y)           # type without a GEMV kernel
     assert e.value.code == l3p.E_UNSUPPORTED
     with pytest.raises(l3p.L3PError) as e:
         ctx.gemv(l3p.Q8_0, 0, 8, 512, x, y)          # null weight pointer
@@ -201,10 +208,12 @@ def test_gemv_deterministic(ctx, torch_gpu):
     assert torch_gpu.equal(y1, y2)
 
 
-def test_gemm_q4_0_equals_gemv_rows(ctx, torch_gpu):
-    """Q4_0 batches run the GEMV per row (the reference's integer Q8_0-activation
-    dot, c:2305-2318): per batch element exactly the GEMV result."""
-    qtype, rows, cols, batch = l3p.Q4_0, 1024, 2048, 7
+@pytest.mark.parametrize("qtype", Q8_ACT)
+def test_gemm_q8_activation_equals_gemv_rows(ctx, torch_gpu, qtype):
+    """Batches of the Q8_0-activation types run the GEMV per row (the
+    reference's integer Q8_0-activation dot, c:2305-2318): per batch element
+    exactly the GEMV result."""
+    rows, cols, batch = 1024, 2048, 7
     w = dev(torch_gpu, synth.random_blocks(qtype, rows, cols, seed=5))
     xb = synth.random_x(cols, seed=6, batch=batch)
     xd = dev(torch_gpu, xb)
@@ -221,31 +230,12 @@ def test_gemm_q4_0_equals_gemv_rows(ctx, torch_gpu):
 
 def _dequant_bound(cpuref, qtype, w, rows, cols):
     """(W, A): the exact dequantized weights in float64 and the per-element
-    magnitudes whose products with |x| bound either side's fp32 sums (module doc)."""
+    magnitudes whose products with |x| bound either side's fp32 sums (module
+    doc; the GEMM forms the exact w = d1 q - m1, which A also bounds)."""
     W = np.stack([cpuref.dequant(qtype, w[r], cols) for r in range(rows)]).astype(np.float64)
-    if qtype == l3p.Q8_0:
-        return W, np.abs(W)
-    if qtype == l3p.Q6_K:
-        wb = w.reshape(rows, -1, 210)
-        d = wb[:, :, 208:210].copy().view(np.float16).astype(np.float64)[:, :, 0]
-        sc = wb[:, :, 192:208].view(np.int8).astype(np.float64)
-        return W, np.repeat(np.abs(d[:, :, None] * sc), 16, axis=2).reshape(rows, cols) * 95.0
-    # Q4_K: |d1 q| + |m1| (see _bound_terms); the GEMM forms exact w = d1 q - m1, which this also bounds
-    wb = w.reshape(rows, -1, 144)
-    d = wb[:, :, 0:2].copy().view(np.float16).astype(np.float64)[:, :, 0]
-    dmin = wb[:, :, 2:4].copy().view(np.float16).astype(np.float64)[:, :, 0]
-    sb = wb[:, :, 4:16].astype(np.int64)
-    A = np.empty((rows, cols))
-    for j in range(8):
-        if j < 4:
-            sc, m = sb[:, :, j] & 63, sb[:, :, j + 4] & 63
-        else:
-            sc = (sb[:, :, j + 4] & 15) | ((sb[:, :, j - 4] >> 6) << 4)
-            m = (sb[:, :, j + 4] >> 4) | ((sb[:, :, j] >> 6) << 4)
-        q = wb[:, :, 16 + 32 * (j // 2): 48 + 32 * (j // 2)].astype(np.int64)
-        q = (q >> 4) if j % 2 else (q & 15)
-        A.reshape(rows, -1, 8, 32)[:, :, j, :] = np.abs(d * sc)[:, :, None] * q + np.abs(dmin * m)[:, :, None]
-    return W, A
+    if qtype in K_QUANTS:
+        return W, kquant_magnitudes(qtype, w, rows, cols)
+    return W, np.abs(W)
 
 
 @pytest.mark.parametrize("qtype,rows,cols,batch", [
@@ -256,6 +246,11 @@ def _dequant_bound(cpuref, qtype, w, rows, cols):
     (l3p.Q8_0, 77, 14336, 1),
     (l3p.Q4_K, 1000, 2304, 17),
     (l3p.Q6_K, 513, 1536, 40),
+    (l3p.Q2_K, 300, 2304, 9),
+    (l3p.Q3_K, 260, 1024, 66),
+    (l3p.Q5_K, 1000, 2304, 17),
+    (l3p.F16, 130, 320, 5),
+    (l3p.BF16, 257, 2048, 64),
 ])
 def test_gemm_mfma_parity(ctx, torch_gpu, cpuref, qtype, rows, cols, batch):
     """MFMA GEMM against the float64 value of the reference's dequantize-then-

@@ -29,6 +29,27 @@ CASES = {
     "llama_q4_k_m": dict(arch="llama", dim=256, hidden=512, n_layers=2, n_heads=8, n_kv=2, vocab=512, ctx=128,
                          qtype=synth.Q4_K, seed=4, norm_jitter=0.1,
                          qtypes={"ffn_down": synth.Q6_K, "attn_v": synth.Q6_K, "output": synth.Q6_K}),
+    # the other K-quants: Q5_K_M-, Q3_K_M- and Q2_K-style mixes
+    "llama_q5_k_m": dict(arch="llama", dim=256, hidden=512, n_layers=2, n_heads=8, n_kv=2, vocab=512, ctx=128,
+                         qtype=synth.Q5_K, seed=5, norm_jitter=0.1,
+                         qtypes={"ffn_down": synth.Q6_K, "attn_v": synth.Q6_K, "output": synth.Q6_K}),
+    "llama_q3_k_m": dict(arch="llama", dim=256, hidden=512, n_layers=2, n_heads=8, n_kv=2, vocab=512, ctx=128,
+                         qtype=synth.Q3_K, seed=6, norm_jitter=0.1,
+                         qtypes={"ffn_down": synth.Q4_K, "attn_v": synth.Q5_K, "output": synth.Q6_K}),
+    "llama_q2_k": dict(arch="llama", dim=256, hidden=512, n_layers=2, n_heads=8, n_kv=2, vocab=512, ctx=128,
+                       qtype=synth.Q2_K, seed=7, norm_jitter=0.1,
+                       qtypes={"ffn_down": synth.Q3_K, "attn_v": synth.Q3_K, "output": synth.Q6_K}),
+    # the Q8_0-activation types (Q5_0 with Q5_1 V, Q4_1 down, IQ4_NL output
+    # projection) and the half-precision types
+    "llama_q5_0_mix": dict(arch="llama", dim=256, hidden=512, n_layers=2, n_heads=8, n_kv=2, vocab=512, ctx=128,
+                           qtype=synth.Q5_0, seed=8, norm_jitter=0.1,
+                           qtypes={"output": synth.Q8_0, "attn_v": synth.Q5_1, "ffn_down": synth.Q4_1,
+                                   "attn_output": synth.IQ4_NL}),   # later keys win ("output" is in "attn_output")
+    "llama_f16_bf16": dict(arch="llama", dim=256, hidden=512, n_layers=2, n_heads=8, n_kv=2, vocab=512, ctx=128,
+                           qtype=synth.F16, seed=9, norm_jitter=0.1,
+                           qtypes={"ffn_down": synth.BF16, "attn_output": synth.BF16}),
+    "gemma_bf16": dict(arch="gemma3", dim=256, hidden=768, n_layers=7, n_heads=4, n_kv=2, head_dim=64, vocab=512,
+                       ctx=128, qtype=synth.BF16, seed=10, softcap=30.0, swa_window=12, norm_jitter=0.1, tied=True),
 }
 
 

@@ -10,6 +10,7 @@ import numpy as np
 import pytest
 
 import oracle
+from block_math import codes_32
 from llama3pure_amd import synth
 
 ALL16 = np.arange(65536, dtype=np.uint32).astype(np.uint16)
@@ -146,7 +147,93 @@ def _exact_dequant_block(qtype, blk):
                     ds = _mul(d, dn, Fraction(c), c < 0)
                     out[128 * half + 32 * g + l] = _mul(*ds, Fraction(q[g] - 32), q[g] < 32)
         return out
+    if qtype in (oracle.Q4_1, oracle.Q5_1):
+        # y = q*d + m: q*d is exact, the sum rounds once
+        d, dn = _fp16(blk[0:2]), _neg16(blk[0:2])
+        m, mn = _fp16(blk[2:4]), _neg16(blk[2:4])
+        if qtype == oracle.Q4_1:
+            q = [blk[4 + j] & 15 for j in range(16)] + [blk[4 + j] >> 4 for j in range(16)]
+        else:
+            qh = blk[4] | (blk[5] << 8) | (blk[6] << 16) | (blk[7] << 24)
+            q = [(blk[8 + j] & 15) | (((qh >> j) & 1) << 4) for j in range(16)] + \
+                [(blk[8 + j] >> 4) | (((qh >> (j + 16)) & 1) << 4) for j in range(16)]
+        return [_add(*_mul(Fraction(v), False, d, dn), m, mn) for v in q]
+    if qtype == oracle.Q5_0:
+        d, dn = _fp16(blk[0:2]), _neg16(blk[0:2])
+        qh = blk[2] | (blk[3] << 8) | (blk[4] << 16) | (blk[5] << 24)
+        q = [(blk[6 + j] & 15) | (((qh >> j) & 1) << 4) for j in range(16)] + \
+            [(blk[6 + j] >> 4) | (((qh >> (j + 16)) & 1) << 4) for j in range(16)]
+        return [_mul(Fraction(v - 16), v < 16, d, dn) for v in q]
+    if qtype == oracle.IQ4_NL:
+        d, dn = _fp16(blk[0:2]), _neg16(blk[0:2])
+        q = [synth.IQ4_NL_VALUES[blk[2 + j] & 15] for j in range(16)] + \
+            [synth.IQ4_NL_VALUES[blk[2 + j] >> 4] for j in range(16)]
+        return [_mul(d, dn, Fraction(int(v)), v < 0) for v in q]
+    if qtype == oracle.Q2_K:
+        # 16 groups of 16: group g = 8*half + 2*j + second, 2-bit codes of
+        # qs[32*half + 16*second + l] at bit 2*j; y = (d*(s&15))*u - dmin*(s>>4)
+        d, dn = _fp16(blk[80:82]), _neg16(blk[80:82])
+        dmin, mn = _fp16(blk[82:84]), _neg16(blk[82:84])
+        out = []
+        for g in range(16):
+            half, j, second = g // 8, (g // 2) % 4, g % 2
+            sc = blk[g]
+            for l in range(16):
+                u = (blk[16 + 32 * half + 16 * second + l] >> (2 * j)) & 3
+                a, an = _mul(*_mul(d, dn, Fraction(sc & 15), False), Fraction(u), False)
+                b, bn = _mul(dmin, mn, Fraction(sc >> 4), False)
+                out.append(_sub(a, an, b, bn))
+        return out
+    if qtype == oracle.Q3_K:
+        # 16 groups as Q2_K, value u - 4 unless bit 4*half + j of
+        # hmask[16*second + l] is set, scale d*(s_g - 32) with s_g the 6-bit
+        # field: low 4 bits from byte g (g < 8) or the high nibble of byte
+        # g - 8, high 2 bits from byte 8 + g%4 at bit 2*(g/4)
+        d, dn = _fp16(blk[108:110]), _neg16(blk[108:110])
+        sb = blk[96:108]
+        out = []
+        for g in range(16):
+            half, j, second = g // 8, (g // 2) % 4, g % 2
+            lo = (sb[g] & 15) if g < 8 else (sb[g - 8] >> 4)
+            sg = (lo | (((sb[8 + g % 4] >> (2 * (g // 4))) & 3) << 4)) - 32
+            ds = _mul(d, dn, Fraction(sg), sg < 0)
+            for l in range(16):
+                u = (blk[32 + 32 * half + 16 * second + l] >> (2 * j)) & 3
+                h = (blk[16 * second + l] >> (4 * half + j)) & 1
+                v = u - (0 if h else 4)
+                out.append(_mul(*ds, Fraction(v), v < 0))
+        return out
+    if qtype == oracle.Q5_K:
+        d, dn = _fp16(blk[0:2]), _neg16(blk[0:2])
+        dmin, mn = _fp16(blk[2:4]), _neg16(blk[2:4])
+        s = blk[4:16]
+        out = []
+        for k in range(8):
+            if k < 4:
+                sc, m = s[k] & 63, s[k + 4] & 63
+            else:
+                sc = (s[k + 4] & 0xF) | ((s[k - 4] >> 6) << 4)
+                m = (s[k + 4] >> 4) | ((s[k] >> 6) << 4)
+            for l in range(32):
+                byte = blk[48 + 32 * (k // 2) + l]
+                q = ((byte >> 4) if k % 2 else (byte & 15)) + 16 * ((blk[16 + l] >> k) & 1)
+                a, an = _mul(*_mul(d, dn, Fraction(sc), False), Fraction(q), False)
+                b, bn = _mul(dmin, mn, Fraction(m), False)
+                out.append(_sub(a, an, b, bn))
+        return out
     raise ValueError(qtype)
+
+
+def _add(a, an, b, bn):
+    """Exact a + b with the IEEE sign of a zero sum (-0 only for -0 + -0)."""
+    v = a + b
+    return v, v == 0 and a == 0 and b == 0 and an and bn
+
+
+def _sub(a, an, b, bn):
+    """Exact a - b with the IEEE sign of a zero result (-0 only for -0 - +0)."""
+    v = a - b
+    return v, v == 0 and a == 0 and b == 0 and an and not bn
 
 
 def _to_f32(vs):
@@ -154,10 +241,12 @@ def _to_f32(vs):
                     np.float32)
 
 
-@pytest.mark.parametrize("qtype", [oracle.Q8_0, oracle.Q4_0, oracle.Q4_K, oracle.Q6_K])
+@pytest.mark.parametrize("qtype", [oracle.Q8_0, oracle.Q4_0, oracle.Q4_1, oracle.Q5_0, oracle.Q5_1, oracle.IQ4_NL,
+                                   oracle.Q2_K, oracle.Q3_K, oracle.Q4_K, oracle.Q5_K, oracle.Q6_K])
 def test_dequant_closed_form(cpuref, qtype):
     """Every dequantized value is the float32 rounding of the exact rational
-    the format defines (only Q4_K's subtraction rounds)."""
+    the format defines (only the offset additions of Q4_1 / Q5_1 and the
+    min subtractions of Q2_K / Q4_K / Q5_K round)."""
     e, bb = oracle.BLOCK[qtype]
     rows = synth.random_blocks(qtype, 1, e * 6, seed=qtype)
     got = cpuref.dequant(qtype, rows[0], e * 6)
@@ -165,8 +254,9 @@ def test_dequant_closed_form(cpuref, qtype):
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
-@pytest.mark.parametrize("qtype", [oracle.Q8_0, oracle.Q4_0, oracle.Q4_1, oracle.Q5_0, oracle.Q5_1, oracle.Q4_K,
-                                   oracle.Q6_K, oracle.IQ4_NL, oracle.F16, oracle.BF16])
+@pytest.mark.parametrize("qtype", [oracle.Q8_0, oracle.Q4_0, oracle.Q4_1, oracle.Q5_0, oracle.Q5_1, oracle.Q2_K,
+                                   oracle.Q3_K, oracle.Q4_K, oracle.Q5_K, oracle.Q6_K, oracle.IQ4_NL, oracle.F16,
+                                   oracle.BF16])
 def test_dequant_matches_reference(cpuref, refc, qtype):
     e, bb = oracle.BLOCK[qtype]
     n = max(e, 32) * 16
@@ -224,8 +314,9 @@ def _dequant_rows_f64(cpuref, qtype, w, rows, cols):
     return np.stack([cpuref.dequant(qtype, w[r], cols) for r in range(rows)]).astype(np.float64)
 
 
-@pytest.mark.parametrize("qtype,rows,cols", [(oracle.Q8_0, 37, 512), (oracle.Q4_K, 19, 1024),
-                                             (oracle.Q6_K, 13, 512)])
+@pytest.mark.parametrize("qtype,rows,cols", [(oracle.Q8_0, 37, 512), (oracle.Q2_K, 11, 768), (oracle.Q3_K, 9, 512),
+                                             (oracle.Q4_K, 19, 1024), (oracle.Q5_K, 7, 512), (oracle.Q6_K, 13, 512),
+                                             (oracle.F16, 5, 320), (oracle.BF16, 6, 256)])
 def test_matmul_float_bound(cpuref, qtype, rows, cols):
     """Float-input types: |y - y64| <= gamma_K * sum|w x| (any fp32 order)."""
     w = synth.random_blocks(qtype, rows, cols, seed=11)
@@ -240,26 +331,37 @@ def test_matmul_float_bound(cpuref, qtype, rows, cols):
     assert np.any(np.abs(y_bad - y64) > bound)
 
 
-def test_matmul_q4_0_integer_path(cpuref):
-    """Q4_0: x is quantized to Q8_0 and each block dot is an exact integer."""
+@pytest.mark.parametrize("qtype", [oracle.Q4_0, oracle.Q4_1, oracle.Q5_0, oracle.Q5_1, oracle.IQ4_NL])
+def test_matmul_q8_activation_integer_path(cpuref, qtype):
+    """Q4_0, Q4_1, Q5_0, Q5_1, IQ4_NL: x is quantized to Q8_0 and every block
+    contributes dw*dx*isum (+ mw*dx*xsum for the types with a min), isum and
+    xsum exact integers: the sum is within gamma of the float64 sum of those
+    terms, and dropping a block's min term breaks the bound."""
     rows, cols = 23, 512
-    w = synth.random_blocks(oracle.Q4_0, rows, cols, seed=13)
+    e, bb = oracle.BLOCK[qtype]
+    w = synth.random_blocks(qtype, rows, cols, seed=13 + qtype)
     x = synth.random_x(cols, seed=14)
-    y = cpuref.matmul(oracle.Q4_0, w, rows, cols, x)
+    y = cpuref.matmul(qtype, w, rows, cols, x)
     xq = cpuref.quantize_q8_0(x).reshape(-1, 34)
     dx = xq[:, 0:2].copy().view(np.float16).astype(np.float64)[:, 0]
     qx = xq[:, 2:].view(np.int8).astype(np.int64)
-    wb = w.reshape(rows, -1, 18)
+    wb = w.reshape(rows, -1, bb)
     dw = wb[:, :, 0:2].copy().view(np.float16).astype(np.float64)[:, :, 0]
-    nib = np.concatenate([(wb[:, :, 2:] & 15), (wb[:, :, 2:] >> 4)], axis=2).astype(np.int64) - 8
-    isum = (nib * qx[None]).sum(axis=2)
-    terms = dw * dx[None] * isum
+    code, mo = codes_32(qtype, wb)
+    terms = dw * dx[None] * (code * qx[None]).sum(axis=2)
+    if mo is not None:
+        mw = wb[:, :, mo:mo + 2].copy().view(np.float16).astype(np.float64)[:, :, 0]
+        mterms = mw * dx[None] * qx.sum(axis=1)[None]
+        assert np.any(np.abs(y - terms.sum(axis=1)) > gamma(2 * cols // 32 + 2) * np.abs(terms).sum(axis=1))
+        terms = terms + mterms
     y64 = terms.sum(axis=1)
-    assert np.all(np.abs(y - y64) <= gamma(cols // 32 + 2) * np.abs(terms).sum(axis=1))
+    assert np.all(np.abs(y - y64) <= gamma(2 * cols // 32 + 2) * np.abs(terms).sum(axis=1))
 
 
-@pytest.mark.parametrize("qtype,cols", [(oracle.Q8_0, 256), (oracle.Q4_0, 256), (oracle.Q4_K, 512),
-                                        (oracle.Q6_K, 512)])
+@pytest.mark.parametrize("qtype,cols", [(oracle.Q8_0, 256), (oracle.Q4_0, 256), (oracle.Q4_1, 256), (oracle.Q5_0, 288),
+                                        (oracle.Q5_1, 256), (oracle.IQ4_NL, 224), (oracle.Q2_K, 512),
+                                        (oracle.Q3_K, 768), (oracle.Q4_K, 512), (oracle.Q5_K, 512),
+                                        (oracle.Q6_K, 512), (oracle.F16, 192), (oracle.BF16, 160)])
 def test_matmul_matches_reference(cpuref, refc, qtype, cols):
     rows = 21   # not a multiple of 4: exercises the reference's tail rows
     w = synth.random_blocks(qtype, rows, cols, seed=3)
