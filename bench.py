@@ -11,12 +11,13 @@ Printed as one JSON line:
   value        decode tok/s over exactly --steps timed steps (weights, KV
                cache and run state already resident in HBM);
   roofline     the dominant GEMV launch class: algorithmic bytes per launch
-               over its average launch duration, from HIP events recorded by
-               the library on its stream around every GEMV launch, over a
-               second pass of --steps decode steps;
+               over its average kernel duration, from the HIP events each
+               GEMV dispatch records at its own start and end
+               (hipExtLaunchKernelGGL), over a second pass of --steps decode
+               steps (run eagerly);
   gemv         standalone GEMV launches at the Llama-3-8B shapes (Q8_0, Q4_0,
-               Q4_K, Q6_K), weight copies rotated through >= 1 GiB so the
-               256 MB last-level cache does not serve them;
+               Q4_K, Q6_K), timed the same way, weight copies rotated through
+               >= 1 GiB so the 256 MB last-level cache does not serve them;
   prefill      the 1024-position prompt before the decode: positions/s and
                the fp32-MFMA roofline of the dominant prefill GEMM class;
   cpu_baseline the reference C engine (oracle/_ref/libref_omp.so: its own
@@ -72,8 +73,9 @@ def gpu_q8_0_maker(ctx, torch, seed):
 
 
 def time_gemv_shapes(ctx, torch, l3p, synth):
-    """GB/s of single GEMV launches (library call: input preparation + GEMV)."""
-    st = torch.cuda.ExternalStream(ctx.stream)
+    """GB/s of single GEMV launches: l3p_gemv calls over rotating weight
+    copies (>= 1 GiB, so no launch finds its weights in a cache), each kernel
+    timed by its own dispatch events (the library's launch timing)."""
     shapes = [("q8_0", l3p.Q8_0, 4096, 4096), ("q4_0", l3p.Q4_0, 14336, 4096), ("q4_0", l3p.Q4_0, 4096, 14336),
               ("q4_k", l3p.Q4_K, 14336, 4096), ("q6_k", l3p.Q6_K, 128256, 4096)]
     out = []
@@ -89,18 +91,16 @@ def time_gemv_shapes(ctx, torch, l3p, synth):
             ctx.gemv(qt, ws[i], rows, cols, x, y)
         ctx.synchronize()
         n = max(40, 2 * copies)
-        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
-        with torch.cuda.stream(st):
-            for i in range(n):
-                ev[i][0].record(st)
-                ctx.gemv(qt, ws[i % copies], rows, cols, x, y)
-                ev[i][1].record(st)
-        ctx.synchronize()
-        us = sorted(a.elapsed_time(b) * 1e3 for a, b in ev)
-        med = us[len(us) // 2]
+        ctx.profile(True)
+        for i in range(n):
+            ctx.gemv(qt, ws[i % copies], rows, cols, x, y)
+        stats = ctx.profile_read()
+        ctx.profile(False)
+        launches, ms, _ = next(iter(stats.values()))
+        avg = ms * 1e3 / launches
         alg = wbytes + 4 * cols + 4 * rows
-        out.append({"shape": f"{name} {rows}x{cols}", "us": round(med, 2), "GB/s": round(alg / med / 1e3, 1),
-                    "frac": round(alg / med / 1e3 / HBM_PEAK_GBS, 4)})
+        out.append({"shape": f"{name} {rows}x{cols}", "us": round(avg, 2), "GB/s": round(alg / avg / 1e3, 1),
+                    "frac": round(alg / avg / 1e3 / HBM_PEAK_GBS, 4)})
         del ws, base
         torch.cuda.empty_cache()
     return out
@@ -297,7 +297,7 @@ def main():
     tps = a.steps / dt
     print(f"[bench] {a.steps} decode steps in {dt * 1e3:.1f} ms: {tps:.1f} tok/s", file=sys.stderr, flush=True)
 
-    # second pass with per-launch events: the roofline of the dominant GEMV class
+    # second pass with per-kernel dispatch events: the roofline of the dominant GEMV class
     ctx.profile(True)
     tok, pos = run(a.steps, tok, pos)
     stats = ctx.profile_read()

@@ -152,8 +152,7 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmArgs a) {
 template <int QT>
 void launch_typed(const GemmArgs& a, hipStream_t st) {
     const dim3 grid((a.n + kBN - 1) / kBN, (a.m + kBM - 1) / kBM);
-    hipLaunchKernelGGL(gemm_kernel<QT>, grid, dim3(256), 0, st, a);
-    L3P_HIP(hipGetLastError());
+    launch_kernel(gemm_kernel<QT>, grid, dim3(256), 0u, st, a);
 }
 
 }  // namespace

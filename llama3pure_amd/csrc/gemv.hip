@@ -1050,8 +1050,7 @@ void launch_rows(GemvArgs a, hipStream_t st) {
     const size_t lds = lds_for(grid);
     if (lds > 65536)
         L3P_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-    hipLaunchKernelGGL(kern, dim3(grid), dim3(threads), lds, st, a);
-    L3P_HIP(hipGetLastError());
+    launch_kernel(kern, dim3(grid), dim3(threads), (uint32_t)lds, st, a);
 }
 
 // Ring depth: 3 buffers per wave (deeper rings measured no faster on

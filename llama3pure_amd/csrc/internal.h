@@ -1,6 +1,7 @@
 // internal.h — shared declarations of libl3p (host and device).
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <stdio.h>
@@ -33,6 +34,28 @@ struct L3pError {
             throw L3pError{code, b_};                                                        \
         }                                                                                    \
     } while (0)
+
+// ---------------------------------------------------------------------------
+// kernel timing: a timed range (ProfRange) hands an event pair to the next
+// GEMV or GEMM launch, which has the dispatch itself record them at the
+// kernel's start and end (hipExtLaunchKernelGGL), so the range measures the
+// kernel alone and not the stream's dispatch latency around it.
+// ---------------------------------------------------------------------------
+struct KernelEvents {
+    hipEvent_t start = nullptr, stop = nullptr;   // null: no range open
+    int launches = 0;                             // launches inside the open range
+};
+KernelEvents& kernel_events();   // per host thread
+
+template <typename K, typename... Args>
+void launch_kernel(K kern, dim3 grid, dim3 block, uint32_t lds, hipStream_t st, Args... args) {
+    KernelEvents& ke = kernel_events();
+    if (ke.start && ke.launches++ == 0)
+        hipExtLaunchKernelGGL(kern, grid, block, lds, st, ke.start, ke.stop, 0, args...);
+    else
+        hipLaunchKernelGGL(kern, grid, block, lds, st, args...);
+    L3P_HIP(hipGetLastError());
+}
 
 // ---------------------------------------------------------------------------
 // block formats (llama3pure-c-engine.c:127-195)

@@ -463,6 +463,16 @@ void Profiler::release() {
     for (hipEvent_t e : pool) hipEventDestroy(e);
     pool.clear();
 }
+KernelEvents& kernel_events() {
+    static thread_local KernelEvents e;
+    return e;
+}
+
+// The start event is recorded on the stream and offered to the range's
+// first GEMV/GEMM launch, which records both events at the kernel's own start
+// and end.  A range of one kernel thus times the kernel alone; one of several
+// kernels (or none) ends with a stream record of the stop event.  Ranges nest:
+// the enclosing range's state is restored at the end.
 ProfRange::ProfRange(Profiler& pr, hipStream_t stream, const std::string& name, double bytes) {
     if (!pr.on) return;
     p = &pr;
@@ -471,10 +481,14 @@ ProfRange::ProfRange(Profiler& pr, hipStream_t stream, const std::string& name, 
     a = pr.event();
     b = pr.event();
     L3P_HIP(hipEventRecord(a, s));
+    outer = kernel_events();
+    kernel_events() = KernelEvents{a, b, 0};
 }
 ProfRange::~ProfRange() {
     if (!p) return;
-    if (hipEventRecord(b, s) == hipSuccess) p->pending.push_back({st, a, b});
+    const int launches = kernel_events().launches;   // direct launches: nested ranges keep their own
+    kernel_events() = outer;
+    if (launches == 1 || hipEventRecord(b, s) == hipSuccess) p->pending.push_back({st, a, b});
     else {
         p->pool.push_back(a);
         p->pool.push_back(b);
@@ -527,6 +541,9 @@ static void gemv_batch(l3p_ctx* c, int type, const GemvBatch& b, int cols, const
 }
 
 void gemv_plain(l3p_ctx* c, int type, const GemvBatch& b, int cols, const float* x) {
+    int rows = 0;
+    for (int i = 0; i < b.nseg; ++i) rows += b.seg[i].rows;
+    ProfRange r(c->prof, c->stream, gemv_label("plain", type, rows, cols), gemv_bytes(type, rows, cols, rows));
     launch_gemv(type, b, cols, x, nullptr, 0.0f, c->stream);
 }
 

@@ -92,6 +92,7 @@ struct ProfRange {
     int st = -1;
     hipEvent_t a{}, b{};
     hipStream_t s{};
+    KernelEvents outer;   // the enclosing range's launch events
     ProfRange(Profiler& pr, hipStream_t stream, const std::string& name, double bytes);
     ~ProfRange();
 };
