@@ -70,10 +70,11 @@ int l3p_quantize_q8_0(l3p_ctx* ctx, const float* x_dev, int64_t n, void* dst_dev
 
 /* y[rows] = W[rows x cols] . x[cols] with W in its native block layout.
  * Replaces matmul_quantized (c:2091-2133; js:3107-3142) for F16 BF16 Q4_0
- * Q4_1 Q5_0 Q5_1 Q8_0 Q2_K Q3_K Q4_K Q5_K Q6_K IQ4_NL with cols <= 32768
- * (F32: L3P_E_UNSUPPORTED).  Semantics per type follow the reference: Q8_0
- * and the K-quants use fp32 x (matmul_deq_4row, c:2136-2176), F16/BF16 the
- * float dot (c:1467-1485); Q4_0 Q4_1 Q5_0 Q5_1 IQ4_NL quantize x to Q8_0
+ * Q4_1 Q5_0 Q5_1 Q8_0 Q2_K Q3_K Q4_K Q5_K Q6_K IQ4_NL with cols <= 32768 and
+ * F32 with cols <= 16384 (wider: L3P_E_UNSUPPORTED).  Semantics per type
+ * follow the reference: Q8_0 and the K-quants use fp32 x (matmul_deq_4row,
+ * c:2136-2176), F16/BF16/F32 the float dot (c:1467-1494); Q4_0 Q4_1 Q5_0
+ * Q5_1 IQ4_NL quantize x to Q8_0
  * first and use their integer block dots (c:2105-2116, c:1625-1717,
  * c:1994-2011).  Results differ from the reference's only by fp32 summation
  * order.  w_dev and x_dev must be 16-byte aligned (l3p_malloc memory is). */
@@ -82,7 +83,7 @@ int l3p_gemv(l3p_ctx* ctx, int type, const void* w_dev, int rows, int cols, cons
 
 /* Batched form for prefill: y[b*out_stride + r] = W[r,:] . x[b*in_stride + :]
  * for b < batch.  Replaces matmul_quantized_batch (c:2291-2331; js:3159-3845).
- * Q8_0, the K-quants, F16 and BF16 run on the fp32-MFMA GEMM (weights
+ * Q8_0, the K-quants, F16, BF16 and F32 run on the fp32-MFMA GEMM (weights
  * dequantized exactly, as matmul_deq_batch_4row, c:2179-2273); Q4_0 Q4_1
  * Q5_0 Q5_1 IQ4_NL run the GEMV per batch row (the reference's
  * Q8_0-activation integer dots, c:2305-2318).  in_stride must be a multiple

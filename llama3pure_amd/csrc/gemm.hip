@@ -163,7 +163,7 @@ void launch_typed(const GemmArgs& a, hipStream_t st) {
 bool gemm_mfma_supported(int type) {
     switch (type) {
     case L3P_Q8_0: case L3P_Q2_K: case L3P_Q3_K: case L3P_Q4_K: case L3P_Q5_K: case L3P_Q6_K:
-    case L3P_F16: case L3P_BF16: return true;
+    case L3P_F16: case L3P_BF16: case L3P_F32: return true;
     default: return false;
     }
 }
@@ -184,6 +184,7 @@ void launch_gemm(int type, const uint8_t* w, int n, int k, const float* x, int m
     case L3P_Q5_K: launch_typed<L3P_Q5_K>(a, st); break;
     case L3P_Q6_K: launch_typed<L3P_Q6_K>(a, st); break;
     case L3P_F16: launch_typed<L3P_F16>(a, st); break;
+    case L3P_F32: launch_typed<L3P_F32>(a, st); break;
     default: launch_typed<L3P_BF16>(a, st); break;
     }
 }

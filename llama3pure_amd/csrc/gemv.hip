@@ -100,6 +100,7 @@ template <> struct Fmt<L3P_Q5_K> : FmtBase<256, 176, 2, 0, true> {};    // 1408 
 template <> struct Fmt<L3P_Q6_K> : FmtBase<256, 210, 2, 0> {};          // 1680 B
 template <> struct Fmt<L3P_F16> : FmtBase<32, 64, 4, 0, true> {};       // 4096 B
 template <> struct Fmt<L3P_BF16> : FmtBase<32, 64, 4, 0, true> {};      // 4096 B
+template <> struct Fmt<L3P_F32> : FmtBase<32, 128, 8, 0, true> {};      // 8192 B
 
 // Types whose reference dot takes the activation as Q8_0 (vec_dot_*_q8_0:
 // q8_func without a row dequantizer, c:2091-2133); the others dot fp32.
@@ -145,16 +146,16 @@ __device__ __forceinline__ void wait_chunk(int younger) {
 // Every chunk is therefore exactly kCI instructions with all lanes active, a
 // constant the waits count on.
 struct DmaLane {
-    int o[4];   // the dwordx4 pieces (kX4 <= 4 of them)
+    int o[8];   // the dwordx4 pieces (kX4 <= 8 of them)
     int ot;     // the dword piece (unused without a tail)
 };
 template <int QT>
 __device__ __forceinline__ DmaLane dma_lane(int lane, int span) {
-    static_assert(Fmt<QT>::kX4 <= 4, "at most four dwordx4 pieces");
+    static_assert(Fmt<QT>::kX4 <= 8, "at most eight dwordx4 pieces");
     const int e16 = ((span + 15) & ~15) - 16, e4 = ((span + 3) & ~3) - 4;
     DmaLane d;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) d.o[i] = min(1024 * i + lane * 16, e16);
+    for (int i = 0; i < Fmt<QT>::kX4; ++i) d.o[i] = min(1024 * i + lane * 16, e16);
     d.ot = min(Fmt<QT>::kX4 * 1024 + lane * 4, e4);
     return d;
 }
@@ -800,6 +801,25 @@ struct LaneHalf {
 template <> struct Lane<L3P_F16> : LaneHalf<L3P_F16> {};
 template <> struct Lane<L3P_BF16> : LaneHalf<L3P_BF16> {};
 
+// F32 rows: the lane's 32 values are the 128 bytes at 128*lane (vec_dot_f32,
+// c:1487-1494, sum in another order).
+template <>
+struct Lane<L3P_F32> {
+    uint32_t first;
+    __device__ __forceinline__ void at(int lane, uint32_t /*sh: always 0*/) { first = 32u * (uint32_t)lane; }
+    __device__ __forceinline__ float dot(const uint32_t* buf, const XBlock& xb) const {
+        float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 32; i += 4) {
+            s0 = fmaf(__uint_as_float(buf[first + i]), xb.x[i], s0);
+            s1 = fmaf(__uint_as_float(buf[first + i + 1]), xb.x[i + 1], s1);
+            s2 = fmaf(__uint_as_float(buf[first + i + 2]), xb.x[i + 2], s2);
+            s3 = fmaf(__uint_as_float(buf[first + i + 3]), xb.x[i + 3], s3);
+        }
+        return (s0 + s1) + (s2 + s3);
+    }
+};
+
 template <int QT, int G, int NB, bool PAIR, bool UA>
 __global__ void __launch_bounds__(1024) gemv_kernel(GemvArgs a) {
     constexpr int CB = Fmt<QT>::kChunkBytes;
@@ -1054,7 +1074,7 @@ void launch_rows(GemvArgs a, hipStream_t st) {
 }
 
 // Ring depth: 3 buffers per wave (deeper rings measured no faster on
-// MI355X); 2 for the 4 KB F16/BF16 chunks of rows too wide for 3.
+// MI355X); 2 for the 4 KB F16/BF16 and 8 KB F32 chunks of rows too wide for 3.
 template <int QT, int G, bool PAIR, bool UA>
 void launch_nb(GemvArgs a, int nbuf, hipStream_t st) {
     if constexpr (Fmt<QT>::kBufBytes >= 4096) {
@@ -1088,7 +1108,7 @@ void launch_type(GemvArgs a, bool pair, int G, int nbuf, hipStream_t st) {
     const int per = pair ? G / 2 : G;
     a.ngroups = (units + per - 1) / per;
     // three buffers per wave when they fit the 160 KB of LDS with room for
-    // the result slots, else two
+    // the result slots, else two (gemv_supported keeps F32 rows narrow enough)
     const int nw = (a.cols / 32 + 63) / 64;
     const int nb = (size_t)nw * 3 * Fmt<QT>::kBufBytes + 16384 <= 160 * 1024 ? 3 : 2;
     (void)nbuf;
@@ -1108,6 +1128,7 @@ bool gemv_supported(int type, int cols) {
     case L3P_Q8_0: case L3P_Q4_0: case L3P_Q4_1: case L3P_Q5_0: case L3P_Q5_1: case L3P_IQ4_NL:
     case L3P_F16: case L3P_BF16: unit = 32; break;
     case L3P_Q2_K: case L3P_Q3_K: case L3P_Q4_K: case L3P_Q5_K: case L3P_Q6_K: unit = 256; break;
+    case L3P_F32: return cols > 0 && cols % 32 == 0 && cols <= 16384;   // 8 KB chunks: two per wave fit LDS
     default: return false;
     }
     return cols > 0 && cols % unit == 0 && cols <= kMaxWaves * kChunkElems;
@@ -1169,6 +1190,7 @@ void launch_gemv(int type, const GemvBatch& b, int cols, const float* x, const f
     case L3P_Q5_K: launch_type<L3P_Q5_K>(a, pr, G, 3, st); break;
     case L3P_Q6_K: launch_type<L3P_Q6_K>(a, pr, G, 3, st); break;
     case L3P_F16: launch_type<L3P_F16>(a, pr, G, 3, st); break;
+    case L3P_F32: launch_type<L3P_F32>(a, pr, G, 3, st); break;
     default: launch_type<L3P_BF16>(a, pr, G, 3, st); break;
     }
 }

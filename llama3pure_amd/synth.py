@@ -92,6 +92,8 @@ def random_blocks(qtype: int, rows: int, cols: int, seed: int) -> np.ndarray:
         out[:, :, :] = _f16_bytes(rng.normal(0, 0.02, (rows, nb)))
     elif qtype == BF16:
         out[:, :, :] = _bf16_bytes(rng.normal(0, 0.02, (rows, nb)).astype(np.float32))
+    elif qtype == F32:
+        out[:, :, :] = rng.normal(0, 0.02, (rows, nb)).astype(np.float32).view(np.uint8).reshape(rows, nb, 4)
     else:
         raise ValueError(f"no synthetic generator for type {qtype}")
     return out.reshape(rows, nb * bb)

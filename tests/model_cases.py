@@ -69,6 +69,7 @@ SINGLE_LAYER = {
     "llama_q5_k_768": dict(qtype=synth.Q5_K, dim=768, hidden=1280, n_heads=6, n_kv=2),
     "llama_f16_640": dict(qtype=synth.F16, dim=640, hidden=1536, n_heads=5, n_kv=1),
     "llama_bf16_640": dict(qtype=synth.BF16, dim=640, hidden=1536, n_heads=5, n_kv=1),
+    "llama_f32_640": dict(qtype=synth.F32, dim=640, hidden=1536, n_heads=5, n_kv=1),
 }
 SINGLE_TOKENS = (0, 7, 1234, 42, 555, 1000, 1999, 2047)
 

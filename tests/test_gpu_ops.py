@@ -164,6 +164,9 @@ def _check_gemv(ctx, torch, cpuref, qtype, rows, cols, seed=0, sample_rows=None)
     (l3p.BF16, 1024, 4096),
     (l3p.BF16, 99, 288),
     (l3p.BF16, 65, 30720),
+    (l3p.F32, 1024, 4096),
+    (l3p.F32, 70, 16384),          # 8 chunk columns: two buffers per wave
+    (l3p.F32, 33, 96),
 ])
 def test_gemv_parity(ctx, torch_gpu, cpuref, qtype, rows, cols):
     _check_gemv(ctx, torch_gpu, cpuref, qtype, rows, cols, seed=rows + cols, sample_rows=min(rows, 768))
@@ -190,7 +193,7 @@ def test_gemv_zero_rows_and_errors(ctx, torch_gpu):
         ctx.gemv(l3p.Q8_0, 0, 8, 500, x, y)          # cols not a block multiple
     assert e.value.code == l3p.E_INVALID
     with pytest.raises(l3p.L3PError) as e:
-        ctx.gemv(l3p.F32, 0, 8, 512, x, y)           # type without a GEMV kernel
+        ctx.gemv(l3p.F32, 0, 8, 32768, x, y)         # F32 rows wider than 16384
     assert e.value.code == l3p.E_UNSUPPORTED
     with pytest.raises(l3p.L3PError) as e:
         ctx.gemv(l3p.Q8_0, 0, 8, 512, x, y)          # null weight pointer
@@ -251,6 +254,7 @@ def _dequant_bound(cpuref, qtype, w, rows, cols):
     (l3p.Q5_K, 1000, 2304, 17),
     (l3p.F16, 130, 320, 5),
     (l3p.BF16, 257, 2048, 64),
+    (l3p.F32, 100, 512, 70),
 ])
 def test_gemm_mfma_parity(ctx, torch_gpu, cpuref, qtype, rows, cols, batch):
     """MFMA GEMM against the float64 value of the reference's dequantize-then-

@@ -316,7 +316,7 @@ def _dequant_rows_f64(cpuref, qtype, w, rows, cols):
 
 @pytest.mark.parametrize("qtype,rows,cols", [(oracle.Q8_0, 37, 512), (oracle.Q2_K, 11, 768), (oracle.Q3_K, 9, 512),
                                              (oracle.Q4_K, 19, 1024), (oracle.Q5_K, 7, 512), (oracle.Q6_K, 13, 512),
-                                             (oracle.F16, 5, 320), (oracle.BF16, 6, 256)])
+                                             (oracle.F16, 5, 320), (oracle.BF16, 6, 256), (oracle.F32, 7, 96)])
 def test_matmul_float_bound(cpuref, qtype, rows, cols):
     """Float-input types: |y - y64| <= gamma_K * sum|w x| (any fp32 order)."""
     w = synth.random_blocks(qtype, rows, cols, seed=11)
@@ -361,7 +361,7 @@ def test_matmul_q8_activation_integer_path(cpuref, qtype):
 @pytest.mark.parametrize("qtype,cols", [(oracle.Q8_0, 256), (oracle.Q4_0, 256), (oracle.Q4_1, 256), (oracle.Q5_0, 288),
                                         (oracle.Q5_1, 256), (oracle.IQ4_NL, 224), (oracle.Q2_K, 512),
                                         (oracle.Q3_K, 768), (oracle.Q4_K, 512), (oracle.Q5_K, 512),
-                                        (oracle.Q6_K, 512), (oracle.F16, 192), (oracle.BF16, 160)])
+                                        (oracle.Q6_K, 512), (oracle.F16, 192), (oracle.BF16, 160), (oracle.F32, 128)])
 def test_matmul_matches_reference(cpuref, refc, qtype, cols):
     rows = 21   # not a multiple of 4: exercises the reference's tail rows
     w = synth.random_blocks(qtype, rows, cols, seed=3)
