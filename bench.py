@@ -152,6 +152,39 @@ def calibrate_copy():
     print(json.dumps({"calibrate_copy_bytes": a.numel() * 4, "copies": 5}), flush=True)
 
 
+def attn_sweep():
+    """Both decode attentions at several context lengths, for a kernel trace:
+    a 2-layer Llama-3-8B-shaped model (32 query / 8 KV heads, head_dim 128,
+    4096 positions); per length P, P prompt positions, then 12 decode steps at
+    position P with the per-head kernel (L3P_ATTN_HEAD=1) and 12 with chunks +
+    merge (=0).  Prints the order of the blocks; the kernel durations come
+    from the trace."""
+    import numpy as np
+    import torch
+
+    import llama3pure_amd as l3p
+    from llama3pure_amd import synth
+
+    ctx = l3p.Context(0)
+    g = synth.synthetic_model(arch="llama", dim=4096, hidden=256, n_layers=2, n_heads=32, n_kv=8, vocab=256,
+                              ctx=4096, seed=3)
+    ctx.load_gguf(g)
+    toks = np.random.default_rng(1).integers(0, 256, 4096).astype(np.int32)
+    order = []
+    for P in (64, 256, 512, 1024, 2048, 3000):
+        ctx.prefill(toks[:P], 0)
+        for path in ("0", "1"):
+            os.environ["L3P_ATTN_HEAD"] = path
+            for _ in range(12):
+                ctx.forward(int(toks[P]), P, logits=False)
+            ctx.synchronize()
+            order.append({"positions": P + 1, "attention": "per-head" if path == "1" else "chunks+merge"})
+    os.environ.pop("L3P_ATTN_HEAD", None)
+    torch.cuda.synchronize()
+    print(json.dumps({"attn_sweep": order}), flush=True)
+    ctx.close()
+
+
 def cpu_leg(path: str, seconds: float, max_tokens: int, use_ref: bool) -> dict:
     """Runs in a subprocess: the reference engine (or the oracle) decoding
     greedily from position 0 on the GGUF at path."""
@@ -231,6 +264,8 @@ def main():
                     help="layers of the model (32 = Llama-3-8B; fewer only for short counter-collection runs)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only copy 512 MiB device-to-device 5 times (scale for rocprofv3 FETCH_SIZE/WRITE_SIZE)")
+    ap.add_argument("--attn-sweep", action="store_true",
+                    help="only run both decode attentions at 65..3001 positions (for a kernel trace)")
     ap.add_argument("--cpu-leg", help=argparse.SUPPRESS)
     ap.add_argument("--cpu-ref", type=int, default=1, help=argparse.SUPPRESS)
     a = ap.parse_args()
@@ -240,6 +275,9 @@ def main():
         return
     if a.calibrate_copy:
         calibrate_copy()
+        return
+    if a.attn_sweep:
+        attn_sweep()
         return
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the decode path runs on a single MI355X and has no multi-GPU "

@@ -1103,7 +1103,7 @@ void launch_g(GemvArgs a, bool pair, int G, int nbuf, hipStream_t st) {
 }
 
 template <int QT>
-void launch_type(GemvArgs a, bool pair, int G, int nbuf, hipStream_t st) {
+void launch_type(GemvArgs a, bool pair, int G, hipStream_t st) {
     const int units = pair ? a.rows[0] : a.rows_total;
     const int per = pair ? G / 2 : G;
     a.ngroups = (units + per - 1) / per;
@@ -1111,11 +1111,10 @@ void launch_type(GemvArgs a, bool pair, int G, int nbuf, hipStream_t st) {
     // the result slots, else two (gemv_supported keeps F32 rows narrow enough)
     const int nw = (a.cols / 32 + 63) / 64;
     const int nb = (size_t)nw * 3 * Fmt<QT>::kBufBytes + 16384 <= 160 * 1024 ? 3 : 2;
-    (void)nbuf;
     if (row_bytes<QT>(a.cols) % 16 == 0) {
         launch_g<QT, false>(a, pair, G, nb, st);
     } else {
-        // Q4_K, Q5_K and F16/BF16 rows are always 16-byte multiples
+        // Q4_K, Q5_K, F16, BF16 and F32 rows are always 16-byte multiples
         if constexpr (!Fmt<QT>::kAligned) launch_g<QT, true>(a, pair, G, nb, st);
     }
 }
@@ -1178,19 +1177,19 @@ void launch_gemv(int type, const GemvBatch& b, int cols, const float* x, const f
     }
     const bool pr = b.pair != 0;
     switch (type) {
-    case L3P_Q8_0: launch_type<L3P_Q8_0>(a, pr, G, 3, st); break;
-    case L3P_Q4_0: launch_type<L3P_Q4_0>(a, pr, G, 3, st); break;
-    case L3P_Q4_1: launch_type<L3P_Q4_1>(a, pr, G, 3, st); break;
-    case L3P_Q5_0: launch_type<L3P_Q5_0>(a, pr, G, 3, st); break;
-    case L3P_Q5_1: launch_type<L3P_Q5_1>(a, pr, G, 3, st); break;
-    case L3P_IQ4_NL: launch_type<L3P_IQ4_NL>(a, pr, G, 3, st); break;
-    case L3P_Q2_K: launch_type<L3P_Q2_K>(a, pr, G, 3, st); break;
-    case L3P_Q3_K: launch_type<L3P_Q3_K>(a, pr, G, 3, st); break;
-    case L3P_Q4_K: launch_type<L3P_Q4_K>(a, pr, G, 3, st); break;
-    case L3P_Q5_K: launch_type<L3P_Q5_K>(a, pr, G, 3, st); break;
-    case L3P_Q6_K: launch_type<L3P_Q6_K>(a, pr, G, 3, st); break;
-    case L3P_F16: launch_type<L3P_F16>(a, pr, G, 3, st); break;
-    case L3P_F32: launch_type<L3P_F32>(a, pr, G, 3, st); break;
-    default: launch_type<L3P_BF16>(a, pr, G, 3, st); break;
+    case L3P_Q8_0: launch_type<L3P_Q8_0>(a, pr, G, st); break;
+    case L3P_Q4_0: launch_type<L3P_Q4_0>(a, pr, G, st); break;
+    case L3P_Q4_1: launch_type<L3P_Q4_1>(a, pr, G, st); break;
+    case L3P_Q5_0: launch_type<L3P_Q5_0>(a, pr, G, st); break;
+    case L3P_Q5_1: launch_type<L3P_Q5_1>(a, pr, G, st); break;
+    case L3P_IQ4_NL: launch_type<L3P_IQ4_NL>(a, pr, G, st); break;
+    case L3P_Q2_K: launch_type<L3P_Q2_K>(a, pr, G, st); break;
+    case L3P_Q3_K: launch_type<L3P_Q3_K>(a, pr, G, st); break;
+    case L3P_Q4_K: launch_type<L3P_Q4_K>(a, pr, G, st); break;
+    case L3P_Q5_K: launch_type<L3P_Q5_K>(a, pr, G, st); break;
+    case L3P_Q6_K: launch_type<L3P_Q6_K>(a, pr, G, st); break;
+    case L3P_F16: launch_type<L3P_F16>(a, pr, G, st); break;
+    case L3P_F32: launch_type<L3P_F32>(a, pr, G, st); break;
+    default: launch_type<L3P_BF16>(a, pr, G, st); break;
     }
 }
