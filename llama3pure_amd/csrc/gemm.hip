@@ -10,13 +10,15 @@
 //
 // Tiling.  A workgroup owns a 64 x 64 tile of Y and walks K in steps of 64:
 //   1. the 64 x 64 X tile (fp32, from L2) and the dequantized 64 x 64 W tile
-//      go to LDS, rows padded to 68 floats;
+//      go to LDS, rows padded to 68 floats; their global loads were issued
+//      one step earlier, before that step's matrix work;
 //   2. four waves each compute a 32 x 32 quarter with v_mfma_f32_16x16x4_f32
 //      (2 x 2 tiles of 16 x 16).  The instruction contracts over 4 k-slots,
 //      slot g held by lanes 16g..16g+15; here slot g of step s is
 //      k = kk + 4g + s, the same for A (X) and B (W), so each lane fetches
 //      its four k values of a 16-wide slab with one ds_read_b128.
-// Several workgroups per CU hide the load and dequantization latency.
+// Several workgroups per CU (a 1024-row prompt pass gives four per CU at
+// N = 4096) and the one-step-ahead loads hide the load latency.
 #include "dequant.h"
 #include "device_common.h"
 #include "internal.h"
@@ -41,30 +43,62 @@ struct GemmArgs {
     int add;          // 1: Y += W.X (residual), 0: Y = W.X
 };
 
-// Rows [n0, n0+64) x columns [k0, k0+64) of W, dequantized into ws[r][c].
-// Q8_0 (blocks of 32, 34 B): thread t expands 16 values of one block,
-// (float)q * d as in dequantize_row_q8_0 (c:691-702).  Other types go
-// element by element through the reference-exact dequantizer.
+// The global data of one K step, held in registers from the step before so
+// that its loads are in flight while the matrix cores work on the current
+// step: the X tile (4 float4 per thread) and, for Q8_0, this thread's 16
+// quants and block scale (t: row t/4, block (t/2)&1, half t&1).
 template <int QT>
-__device__ __forceinline__ void load_w_tile(float* ws, const GemmArgs& a, int n0, int k0, int t) {
+struct StepRegs {
+    float4 x[4];
+    uint4 q;         // Q8_0: the 16 quants as fetched (bytes in order)
+    uint32_t d;      // Q8_0: fp16 scale bits
+};
+
+template <int QT>
+__device__ __forceinline__ void fetch_step(StepRegs<QT>& sr, const GemmArgs& a, int m0, int n0, int k0, int t) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int i = t + 256 * u, r = i >> 4, c = i & 15;
+        const int m = m0 + r, kk = k0 + 4 * c;
+        sr.x[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (m < a.m && kk < a.k) sr.x[u] = *reinterpret_cast<const float4*>(a.x + (size_t)m * a.ldx + kk);
+    }
     if (QT == L3P_Q8_0) {
         const int r = t >> 2, blk = (t >> 1) & 1, half = t & 1;
         const int n = n0 + r, kb = (k0 >> 5) + blk;
-        float v[16];
         if (n < a.n && 32 * kb < a.k) {
             const uint8_t* b = a.w + (size_t)n * a.rb + (size_t)kb * 34;
-            const float d = ldh(b);
-            const uint16_t* q = reinterpret_cast<const uint16_t*>(b + 2 + 16 * half);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const uint32_t u = q[j];
-                v[2 * j] = (float)(int8_t)(u & 0xffu) * d;
-                v[2 * j + 1] = (float)(int8_t)(u >> 8) * d;
-            }
+            sr.d = *reinterpret_cast<const uint16_t*>(b);
+            // 2-byte aligned: one unaligned 16-byte load, left untouched until
+            // store_step so that nothing waits for it here
+            __builtin_memcpy(&sr.q, b + 2 + 16 * half, 16);
         } else {
-#pragma unroll
-            for (int j = 0; j < 16; ++j) v[j] = 0.0f;
+            sr.d = 0u;
+            sr.q = make_uint4(0u, 0u, 0u, 0u);
         }
+    }
+}
+
+// The step's tiles into LDS, rows padded to kLDK floats: X as fetched, W rows
+// [n0, n0+64) x columns [k0, k0+64) dequantized exactly.  Q8_0 expands
+// (float)q * d as dequantize_row_q8_0 (c:691-702); the other types go
+// element by element through the reference-exact dequantizer, reading the
+// weight bytes here.
+template <int QT>
+__device__ __forceinline__ void store_step(float* xs, float* ws, const StepRegs<QT>& sr, const GemmArgs& a, int n0,
+                                           int k0, int t) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int i = t + 256 * u, r = i >> 4, c = i & 15;
+        *reinterpret_cast<float4*>(xs + r * kLDK + 4 * c) = sr.x[u];
+    }
+    if (QT == L3P_Q8_0) {
+        const int r = t >> 2, blk = (t >> 1) & 1, half = t & 1;
+        const float d = h2f_exact(sr.d);
+        const uint32_t qw[4] = {sr.q.x, sr.q.y, sr.q.z, sr.q.w};
+        float v[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) v[j] = (float)(int8_t)((qw[j >> 2] >> (8 * (j & 3))) & 0xffu) * d;
         float4* dst = reinterpret_cast<float4*>(ws + r * kLDK + 32 * blk + 16 * half);
 #pragma unroll
         for (int j = 0; j < 4; ++j) dst[j] = make_float4(v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
@@ -96,18 +130,13 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmArgs a) {
 #pragma unroll
         for (int in = 0; in < 2; ++in) acc[im][in] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 
+    StepRegs<QT> sr;
+    fetch_step<QT>(sr, a, m0, n0, 0, t);
     for (int k0 = 0; k0 < a.k; k0 += kBK) {
-        // X tile: 64 rows x 16 float4, four per thread
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int i = t + 256 * u, r = i >> 4, c = i & 15;
-            const int m = m0 + r, kk = k0 + 4 * c;
-            float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            if (m < a.m && kk < a.k) v = *reinterpret_cast<const float4*>(a.x + (size_t)m * a.ldx + kk);
-            *reinterpret_cast<float4*>(xs + r * kLDK + 4 * c) = v;
-        }
-        load_w_tile<QT>(ws, a, n0, k0, t);
+        store_step<QT>(xs, ws, sr, a, n0, k0, t);
         __syncthreads();
+        // the next step's loads go out before this step's matrix work
+        if (k0 + kBK < a.k) fetch_step<QT>(sr, a, m0, n0, k0 + kBK, t);
 #pragma unroll
         for (int kk = 0; kk < kBK; kk += 16) {
             float4 af[2], bf[2];

@@ -614,7 +614,10 @@ static void layers_impl(l3p_ctx* c, bool with_logits) {
 // ---------------------------------------------------------------------------
 // batched prefill (transformer_prefill, c:3439-3680)
 // ---------------------------------------------------------------------------
-static constexpr int kPrefillRows = 256;   // prompt tokens per pass over the weights
+// Prompt tokens per pass over the weights: 1024 rows give the GEMMs 16 tile
+// rows (several workgroups per CU) and cost 218 MB of row buffers at
+// Llama-3-8B's sizes.
+static constexpr int kPrefillRows = 1024;
 
 static void ensure_prefill_rows(Model& m) {
     if (m.pf_rows) return;
@@ -631,9 +634,9 @@ static void ensure_prefill_rows(Model& m) {
     m.pf_hb2 = f(m.hidden);
     m.pf_tok = (int*)m.dalloc((size_t)R * 4);
     m.pf_steps = (int*)m.dalloc((size_t)R * 8);
-    // partials for up to R tokens at the longest context, within 128 MB
+    // partials for up to R tokens at the longest context, within 512 MB
     const size_t per_token = (size_t)m.n_heads * m.max_chunks * (m.hs + 2);
-    m.pf_part_cap = std::max(per_token, std::min(per_token * R, (size_t)32 << 20));
+    m.pf_part_cap = std::max(per_token, std::min(per_token * R, (size_t)128 << 20));
     m.pf_part = (float*)m.dalloc(m.pf_part_cap * 4);
     m.pf_rows = R;
 }
