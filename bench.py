@@ -48,6 +48,15 @@ LLAMA3_8B = dict(arch="llama", dim=4096, hidden=14336, n_layers=32, n_heads=32, 
                  rope_theta=500000.0, eps=1e-5, std=0.02, seed=1234)
 
 
+# Gemma-2-2B dimensions on the reference's Gemma path (QK-norm, post norms,
+# NEOX RoPE, GeGLU, tied embedding, final logit soft-cap 30); the 4096-position
+# local window covers the whole 1024-position context, as in Gemma-2 at this
+# length.  Attention soft-capping is in neither reference engine.
+GEMMA2_2B = dict(arch="gemma3", dim=2304, hidden=9216, n_layers=26, n_heads=8, n_kv=4, head_dim=256, vocab=256000,
+                 ctx=1024, softcap=30.0, swa_window=4096, tied=True, rope_theta=10000.0, eps=1e-6, std=0.02,
+                 seed=4321)
+
+
 def gpu_q8_0_maker(ctx, torch, seed):
     """make_mat for synth.synthetic_model: N(0, std) drawn on the GPU and
     quantized to Q8_0 blocks by the library's quantizer."""
@@ -124,6 +133,49 @@ def prefill_summary(positions: int, seconds: float, stats: dict) -> dict:
                        "unit": "TFLOP/s", "frac": round(tf / MFMA_F32_PEAK_TFLOPS, 4), "flops_per_launch": flops,
                        "avg_launch_us": round(avg_us, 2), "launches": launches}
     return out
+
+
+def gemma_prompt_decode(np, torch, l3p, synth, prompt_len=512, steps=128, warmup=4):
+    """A 512-token prompt, then 128 sampled decode steps (temperature 0.9,
+    top-k 40, top-p 0.9, fixed seed) on a random-init Gemma-2-2B-architecture
+    Q8_0 model.  The prompt is run once untimed (settling launch
+    configurations) with `warmup` decode steps after it, then timed; the
+    decode steps then continue from the timed prompt."""
+    ctx = l3p.Context(0)
+    img = synth.synthetic_model(qtype=synth.Q8_0, make_mat=gpu_q8_0_maker(ctx, torch, 77), **GEMMA2_2B)
+    mi = ctx.load_gguf(img)
+    del img
+    prompt = np.random.default_rng(6).integers(0, mi.vocab_size, prompt_len).astype(np.int32)
+    sampler = dict(temperature=0.9, top_k=40, top_p=0.9)
+
+    def run(n, tok, pos, rng):
+        for _ in range(n):
+            tok, rng = ctx.decode(tok, pos, rng=rng, **sampler)
+            pos += 1
+        return tok, pos, rng
+
+    ctx.prefill(prompt[:-1], 0)
+    run(warmup, int(prompt[-1]), prompt_len - 1, 42)
+    ctx.synchronize()
+    t0 = time.perf_counter()
+    ctx.prefill(prompt[:-1], 0)
+    ctx.synchronize()
+    t_pre = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    tok, pos, rng = run(steps, int(prompt[-1]), prompt_len - 1, 42)
+    ctx.synchronize()
+    t_dec = time.perf_counter() - t0
+    ctx.profile(True)
+    ctx.prefill(prompt[:-1], 0)
+    pstats = ctx.profile_read()
+    ctx.profile(False)
+    ctx.close()
+    pre = prefill_summary(prompt_len - 1, t_pre, pstats)
+    return {"workload": "Gemma-2-2B architecture, all matrices Q8_0: 512-token prompt, then 128 decode steps "
+                        "sampled at temperature 0.9, top-k 40, top-p 0.9",
+            "layers": 26, "dim": 2304, "heads": 8, "kv_heads": 4, "head_dim": 256, "ffn": 9216, "vocab": 256000,
+            "prefill": pre, "decode_steps": steps, "decode_ms": round(t_dec * 1e3, 2),
+            "decode_tok_s": round(steps / t_dec, 1), "last_token": int(tok)}
 
 
 def measured_traffic(kernel: str):
@@ -260,6 +312,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-gemv", action="store_true", help="skip the standalone GEMV shapes")
+    ap.add_argument("--no-gemma", action="store_true", help="skip the Gemma-2-2B prompt + sampled decode run")
     ap.add_argument("--layers", type=int, default=32,
                     help="layers of the model (32 = Llama-3-8B; fewer only for short counter-collection runs)")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -353,6 +406,10 @@ def main():
 
     base = None if a.no_cpu else cpu_baseline(img, a.cpu_seconds)
     del img
+    ctx.close()
+    gemma = None if a.no_gemma else gemma_prompt_decode(np, torch, l3p, synth)
+    if gemma:
+        print(f"[bench] gemma-2-2b: {json.dumps(gemma)}", file=sys.stderr, flush=True)
 
     line = {
         "metric": "quant GEMV HBM GB/s (% of peak); decode tok/s Llama-3-8B-arch Q8_0, 1 GPU",
@@ -376,6 +433,7 @@ def main():
         "gemv_classes": kernels,
         "prefill": prefill,
         "gemv": gemv,
+        "gemma_2b_prompt_decode": gemma,
         "cpu_baseline": base,
     }
     print(json.dumps(line), flush=True)

@@ -245,6 +245,10 @@ PATH_CASES = {
     "gemma_hs128": (dict(arch="gemma3", dim=512, hidden=512, n_layers=6, n_heads=8, n_kv=2, head_dim=128, vocab=512,
                          ctx=1024, qtype=synth.Q8_0, seed=34, softcap=30.0, swa_window=101, norm_jitter=0.1,
                          tied=True), 600),
+    # more than 64 chunks of 64 positions (4300 positions: 68 chunks), so the
+    # chunk merge takes two rounds
+    "llama_long": (dict(arch="llama", dim=256, hidden=256, n_layers=2, n_heads=4, n_kv=2, vocab=512, ctx=4608,
+                        qtype=synth.Q8_0, seed=35, norm_jitter=0.1), 4300),
 }
 
 
