@@ -50,6 +50,14 @@ int l3p_create(int device, l3p_ctx** out) {
             delete c;
             throw L3pError{L3P_E_HIP, std::string("hipStreamCreate: ") + hipGetErrorString(e)};
         }
+        const size_t ws_floats = (size_t)16 << 20;   // 64 MB of GEMM split-K partials
+        e = hipMalloc(&c->gemm_ws, ws_floats * 4);
+        if (e != hipSuccess) {
+            hipStreamDestroy(c->stream);
+            delete c;
+            throw L3pError{L3P_E_HIP, std::string("hipMalloc: ") + hipGetErrorString(e)};
+        }
+        c->gemm_ws_floats = ws_floats;
         *out = c;
     });
 }
@@ -62,6 +70,7 @@ void l3p_destroy(l3p_ctx* c) {
     delete c->model;
     c->model = nullptr;
     c->prof.release();
+    if (c->gemm_ws) hipFree(c->gemm_ws);
     hipStreamDestroy(c->stream);
     delete c;
 }

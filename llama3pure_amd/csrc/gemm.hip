@@ -19,6 +19,15 @@
 //      its four k values of a 16-wide slab with one ds_read_b128.
 // Several workgroups per CU (a 1024-row prompt pass gives four per CU at
 // N = 4096) and the one-step-ahead loads hide the load latency.
+//
+// One launch covers up to three matrices with the same K and X (q|k|v,
+// gate|up): blockIdx.x runs over the N tiles of the segments in order.  When
+// the tiles cannot give every CU four workgroups, K is split over blockIdx.z:
+// each split writes its fp32 partial tile to a workspace and
+// gemm_reduce_kernel adds the splits in split order, so results do not
+// depend on scheduling.
+#include <algorithm>
+
 #include "dequant.h"
 #include "device_common.h"
 #include "internal.h"
@@ -33,14 +42,21 @@ constexpr int kLDK = kBK + 4;   // LDS row stride in floats (b128 reads spread o
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 struct GemmArgs {
-    const uint8_t* w;
-    size_t rb;        // bytes per weight row
-    int n, k, m;      // output features, inputs, batch rows
+    const uint8_t* w[3];   // per segment: weight rows,
+    float* y[3];           // output rows [m][ldy],
+    int ldy[3];
+    int n[3];              // output features,
+    int noff[3];           // first column in the split workspace's rows
+    int tbeg[4];           // first N tile (tbeg[nseg] = all tiles)
+    int nseg;
+    size_t rb;             // bytes per weight row (same K and type for every segment)
+    int k, m;              // inputs, batch rows
     const float* x;
     int ldx;
-    float* y;
-    int ldy;
-    int add;          // 1: Y += W.X (residual), 0: Y = W.X
+    int add;               // 1: Y += W.X (residual), 0: Y = W.X
+    int nsplit, ksteps;    // K splits and kBK-steps per split
+    float* part;           // [nsplit][m][ntot] partials when nsplit > 1
+    int ntot;
 };
 
 // The global data of one K step, held in registers from the step before so
@@ -55,7 +71,8 @@ struct StepRegs {
 };
 
 template <int QT>
-__device__ __forceinline__ void fetch_step(StepRegs<QT>& sr, const GemmArgs& a, int m0, int n0, int k0, int t) {
+__device__ __forceinline__ void fetch_step(StepRegs<QT>& sr, const GemmArgs& a, const uint8_t* W, int N, int m0, int n0,
+                                           int k0, int t) {
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
         const int i = t + 256 * u, r = i >> 4, c = i & 15;
@@ -66,8 +83,8 @@ __device__ __forceinline__ void fetch_step(StepRegs<QT>& sr, const GemmArgs& a, 
     if (QT == L3P_Q8_0) {
         const int r = t >> 2, blk = (t >> 1) & 1, half = t & 1;
         const int n = n0 + r, kb = (k0 >> 5) + blk;
-        if (n < a.n && 32 * kb < a.k) {
-            const uint8_t* b = a.w + (size_t)n * a.rb + (size_t)kb * 34;
+        if (n < N && 32 * kb < a.k) {
+            const uint8_t* b = W + (size_t)n * a.rb + (size_t)kb * 34;
             sr.d = *reinterpret_cast<const uint16_t*>(b);
             // 2-byte aligned: one unaligned 16-byte load, left untouched until
             // store_step so that nothing waits for it here
@@ -85,8 +102,8 @@ __device__ __forceinline__ void fetch_step(StepRegs<QT>& sr, const GemmArgs& a, 
 // element by element through the reference-exact dequantizer, reading the
 // weight bytes here.
 template <int QT>
-__device__ __forceinline__ void store_step(float* xs, float* ws, const StepRegs<QT>& sr, const GemmArgs& a, int n0,
-                                           int k0, int t) {
+__device__ __forceinline__ void store_step(float* xs, float* ws, const StepRegs<QT>& sr, const GemmArgs& a,
+                                           const uint8_t* W, int N, int n0, int k0, int t) {
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
         const int i = t + 256 * u, r = i >> 4, c = i & 15;
@@ -106,8 +123,8 @@ __device__ __forceinline__ void store_step(float* xs, float* ws, const StepRegs<
         // 4096 values, 16 per thread: row t/4, columns 16*(t%4) .. +16
         const int r = t >> 2, c0 = 16 * (t & 3);
         const int n = n0 + r;
-        const bool ok = n < a.n;
-        const uint8_t* row = a.w + (size_t)(ok ? n : 0) * a.rb;
+        const bool ok = n < N;
+        const uint8_t* row = W + (size_t)(ok ? n : 0) * a.rb;
 #pragma unroll 4
         for (int j = 0; j < 16; ++j) {
             const int kk = k0 + c0 + j;
@@ -121,7 +138,12 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmArgs a) {
     __shared__ __align__(16) float xs[kBM * kLDK];
     __shared__ __align__(16) float ws[kBN * kLDK];
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-    const int n0 = blockIdx.x * kBN, m0 = blockIdx.y * kBM;
+    const int tile = blockIdx.x;
+    const int sg = (a.nseg > 1 && tile >= a.tbeg[1]) ? ((a.nseg > 2 && tile >= a.tbeg[2]) ? 2 : 1) : 0;
+    const uint8_t* W = a.w[sg];
+    const int N = a.n[sg];
+    const int n0 = (tile - a.tbeg[sg]) * kBN, m0 = blockIdx.y * kBM;
+    const int kbeg = blockIdx.z * a.ksteps * kBK, kend = min(a.k, kbeg + a.ksteps * kBK);
     const int wm = w >> 1, wn = w & 1;      // this wave's 32 x 32 quarter
     const int g = lane >> 4, i16 = lane & 15;
     floatx4 acc[2][2];
@@ -131,12 +153,12 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmArgs a) {
         for (int in = 0; in < 2; ++in) acc[im][in] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 
     StepRegs<QT> sr;
-    fetch_step<QT>(sr, a, m0, n0, 0, t);
-    for (int k0 = 0; k0 < a.k; k0 += kBK) {
-        store_step<QT>(xs, ws, sr, a, n0, k0, t);
+    fetch_step<QT>(sr, a, W, N, m0, n0, kbeg, t);
+    for (int k0 = kbeg; k0 < kend; k0 += kBK) {
+        store_step<QT>(xs, ws, sr, a, W, N, n0, k0, t);
         __syncthreads();
         // the next step's loads go out before this step's matrix work
-        if (k0 + kBK < a.k) fetch_step<QT>(sr, a, m0, n0, k0 + kBK, t);
+        if (k0 + kBK < kend) fetch_step<QT>(sr, a, W, N, m0, n0, k0 + kBK, t);
 #pragma unroll
         for (int kk = 0; kk < kBK; kk += 16) {
             float4 af[2], bf[2];
@@ -161,6 +183,9 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmArgs a) {
         __syncthreads();
     }
     // D layout of the 16 x 16 tile: lane (g, i16) holds rows 4g..4g+3 of column i16
+    float* const Y = a.y[sg];
+    const int ldy = a.ldy[sg];
+    float* const P = a.nsplit > 1 ? a.part + (size_t)blockIdx.z * a.m * a.ntot + a.noff[sg] : nullptr;
 #pragma unroll
     for (int im = 0; im < 2; ++im)
 #pragma unroll
@@ -169,18 +194,36 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmArgs a) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int m = m0 + 32 * wm + 16 * im + 4 * g + r;
-                if (m < a.m && n < a.n) {
-                    float* p = a.y + (size_t)m * a.ldy + n;
+                if (m < a.m && n < N) {
                     const float v = acc[im][in][r];
-                    *p = a.add ? *p + v : v;
+                    if (a.nsplit > 1) {
+                        P[(size_t)m * a.ntot + n] = v;
+                    } else {
+                        float* p = Y + (size_t)m * ldy + n;
+                        *p = a.add ? *p + v : v;
+                    }
                 }
             }
         }
 }
 
+// Y (=|+=) the sum of the K splits' partials, in split order: one thread per
+// output, blockIdx.y = batch row.
+__global__ void __launch_bounds__(256) gemm_reduce_kernel(GemmArgs a) {
+    const int c = blockIdx.x * 256 + threadIdx.x, m = blockIdx.y;
+    if (c >= a.ntot) return;
+    const int sg = (a.nseg > 1 && c >= a.noff[1]) ? ((a.nseg > 2 && c >= a.noff[2]) ? 2 : 1) : 0;
+    const float* p = a.part + (size_t)m * a.ntot + c;
+    const size_t zs = (size_t)a.m * a.ntot;
+    float v = p[0];
+    for (int z = 1; z < a.nsplit; ++z) v += p[z * zs];
+    float* y = a.y[sg] + (size_t)m * a.ldy[sg] + (c - a.noff[sg]);
+    *y = a.add ? *y + v : v;
+}
+
 template <int QT>
 void launch_typed(const GemmArgs& a, hipStream_t st) {
-    const dim3 grid((a.n + kBN - 1) / kBN, (a.m + kBM - 1) / kBM);
+    const dim3 grid(a.tbeg[a.nseg], (a.m + kBM - 1) / kBM, a.nsplit);
     launch_kernel(gemm_kernel<QT>, grid, dim3(256), 0u, st, a);
 }
 
@@ -197,15 +240,51 @@ bool gemm_mfma_supported(int type) {
     }
 }
 
-void launch_gemm(int type, const uint8_t* w, int n, int k, const float* x, int m, int ldx, float* y, int ldy,
-                 bool add, hipStream_t st) {
-    L3P_REQUIRE(gemm_mfma_supported(type), L3P_E_UNSUPPORTED, "gemm: type %d has no MFMA path", type);
-    L3P_REQUIRE(k % 32 == 0 && ldx % 4 == 0 && ((uintptr_t)x & 15) == 0, L3P_E_INVALID,
+void launch_gemm(const GemmJob& j, float* ws, size_t ws_floats, hipStream_t st) {
+    L3P_REQUIRE(gemm_mfma_supported(j.type), L3P_E_UNSUPPORTED, "gemm: type %d has no MFMA path", j.type);
+    L3P_REQUIRE(j.k % 32 == 0 && j.ldx % 4 == 0 && ((uintptr_t)j.x & 15) == 0, L3P_E_INVALID,
                 "gemm: x rows must be 16-byte aligned");
-    L3P_REQUIRE(m <= 65535 * kBM, L3P_E_INVALID, "gemm: batch %d too large", m);
-    if (m == 0 || n == 0) return;
-    GemmArgs a{w, type_row_bytes(type, k), n, k, m, x, ldx, y, ldy, add ? 1 : 0};
-    switch (type) {
+    L3P_REQUIRE(j.m <= 65535 * kBM, L3P_E_INVALID, "gemm: batch %d too large", j.m);
+    L3P_REQUIRE(j.nseg >= 1 && j.nseg <= 3, L3P_E_INVALID, "gemm: %d segments", j.nseg);
+    GemmArgs a{};
+    a.nseg = 0;
+    int tiles = 0, ntot = 0;
+    for (int i = 0; i < j.nseg; ++i) {
+        if (j.seg[i].n == 0) continue;
+        a.w[a.nseg] = j.seg[i].w;
+        a.y[a.nseg] = j.seg[i].y;
+        a.ldy[a.nseg] = j.seg[i].ldy;
+        a.n[a.nseg] = j.seg[i].n;
+        a.noff[a.nseg] = ntot;
+        a.tbeg[a.nseg] = tiles;
+        tiles += (j.seg[i].n + kBN - 1) / kBN;
+        ntot += j.seg[i].n;
+        ++a.nseg;
+    }
+    if (j.m == 0 || a.nseg == 0) return;
+    a.tbeg[a.nseg] = tiles;
+    a.rb = type_row_bytes(j.type, j.k);
+    a.k = j.k;
+    a.m = j.m;
+    a.x = j.x;
+    a.ldx = j.ldx;
+    a.add = j.add ? 1 : 0;
+    a.ntot = ntot;
+    // K splits while the tiles give fewer than four workgroups per CU (the
+    // LDS of four fits a CU), each split at least eight K steps long
+    const int steps = (j.k + kBK - 1) / kBK;
+    const int mt = (j.m + kBM - 1) / kBM;
+    const int want = 4 * device_cus();
+    int split = 1;
+    if (ws && (long)tiles * mt < want) {
+        split = std::min({(int)((want + (long)tiles * mt - 1) / ((long)tiles * mt)), steps / 8, 8});
+        while (split > 1 && (size_t)split * j.m * ntot > ws_floats) --split;
+        split = std::max(split, 1);
+    }
+    a.ksteps = (steps + split - 1) / split;
+    a.nsplit = (steps + a.ksteps - 1) / a.ksteps;   // no empty split
+    a.part = a.nsplit > 1 ? ws : nullptr;
+    switch (j.type) {
     case L3P_Q8_0: launch_typed<L3P_Q8_0>(a, st); break;
     case L3P_Q2_K: launch_typed<L3P_Q2_K>(a, st); break;
     case L3P_Q3_K: launch_typed<L3P_Q3_K>(a, st); break;
@@ -216,4 +295,5 @@ void launch_gemm(int type, const uint8_t* w, int n, int k, const float* x, int m
     case L3P_F32: launch_typed<L3P_F32>(a, st); break;
     default: launch_typed<L3P_BF16>(a, st); break;
     }
+    if (a.nsplit > 1) launch_kernel(gemm_reduce_kernel, dim3((ntot + 255) / 256, j.m), dim3(256), 0u, st, a);
 }

@@ -1010,17 +1010,7 @@ __global__ void __launch_bounds__(1024) gemv_kernel(GemvArgs a) {
 // ---------------------------------------------------------------------------
 // launch
 // ---------------------------------------------------------------------------
-int cus() {
-    static int n = 0;
-    if (!n) {
-        int dev = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-            n = 0;
-        if (n <= 0) n = 256;
-    }
-    return n;
-}
+int cus() { return device_cus(); }
 
 template <typename K>
 int occupancy(K kern, int threads, size_t lds) {
@@ -1120,6 +1110,18 @@ void launch_type(GemvArgs a, bool pair, int G, hipStream_t st) {
 }
 
 }  // namespace
+
+int device_cus() {
+    static int n = 0;
+    if (!n) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            n = 0;
+        if (n <= 0) n = 256;
+    }
+    return n;
+}
 
 bool gemv_supported(int type, int cols) {
     int unit;

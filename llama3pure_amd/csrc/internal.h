@@ -126,11 +126,30 @@ bool gemv_supported(int type, int cols);
 void launch_gemv(int type, const GemvBatch& b, int cols, const float* x, const float* norm, float eps,
                  hipStream_t s);
 // gemm.hip: Y[m][n] (=|+=) W[n,:] . X[m,:] on the fp32 matrix cores, for the
-// types the reference dequantizes before its batched dot (Q8_0, Q4_K, Q6_K).
-// x rows must be 16-byte aligned (ldx a multiple of 4).
+// types the reference dequantizes before its batched dot (Q8_0, the K-quants,
+// F16, BF16, F32).  x rows must be 16-byte aligned (ldx a multiple of 4).
+// One launch takes up to three matrices of one type and K over the same X
+// (q|k|v, gate|up); with a workspace ws of ws_floats floats, K is split when
+// the output tiles are too few to fill the GPU.
+struct GemmSegment {
+    const uint8_t* w;
+    int n;        // output features (weight rows)
+    float* y;
+    int ldy;
+};
+struct GemmJob {
+    int type;
+    GemmSegment seg[3];
+    int nseg;
+    int k;
+    const float* x;
+    int m, ldx;
+    bool add;
+};
 bool gemm_mfma_supported(int type);
-void launch_gemm(int type, const uint8_t* w, int n, int k, const float* x, int m, int ldx, float* y, int ldy,
-                 bool add, hipStream_t s);
+void launch_gemm(const GemmJob& j, float* ws, size_t ws_floats, hipStream_t s);
+// compute units of the current device
+int device_cus();
 // blocks.hip
 void launch_quantize_q8_0_blocks(const float* x, int64_t n, uint8_t* dst, hipStream_t s);
 void launch_dequant(int type, const uint8_t* src, int64_t n, float* dst, hipStream_t s);

@@ -8,6 +8,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <initializer_list>
 #include <memory>
 #include <new>
 #include <string>
@@ -647,21 +648,59 @@ static std::string gemm_label(const char* what, int type, int rows, int n, int k
     return b;
 }
 
-// y rows (=|+=) W . x rows for `rows` prompt tokens: the MFMA GEMM, or for
-// Q4_0 the GEMV per row, which quantizes each row to Q8_0 and takes the
-// reference's integer block dots (matmul_quantized_batch, c:2305-2318).
-static void gemm_rows(l3p_ctx* c, const Mat& W, const float* x, int ldx, int rows, float* y, int ldy, bool add,
+// One matrix of a prompt pass: W . x rows into y rows [rows][ldy].
+struct RowsOut {
+    const Mat* W;
+    float* y;
+    int ldy;
+    const char* what;
+};
+
+// y rows (=|+=) W . x rows for `rows` prompt tokens, for one to three
+// matrices over the same x rows.  Matrices of one MFMA type and width run as
+// one GEMM launch (label `what`); the Q8_0-activation types run the GEMV per
+// row, which quantizes each row to Q8_0 and takes the reference's integer
+// block dots (matmul_quantized_batch, c:2305-2318).
+static void gemm_rows(l3p_ctx* c, std::initializer_list<RowsOut> outs, const float* x, int ldx, int rows, bool add,
                       const char* what) {
     hipStream_t s = c->stream;
-    ProfRange r(c->prof, s, gemm_label(what, W.type, rows, W.rows, W.cols),
-                gemv_bytes(W.type, W.rows, W.cols, W.rows) + 4.0 * rows * (W.cols + W.rows));
-    if (gemm_mfma_supported(W.type)) {
-        launch_gemm(W.type, W.w, W.rows, W.cols, x, rows, ldx, y, ldy, add, s);
+    const RowsOut* o = outs.begin();
+    const int n = (int)outs.size();
+    bool together = gemm_mfma_supported(o[0].W->type);
+    for (int i = 1; i < n; ++i) together = together && o[i].W->type == o[0].W->type && o[i].W->cols == o[0].W->cols;
+    if (together) {
+        GemmJob j{};
+        j.type = o[0].W->type;
+        j.nseg = n;
+        j.k = o[0].W->cols;
+        j.x = x;
+        j.m = rows;
+        j.ldx = ldx;
+        j.add = add;
+        int ntot = 0;
+        double bytes = 0.0;
+        for (int i = 0; i < n; ++i) {
+            j.seg[i] = GemmSegment{o[i].W->w, o[i].W->rows, o[i].y, o[i].ldy};
+            ntot += o[i].W->rows;
+            bytes += gemv_bytes(j.type, o[i].W->rows, j.k, o[i].W->rows);
+        }
+        ProfRange r(c->prof, s, gemm_label(n > 1 ? what : o[0].what, j.type, rows, ntot, j.k),
+                    bytes + 4.0 * rows * (j.k + ntot));
+        launch_gemm(j, c->gemm_ws, c->gemm_ws_floats, s);
         return;
     }
-    for (int b = 0; b < rows; ++b)
-        launch_gemv(W.type, one(W, y + (size_t)b * ldy, add ? EPI_ADD : EPI_STORE), W.cols, x + (size_t)b * ldx,
-                    nullptr, 0.0f, s);
+    for (int i = 0; i < n; ++i) {
+        const Mat& W = *o[i].W;
+        if (gemm_mfma_supported(W.type)) {
+            gemm_rows(c, {o[i]}, x, ldx, rows, add, o[i].what);
+            continue;
+        }
+        ProfRange r(c->prof, s, gemm_label(o[i].what, W.type, rows, W.rows, W.cols),
+                    gemv_bytes(W.type, W.rows, W.cols, W.rows) + 4.0 * rows * (W.cols + W.rows));
+        for (int b = 0; b < rows; ++b)
+            launch_gemv(W.type, one(W, o[i].y + (size_t)b * o[i].ldy, add ? EPI_ADD : EPI_STORE), W.cols,
+                        x + (size_t)b * ldx, nullptr, 0.0f, s);
+    }
 }
 
 // Positions [start, start + n) of a prompt, kPrefillRows tokens per pass:
@@ -684,9 +723,8 @@ static void prefill_batched(l3p_ctx* c, const int32_t* tokens, int n, int start)
         for (int l = 0; l < m.n_layers; ++l) {
             const Layer& L = m.layers[l];
             launch_rmsnorm_rows(m.pf_x, D, L.att_norm, D, m.inv_dim, eps, m.pf_xb, XB, R, s);
-            gemm_rows(c, L.wq, m.pf_xb, XB, R, m.pf_q, QD, false, "q");
-            gemm_rows(c, L.wk, m.pf_xb, XB, R, m.pf_k, KD, false, "k");
-            gemm_rows(c, L.wv, m.pf_xb, XB, R, m.pf_v, KD, false, "v");
+            gemm_rows(c, {{&L.wq, m.pf_q, QD, "q"}, {&L.wk, m.pf_k, KD, "k"}, {&L.wv, m.pf_v, KD, "v"}}, m.pf_xb, XB,
+                      R, false, "q|k|v");
             // attention of the rows, as many tokens per launch as the partials hold
             const size_t per_token =
                 (size_t)m.n_heads * attention_chunks(m, l, start + b0 + R - 1) * (m.hs + 2);
@@ -699,20 +737,19 @@ static void prefill_batched(l3p_ctx* c, const int32_t* tokens, int n, int start)
                                       QD, KD, QD, nz, start + b0 + z0 + nz - 1, m.pf_part, m.pf_part_cap, s);
             }
             if (m.is_gemma) {
-                gemm_rows(c, L.wo, m.pf_att, QD, R, m.pf_xb2, D, false, "wo");
+                gemm_rows(c, {{&L.wo, m.pf_xb2, D, "wo"}}, m.pf_att, QD, R, false, "wo");
                 launch_rmsnorm_add_rows(m.pf_xb2, D, L.post_att, D, m.inv_dim, eps, m.pf_x, D, R, s);
             } else {
-                gemm_rows(c, L.wo, m.pf_att, QD, R, m.pf_x, D, true, "wo");
+                gemm_rows(c, {{&L.wo, m.pf_x, D, "wo"}}, m.pf_att, QD, R, true, "wo");
             }
             launch_rmsnorm_rows(m.pf_x, D, L.ffn_norm, D, m.inv_dim, eps, m.pf_xb, XB, R, s);
-            gemm_rows(c, L.w1, m.pf_xb, XB, R, m.pf_hb, H, false, "gate");
-            gemm_rows(c, L.w3, m.pf_xb, XB, R, m.pf_hb2, H, false, "up");
+            gemm_rows(c, {{&L.w1, m.pf_hb, H, "gate"}, {&L.w3, m.pf_hb2, H, "up"}}, m.pf_xb, XB, R, false, "gate|up");
             launch_act_rows(m.pf_hb, m.pf_hb2, (int64_t)R * H, m.is_gemma, s);
             if (m.is_gemma) {
-                gemm_rows(c, L.w2, m.pf_hb, H, R, m.pf_xb2, D, false, "down");
+                gemm_rows(c, {{&L.w2, m.pf_xb2, D, "down"}}, m.pf_hb, H, R, false, "down");
                 launch_rmsnorm_add_rows(m.pf_xb2, D, L.post_ffn, D, m.inv_dim, eps, m.pf_x, D, R, s);
             } else {
-                gemm_rows(c, L.w2, m.pf_hb, H, R, m.pf_x, D, true, "down");
+                gemm_rows(c, {{&L.w2, m.pf_x, D, "down"}}, m.pf_hb, H, R, true, "down");
             }
         }
     }
@@ -872,7 +909,15 @@ static void sample_impl(l3p_ctx* c, const float* logits, int n, const l3p_sample
 void run_gemm(l3p_ctx* c, int type, const uint8_t* w, int rows, int cols, const float* x, int batch, int in_stride,
               float* y, int out_stride) {
     if (gemm_mfma_supported(type)) {
-        launch_gemm(type, w, rows, cols, x, batch, in_stride, y, out_stride, false, c->stream);
+        GemmJob j{};
+        j.type = type;
+        j.seg[0] = GemmSegment{w, rows, y, out_stride};
+        j.nseg = 1;
+        j.k = cols;
+        j.x = x;
+        j.m = batch;
+        j.ldx = in_stride;
+        launch_gemm(j, c->gemm_ws, c->gemm_ws_floats, c->stream);
         return;
     }
     // Q4_0: the reference quantizes every batch row to Q8_0 and takes integer

@@ -109,6 +109,10 @@ struct l3p_ctx {
     hipGraphExec_t graph[4] = {nullptr, nullptr, nullptr, nullptr};
     int graph_runs[4] = {0, 0, 0, 0};
     bool attn_per_head = false;   // the attention of the step being recorded
+    // split-K partials of the prefill GEMM (allocated with the context, so
+    // no GEMM call allocates)
+    float* gemm_ws = nullptr;
+    size_t gemm_ws_floats = 0;
     void drop_graphs();
 };
 

@@ -228,6 +228,26 @@ def test_head_shapes(torch_gpu, cpuref, dim, heads, kv):
         m.close()
 
 
+def test_prefill_split_k_residual(torch_gpu, cpuref):
+    """A prompt pass whose down projection (K = 2048 over 4 output tiles) runs
+    as a split-K GEMM adding into the residual rows through the split
+    reduction: the logits of the next steps within the full-model
+    tolerance."""
+    g = synth.synthetic_model(arch="llama", dim=256, hidden=2048, n_layers=2, n_heads=8, n_kv=2, vocab=512, ctx=128,
+                              qtype=synth.Q8_0, seed=41, norm_jitter=0.1)
+    toks = np.random.default_rng(41).integers(0, 512, 45).astype(np.int32)
+    with l3p.Context(0) as c2:
+        c2.load_gguf(g)
+        m = cpuref.open_model(g)
+        c2.prefill(toks[:40], 0)
+        m.prefill(toks, 0, 40)
+        for i in range(40, 45):
+            a = m.forward(int(toks[i]), i)
+            b = c2.forward(int(toks[i]), i)
+            assert float(np.max(np.abs(a - b))) <= 1e-2 * rms(a), i
+        m.close()
+
+
 PATH_CASES = {
     # head size 64 (60-position chunks), 1400 positions: 24 chunks, 2 per wave for most waves
     "llama_hs64": (dict(arch="llama", dim=512, hidden=512, n_layers=3, n_heads=8, n_kv=2, vocab=512, ctx=2048,
