@@ -948,10 +948,14 @@ __global__ void argmax_final_kernel(const float* cv, const int* ci, int nc, int*
 // it is strictly greater.  The final slot order matters to the reference's
 // later arithmetic (its pre-sort sum and, with top_p >= 1, its CDF walk), so
 // it is reproduced, not just the top-k set.  Kernel 1 computes the maximum of
-// every group of 64 logits (indices >= k); kernel 2, one wave, walks the
-// groups in order and only visits groups whose maximum beats the current
-// minimum.
+// every group of 64 logits (indices >= k); kernel 2 walks the groups in order
+// and only visits groups whose maximum beats the current minimum.  Kernel 2
+// is one workgroup: waves 1..15 stream the logits and group maxima through
+// LDS in blocks of kScanBlock while wave 0, which holds the slots, scans the
+// previous block there, so a visited group costs an LDS read rather than a
+// dependent global load.
 constexpr int kSlotsPerLane = 16;            // k <= 1024
+constexpr int kScanBlock = 16384;            // logits per LDS block (256 groups)
 
 __global__ void __launch_bounds__(1024) topk_groupmax_kernel(const float* __restrict__ l, int n, int k, int ng,
                                                              float* gmax) {
@@ -963,73 +967,119 @@ __global__ void __launch_bounds__(1024) topk_groupmax_kernel(const float* __rest
     if (lane == 0 && g < ng) gmax[g] = v;
 }
 
-__device__ __forceinline__ bool slot_less(float v, int s, float bv, int bs) {
-    return v < bv || (v == bv && s < bs);
-}
-
-__global__ void __launch_bounds__(64) topk_scan_kernel(const float* __restrict__ l, int n, int k,
-                                                       const float* __restrict__ gmax, int ng, float* out_v,
-                                                       int* out_i) {
-    const int lane = threadIdx.x;
-    float sv[kSlotsPerLane];
-    int si[kSlotsPerLane];
-#pragma unroll
-    for (int j = 0; j < kSlotsPerLane; ++j) {
-        const int s = lane + 64 * j;
-        sv[j] = s < k ? l[s] : INFINITY;
-        si[j] = s < k ? s : -1;
-    }
-    // current minimum over slots: (value, slot) with the lowest slot on ties
-    auto find_min = [&](float& mv, int& ms) {
-        float bv = INFINITY;
-        int bs = 0x7fffffff;
-#pragma unroll
-        for (int j = 0; j < kSlotsPerLane; ++j) {
-            const int s = lane + 64 * j;
-            if (s < k && slot_less(sv[j], s, bv, bs)) { bv = sv[j]; bs = s; }
+// R: slot rows of 64 in use (k <= 64 R), so the minimum search after each
+// replacement only visits live rows
+template <int R>
+__global__ void __launch_bounds__(1024) topk_scan_kernel(const float* __restrict__ l, int n, int k,
+                                                         const float* __restrict__ gmax, int ng, float* out_v,
+                                                         int* out_i) {
+    static_assert(R >= 1 && R <= kSlotsPerLane, "slot rows");
+    extern __shared__ __align__(16) float tl[];   // [2][kScanBlock] logits, then [2][256] group maxima
+    float* tg = tl + 2 * kScanBlock;
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int nblk = (n + kScanBlock - 1) / kScanBlock;
+    // block b into buffer b & 1 by waves 1..15: 64-float pieces, each lane one
+    // dword (indices past the end repeat the last logit or group maximum; the
+    // scan masks them by index)
+    auto fill = [&](int b) {
+        float* dst = tl + (b & 1) * kScanBlock;
+        for (int pc = w - 1; pc < kScanBlock / 64; pc += 15) {
+            const int i = min(b * kScanBlock + 64 * pc + lane, n - 1);
+            __builtin_amdgcn_global_load_lds(l + i, (lds_void*)(dst + 64 * pc), 4, 0, 0);
         }
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
-            const float ov = __shfl_xor(bv, o, 64);
-            const int os = __shfl_xor(bs, o, 64);
-            if (slot_less(ov, os, bv, bs)) { bv = ov; bs = os; }
+        if (w <= 4) {
+            const int gi = min(b * (kScanBlock / 64) + 64 * (w - 1) + lane, ng - 1);
+            __builtin_amdgcn_global_load_lds(gmax + gi, (lds_void*)(tg + (b & 1) * 256 + 64 * (w - 1)), 4, 0, 0);
         }
-        mv = bv;
-        ms = bs;
     };
-    float cur;
-    int cur_slot;
-    find_min(cur, cur_slot);
-    for (int g0 = 0; g0 < ng; g0 += 64) {
-        const float gm = (g0 + lane < ng) ? gmax[g0 + lane] : -INFINITY;
-        uint64_t flagged = __ballot(gm > cur);
-        while (flagged) {
-            const int j = __ffsll((unsigned long long)flagged) - 1;
-            flagged &= flagged - 1;
-            if (!(__shfl(gm, j, 64) > cur)) continue;
-            const int base = 64 * (g0 + j);
-            const int i = base + lane;
-            const float v = (i >= k && i < n) ? l[i] : -INFINITY;
-            uint64_t cand = __ballot(v > cur);
-            while (cand) {
-                const int c = __ffsll((unsigned long long)cand) - 1;
-                cand &= cand - 1;
-                const float bv = __shfl(v, c, 64);
-                if (bv > cur) {
-                    if (lane == (cur_slot & 63)) {
+    if (w > 0) fill(0);
+    float sv[R];
+    int si[R];
+    float cur = 0.0f;
+    int cur_slot = 0;
+    // The reference's minimum (c:4819-4826, 4835-4842): it starts at slot 0
+    // and moves to a slot only on a strictly smaller value, so it is the
+    // first slot holding the smallest value, NaN slots never chosen unless
+    // slot 0 is NaN (which then stays the minimum).  Lane minima, a register
+    // butterfly minimum, then the first slot row whose ballot holds it.
+    auto find_min = [&](float& mv, int& ms) {
+        float lv = INFINITY;
 #pragma unroll
-                        for (int jj = 0; jj < kSlotsPerLane; ++jj)
-                            if (jj == (cur_slot >> 6)) { sv[jj] = bv; si[jj] = base + c; }
+        for (int j = 0; j < R; ++j)
+            if (lane + 64 * j < k) lv = fminf(lv, sv[j]);
+        float m = -wave_max(-lv);
+        int slot = 0;
+#pragma unroll
+        for (int j = R - 1; j >= 0; --j) {
+            if (64 * j < k) {
+                const uint64_t hit = __ballot(lane + 64 * j < k && sv[j] == m);
+                if (hit) slot = 64 * j + __ffsll((unsigned long long)hit) - 1;
+            }
+        }
+        const float s0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sv[0]), 0));
+        if (s0 != s0) {
+            m = s0;
+            slot = 0;
+        }
+        mv = m;
+        ms = slot;
+    };
+    auto lane_val = [](float v, int j) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), j)); };
+    if (w == 0) {
+#pragma unroll
+        for (int j = 0; j < R; ++j) {
+            const int s = lane + 64 * j;
+            sv[j] = s < k ? l[s] : INFINITY;
+            si[j] = s < k ? s : -1;
+        }
+        find_min(cur, cur_slot);
+    }
+    wait_vm<0>();
+    __syncthreads();
+    for (int b = 0; b < nblk; ++b) {
+        if (w > 0) {
+            if (b + 1 < nblk) fill(b + 1);
+        } else {
+            const float* lb = tl + (b & 1) * kScanBlock;
+            const float* gb = tg + (b & 1) * 256;
+            for (int j0 = 0; j0 < kScanBlock / 64; j0 += 64) {
+                const int G = b * (kScanBlock / 64) + j0 + lane;
+                const float gm = G < ng ? gb[j0 + lane] : -INFINITY;
+                uint64_t flagged = __ballot(gm > cur);
+                while (flagged) {
+                    const int j = __ffsll((unsigned long long)flagged) - 1;
+                    flagged &= flagged - 1;
+                    if (!(lane_val(gm, j) > cur)) continue;
+                    const int gofs = 64 * (j0 + j);
+                    const int base = b * kScanBlock + gofs;
+                    const int i = base + lane;
+                    const float v = (i >= k && i < n) ? lb[gofs + lane] : -INFINITY;
+                    uint64_t cand = __ballot(v > cur);
+                    while (cand) {
+                        const int c = __ffsll((unsigned long long)cand) - 1;
+                        cand &= cand - 1;
+                        const float bv = lane_val(v, c);
+                        if (bv > cur) {
+                            if (lane == (cur_slot & 63)) {
+#pragma unroll
+                                for (int jj = 0; jj < R; ++jj)
+                                    if (jj == (cur_slot >> 6)) { sv[jj] = bv; si[jj] = base + c; }
+                            }
+                            find_min(cur, cur_slot);
+                        }
                     }
-                    find_min(cur, cur_slot);
                 }
             }
         }
+        wait_vm<0>();      // this wave's copies of block b + 1 have landed
+        __syncthreads();   // and every wave's; wave 0 is done with block b
     }
+    if (w == 0) {
 #pragma unroll
-    for (int j = 0; j < kSlotsPerLane; ++j) {
-        const int s = lane + 64 * j;
-        if (s < k) { out_v[s] = sv[j]; out_i[s] = si[j]; }
+        for (int j = 0; j < R; ++j) {
+            const int s = lane + 64 * j;
+            if (s < k) { out_v[s] = sv[j]; out_i[s] = si[j]; }
+        }
     }
 }
 
@@ -1222,12 +1272,29 @@ void launch_argmax(const float* l, int n, int* out, hipStream_t s, float* cv, in
     L3P_HIP(hipGetLastError());
 }
 
+template <int R>
+static void launch_topk_scan(const float* l, int n, int k, const float* gmax, int ng, float* out_v, int* out_i,
+                             hipStream_t s) {
+    const size_t lds = (2 * (size_t)kScanBlock + 2 * 256) * 4;
+    static bool lds_set = false;   // dynamic LDS above 64 KB must be allowed first
+    if (!lds_set) {
+        L3P_HIP(hipFuncSetAttribute((const void*)topk_scan_kernel<R>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    (int)lds));
+        lds_set = true;
+    }
+    hipLaunchKernelGGL(topk_scan_kernel<R>, dim3(1), dim3(1024), lds, s, l, n, k, gmax, ng, out_v, out_i);
+    L3P_HIP(hipGetLastError());
+}
+
 void launch_topk_slots(const float* l, int n, int k, float* gmax, float* out_v, int* out_i, hipStream_t s) {
     L3P_REQUIRE(k >= 1 && k <= 64 * kSlotsPerLane && k <= n, L3P_E_UNSUPPORTED, "sampler: top_k=%d outside [1, %d]",
                 k, 64 * kSlotsPerLane);
     const int ng = sample_groups(n);
     hipLaunchKernelGGL(topk_groupmax_kernel, dim3((ng + 15) / 16), dim3(1024), 0, s, l, n, k, ng, gmax);
     L3P_HIP(hipGetLastError());
-    hipLaunchKernelGGL(topk_scan_kernel, dim3(1), dim3(64), 0, s, l, n, k, gmax, ng, out_v, out_i);
-    L3P_HIP(hipGetLastError());
+    const int rows = (k + 63) / 64;
+    if (rows <= 1) launch_topk_scan<1>(l, n, k, gmax, ng, out_v, out_i, s);
+    else if (rows <= 2) launch_topk_scan<2>(l, n, k, gmax, ng, out_v, out_i, s);
+    else if (rows <= 4) launch_topk_scan<4>(l, n, k, gmax, ng, out_v, out_i, s);
+    else launch_topk_scan<kSlotsPerLane>(l, n, k, gmax, ng, out_v, out_i, s);
 }

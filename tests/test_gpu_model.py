@@ -174,6 +174,33 @@ def test_sampler_matches_oracle(pair, ctx, cpuref, torch_gpu):
     assert t_gpu == int(np.argmax(lo))
 
 
+@pytest.mark.parametrize("vocab", [128256, 256000])
+def test_sampler_full_vocab(torch_gpu, cpuref, vocab):
+    """Top-k/top-p over full-size vocabularies (several LDS blocks of the
+    top-k scan) picks the oracle's token and RNG state: normal logits, logits
+    rounded to halves (many ties, so the lowest-slot rule decides), and
+    increasing logits (every index replaces a slot)."""
+    g = synth.synthetic_model(arch="llama", dim=64, hidden=64, n_layers=1, n_heads=2, n_kv=1, vocab=vocab, ctx=32,
+                              qtype=synth.Q8_0, seed=vocab % 1000)
+    rng = np.random.default_rng(vocab)
+    seed = 0x9E3779B97F4A7C15
+    with l3p.Context(0) as c:
+        c.load_gguf(g)
+        for trial in range(12):
+            lo = (rng.standard_normal(vocab) * 3).astype(np.float32)
+            if trial % 3 == 1:
+                lo = (np.round(lo * 2) / 2).astype(np.float32)
+            elif trial % 3 == 2:
+                lo = np.sort(lo)
+            k = [1, 40, 1000, 100, 200, 65][trial % 6]   # one to sixteen slot rows of 64
+            p = [0.9, 1.0, 0.95, 0.5][trial % 4]
+            t_gpu, s_gpu = c.sample(torch_gpu.from_numpy(lo).cuda(), vocab, temperature=0.9, top_k=k, top_p=p,
+                                    rng=seed)
+            t_ref, s_ref = cpuref.sample(lo, 0.9, k, p, seed)
+            assert (t_gpu, s_gpu) == (t_ref, s_ref), (vocab, trial, k, p)
+            seed = s_ref
+
+
 def test_graph_replay_equals_eager(torch_gpu):
     """From the second step on, the layer stack replays a captured HIP graph.
     Every replay must give exactly the eager logits and KV cache; the eager
