@@ -204,10 +204,11 @@ def calibrate_copy():
     print(json.dumps({"calibrate_copy_bytes": a.numel() * 4, "copies": 5}), flush=True)
 
 
-def attn_sweep():
+def attn_sweep(shape: str):
     """Both decode attentions at several context lengths, for a kernel trace:
-    a 2-layer Llama-3-8B-shaped model (32 query / 8 KV heads, head_dim 128,
-    4096 positions); per length P, P prompt positions, then 12 decode steps at
+    a 2-layer model with the attention of Llama-3-8B (32 query / 8 KV heads,
+    head_dim 128) or Gemma-2-2B (8 query / 4 KV heads, head_dim 256, QK-norm),
+    4096 positions; per length P, P prompt positions, then 12 decode steps at
     position P with the per-head kernel (L3P_ATTN_HEAD=1) and 12 with chunks +
     merge (=0).  Prints the order of the blocks; the kernel durations come
     from the trace."""
@@ -218,12 +219,16 @@ def attn_sweep():
     from llama3pure_amd import synth
 
     ctx = l3p.Context(0)
-    g = synth.synthetic_model(arch="llama", dim=4096, hidden=256, n_layers=2, n_heads=32, n_kv=8, vocab=256,
-                              ctx=4096, seed=3)
+    if shape == "gemma2b":
+        g = synth.synthetic_model(arch="gemma3", dim=2304, hidden=256, n_layers=2, n_heads=8, n_kv=4, head_dim=256,
+                                  vocab=256, ctx=4096, softcap=30.0, swa_window=4096, tied=True, seed=3)
+    else:
+        g = synth.synthetic_model(arch="llama", dim=4096, hidden=256, n_layers=2, n_heads=32, n_kv=8, vocab=256,
+                                  ctx=4096, seed=3)
     ctx.load_gguf(g)
     toks = np.random.default_rng(1).integers(0, 256, 4096).astype(np.int32)
     order = []
-    for P in (64, 256, 512, 1024, 2048, 3000):
+    for P in (64, 256, 512, 640, 1024, 2048, 3000):
         ctx.prefill(toks[:P], 0)
         for path in ("0", "1"):
             os.environ["L3P_ATTN_HEAD"] = path
@@ -237,9 +242,39 @@ def attn_sweep():
     ctx.close()
 
 
+GEMV_SHAPES = [("q8_0", 8, 4096, 4096), ("q4_0", 2, 14336, 4096), ("q4_0", 2, 4096, 14336), ("q4_k", 12, 14336, 4096),
+               ("q6_k", 14, 128256, 4096)]   # name, GGML type id, rows, cols
+
+
+def cpu_gemv(ref, synth) -> list:
+    """The reference's matmul_quantized (c:2091-2133) on the weight blocks
+    and activation the GPU's standalone GEMV lines use (same seeds): median of
+    repeated calls, at least 5 and about 0.5 s per shape."""
+    import numpy as np
+
+    out = []
+    for name, qt, rows, cols in GEMV_SHAPES:
+        w = synth.random_blocks(qt, rows, cols, seed=7)
+        x = synth.random_x(cols, seed=8)
+        y = np.empty(rows, np.float32)
+        call = lambda: ref.lib.ref_matmul(qt, w.ctypes.data, rows, cols, x.ctypes.data, y.ctypes.data)
+        call()
+        ts, t_end = [], time.perf_counter() + 0.5
+        while len(ts) < 5 or time.perf_counter() < t_end:
+            t0 = time.perf_counter()
+            call()
+            ts.append(time.perf_counter() - t0)
+        us = float(np.median(ts)) * 1e6
+        alg = w.nbytes + 4 * cols + 4 * rows
+        out.append({"shape": f"{name} {rows}x{cols}", "us": round(us, 1), "GB/s": round(alg / us / 1e3, 2)})
+        del w
+    return out
+
+
 def cpu_leg(path: str, seconds: float, max_tokens: int, use_ref: bool) -> dict:
     """Runs in a subprocess: the reference engine (or the oracle) decoding
-    greedily from position 0 on the GGUF at path."""
+    greedily from position 0 on the GGUF at path, then (reference only) its
+    GEMV at the standalone GEMV shapes."""
     import ctypes
 
     import numpy as np
@@ -258,6 +293,10 @@ def cpu_leg(path: str, seconds: float, max_tokens: int, use_ref: bool) -> dict:
             tok = int(ref.lib.ref_generate_token(tok, n, 0.0, 40, 0.9, ctypes.byref(seed)))
             n += 1
         dt = time.perf_counter() - t0
+        from llama3pure_amd import synth
+
+        gemv = cpu_gemv(ref, synth)
+        return {"tokens": n, "seconds": dt, "load_seconds": load_s, "gemv": gemv}
     else:
         cr = oracle.CpuRef()
         img = np.fromfile(path, np.uint8)
@@ -296,11 +335,14 @@ def cpu_baseline(img, seconds: float) -> dict | None:
         os.unlink(path)
     what = ("reference C engine built -Ofast -fopenmp (its Makefile OpenMP line)" if use_ref
             else "oracle (C restatement of the reference, -O2, one thread)")
-    return {"value": round(res["tokens"] / res["seconds"], 4), "unit": "tok/s", "cores": cores,
-            "kind": "reference" if use_ref else "port",
-            "sample": f"{what}: {res['tokens']} greedy decode tokens from position 0 of the same GGUF "
-                      f"({res['seconds']:.1f} s); per-token cost is the 8.0 GB weight stream, attention "
-                      f"over <= {res['tokens']} positions instead of 1024"}
+    out = {"value": round(res["tokens"] / res["seconds"], 4), "unit": "tok/s", "cores": cores,
+           "kind": "reference" if use_ref else "port",
+           "sample": f"{what}: {res['tokens']} greedy decode tokens from position 0 of the same GGUF "
+                     f"({res['seconds']:.1f} s); per-token cost is the 8.0 GB weight stream, attention "
+                     f"over <= {res['tokens']} positions instead of 1024"}
+    if res.get("gemv"):
+        out["gemv"] = res["gemv"]   # matmul_quantized at the standalone GEMV shapes, same blocks and x
+    return out
 
 
 def main():
@@ -317,8 +359,9 @@ def main():
                     help="layers of the model (32 = Llama-3-8B; fewer only for short counter-collection runs)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only copy 512 MiB device-to-device 5 times (scale for rocprofv3 FETCH_SIZE/WRITE_SIZE)")
-    ap.add_argument("--attn-sweep", action="store_true",
-                    help="only run both decode attentions at 65..3001 positions (for a kernel trace)")
+    ap.add_argument("--attn-sweep", nargs="?", const="llama3-8b", choices=["llama3-8b", "gemma2b"],
+                    help="only run both decode attentions at 65..3001 positions of the named attention shape "
+                         "(for a kernel trace)")
     ap.add_argument("--cpu-leg", help=argparse.SUPPRESS)
     ap.add_argument("--cpu-ref", type=int, default=1, help=argparse.SUPPRESS)
     a = ap.parse_args()
@@ -330,7 +373,7 @@ def main():
         calibrate_copy()
         return
     if a.attn_sweep:
-        attn_sweep()
+        attn_sweep(a.attn_sweep)
         return
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the decode path runs on a single MI355X and has no multi-GPU "
