@@ -5,6 +5,8 @@
 // sampler.  Arithmetic follows llama3pure-c-engine.c (cited per kernel); the
 // library is built with -ffp-contract=off so elementwise expressions round
 // exactly as the reference's scalar C does.
+#include <string.h>
+
 #include "dequant.h"
 #include "device_common.h"
 #include "model.h"
@@ -566,6 +568,269 @@ __global__ void __launch_bounds__(256) attn_merge_kernel(AttnCArgs a0) {
             a.out[(size_t)h * hs + i] = tot;
         }
         __syncthreads();
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Attention of a prompt batch (c:3232-3359 for each token), FlashAttention
+// style: workgroup = one KV group x kPT consecutive tokens of the batch, one
+// wave per query head of the group.  The tokens' K/V rows are already in the
+// cache (kv_rows_kernel).  Each token's Q row goes through attn_chunk_kernel's
+// arithmetic (QK-norm, RoPE with attn_scale, Q8_0), so its Q8_0 row is the
+// same; the workgroup then walks the positions its tokens attend to in steps
+// of kPP:
+//   * the step's K and V rows go HBM -> LDS; K is repacked into int8 rows and
+//     fp32 block scales, V dequantized exactly to fp32 and transposed;
+//   * scores S^T[pos][tok] per 32-element block on the int8 matrix cores
+//     (v_mfma_i32_16x16x32_i8: one instruction is one exact Q8_0 block dot),
+//     combined in fp32 in block order as dot_q8_0_q8_0_cache (c:1574-1597):
+//     s += (dq * dk) * isum;
+//   * a running softmax per token (max m, sum l, earlier terms rescaled by
+//     expf(m_old - m)); a position adds to V only when e = expf(s - m) >=
+//     1e-8, as in attn_chunk_kernel (e >= the final weight, so every
+//     position skipped here is one the reference skips, c:1602);
+//   * O^T[d][tok] += V^T[d][pos] e[pos][tok] on the fp32 matrix cores.
+// The output is O / l.  Lane l of a wave holds token l % 16 throughout (the
+// C layout of a 16 x 16 tile: rows 4(l / 16) .. +3, column l % 16).
+// ---------------------------------------------------------------------------
+constexpr int kPT = 16;         // tokens per workgroup
+constexpr int kPP = 64;         // positions per step
+constexpr int kPV = kPP + 4;    // floats per transposed V row in LDS
+
+typedef int int32x4 __attribute__((ext_vector_type(4)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+__host__ __device__ constexpr int prefill_raw_dwords(int hq8) { return (kPP * hq8 + 8) / 4 + 1; }
+
+// LDS bytes of attn_prefill_kernel
+__host__ __device__ constexpr size_t prefill_attn_lds(int nb, int km) {
+    return (size_t)32 * nb * kPV * 4 + (size_t)kPP * nb * 4 + (size_t)km * kPT * nb * 4 + (size_t)km * 32 * nb * 4 +
+           2 * kPT * 4 + (size_t)kPP * 32 * nb + (size_t)km * kPT * 32 * nb + 2 * (size_t)prefill_raw_dwords(34 * nb) * 4;
+}
+
+template <int NB>
+__global__ void __launch_bounds__(1024) attn_prefill_kernel(AttnCArgs a0, int ntok) {
+    constexpr int hs = 32 * NB, half = hs / 2, hq8 = 34 * NB, ND = 2 * NB;   // ND: 16-wide d tiles
+    extern __shared__ __align__(16) float psm[];
+    const int g = blockIdx.x, z0 = blockIdx.y * kPT;
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, nt = blockDim.x, nw = nt >> 6;
+    const int km = a0.kv_mul, h = g * km + w;
+    const int rawdw = prefill_raw_dwords(hq8);
+    float* vt = psm;                                        // [hs][kPV] V^T of the step, dequantized
+    float* kd = vt + hs * kPV;                              // [kPP][NB] K block scales
+    float* qd = kd + kPP * NB;                              // [km][kPT][NB] Q block scales
+    float* stg = qd + km * kPT * NB;                        // [km][hs] one Q row being prepared
+    int* tpos = reinterpret_cast<int*>(stg + km * hs);      // [kPT] token positions (-1 past the batch)
+    int* tbeg = tpos + kPT;                                 // [kPT] first position each token attends to
+    int8_t* kq = reinterpret_cast<int8_t*>(tbeg + kPT);     // [kPP][hs] K quants of the step
+    int8_t* qq = kq + kPP * hs;                             // [km][kPT][hs] Q quants
+    uint32_t* kraw = reinterpret_cast<uint32_t*>(qq + km * kPT * hs);   // the step's K rows as copied
+    uint32_t* vraw = kraw + rawdw;                                       // and V rows
+
+    if (threadIdx.x < kPT) {
+        const int z = z0 + threadIdx.x;
+        int p = -1, b = 0;
+        if (z < ntok) {
+            p = a0.step[2 * z + 1];
+            b = a0.window > 0 ? max(0, p - a0.window + 1) : 0;   // c:3316-3321
+        }
+        tpos[threadIdx.x] = p;
+        tbeg[threadIdx.x] = b;
+    }
+
+    // ---- Q rows of the tile's tokens for head h (attn_chunk_kernel's arithmetic)
+    float* row = stg + w * hs;
+    for (int tt = 0; tt < kPT; ++tt) {
+        const int z = z0 + tt;
+        int8_t* qrow = qq + (w * kPT + tt) * hs;
+        float* qsc = qd + (w * kPT + tt) * NB;
+        if (z >= ntok) {   // uniform over the workgroup
+            for (int j = lane; j < hs; j += 64) qrow[j] = 0;
+            if (lane < NB) qsc[lane] = 0.0f;
+            continue;
+        }
+        const AttnCArgs a = token_args(a0, z);
+        const int pos = a.step[1];
+        float qn[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int j = lane + 64 * k;
+            if (j < hs) row[j] = a.q[(size_t)h * hs + j];
+            qn[k] = (a.q_norm && j < hs) ? a.q_norm[j] : 0.0f;
+        }
+        __syncthreads();
+        if (a.q_norm) {   // per-head rmsnorm (c:3151-3165)
+            float ssq = 0.0f;
+            for (int j = lane; j < hs; j += 64) ssq += row[j] * row[j];
+            ssq = wave_sum(ssq);
+            const float rq = 1.0f / sqrtf(ssq * a.inv_hs + a.eps);
+            __syncthreads();
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int j = lane + 64 * k;
+                if (j < hs) row[j] = qn[k] * (rq * row[j]);
+            }
+            __syncthreads();
+        }
+        const float* cosr = a.cos + (size_t)pos * half;
+        const float* sinr = a.sin + (size_t)pos * half;
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {   // RoPE with the attention scale (c:3240-3296)
+            const int p = lane + 64 * k;
+            if (p < half) {
+                const int i0 = a.neox ? p : 2 * p;
+                const int i1 = a.neox ? p + half : 2 * p + 1;
+                const float v0 = row[i0], v1 = row[i1], cs = cosr[p], sn = sinr[p];
+                row[i0] = (v0 * cs - v1 * sn) * a.attn_scale;
+                row[i1] = (v0 * sn + v1 * cs) * a.attn_scale;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {   // Q8_0 of q (c:3311-3312), one value per lane
+            const int j = lane + 64 * k;
+            if (k * 64 < hs) {
+                uint32_t dh;
+                const int8_t q8 = quant_lane(j < hs ? row[j] : 0.0f, dh);   // all lanes take part
+                if (j < hs) {
+                    qrow[j] = q8;
+                    if ((lane & 31) == 0) qsc[j >> 5] = h2f_exact(dh);
+                }
+            }
+        }
+        __syncthreads();
+    }
+
+    __syncthreads();
+    // ---- positions the tile attends to
+    int lo = 0x7fffffff, hi = -1;
+    for (int tt = 0; tt < kPT; ++tt) {
+        if (tpos[tt] >= 0) {
+            lo = min(lo, tbeg[tt]);
+            hi = max(hi, tpos[tt]);
+        }
+    }
+    const int tok = lane & 15, gq = lane >> 4;
+    const int my_pos = tpos[tok], my_beg = tbeg[tok];
+    const int8_t* qrow = qq + (w * kPT + tok) * hs;
+    const float* qsc = qd + (w * kPT + tok) * NB;
+    float m_run = -INFINITY, l_run = 0.0f;
+    floatx4 acc[ND];
+#pragma unroll
+    for (int d = 0; d < ND; ++d) acc[d] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    const size_t head_base = (size_t)g * a0.head_seq;
+    const uint32_t* kc4 = reinterpret_cast<const uint32_t*>(a0.kc);
+    const uint32_t* vc4 = reinterpret_cast<const uint32_t*>(a0.vc);
+
+    for (int p0 = hi < 0 ? 0 : (lo & ~(kPP - 1)); p0 <= hi; p0 += kPP) {
+        const int cnt = min(kPP, hi + 1 - p0);   // rows p0 .. p0 + cnt - 1
+        // the step's K and V rows, HBM -> LDS, dword pieces from the 4-byte
+        // aligned start
+        const size_t start = head_base + (size_t)p0 * hq8;
+        const size_t s4 = start & ~(size_t)3;
+        const int nd = (int)((start + (size_t)cnt * hq8 - s4 + 3) >> 2);
+        __syncthreads();   // the previous step's LDS reads are done
+        for (int i = w; i * 64 < nd; i += nw) {
+            if (i * 64 + lane < nd) {
+                __builtin_amdgcn_global_load_lds(kc4 + (s4 >> 2) + i * 64 + lane, (lds_void*)(kraw + i * 64), 4, 0, 0);
+                __builtin_amdgcn_global_load_lds(vc4 + (s4 >> 2) + i * 64 + lane, (lds_void*)(vraw + i * 64), 4, 0, 0);
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0x0070);   // vmcnt(0) lgkmcnt(0): this wave's copies have landed
+        __syncthreads();
+        const uint32_t roff = (uint32_t)(start - s4);
+        // repack: K block (p, b) -> int8 row + scale, V block -> fp32 V^T
+        for (int task = threadIdx.x; task < kPP * NB; task += nt) {
+            const int p = task % kPP, b = task / kPP;
+            uint32_t kqw[8], vqw[8];
+            float dk = 0.0f, dv = 0.0f;
+            if (p < cnt) {
+                dk = row_block(kraw, roff + (uint32_t)(p * hq8 + 34 * b), kqw);
+                dv = row_block(vraw, roff + (uint32_t)(p * hq8 + 34 * b), vqw);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) kqw[e] = vqw[e] = 0u;
+            }
+            kd[p * NB + b] = dk;
+            uint4* kdst = reinterpret_cast<uint4*>(kq + p * hs + 32 * b);
+            kdst[0] = make_uint4(kqw[0], kqw[1], kqw[2], kqw[3]);
+            kdst[1] = make_uint4(kqw[4], kqw[5], kqw[6], kqw[7]);
+#pragma unroll
+            for (int e = 0; e < 32; ++e)
+                vt[(32 * b + e) * kPV + p] = (float)(int8_t)((vqw[e >> 2] >> (8 * (e & 3))) & 0xffu) * dv;
+        }
+        __syncthreads();
+
+        // scores of head h: S^T[pos][tok], pos = st * 16 + 4 gq + r, tok = lane % 16
+        float sc[4][4];
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) sc[st][r] = 0.0f;
+            const int8_t* krow = kq + (st * 16 + tok) * hs + 8 * gq;   // A: position row lane % 16
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                const long av = *reinterpret_cast<const long*>(krow + 32 * b);
+                const long bv = *reinterpret_cast<const long*>(qrow + 32 * b + 8 * gq);
+                const int32x4 is = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bv, int32x4{0, 0, 0, 0}, 0, 0, 0);
+                const float qs = qsc[b];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) sc[st][r] += qs * kd[(st * 16 + 4 * gq + r) * NB + b] * (float)is[r];
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int pa = p0 + st * 16 + 4 * gq + r;
+                if (my_pos < 0 || pa > my_pos || pa < my_beg) sc[st][r] = -INFINITY;
+            }
+        }
+        // running softmax of token tok (its positions sit in lanes tok + 16 j)
+        float cm = -INFINITY;
+#pragma unroll
+        for (int st = 0; st < 4; ++st)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) cm = fmaxf(cm, sc[st][r]);
+        cm = fmaxf(cm, lane_partner<16>(cm));
+        cm = fmaxf(cm, lane_partner<32>(cm));
+        const float mn = fmaxf(m_run, cm);
+        const bool none = mn == -INFINITY;   // nothing attended yet
+        const float alpha = none ? 1.0f : expf(m_run - mn);
+        float f[4][4], ls = 0.0f;
+#pragma unroll
+        for (int st = 0; st < 4; ++st)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float e = sc[st][r] == -INFINITY ? 0.0f : expf(sc[st][r] - mn);
+                ls += e;
+                f[st][r] = e < 1e-8f ? 0.0f : e;
+            }
+        ls += lane_partner<16>(ls);
+        ls += lane_partner<32>(ls);
+        l_run = l_run * alpha + ls;
+        m_run = mn;
+        // O^T[d][tok] = alpha O^T + V^T[d][pos] f[pos][tok]
+#pragma unroll
+        for (int d = 0; d < ND; ++d) {
+            acc[d] *= alpha;
+            const float* vrow = vt + (d * 16 + tok) * kPV + 4 * gq;   // A: V^T row d, positions 4 gq ..
+#pragma unroll
+            for (int st = 0; st < 4; ++st) {
+                const float4 v4 = *reinterpret_cast<const float4*>(vrow + st * 16);
+                acc[d] = __builtin_amdgcn_mfma_f32_16x16x4f32(v4.x, f[st][0], acc[d], 0, 0, 0);
+                acc[d] = __builtin_amdgcn_mfma_f32_16x16x4f32(v4.y, f[st][1], acc[d], 0, 0, 0);
+                acc[d] = __builtin_amdgcn_mfma_f32_16x16x4f32(v4.z, f[st][2], acc[d], 0, 0, 0);
+                acc[d] = __builtin_amdgcn_mfma_f32_16x16x4f32(v4.w, f[st][3], acc[d], 0, 0, 0);
+            }
+        }
+    }
+    // out[tok][h][d] = O / l: lane holds d = 16 dt + 4 gq .. + 3 of token tok
+    const int z = z0 + tok;
+    if (z < ntok && my_pos >= 0) {
+        const float inv = 1.0f / l_run;
+        float* o = a0.out + (size_t)z * a0.out_stride + (size_t)h * hs + 4 * gq;
+#pragma unroll
+        for (int d = 0; d < ND; ++d)
+            *reinterpret_cast<float4*>(o + d * 16) = make_float4(acc[d][0] * inv, acc[d][1] * inv, acc[d][2] * inv,
+                                                                 acc[d][3] * inv);
     }
 }
 
@@ -1231,6 +1496,31 @@ void launch_attention(const Model& m, int l, const AttnIO& io, bool per_head, hi
     }
 }
 
+// Prompt batches take attn_prefill_kernel when its LDS fits a CU
+// (L3P_PREFILL_ATTN=chunks keeps them on the chunk + merge kernels).
+static bool prefill_attention_fits(const Model& m) {
+    static int forced = -1;
+    if (forced < 0) {
+        const char* e = getenv("L3P_PREFILL_ATTN");
+        forced = (e && strcmp(e, "chunks") == 0) ? 1 : 0;
+    }
+    return !forced && prefill_attn_lds(m.hs / 32, m.kv_mul) <= 160 * 1024;
+}
+
+template <int NB>
+static void launch_prefill_attn(const Model& m, const AttnCArgs& a, int tokens, hipStream_t s) {
+    const size_t lds = prefill_attn_lds(NB, m.kv_mul);
+    static size_t lds_set = 65536;   // dynamic LDS above 64 KB must be allowed first
+    if (lds > lds_set) {
+        L3P_HIP(hipFuncSetAttribute((const void*)attn_prefill_kernel<NB>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    (int)lds));
+        lds_set = lds;
+    }
+    hipLaunchKernelGGL(attn_prefill_kernel<NB>, dim3(m.n_kv, (tokens + kPT - 1) / kPT), dim3(64 * m.kv_mul), lds, s, a,
+                       tokens);
+    L3P_HIP(hipGetLastError());
+}
+
 int attention_chunks(const Model& m, int l, int last_pos) {
     const AttnCArgs a = attn_args(m, l, AttnIO{});
     const int t0 = a.window > 0 ? std::max(0, last_pos - a.window + 1) : 0;
@@ -1253,6 +1543,19 @@ void launch_attention_rows(const Model& m, int l, const AttnIO& io, int q_stride
                 tokens);
     hipLaunchKernelGGL(kv_rows_kernel, dim3(m.n_kv, tokens), dim3(64), 0, s, a);
     L3P_HIP(hipGetLastError());
+    if (prefill_attention_fits(m)) {
+        switch (m.hs / 32) {
+        case 1: launch_prefill_attn<1>(m, a, tokens, s); break;
+        case 2: launch_prefill_attn<2>(m, a, tokens, s); break;
+        case 3: launch_prefill_attn<3>(m, a, tokens, s); break;
+        case 4: launch_prefill_attn<4>(m, a, tokens, s); break;
+        case 5: launch_prefill_attn<5>(m, a, tokens, s); break;
+        case 6: launch_prefill_attn<6>(m, a, tokens, s); break;
+        case 7: launch_prefill_attn<7>(m, a, tokens, s); break;
+        default: launch_prefill_attn<8>(m, a, tokens, s); break;
+        }
+        return;
+    }
     launch_chunks(m, a, chunks, tokens, s);
 }
 
