@@ -595,7 +595,7 @@ __global__ void __launch_bounds__(256) attn_merge_kernel(AttnCArgs a0) {
 // ---------------------------------------------------------------------------
 constexpr int kPT = 16;         // tokens per workgroup
 constexpr int kPP = 64;         // positions per step
-constexpr int kPV = kPP + 4;    // floats per transposed V row in LDS
+constexpr int kPV = kPP + 4;    // bytes per transposed V row in LDS
 
 typedef int int32x4 __attribute__((ext_vector_type(4)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
@@ -604,8 +604,9 @@ __host__ __device__ constexpr int prefill_raw_dwords(int hq8) { return (kPP * hq
 
 // LDS bytes of attn_prefill_kernel
 __host__ __device__ constexpr size_t prefill_attn_lds(int nb, int km) {
-    return (size_t)32 * nb * kPV * 4 + (size_t)kPP * nb * 4 + (size_t)km * kPT * nb * 4 + (size_t)km * 32 * nb * 4 +
-           2 * kPT * 4 + (size_t)kPP * 32 * nb + (size_t)km * kPT * 32 * nb + 2 * (size_t)prefill_raw_dwords(34 * nb) * 4;
+    return (size_t)nb * kPP * 4 * 2 + (size_t)km * kPT * nb * 4 + (size_t)km * 32 * nb * 4 + 2 * kPT * 4 +
+           (size_t)32 * nb * kPV + (size_t)kPP * 32 * nb + (size_t)km * kPT * 32 * nb +
+           4 * (size_t)prefill_raw_dwords(34 * nb) * 4;
 }
 
 template <int NB>
@@ -616,16 +617,16 @@ __global__ void __launch_bounds__(1024) attn_prefill_kernel(AttnCArgs a0, int nt
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, nt = blockDim.x, nw = nt >> 6;
     const int km = a0.kv_mul, h = g * km + w;
     const int rawdw = prefill_raw_dwords(hq8);
-    float* vt = psm;                                        // [hs][kPV] V^T of the step, dequantized
-    float* kd = vt + hs * kPV;                              // [kPP][NB] K block scales
-    float* qd = kd + kPP * NB;                              // [km][kPT][NB] Q block scales
+    float* kd = psm;                                        // [kPP][NB] K block scales of the step
+    float* dvt = kd + kPP * NB;                             // [NB][kPP] V block scales
+    float* qd = dvt + kPP * NB;                             // [km][kPT][NB] Q block scales
     float* stg = qd + km * kPT * NB;                        // [km][hs] one Q row being prepared
     int* tpos = reinterpret_cast<int*>(stg + km * hs);      // [kPT] token positions (-1 past the batch)
     int* tbeg = tpos + kPT;                                 // [kPT] first position each token attends to
-    int8_t* kq = reinterpret_cast<int8_t*>(tbeg + kPT);     // [kPP][hs] K quants of the step
+    int8_t* vqt = reinterpret_cast<int8_t*>(tbeg + kPT);    // [hs][kPV] V quants, transposed
+    int8_t* kq = vqt + hs * kPV;                            // [kPP][hs] K quants of the step
     int8_t* qq = kq + kPP * hs;                             // [km][kPT][hs] Q quants
-    uint32_t* kraw = reinterpret_cast<uint32_t*>(qq + km * kPT * hs);   // the step's K rows as copied
-    uint32_t* vraw = kraw + rawdw;                                       // and V rows
+    uint32_t* raw = reinterpret_cast<uint32_t*>(qq + km * kPT * hs);   // [2 buffers][K, V] rows as copied
 
     if (threadIdx.x < kPT) {
         const int z = z0 + threadIdx.x;
@@ -722,24 +723,34 @@ __global__ void __launch_bounds__(1024) attn_prefill_kernel(AttnCArgs a0, int nt
     const uint32_t* kc4 = reinterpret_cast<const uint32_t*>(a0.kc);
     const uint32_t* vc4 = reinterpret_cast<const uint32_t*>(a0.vc);
 
-    for (int p0 = hi < 0 ? 0 : (lo & ~(kPP - 1)); p0 <= hi; p0 += kPP) {
-        const int cnt = min(kPP, hi + 1 - p0);   // rows p0 .. p0 + cnt - 1
-        // the step's K and V rows, HBM -> LDS, dword pieces from the 4-byte
-        // aligned start
+    // the K and V rows of the step at p0 into raw buffer `buf`: dword pieces
+    // from the 4-byte aligned start (the copies of the next step are in
+    // flight while this step is computed)
+    const int p_first = hi < 0 ? 0 : (lo & ~(kPP - 1));
+    auto copy_rows = [&](int p0, int buf) {
+        const int cnt = min(kPP, hi + 1 - p0);
         const size_t start = head_base + (size_t)p0 * hq8;
         const size_t s4 = start & ~(size_t)3;
         const int nd = (int)((start + (size_t)cnt * hq8 - s4 + 3) >> 2);
-        __syncthreads();   // the previous step's LDS reads are done
+        uint32_t* kr = raw + (size_t)buf * 2 * rawdw;
         for (int i = w; i * 64 < nd; i += nw) {
             if (i * 64 + lane < nd) {
-                __builtin_amdgcn_global_load_lds(kc4 + (s4 >> 2) + i * 64 + lane, (lds_void*)(kraw + i * 64), 4, 0, 0);
-                __builtin_amdgcn_global_load_lds(vc4 + (s4 >> 2) + i * 64 + lane, (lds_void*)(vraw + i * 64), 4, 0, 0);
+                __builtin_amdgcn_global_load_lds(kc4 + (s4 >> 2) + i * 64 + lane, (lds_void*)(kr + i * 64), 4, 0, 0);
+                __builtin_amdgcn_global_load_lds(vc4 + (s4 >> 2) + i * 64 + lane, (lds_void*)(kr + rawdw + i * 64), 4,
+                                                 0, 0);
             }
         }
+    };
+    if (hi >= 0) copy_rows(p_first, 0);
+    int buf = 0;
+    for (int p0 = p_first; p0 <= hi; p0 += kPP, buf ^= 1) {
+        const int cnt = min(kPP, hi + 1 - p0);   // rows p0 .. p0 + cnt - 1
+        const uint32_t roff = (uint32_t)((head_base + (size_t)p0 * hq8) & 3);
+        const uint32_t* kraw = raw + (size_t)buf * 2 * rawdw;
+        const uint32_t* vraw = kraw + rawdw;
         __builtin_amdgcn_s_waitcnt(0x0070);   // vmcnt(0) lgkmcnt(0): this wave's copies have landed
-        __syncthreads();
-        const uint32_t roff = (uint32_t)(start - s4);
-        // repack: K block (p, b) -> int8 row + scale, V block -> fp32 V^T
+        __syncthreads();   // every wave's copies landed; the previous step's LDS reads are done
+        // repack: K block (p, b) -> int8 row + scale, V block -> int8 V^T + scale
         for (int task = threadIdx.x; task < kPP * NB; task += nt) {
             const int p = task % kPP, b = task / kPP;
             uint32_t kqw[8], vqw[8];
@@ -752,14 +763,16 @@ __global__ void __launch_bounds__(1024) attn_prefill_kernel(AttnCArgs a0, int nt
                 for (int e = 0; e < 8; ++e) kqw[e] = vqw[e] = 0u;
             }
             kd[p * NB + b] = dk;
+            dvt[b * kPP + p] = dv;
             uint4* kdst = reinterpret_cast<uint4*>(kq + p * hs + 32 * b);
             kdst[0] = make_uint4(kqw[0], kqw[1], kqw[2], kqw[3]);
             kdst[1] = make_uint4(kqw[4], kqw[5], kqw[6], kqw[7]);
 #pragma unroll
-            for (int e = 0; e < 32; ++e)
-                vt[(32 * b + e) * kPV + p] = (float)(int8_t)((vqw[e >> 2] >> (8 * (e & 3))) & 0xffu) * dv;
+            for (int e = 0; e < 32; ++e) vqt[(32 * b + e) * kPV + p] = (int8_t)((vqw[e >> 2] >> (8 * (e & 3))) & 0xffu);
         }
         __syncthreads();
+        // the next step's rows go into the other buffer while this one is used
+        if (p0 + kPP <= hi) copy_rows(p0 + kPP, buf ^ 1);
 
         // scores of head h: S^T[pos][tok], pos = st * 16 + 4 gq + r, tok = lane % 16
         float sc[4][4];
@@ -807,18 +820,23 @@ __global__ void __launch_bounds__(1024) attn_prefill_kernel(AttnCArgs a0, int nt
         ls += lane_partner<32>(ls);
         l_run = l_run * alpha + ls;
         m_run = mn;
-        // O^T[d][tok] = alpha O^T + V^T[d][pos] f[pos][tok]
+        // O^T[d][tok] = alpha O^T + V^T[d][pos] f[pos][tok], V^T expanded
+        // exactly (q * d) right before its matrix instruction
 #pragma unroll
         for (int d = 0; d < ND; ++d) {
             acc[d] *= alpha;
-            const float* vrow = vt + (d * 16 + tok) * kPV + 4 * gq;   // A: V^T row d, positions 4 gq ..
+            const int8_t* vrow = vqt + (d * 16 + tok) * kPV + 4 * gq;   // A: V^T row d, positions 4 gq ..
+            const float* dvr = dvt + (d >> 1) * kPP + 4 * gq;            // block d * 16 / 32 of those positions
 #pragma unroll
             for (int st = 0; st < 4; ++st) {
-                const float4 v4 = *reinterpret_cast<const float4*>(vrow + st * 16);
-                acc[d] = __builtin_amdgcn_mfma_f32_16x16x4f32(v4.x, f[st][0], acc[d], 0, 0, 0);
-                acc[d] = __builtin_amdgcn_mfma_f32_16x16x4f32(v4.y, f[st][1], acc[d], 0, 0, 0);
-                acc[d] = __builtin_amdgcn_mfma_f32_16x16x4f32(v4.z, f[st][2], acc[d], 0, 0, 0);
-                acc[d] = __builtin_amdgcn_mfma_f32_16x16x4f32(v4.w, f[st][3], acc[d], 0, 0, 0);
+                const uint32_t q4 = *reinterpret_cast<const uint32_t*>(vrow + st * 16);
+                const float4 d4 = *reinterpret_cast<const float4*>(dvr + st * 16);
+                acc[d] = __builtin_amdgcn_mfma_f32_16x16x4f32((float)(int8_t)(q4 & 0xffu) * d4.x, f[st][0], acc[d], 0, 0, 0);
+                acc[d] = __builtin_amdgcn_mfma_f32_16x16x4f32((float)(int8_t)((q4 >> 8) & 0xffu) * d4.y, f[st][1], acc[d], 0,
+                                                              0, 0);
+                acc[d] = __builtin_amdgcn_mfma_f32_16x16x4f32((float)(int8_t)((q4 >> 16) & 0xffu) * d4.z, f[st][2], acc[d], 0,
+                                                              0, 0);
+                acc[d] = __builtin_amdgcn_mfma_f32_16x16x4f32((float)(int8_t)(q4 >> 24) * d4.w, f[st][3], acc[d], 0, 0, 0);
             }
         }
     }
