@@ -1517,12 +1517,9 @@ void launch_attention(const Model& m, int l, const AttnIO& io, bool per_head, hi
 // Prompt batches take attn_prefill_kernel when its LDS fits a CU
 // (L3P_PREFILL_ATTN=chunks keeps them on the chunk + merge kernels).
 static bool prefill_attention_fits(const Model& m) {
-    static int forced = -1;
-    if (forced < 0) {
-        const char* e = getenv("L3P_PREFILL_ATTN");
-        forced = (e && strcmp(e, "chunks") == 0) ? 1 : 0;
-    }
-    return !forced && prefill_attn_lds(m.hs / 32, m.kv_mul) <= 160 * 1024;
+    const char* e = getenv("L3P_PREFILL_ATTN");
+    if (e && strcmp(e, "chunks") == 0) return false;
+    return prefill_attn_lds(m.hs / 32, m.kv_mul) <= 160 * 1024;
 }
 
 template <int NB>

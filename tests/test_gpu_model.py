@@ -300,6 +300,42 @@ PATH_CASES = {
 
 
 @pytest.mark.parametrize("case", list(PATH_CASES))
+def test_prompt_attention_paths_agree(torch_gpu, monkeypatch, case):
+    """A prompt through attn_prefill_kernel (the default) and through chunks +
+    merge over a token grid dimension (L3P_PREFILL_ATTN=chunks): both score
+    with the same exact Q8_0 block dots and differ only in the softmax and V
+    summation order, so the layer-0 cache (written before any attention) is
+    identical, deeper layers differ by at most one-step quant flips, and the
+    next step's logits agree to 1e-2 * rms, the full-model tolerance after a
+    prompt (each layer's difference reaches the K/V rows of every position of
+    the next).  The cases cover head sizes 64 to 256, GQA groups of 2 and 4,
+    sliding windows and 4300 positions."""
+    kw, n_prompt = PATH_CASES[case]
+    g = synth.synthetic_model(**kw)
+    toks = np.random.default_rng(kw["seed"] + 1).integers(0, kw["vocab"], n_prompt + 1).astype(np.int32)
+    with l3p.Context(0) as cf, l3p.Context(0) as cc:
+        for c, path in ((cf, None), (cc, "chunks")):
+            if path:
+                monkeypatch.setenv("L3P_PREFILL_ATTN", path)
+            else:
+                monkeypatch.delenv("L3P_PREFILL_ATTN", raising=False)
+            c.load_gguf(g)
+            c.prefill(toks[:n_prompt], 0)
+        monkeypatch.delenv("L3P_PREFILL_ATTN", raising=False)
+        a = cf.forward(int(toks[n_prompt]), n_prompt)
+        b = cc.forward(int(toks[n_prompt]), n_prompt)
+        assert float(np.max(np.abs(a - b))) <= 1e-2 * rms(b), case
+        mi = cf.model_info()
+        for wv in (False, True):
+            assert np.array_equal(cf.copy_kv(0, wv), cc.copy_kv(0, wv)), (case, wv)
+            for layer in range(1, mi.n_layers):
+                qa = cf.copy_kv(layer, wv).reshape(mi.n_kv_heads, mi.seq_len, -1, 34)[:, :n_prompt + 1, :, 2:]
+                qb = cc.copy_kv(layer, wv).reshape(mi.n_kv_heads, mi.seq_len, -1, 34)[:, :n_prompt + 1, :, 2:]
+                d = np.abs(qa.view(np.int8).astype(np.int32) - qb.view(np.int8).astype(np.int32))
+                assert d.max() <= 1, (case, layer, wv, int(d.max()))
+
+
+@pytest.mark.parametrize("case", list(PATH_CASES))
 def test_attention_paths_agree(torch_gpu, monkeypatch, case):
     """The two decode attentions give the same steps: one workgroup per query
     head (L3P_ATTN_HEAD=1; by default for steps attending to fewer than 512
