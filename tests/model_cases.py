@@ -55,6 +55,9 @@ SINGLE_LAYER = {
     # of 1224 B), Gemma-3-270M width 640 (Q4_0 rows of 360 B), Q6_K at
     # widths 768 and 1280 (rows of 630 and 1050 B)
     "gemma_q8_0_1152": dict(qtype=synth.Q8_0, dim=1152, hidden=1536, n_heads=4, n_kv=1, **_GEMMA),
+    # Gemma-2-2B widths (rows of 2304 and 9216 elements: short last chunk
+    # columns), fused RMSNorm, GeGLU pair and post norms
+    "gemma_q8_0_2304": dict(qtype=synth.Q8_0, dim=2304, hidden=9216, n_heads=8, n_kv=4, **_GEMMA),
     "llama_q4_0_640": dict(qtype=synth.Q4_0, dim=640, hidden=2048, n_heads=5, n_kv=1),
     "llama_q6_k_768": dict(qtype=synth.Q6_K, dim=768, hidden=1280, n_heads=6, n_kv=2),
     # every other weight type on its own, at widths that are not multiples of

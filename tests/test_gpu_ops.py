@@ -151,6 +151,13 @@ def _check_gemv(ctx, torch, cpuref, qtype, rows, cols, seed=0, sample_rows=None)
     (l3p.Q5_1, 515, 1120),         # 840 B rows
     (l3p.IQ4_NL, 2048, 4096),
     (l3p.IQ4_NL, 333, 160),
+    # widths that leave a short last chunk column: 4160 columns (64 + 64 + 2
+    # blocks), 2304 (64 + 8), 6400 (3 x 64 + 8)
+    (l3p.Q8_0, 100, 4160),
+    (l3p.Q4_1, 300, 4160),
+    (l3p.Q5_0, 200, 2304),
+    (l3p.IQ4_NL, 257, 2304),
+    (l3p.Q5_1, 300, 6400),
     (l3p.Q2_K, 2048, 4096),
     (l3p.Q2_K, 1000, 2304),        # 756 B rows
     (l3p.Q3_K, 2048, 4096),
