@@ -609,13 +609,20 @@ __host__ __device__ constexpr size_t prefill_attn_lds(int nb, int km) {
            4 * (size_t)prefill_raw_dwords(34 * nb) * 4;
 }
 
-template <int NB>
+// WPH waves per query head: with 2, each takes two of a step's four 16-position
+// subtiles with its own running softmax, and the two states are merged at the
+// end (the second one through LDS).
+template <int NB, int WPH>
 __global__ void __launch_bounds__(1024) attn_prefill_kernel(AttnCArgs a0, int ntok) {
+    static_assert(WPH == 1 || WPH == 2, "waves per head");
     constexpr int hs = 32 * NB, half = hs / 2, hq8 = 34 * NB, ND = 2 * NB;   // ND: 16-wide d tiles
+    constexpr int SPW = 4 / WPH;                                             // subtiles per wave
     extern __shared__ __align__(16) float psm[];
     const int g = blockIdx.x, z0 = blockIdx.y * kPT;
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, nt = blockDim.x, nw = nt >> 6;
-    const int km = a0.kv_mul, h = g * km + w;
+    const int hw = w / WPH, pt = w % WPH;   // head in the group, part
+    const int km = a0.kv_mul, h = g * km + hw;
+    const bool qwave = pt == 0;              // forms the head's Q rows
     const int rawdw = prefill_raw_dwords(hq8);
     float* kd = psm;                                        // [kPP][NB] K block scales of the step
     float* dvt = kd + kPP * NB;                             // [NB][kPP] V block scales
@@ -640,14 +647,16 @@ __global__ void __launch_bounds__(1024) attn_prefill_kernel(AttnCArgs a0, int nt
     }
 
     // ---- Q rows of the tile's tokens for head h (attn_chunk_kernel's arithmetic)
-    float* row = stg + w * hs;
+    float* row = stg + hw * hs;
     for (int tt = 0; tt < kPT; ++tt) {
         const int z = z0 + tt;
-        int8_t* qrow = qq + (w * kPT + tt) * hs;
-        float* qsc = qd + (w * kPT + tt) * NB;
+        int8_t* qrow = qq + (hw * kPT + tt) * hs;
+        float* qsc = qd + (hw * kPT + tt) * NB;
         if (z >= ntok) {   // uniform over the workgroup
-            for (int j = lane; j < hs; j += 64) qrow[j] = 0;
-            if (lane < NB) qsc[lane] = 0.0f;
+            if (qwave) {
+                for (int j = lane; j < hs; j += 64) qrow[j] = 0;
+                if (lane < NB) qsc[lane] = 0.0f;
+            }
             continue;
         }
         const AttnCArgs a = token_args(a0, z);
@@ -656,20 +665,25 @@ __global__ void __launch_bounds__(1024) attn_prefill_kernel(AttnCArgs a0, int nt
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             const int j = lane + 64 * k;
-            if (j < hs) row[j] = a.q[(size_t)h * hs + j];
+            if (qwave && j < hs) row[j] = a.q[(size_t)h * hs + j];
             qn[k] = (a.q_norm && j < hs) ? a.q_norm[j] : 0.0f;
         }
         __syncthreads();
         if (a.q_norm) {   // per-head rmsnorm (c:3151-3165)
-            float ssq = 0.0f;
-            for (int j = lane; j < hs; j += 64) ssq += row[j] * row[j];
-            ssq = wave_sum(ssq);
-            const float rq = 1.0f / sqrtf(ssq * a.inv_hs + a.eps);
+            float rq = 0.0f;
+            if (qwave) {
+                float ssq = 0.0f;
+                for (int j = lane; j < hs; j += 64) ssq += row[j] * row[j];
+                ssq = wave_sum(ssq);
+                rq = 1.0f / sqrtf(ssq * a.inv_hs + a.eps);
+            }
             __syncthreads();
+            if (qwave) {
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const int j = lane + 64 * k;
-                if (j < hs) row[j] = qn[k] * (rq * row[j]);
+                for (int k = 0; k < 4; ++k) {
+                    const int j = lane + 64 * k;
+                    if (j < hs) row[j] = qn[k] * (rq * row[j]);
+                }
             }
             __syncthreads();
         }
@@ -678,7 +692,7 @@ __global__ void __launch_bounds__(1024) attn_prefill_kernel(AttnCArgs a0, int nt
 #pragma unroll
         for (int k = 0; k < 2; ++k) {   // RoPE with the attention scale (c:3240-3296)
             const int p = lane + 64 * k;
-            if (p < half) {
+            if (qwave && p < half) {
                 const int i0 = a.neox ? p : 2 * p;
                 const int i1 = a.neox ? p + half : 2 * p + 1;
                 const float v0 = row[i0], v1 = row[i1], cs = cosr[p], sn = sinr[p];
@@ -690,7 +704,7 @@ __global__ void __launch_bounds__(1024) attn_prefill_kernel(AttnCArgs a0, int nt
 #pragma unroll
         for (int k = 0; k < 4; ++k) {   // Q8_0 of q (c:3311-3312), one value per lane
             const int j = lane + 64 * k;
-            if (k * 64 < hs) {
+            if (qwave && k * 64 < hs) {
                 uint32_t dh;
                 const int8_t q8 = quant_lane(j < hs ? row[j] : 0.0f, dh);   // all lanes take part
                 if (j < hs) {
@@ -713,8 +727,8 @@ __global__ void __launch_bounds__(1024) attn_prefill_kernel(AttnCArgs a0, int nt
     }
     const int tok = lane & 15, gq = lane >> 4;
     const int my_pos = tpos[tok], my_beg = tbeg[tok];
-    const int8_t* qrow = qq + (w * kPT + tok) * hs;
-    const float* qsc = qd + (w * kPT + tok) * NB;
+    const int8_t* qrow = qq + (hw * kPT + tok) * hs;
+    const float* qsc = qd + (hw * kPT + tok) * NB;
     float m_run = -INFINITY, l_run = 0.0f;
     floatx4 acc[ND];
 #pragma unroll
@@ -774,12 +788,14 @@ __global__ void __launch_bounds__(1024) attn_prefill_kernel(AttnCArgs a0, int nt
         // the next step's rows go into the other buffer while this one is used
         if (p0 + kPP <= hi) copy_rows(p0 + kPP, buf ^ 1);
 
-        // scores of head h: S^T[pos][tok], pos = st * 16 + 4 gq + r, tok = lane % 16
-        float sc[4][4];
+        // scores of head h over this wave's subtiles: S^T[pos][tok], pos =
+        // st * 16 + 4 gq + r, tok = lane % 16
+        float sc[SPW][4];
 #pragma unroll
-        for (int st = 0; st < 4; ++st) {
+        for (int s2 = 0; s2 < SPW; ++s2) {
+            const int st = pt * SPW + s2;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) sc[st][r] = 0.0f;
+            for (int r = 0; r < 4; ++r) sc[s2][r] = 0.0f;
             const int8_t* krow = kq + (st * 16 + tok) * hs + 8 * gq;   // A: position row lane % 16
 #pragma unroll
             for (int b = 0; b < NB; ++b) {
@@ -788,33 +804,33 @@ __global__ void __launch_bounds__(1024) attn_prefill_kernel(AttnCArgs a0, int nt
                 const int32x4 is = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bv, int32x4{0, 0, 0, 0}, 0, 0, 0);
                 const float qs = qsc[b];
 #pragma unroll
-                for (int r = 0; r < 4; ++r) sc[st][r] += qs * kd[(st * 16 + 4 * gq + r) * NB + b] * (float)is[r];
+                for (int r = 0; r < 4; ++r) sc[s2][r] += qs * kd[(st * 16 + 4 * gq + r) * NB + b] * (float)is[r];
             }
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int pa = p0 + st * 16 + 4 * gq + r;
-                if (my_pos < 0 || pa > my_pos || pa < my_beg) sc[st][r] = -INFINITY;
+                if (my_pos < 0 || pa > my_pos || pa < my_beg) sc[s2][r] = -INFINITY;
             }
         }
         // running softmax of token tok (its positions sit in lanes tok + 16 j)
         float cm = -INFINITY;
 #pragma unroll
-        for (int st = 0; st < 4; ++st)
+        for (int s2 = 0; s2 < SPW; ++s2)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) cm = fmaxf(cm, sc[st][r]);
+            for (int r = 0; r < 4; ++r) cm = fmaxf(cm, sc[s2][r]);
         cm = fmaxf(cm, lane_partner<16>(cm));
         cm = fmaxf(cm, lane_partner<32>(cm));
         const float mn = fmaxf(m_run, cm);
         const bool none = mn == -INFINITY;   // nothing attended yet
         const float alpha = none ? 1.0f : expf(m_run - mn);
-        float f[4][4], ls = 0.0f;
+        float f[SPW][4], ls = 0.0f;
 #pragma unroll
-        for (int st = 0; st < 4; ++st)
+        for (int s2 = 0; s2 < SPW; ++s2)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const float e = sc[st][r] == -INFINITY ? 0.0f : expf(sc[st][r] - mn);
+                const float e = sc[s2][r] == -INFINITY ? 0.0f : expf(sc[s2][r] - mn);
                 ls += e;
-                f[st][r] = e < 1e-8f ? 0.0f : e;
+                f[s2][r] = e < 1e-8f ? 0.0f : e;
             }
         ls += lane_partner<16>(ls);
         ls += lane_partner<32>(ls);
@@ -828,21 +844,48 @@ __global__ void __launch_bounds__(1024) attn_prefill_kernel(AttnCArgs a0, int nt
             const int8_t* vrow = vqt + (d * 16 + tok) * kPV + 4 * gq;   // A: V^T row d, positions 4 gq ..
             const float* dvr = dvt + (d >> 1) * kPP + 4 * gq;            // block d * 16 / 32 of those positions
 #pragma unroll
-            for (int st = 0; st < 4; ++st) {
+            for (int s2 = 0; s2 < SPW; ++s2) {
+                const int st = pt * SPW + s2;
                 const uint32_t q4 = *reinterpret_cast<const uint32_t*>(vrow + st * 16);
                 const float4 d4 = *reinterpret_cast<const float4*>(dvr + st * 16);
-                acc[d] = __builtin_amdgcn_mfma_f32_16x16x4f32((float)(int8_t)(q4 & 0xffu) * d4.x, f[st][0], acc[d], 0, 0, 0);
-                acc[d] = __builtin_amdgcn_mfma_f32_16x16x4f32((float)(int8_t)((q4 >> 8) & 0xffu) * d4.y, f[st][1], acc[d], 0,
+                acc[d] = __builtin_amdgcn_mfma_f32_16x16x4f32((float)(int8_t)(q4 & 0xffu) * d4.x, f[s2][0], acc[d], 0, 0, 0);
+                acc[d] = __builtin_amdgcn_mfma_f32_16x16x4f32((float)(int8_t)((q4 >> 8) & 0xffu) * d4.y, f[s2][1], acc[d], 0,
                                                               0, 0);
-                acc[d] = __builtin_amdgcn_mfma_f32_16x16x4f32((float)(int8_t)((q4 >> 16) & 0xffu) * d4.z, f[st][2], acc[d], 0,
+                acc[d] = __builtin_amdgcn_mfma_f32_16x16x4f32((float)(int8_t)((q4 >> 16) & 0xffu) * d4.z, f[s2][2], acc[d], 0,
                                                               0, 0);
-                acc[d] = __builtin_amdgcn_mfma_f32_16x16x4f32((float)(int8_t)(q4 >> 24) * d4.w, f[st][3], acc[d], 0, 0, 0);
+                acc[d] = __builtin_amdgcn_mfma_f32_16x16x4f32((float)(int8_t)(q4 >> 24) * d4.w, f[s2][3], acc[d], 0, 0, 0);
             }
+        }
+    }
+    if constexpr (WPH == 2) {
+        // the second part's (m, l, O) through LDS (the copy buffers are free:
+        // no copy is in flight after the last step), merged into the first's
+        __syncthreads();
+        float* mg = reinterpret_cast<float*>(raw) + (size_t)(hw * 64 + lane) * (2 + 4 * ND);
+        if (pt == 1) {
+            mg[0] = m_run;
+            mg[1] = l_run;
+#pragma unroll
+            for (int d = 0; d < ND; ++d)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) mg[2 + 4 * d + r] = acc[d][r];
+        }
+        __syncthreads();
+        if (pt == 0) {
+            const float m1 = mg[0], l1 = mg[1];
+            const float M = fmaxf(m_run, m1);
+            const float s0 = m_run == -INFINITY ? 0.0f : expf(m_run - M);
+            const float s1 = m1 == -INFINITY ? 0.0f : expf(m1 - M);
+            l_run = l_run * s0 + l1 * s1;
+#pragma unroll
+            for (int d = 0; d < ND; ++d)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) acc[d][r] = acc[d][r] * s0 + mg[2 + 4 * d + r] * s1;
         }
     }
     // out[tok][h][d] = O / l: lane holds d = 16 dt + 4 gq .. + 3 of token tok
     const int z = z0 + tok;
-    if (z < ntok && my_pos >= 0) {
+    if (pt == 0 && z < ntok && my_pos >= 0) {
         const float inv = 1.0f / l_run;
         float* o = a0.out + (size_t)z * a0.out_stride + (size_t)h * hs + 4 * gq;
 #pragma unroll
@@ -1522,18 +1565,28 @@ static bool prefill_attention_fits(const Model& m) {
     return prefill_attn_lds(m.hs / 32, m.kv_mul) <= 160 * 1024;
 }
 
+template <int NB, int WPH>
+static void launch_prefill_attn_w(const Model& m, const AttnCArgs& a, int tokens, size_t lds, hipStream_t s) {
+    static size_t lds_set = 65536;   // dynamic LDS above 64 KB must be allowed first
+    if (lds > lds_set) {
+        L3P_HIP(hipFuncSetAttribute((const void*)attn_prefill_kernel<NB, WPH>,
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+        lds_set = lds;
+    }
+    hipLaunchKernelGGL((attn_prefill_kernel<NB, WPH>), dim3(m.n_kv, (tokens + kPT - 1) / kPT),
+                       dim3(64 * m.kv_mul * WPH), lds, s, a, tokens);
+    L3P_HIP(hipGetLastError());
+}
+
+// Two waves per head when the group's threads stay within 1024 and the
+// second parts' states fit the copy buffers for the final merge.
 template <int NB>
 static void launch_prefill_attn(const Model& m, const AttnCArgs& a, int tokens, hipStream_t s) {
     const size_t lds = prefill_attn_lds(NB, m.kv_mul);
-    static size_t lds_set = 65536;   // dynamic LDS above 64 KB must be allowed first
-    if (lds > lds_set) {
-        L3P_HIP(hipFuncSetAttribute((const void*)attn_prefill_kernel<NB>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                    (int)lds));
-        lds_set = lds;
-    }
-    hipLaunchKernelGGL(attn_prefill_kernel<NB>, dim3(m.n_kv, (tokens + kPT - 1) / kPT), dim3(64 * m.kv_mul), lds, s, a,
-                       tokens);
-    L3P_HIP(hipGetLastError());
+    const size_t merge = (size_t)m.kv_mul * 64 * (2 + 8 * NB) * 4;
+    const size_t raw = 4 * (size_t)prefill_raw_dwords(34 * NB) * 4;
+    if (m.kv_mul <= 8 && merge <= raw) launch_prefill_attn_w<NB, 2>(m, a, tokens, lds, s);
+    else launch_prefill_attn_w<NB, 1>(m, a, tokens, lds, s);
 }
 
 int attention_chunks(const Model& m, int l, int last_pos) {
