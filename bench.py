@@ -82,9 +82,10 @@ def gpu_q8_0_maker(ctx, torch, seed):
 
 
 def time_gemv_shapes(ctx, torch, l3p, synth):
-    """GB/s of single GEMV launches: l3p_gemv calls over rotating weight
-    copies (>= 1 GiB, so no launch finds its weights in a cache), each kernel
-    timed by its own dispatch events (the library's launch timing)."""
+    """GB/s of single GEMV launches: at least 200 l3p_gemv calls over rotating
+    weight copies (>= 1 GiB, so no launch finds its weights in a cache), each
+    kernel timed by its own dispatch events (the library's launch timing);
+    mean and p10/p50/p90 of the launch durations."""
     shapes = [("q8_0", l3p.Q8_0, 4096, 4096), ("q4_0", l3p.Q4_0, 14336, 4096), ("q4_0", l3p.Q4_0, 4096, 14336),
               ("q4_k", l3p.Q4_K, 14336, 4096), ("q6_k", l3p.Q6_K, 128256, 4096)]
     out = []
@@ -99,17 +100,19 @@ def time_gemv_shapes(ctx, torch, l3p, synth):
         for i in range(copies):
             ctx.gemv(qt, ws[i], rows, cols, x, y)
         ctx.synchronize()
-        n = max(40, 2 * copies)
+        n = max(200, 2 * copies)
         ctx.profile(True)
         for i in range(n):
             ctx.gemv(qt, ws[i % copies], rows, cols, x, y)
         stats = ctx.profile_read()
+        p10, p50, p90 = next(iter(ctx.profile_percentiles().values()))
         ctx.profile(False)
         launches, ms, _ = next(iter(stats.values()))
         avg = ms * 1e3 / launches
         alg = wbytes + 4 * cols + 4 * rows
-        out.append({"shape": f"{name} {rows}x{cols}", "us": round(avg, 2), "GB/s": round(alg / avg / 1e3, 1),
-                    "frac": round(alg / avg / 1e3 / HBM_PEAK_GBS, 4)})
+        out.append({"shape": f"{name} {rows}x{cols}", "launches": launches, "us": round(avg, 2),
+                    "GB/s": round(alg / avg / 1e3, 1), "frac": round(alg / avg / 1e3 / HBM_PEAK_GBS, 4),
+                    "us_p10_p50_p90": [round(p10 * 1e3, 2), round(p50 * 1e3, 2), round(p90 * 1e3, 2)]})
         del ws, base
         torch.cuda.empty_cache()
     return out

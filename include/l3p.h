@@ -165,6 +165,7 @@ typedef struct {
     int64_t launches;
     double total_ms;          /* summed event-to-event time of the launches */
     double bytes_per_launch;  /* weight blocks + 4*cols + 4*output rows */
+    double p10_ms, p50_ms, p90_ms;   /* percentiles of the launch durations */
 } l3p_kernel_stat;
 int l3p_profile(l3p_ctx* ctx, int on);
 int l3p_profile_read(l3p_ctx* ctx, l3p_kernel_stat* out, int cap, int* n);

@@ -51,7 +51,8 @@ class ModelInfo(C.Structure):
 
 class KernelStat(C.Structure):
     _fields_ = [("name", C.c_char * 64), ("launches", C.c_int64), ("total_ms", C.c_double),
-                ("bytes_per_launch", C.c_double)]
+                ("bytes_per_launch", C.c_double), ("p10_ms", C.c_double), ("p50_ms", C.c_double),
+                ("p90_ms", C.c_double)]
 
 
 class Sampler(C.Structure):
@@ -230,14 +231,20 @@ class Context:
         """Start (clearing earlier figures) or stop GEMV launch timing."""
         self._check(self.L.l3p_profile(self.h, int(on)))
 
-    def profile_read(self):
-        """{label: (launches, total_ms, algorithmic bytes per launch)} of the timed GEMV launches."""
+    def _profile_stats(self):
         n = C.c_int(0)
         self._check(self.L.l3p_profile_read(self.h, None, 0, C.byref(n)))
         arr = (KernelStat * max(1, n.value))()
         self._check(self.L.l3p_profile_read(self.h, arr, n.value, C.byref(n)))
-        return {arr[i].name.decode(): (arr[i].launches, arr[i].total_ms, arr[i].bytes_per_launch)
-                for i in range(n.value)}
+        return [arr[i] for i in range(n.value)]
+
+    def profile_read(self):
+        """{label: (launches, total_ms, algorithmic bytes per launch)} of the timed GEMV launches."""
+        return {s.name.decode(): (s.launches, s.total_ms, s.bytes_per_launch) for s in self._profile_stats()}
+
+    def profile_percentiles(self):
+        """{label: (p10_ms, p50_ms, p90_ms)} of the timed launches' durations."""
+        return {s.name.decode(): (s.p10_ms, s.p50_ms, s.p90_ms) for s in self._profile_stats()}
 
     def rope_row(self, swa: bool, pos: int):
         import numpy as np

@@ -445,6 +445,7 @@ void Profiler::collect() {
         if (hipEventElapsedTime(&ms, q.a, q.b) == hipSuccess) {
             stats[q.stat].ms += ms;
             stats[q.stat].launches += 1;
+            stats[q.stat].each.push_back(ms);
         }
         pool.push_back(q.a);
         pool.push_back(q.b);
@@ -1066,6 +1067,14 @@ int l3p_profile_read(l3p_ctx* c, l3p_kernel_stat* out, int cap, int* n) {
             out[i].launches = st.launches;
             out[i].total_ms = st.ms;
             out[i].bytes_per_launch = st.bytes;
+            if (!st.each.empty()) {   // nearest-rank percentiles
+                std::vector<float> v(st.each);
+                std::sort(v.begin(), v.end());
+                auto pct = [&](double q) { return (double)v[(size_t)(q * (double)(v.size() - 1) + 0.5)]; };
+                out[i].p10_ms = pct(0.1);
+                out[i].p50_ms = pct(0.5);
+                out[i].p90_ms = pct(0.9);
+            }
         }
     });
 }

@@ -69,6 +69,7 @@ struct Profiler {
         int64_t launches = 0;
         double ms = 0.0;
         double bytes = 0.0;   // algorithmic bytes per launch
+        std::vector<float> each;   // every launch's duration (ms)
     };
     struct Pending {
         int stat;
