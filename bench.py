@@ -181,6 +181,28 @@ def gemma_prompt_decode(np, torch, l3p, synth, prompt_len=512, steps=128, warmup
             "decode_tok_s": round(steps / t_dec, 1), "last_token": int(tok)}
 
 
+def read_ceiling(ctx, torch, nbytes: int) -> float:
+    """GB/s of a plain streaming read of nbytes (l3p_stream_read: nontemporal
+    16-byte loads, four in flight per thread): buffers rotated through >= 1
+    GiB so the 256 MB MALL does not serve them, each read timed by its own
+    dispatch events; the median of at least 40 reads."""
+    nbytes = nbytes // 16 * 16
+    copies = max(2, -(-(1 << 30) // nbytes))
+    bufs = [torch.ones(nbytes // 4, dtype=torch.float32, device="cuda") for _ in range(copies)]
+    torch.cuda.synchronize()
+    for b in bufs:
+        ctx.stream_read(b, nbytes)
+    ctx.synchronize()
+    ctx.profile(True)
+    for i in range(max(40, 2 * copies)):
+        ctx.stream_read(bufs[i % copies], nbytes)
+    p50 = next(iter(ctx.profile_percentiles().values()))[1]
+    ctx.profile(False)
+    del bufs
+    torch.cuda.empty_cache()
+    return nbytes / (p50 * 1e-3) / 1e9
+
+
 def measured_traffic(kernel: str):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE +
     WRITE_SIZE summary (a line "traffic <kernel>: <bytes>"), else None."""
@@ -446,6 +468,9 @@ def main():
                    "GB/s": round(v[2] / (v[1] * 1e-3 / v[0]) / 1e9, 1)} for k, v in stats.items()}
     print(f"[bench] GEMV classes: {json.dumps(kernels)}", file=sys.stderr, flush=True)
 
+    ceiling = {"read_2GiB": round(read_ceiling(ctx, torch, 2 << 30), 1),
+               "read_same_bytes": round(read_ceiling(ctx, torch, int(bpl)), 1)}
+    print(f"[bench] streaming-read ceiling (GB/s): {json.dumps(ceiling)}", file=sys.stderr, flush=True)
     gemv = None if a.no_gemv else time_gemv_shapes(ctx, torch, l3p, synth)
     if gemv:
         print(f"[bench] standalone GEMV: {json.dumps(gemv)}", file=sys.stderr, flush=True)
@@ -475,7 +500,9 @@ def main():
                    "ffn": 14336, "vocab": 128256, "start_pos": a.prefill, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "kernel": name, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(name),
-                     "bytes_per_launch": int(bpl), "avg_launch_us": round(avg_us, 2), "launches": launches},
+                     "bytes_per_launch": int(bpl), "avg_launch_us": round(avg_us, 2), "launches": launches,
+                     "read_ceiling_GBps": ceiling,
+                     "frac_of_read_ceiling": round(achieved / ceiling["read_same_bytes"], 4)},
         "gemv_classes": kernels,
         "prefill": prefill,
         "gemv": gemv,

@@ -170,6 +170,12 @@ typedef struct {
 int l3p_profile(l3p_ctx* ctx, int on);
 int l3p_profile_read(l3p_ctx* ctx, l3p_kernel_stat* out, int cap, int* n);
 
+/* A plain streaming read of `bytes` (a multiple of 16) from the 16-byte
+ * aligned device buffer `buf` on the context stream, timed under l3p_profile
+ * as "stream read <bytes>".  No counterpart in the reference: it measures the
+ * HBM read ceiling that the GEMVs' weight stream is compared with. */
+int l3p_stream_read(l3p_ctx* ctx, const void* buf, size_t bytes);
+
 #ifdef __cplusplus
 }
 #endif

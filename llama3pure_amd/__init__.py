@@ -27,7 +27,7 @@ EXPORTS = [
     "l3p_dequant", "l3p_quantize_q8_0", "l3p_gemv", "l3p_gemm",
     "l3p_load_gguf", "l3p_get_model_info", "l3p_forward", "l3p_prefill", "l3p_decode",
     "l3p_sample", "l3p_logits_device", "l3p_copy_kv", "l3p_rope_row",
-    "l3p_profile", "l3p_profile_read",
+    "l3p_profile", "l3p_profile_read", "l3p_stream_read",
 ]
 
 
@@ -98,6 +98,7 @@ def lib() -> C.CDLL:
         "l3p_rope_row": (I, [P, I, I, P, P]),
         "l3p_profile": (I, [P, I]),
         "l3p_profile_read": (I, [P, C.POINTER(KernelStat), I, C.POINTER(I)]),
+        "l3p_stream_read": (I, [P, P, C.c_size_t]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)
@@ -241,6 +242,10 @@ class Context:
     def profile_read(self):
         """{label: (launches, total_ms, algorithmic bytes per launch)} of the timed GEMV launches."""
         return {s.name.decode(): (s.launches, s.total_ms, s.bytes_per_launch) for s in self._profile_stats()}
+
+    def stream_read(self, buf, nbytes: int):
+        """A plain streaming read of nbytes of the device buffer (timed under profile())."""
+        self._check(self.L.l3p_stream_read(self.h, _ptr(buf), nbytes))
 
     def profile_percentiles(self):
         """{label: (p10_ms, p50_ms, p90_ms)} of the timed launches' durations."""

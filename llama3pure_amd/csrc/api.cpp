@@ -160,6 +160,16 @@ int l3p_gemv(l3p_ctx* c, int type, const void* w, int rows, int cols, const floa
     });
 }
 
+int l3p_stream_read(l3p_ctx* c, const void* buf, size_t bytes) {
+    CHECK_CTX(c);
+    return guard(c, [&] {
+        L3P_REQUIRE(buf && ((uintptr_t)buf & 15) == 0 && bytes % 16 == 0, L3P_E_INVALID,
+                    "stream_read: buffer must be 16-byte aligned and a multiple of 16 bytes");
+        L3P_HIP(hipSetDevice(c->device));
+        run_stream_read(c, buf, bytes);
+    });
+}
+
 int l3p_gemm(l3p_ctx* c, int type, const void* w, int rows, int cols, const float* x, int batch,
              int in_stride, float* y, int out_stride) {
     CHECK_CTX(c);

@@ -2,6 +2,8 @@
 // fp32 values (quantize_row_q8_0, llama3pure-c-engine.c:1508-1528), bit-exact
 // dequantization of every supported type (dequantize_row_*, c:611-934) and
 // the embedding-row gather of a decode step.
+#include <algorithm>
+
 #include "dequant.h"
 #include "device_common.h"
 #include "internal.h"
@@ -48,7 +50,41 @@ __global__ void embed_step_kernel(int type, const uint8_t* __restrict__ s, int n
     }
 }
 
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// A plain streaming read of n 16-byte words, the bandwidth ceiling the decode
+// GEMVs' weight stream is compared with: each workgroup reads contiguous
+// blocks of 256 x kSR words (eight nontemporal loads in flight per thread),
+// folded into one value that is stored only in a case the data would have to
+// be built for (which keeps the loads).
+constexpr int kSR = 8;
+__global__ void __launch_bounds__(256) stream_read_kernel(const u32x4* __restrict__ p, size_t n, uint32_t* out) {
+    const size_t stride = (size_t)gridDim.x * 256 * kSR;
+    size_t i = (size_t)blockIdx.x * 256 * kSR + threadIdx.x;
+    uint32_t acc = 0;
+    for (; i + (kSR - 1) * 256 < n; i += stride) {
+        u32x4 v[kSR];
+#pragma unroll
+        for (int u = 0; u < kSR; ++u) v[u] = __builtin_nontemporal_load(p + i + u * 256);
+#pragma unroll
+        for (int u = 0; u < kSR; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    }
+    for (size_t j = i; j < n && j < i + kSR * 256; j += 256) {   // the one partial block
+        const u32x4 v = __builtin_nontemporal_load(p + j);
+        acc ^= v.x ^ v.y ^ v.z ^ v.w;
+    }
+    if (acc == 0x9e3779b9u) out[blockIdx.x & 255] = acc;
+}
+
 }  // namespace
+
+void launch_stream_read(const void* p, size_t bytes, uint32_t* out, hipStream_t st) {
+    const size_t n = bytes / 16;
+    if (n == 0) return;
+    const size_t want = (size_t)device_cus() * 8;   // 8 workgroups of 256 per CU
+    const unsigned grid = (unsigned)std::min(want, (n + 256 * kSR - 1) / (256 * kSR));
+    launch_kernel(stream_read_kernel, dim3(grid), dim3(256), 0u, st, reinterpret_cast<const u32x4*>(p), n, out);
+}
 
 void launch_quantize_q8_0_blocks(const float* x, int64_t n, uint8_t* dst, hipStream_t st) {
     const int64_t nb = n / 32;

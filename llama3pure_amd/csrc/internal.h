@@ -153,5 +153,8 @@ int device_cus();
 // blocks.hip
 void launch_quantize_q8_0_blocks(const float* x, int64_t n, uint8_t* dst, hipStream_t s);
 void launch_dequant(int type, const uint8_t* src, int64_t n, float* dst, hipStream_t s);
+// a plain streaming read of bytes (a multiple of 16) from 16-byte aligned p;
+// out: 256 words of device scratch
+void launch_stream_read(const void* p, size_t bytes, uint32_t* out, hipStream_t s);
 void launch_embed_row(int type, const uint8_t* row, int n, float scale, float* dst, int token, int pos, int* step,
                       hipStream_t s);

@@ -932,6 +932,11 @@ void run_gemm(l3p_ctx* c, int type, const uint8_t* w, int rows, int cols, const 
     }
 }
 
+void run_stream_read(l3p_ctx* c, const void* p, size_t bytes) {
+    ProfRange r(c->prof, c->stream, "stream read " + std::to_string(bytes), (double)bytes);
+    launch_stream_read(p, bytes, reinterpret_cast<uint32_t*>(c->gemm_ws), c->stream);
+}
+
 // ---------------------------------------------------------------------------
 // C-ABI
 // ---------------------------------------------------------------------------

@@ -161,5 +161,6 @@ int sample_groups(int n);
 int sample_max_k();
 
 // model.cpp
+void run_stream_read(l3p_ctx* c, const void* p, size_t bytes);
 void run_gemm(l3p_ctx* c, int type, const uint8_t* w, int rows, int cols, const float* x, int batch, int in_stride,
               float* y, int out_stride);

@@ -302,3 +302,19 @@ def test_gemm_mfma_equals_gemv_within_bound(ctx, torch_gpu, cpuref):
     tol = 2 * gamma(cols + 4) * (np.abs(xb.astype(np.float64)) @ A.T)
     diff = np.abs(y.view(batch, rows).cpu().numpy() - torch_gpu.stack(ys).cpu().numpy())
     assert np.all(diff <= tol)
+
+
+def test_stream_read(ctx, torch_gpu):
+    """The streaming-read probe takes aligned buffers and is timed under the
+    launch profiler; unaligned sizes and pointers are refused."""
+    buf = torch_gpu.ones(1 << 20, dtype=torch_gpu.float32, device="cuda")
+    ctx.profile(True)
+    ctx.stream_read(buf, 4 << 20)
+    ctx.stream_read(buf, 64)
+    stats = ctx.profile_read()
+    ctx.profile(False)
+    assert stats["stream read 4194304"][0] == 1 and stats["stream read 64"][0] == 1
+    with pytest.raises(l3p.L3PError):
+        ctx.stream_read(buf, 100)
+    with pytest.raises(l3p.L3PError):
+        ctx.stream_read(buf[1:], 64)
