@@ -13,7 +13,8 @@
 
 namespace {
 
-constexpr int kTC = 64;   // positions per attention chunk (one per lane)
+constexpr int kTC = 64;   // positions per attention chunk (one per lane); decode steps of
+                          // models with head_dim >= 192 use 32 (Model::dec_tc)
 typedef __attribute__((address_space(3))) void lds_void;
 
 using namespace l3pd;
@@ -132,6 +133,7 @@ struct AttnCArgs {
     const int* step;                 // device {token, pos}
     float* part;                     // [n_heads][part_chunks][hs + 2]: chunk output, max, sum
     int part_chunks;                 // chunk slots per head in part
+    int tc;                          // positions per chunk (kTC or 32)
     float* out;                      // [n_heads][hs]
     size_t head_seq;
     int n_heads, kv_mul, hs, hq8, window, neox;
@@ -155,16 +157,16 @@ __device__ __forceinline__ AttnCArgs token_args(const AttnCArgs& a0, int z) {
     return a;
 }
 
-// Positions this step attends to: [t0, pos], in chunks of kTC (c:3316-3322).
+// Positions this step attends to: [t0, pos], in chunks of tc (c:3316-3322).
 struct Span {
     int pos, t0, na, n_chunks;
 };
-__device__ __forceinline__ Span span_of(const int* step, int window) {
+__device__ __forceinline__ Span span_of(const int* step, int window, int tc) {
     Span s;
     s.pos = step[1];
     s.t0 = window > 0 ? max(0, s.pos - window + 1) : 0;
     s.na = s.pos - s.t0 + 1;
-    s.n_chunks = (s.na + kTC - 1) / kTC;
+    s.n_chunks = (s.na + tc - 1) / tc;
     return s;
 }
 
@@ -200,7 +202,7 @@ __device__ __forceinline__ void v_accum(uint32_t dh, uint32_t q, float e, float 
     for (int i = 0; i < PER; ++i) acc[i] = fmaf((float)(int8_t)((q >> (8 * i)) & 0xffu), f, acc[i]);
 }
 
-template <int NB>
+template <int NB, int TC>
 __global__ void __launch_bounds__(1024) attn_chunk_kernel(AttnCArgs a0) {
     extern __shared__ __align__(16) float smem[];
     const AttnCArgs a = token_args(a0, blockIdx.z);
@@ -228,22 +230,22 @@ __global__ void __launch_bounds__(1024) attn_chunk_kernel(AttnCArgs a0) {
         const int j = threadIdx.x + nt * k;
         kv2[k] = j < 2 * hs ? (j < hs ? a.k[(size_t)g * hs + j] : a.v[(size_t)g * hs + j - hs]) : 0.0f;
     }
-    const Span sp = span_of(a.step, a.window);
+    const Span sp = span_of(a.step, a.window, a.tc);
     if (c >= sp.n_chunks) return;   // the grid covers the longest context
-    const int jbeg = c * kTC, jend = min(sp.na, jbeg + kTC), cnt = jend - jbeg;
+    const int jbeg = c * TC, jend = min(sp.na, jbeg + TC), cnt = jend - jbeg;
     // the chunk holding the step's position forms and writes its K/V row,
     // unless a prompt batch's kv_rows_kernel already wrote it
     const bool has_pos = c == sp.n_chunks - 1 && !a.kv_ready;
 
-    // LDS: [kv_mul][hs] q rows, [2][hs] k and v rows, [kv_mul][8][kTC] V
+    // LDS: [kv_mul][hs] q rows, [2][hs] k and v rows, [kv_mul][8][TC] V
     // factors, [kv_mul][hs] int8 q, [kv_mul][8] q scales, then the chunk's K
-    // rows and V rows (kTC * hq8 bytes + 8 each, dword aligned)
+    // rows and V rows (TC * hq8 bytes + 8 each, dword aligned)
     float* qh = smem;
     float* kvh = qh + km * hs;
     float* f = kvh + 2 * hs;
-    int8_t* qq = reinterpret_cast<int8_t*>(f + km * 8 * kTC);
+    int8_t* qq = reinterpret_cast<int8_t*>(f + km * 8 * TC);
     float* qd = reinterpret_cast<float*>(qq + km * hs);
-    const int rowdw = (kTC * hq8 + 8 + 3) / 4;
+    const int rowdw = (TC * hq8 + 8 + 3) / 4;
     uint32_t* krows = reinterpret_cast<uint32_t*>(qd + km * 8);
     uint32_t* vrows = krows + rowdw;
 
@@ -399,14 +401,14 @@ __global__ void __launch_bounds__(1024) attn_chunk_kernel(AttnCArgs a0) {
 
     // f[b][j] = d(V row j, block b) * e_j, 0 for skipped positions
     const uint8_t* vbytes = reinterpret_cast<const uint8_t*>(vrows) + roff;
-    float* fw = f + (size_t)w * 8 * kTC;
+    float* fw = f + (size_t)w * 8 * TC;
     if (lane < cnt) {
         const bool skip = e < 1e-8f;
         uint32_t dv[NB];
 #pragma unroll
         for (int bb = 0; bb < NB; ++bb) dv[bb] = *reinterpret_cast<const uint16_t*>(vbytes + (size_t)lane * hq8 + 34 * bb);
 #pragma unroll
-        for (int bb = 0; bb < NB; ++bb) fw[bb * kTC + lane] = skip ? 0.0f : h2f(dv[bb]) * e;
+        for (int bb = 0; bb < NB; ++bb) fw[bb * TC + lane] = skip ? 0.0f : h2f(dv[bb]) * e;
     }
     __syncthreads();
     // V: acc_i += q_ji * f_j over the chunk's rows, eight rows' loads at a time
@@ -414,7 +416,7 @@ __global__ void __launch_bounds__(1024) attn_chunk_kernel(AttnCArgs a0) {
     const bool act = i0 < hs;
     const int b = act ? i0 >> 5 : 0;
     const uint8_t* qrow = vbytes + 34 * b + 2 + (i0 & 31);
-    const float* fb = fw + b * kTC;
+    const float* fb = fw + b * TC;
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     if (act) {
         int j = 0;
@@ -532,7 +534,7 @@ __global__ void __launch_bounds__(64) kv_rows_kernel(AttnCArgs a0) {
 __global__ void __launch_bounds__(256) attn_merge_kernel(AttnCArgs a0) {
     __shared__ float wc[64];
     const AttnCArgs a = token_args(a0, blockIdx.y);
-    const Span sp = span_of(a.step, a.window);
+    const Span sp = span_of(a.step, a.window, a.tc);
     const int h = blockIdx.x, hs = a.hs, nch = sp.n_chunks, t = threadIdx.x;
     const int ps = hs + 2;
     const float* part = a.part + (size_t)h * a.part_chunks * ps;
@@ -957,7 +959,7 @@ __global__ void __launch_bounds__(1024) attn_head_kernel(AttnCArgs a) {
     const int hq8 = 34 * NB;
     const int n_kv = a.n_heads / a.kv_mul;
     const int g = blockIdx.x % n_kv, hg = blockIdx.x / n_kv, h = g * a.kv_mul + hg;
-    const Span sp = span_of(a.step, a.window);
+    const Span sp = span_of(a.step, a.window, a.tc);
     const int cp = head_chunk_positions(hq8);
     const int nch = (sp.na + cp - 1) / cp;
     const int nk = w < nch ? (nch - 1 - w) / kHW + 1 : 0;   // chunks of this wave
@@ -1482,6 +1484,7 @@ static AttnCArgs attn_args(const Model& m, int l, const AttnIO& io) {
     a.step = io.step;
     a.part = m.part_acc;
     a.part_chunks = m.max_chunks;
+    a.tc = kTC;
     a.out = io.out;
     a.head_seq = m.head_seq;
     a.n_heads = m.n_heads;
@@ -1496,32 +1499,44 @@ static AttnCArgs attn_args(const Model& m, int l, const AttnIO& io) {
     return a;
 }
 
-template <int NB>
+template <int NB, int TC>
 static void launch_chunk_kernel(dim3 grid, dim3 block, size_t lds, const AttnCArgs& a, hipStream_t s) {
     static size_t lds_set = 65536;   // dynamic LDS above 64 KB must be allowed first
     if (lds > lds_set) {
-        L3P_HIP(hipFuncSetAttribute((const void*)attn_chunk_kernel<NB>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+        L3P_HIP(hipFuncSetAttribute((const void*)attn_chunk_kernel<NB, TC>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    (int)lds));
         lds_set = lds;
     }
-    hipLaunchKernelGGL(attn_chunk_kernel<NB>, grid, block, lds, s, a);
+    hipLaunchKernelGGL((attn_chunk_kernel<NB, TC>), grid, block, lds, s, a);
     L3P_HIP(hipGetLastError());
 }
 
 // Chunk and merge launches for `tokens` tokens of up to `chunks` chunks each.
 static void launch_chunks(const Model& m, const AttnCArgs& a, int chunks, int tokens, hipStream_t s) {
-    const int rowdw = (kTC * m.hq8 + 8 + 3) / 4;
-    const size_t lds = (size_t)m.kv_mul * m.hs * 4 + 2 * (size_t)m.hs * 4 + (size_t)m.kv_mul * 8 * kTC * 4 +
+    const int tc = a.tc;
+    const int rowdw = (tc * m.hq8 + 8 + 3) / 4;
+    const size_t lds = (size_t)m.kv_mul * m.hs * 4 + 2 * (size_t)m.hs * 4 + (size_t)m.kv_mul * 8 * tc * 4 +
                        (size_t)m.kv_mul * m.hs + (size_t)m.kv_mul * 8 * 4 + 2 * (size_t)rowdw * 4 + 16;
     const dim3 grid(m.n_kv, chunks, tokens), block(64 * m.kv_mul);
+    L3P_REQUIRE(tc == kTC || (tc == 32 && m.hs >= 192), L3P_E_INVALID, "attention: chunk of %d positions", tc);
     switch (m.hs / 32) {
-    case 1: launch_chunk_kernel<1>(grid, block, lds, a, s); break;
-    case 2: launch_chunk_kernel<2>(grid, block, lds, a, s); break;
-    case 3: launch_chunk_kernel<3>(grid, block, lds, a, s); break;
-    case 4: launch_chunk_kernel<4>(grid, block, lds, a, s); break;
-    case 5: launch_chunk_kernel<5>(grid, block, lds, a, s); break;
-    case 6: launch_chunk_kernel<6>(grid, block, lds, a, s); break;
-    case 7: launch_chunk_kernel<7>(grid, block, lds, a, s); break;
-    default: launch_chunk_kernel<8>(grid, block, lds, a, s); break;
+    case 1: launch_chunk_kernel<1, kTC>(grid, block, lds, a, s); break;
+    case 2: launch_chunk_kernel<2, kTC>(grid, block, lds, a, s); break;
+    case 3: launch_chunk_kernel<3, kTC>(grid, block, lds, a, s); break;
+    case 4: launch_chunk_kernel<4, kTC>(grid, block, lds, a, s); break;
+    case 5: launch_chunk_kernel<5, kTC>(grid, block, lds, a, s); break;
+    case 6:
+        if (tc == 32) launch_chunk_kernel<6, 32>(grid, block, lds, a, s);
+        else launch_chunk_kernel<6, kTC>(grid, block, lds, a, s);
+        break;
+    case 7:
+        if (tc == 32) launch_chunk_kernel<7, 32>(grid, block, lds, a, s);
+        else launch_chunk_kernel<7, kTC>(grid, block, lds, a, s);
+        break;
+    default:
+        if (tc == 32) launch_chunk_kernel<8, 32>(grid, block, lds, a, s);
+        else launch_chunk_kernel<8, kTC>(grid, block, lds, a, s);
+        break;
     }
     hipLaunchKernelGGL(attn_merge_kernel, dim3(m.n_heads, tokens), dim3((m.hs + 63) / 64 * 64), 0, s, a);
     L3P_HIP(hipGetLastError());
@@ -1540,8 +1555,9 @@ static void launch_head(const Model& m, const AttnCArgs& a, hipStream_t s) {
 }
 
 void launch_attention(const Model& m, int l, const AttnIO& io, bool per_head, hipStream_t s) {
-    const AttnCArgs a = attn_args(m, l, io);
+    AttnCArgs a = attn_args(m, l, io);
     if (!per_head) {
+        a.tc = m.dec_tc;   // part_chunks = max_chunks counts chunks of dec_tc positions
         launch_chunks(m, a, m.max_chunks, 1, s);
         return;
     }

@@ -399,8 +399,12 @@ static Model* load_model(l3p_ctx* c, const void* bytes, size_t len, const l3p_lo
     m.hb = (float*)m.dalloc((size_t)m.hidden * 4);
     m.hb2 = (float*)m.dalloc((size_t)m.hidden * 4);
     m.logits = (float*)m.dalloc((size_t)m.vocab * 4);
-    m.max_chunks = (m.seq_len + 63) / 64;
-    L3P_REQUIRE(m.max_chunks <= 4096, L3P_E_UNSUPPORTED, "context length %d exceeds 262144", m.seq_len);
+    // decode attention chunks: 64 positions, 32 for head_dim >= 192 (their
+    // chunk workgroups have the longest per-position work, so more and
+    // shorter chunks run in parallel)
+    m.dec_tc = m.hs >= 192 ? 32 : 64;
+    m.max_chunks = (m.seq_len + m.dec_tc - 1) / m.dec_tc;
+    L3P_REQUIRE(m.seq_len <= 262144, L3P_E_UNSUPPORTED, "context length %d exceeds 262144", m.seq_len);
     m.part_acc = (float*)m.dalloc((size_t)m.n_heads * m.max_chunks * (m.hs + 2) * 4);
     m.step = (int*)m.dalloc(4 * sizeof(int));
     const int ncand = std::max(256, sample_groups(m.vocab)) + sample_max_k();

@@ -47,7 +47,8 @@ struct Model {
     int *pf_tok = nullptr, *pf_steps = nullptr;
     float* pf_part = nullptr;      // attention chunk partials of a batch's tokens
     size_t pf_part_cap = 0;        // floats
-    int max_chunks = 0;
+    int max_chunks = 0;            // decode attention chunk slots per head
+    int dec_tc = 64;               // positions per decode attention chunk
     // sampler scratch
     float* cand_val = nullptr;     // device: group maxima, then top-k slot values
     int* cand_idx = nullptr;       // device: top-k slot indices
