@@ -224,6 +224,10 @@ struct GemvArgs {
     const float* x;     // fp32 activation
     const float* norm;  // RMSNorm weights, or null for x as is
     float eps, inv_n;
+    // x := x + post_w * (r_y * post_y) first, r_y = 1/sqrt(sum(post_y^2)/cols
+    // + eps), written to post_out by workgroup 0 (post_y null: x as is)
+    const float *post_y, *post_w;
+    float* post_out;
 };
 
 // Row `i` of the concatenated row space -> (segment, local row).
@@ -820,7 +824,7 @@ struct Lane<L3P_F32> {
     }
 };
 
-template <int QT, int G, int NB, bool PAIR, bool UA>
+template <int QT, int G, int NB, bool PAIR, bool UA, bool POST>
 __global__ void __launch_bounds__(1024) gemv_kernel(GemvArgs a) {
     constexpr int CB = Fmt<QT>::kChunkBytes;
     constexpr int CDW = Fmt<QT>::kBufBytes / 4;
@@ -859,7 +863,8 @@ __global__ void __launch_bounds__(1024) gemv_kernel(GemvArgs a) {
     };
     float* red = reinterpret_cast<float*>(lds + (size_t)nw * NB * CDW);   // [2][nw][G]
     float* ssred = red + 2 * nw * G;                                      // [nw]
-    float* out_lds = ssred + nw;                                          // [groups of this WG][NOUT]
+    float* ssy = ssred + nw;                                              // [nw] (post norm)
+    float* out_lds = ssy + nw;                                            // [groups of this WG][NOUT]
 
     // ---- this lane's activation block (and the norm weights), issued first:
     // they come from L2 while the weight copies below are in flight
@@ -874,7 +879,7 @@ __global__ void __launch_bounds__(1024) gemv_kernel(GemvArgs a) {
             const float4 q = xp[e];
             v[4 * e] = q.x; v[4 * e + 1] = q.y; v[4 * e + 2] = q.z; v[4 * e + 3] = q.w;
         }
-        if (a.norm) {
+        if (a.norm && !POST) {
             const float4* np = reinterpret_cast<const float4*>(a.norm + 32 * blk);
 #pragma unroll
             for (int e = 0; e < 8; ++e) nv[e] = np[e];
@@ -883,6 +888,25 @@ __global__ void __launch_bounds__(1024) gemv_kernel(GemvArgs a) {
 #pragma unroll
         for (int j = 0; j < 32; ++j) v[j] = 0.0f;
     }
+    // ---- optional residual update (rmsnorm_add_kernel's arithmetic): y is
+    // loaded here, ahead of the weight copies, in place of the norm weights,
+    // which are loaded with the post weights once the weight copies are
+    // issued (fewer live registers in the prologue)
+    float yv[32];
+    if (POST) {
+        if (active) {
+            const float4* yp = reinterpret_cast<const float4*>(a.post_y + 32 * blk);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float4 q = yp[e];
+                yv[4 * e] = q.x; yv[4 * e + 1] = q.y; yv[4 * e + 2] = q.z; yv[4 * e + 3] = q.w;
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 32; ++j) yv[j] = 0.0f;
+        }
+    }
+
     // ---- weight copies: the first NB-1 chunks of this workgroup's sequence,
     // CI instructions each.  nk = number of row-chunks this wave processes.
     const int ngroups_mine =
@@ -891,6 +915,41 @@ __global__ void __launch_bounds__(1024) gemv_kernel(GemvArgs a) {
 #pragma unroll
     for (int b = 0; b < NB - 1; ++b)
         if (b < nk) issue(b, b);
+
+    // x := x + post_w * (r_y * post_y), the same in every workgroup; the
+    // first workgroup stores it
+    if (POST) {
+        float sy = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 32; ++j) sy += yv[j] * yv[j];
+        sy = wave_sum(sy);
+        if (lane == 0) ssy[w] = sy;
+        lds_sync();
+        sy = 0.0f;
+        for (int i = 0; i < nw; ++i) sy += ssy[i];
+        const float ry = 1.0f / sqrtf(sy * a.inv_n + a.eps);
+        if (active) {
+            const float4* wp = reinterpret_cast<const float4*>(a.post_w + 32 * blk);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float4 pw = wp[e];
+                v[4 * e] = v[4 * e] + pw.x * (ry * yv[4 * e]);
+                v[4 * e + 1] = v[4 * e + 1] + pw.y * (ry * yv[4 * e + 1]);
+                v[4 * e + 2] = v[4 * e + 2] + pw.z * (ry * yv[4 * e + 2]);
+                v[4 * e + 3] = v[4 * e + 3] + pw.w * (ry * yv[4 * e + 3]);
+            }
+            if (blockIdx.x == 0) {
+                float4* op = reinterpret_cast<float4*>(a.post_out + 32 * blk);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) op[e] = make_float4(v[4 * e], v[4 * e + 1], v[4 * e + 2], v[4 * e + 3]);
+            }
+            if (a.norm) {
+                const float4* np = reinterpret_cast<const float4*>(a.norm + 32 * blk);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) nv[e] = np[e];
+            }
+        }
+    }
 
     // ---- optional RMSNorm.  Every block of x belongs to exactly one lane, so
     // ss = sum over lanes of the lane's 32 squares, then over lanes and waves
@@ -1040,9 +1099,11 @@ void launch_rows(GemvArgs a, hipStream_t st) {
     const int nb = a.cols / 32;
     const int nw = (nb + 63) / 64;
     const int threads = nw * 64;
-    const size_t base = (size_t)nw * NB * Fmt<QT>::kBufBytes + (size_t)2 * nw * G * 4 + (size_t)nw * 4;
+    const size_t base = (size_t)nw * NB * Fmt<QT>::kBufBytes + (size_t)2 * nw * G * 4 + (size_t)2 * nw * 4;
     auto lds_for = [&](int grid) { return base + (size_t)((a.ngroups + grid - 1) / grid) * NOUT * 4; };
-    auto kern = gemv_kernel<QT, G, NB, PAIR, UA>;
+    // the residual update is a separate instantiation: its registers would
+    // otherwise count against every GEMV
+    auto kern = a.post_y ? gemv_kernel<QT, G, NB, PAIR, UA, true> : gemv_kernel<QT, G, NB, PAIR, UA, false>;
     // Every workgroup reads the whole activation (and the norm weights when
     // fused), so workgroups per CU are also capped to keep that traffic near
     // 128 KB per CU: more workgroups than this only add x reads that compete
@@ -1160,6 +1221,12 @@ void launch_gemv(int type, const GemvBatch& b, int cols, const float* x, const f
     a.norm = norm;
     a.eps = eps;
     a.inv_n = 1.0f / (float)cols;
+    a.post_y = b.post_y;
+    a.post_w = b.post_w;
+    a.post_out = b.post_out;
+    L3P_REQUIRE(!b.post_y || (b.post_w && b.post_out && b.post_out != x && ((uintptr_t)b.post_y & 15) == 0 &&
+                              ((uintptr_t)b.post_w & 15) == 0 && ((uintptr_t)b.post_out & 15) == 0),
+                L3P_E_INVALID, "gemv: bad residual update arguments");
     // Rows per group G: the largest of 16, 8, 4 that still gives about six
     // waves per CU (groups x column chunks); ring depth 3.  (Measured on
     // MI355X at the Llama-3-8B shapes.)

@@ -117,6 +117,13 @@ struct GemvBatch {
     int nseg;
     int pair;      // 1: seg[0] and seg[1] are (gate, up) processed together
     int epilogue;  // GemvEpilogue
+    // Optional residual update before the GEMV's own norm (Gemma's post
+    // norms): x := x + post_w * rmsnorm(post_y) with the GEMV's eps and width,
+    // the updated x written to post_out (not x: the launch's workgroups all
+    // read x) by the first workgroup.
+    const float* post_y;
+    const float* post_w;
+    float* post_out;
 };
 
 // gemv.hip: the decode GEMV over Q8_0 / Q4_0 / Q4_K / Q6_K rows, with an

@@ -1420,10 +1420,6 @@ void launch_embed_step(const Mat& emb, int token, int pos, float scale, float* x
     launch_embed_row(emb.type, emb.w + (size_t)token * emb.rb, emb.cols, scale, x, token, pos, step, s);
 }
 
-void launch_rmsnorm_add(const float* y, const float* w, int n, float inv_n, float eps, float* x, hipStream_t s) {
-    launch_rmsnorm_add_rows(y, 0, w, n, inv_n, eps, x, 0, 1, s);
-}
-
 void launch_rmsnorm_add_rows(const float* y, int ldy, const float* w, int n, float inv_n, float eps, float* x,
                              int ldx, int rows, hipStream_t s) {
     if (rows == 0) return;

@@ -391,6 +391,7 @@ static Model* load_model(l3p_ctx* c, const void* bytes, size_t len, const l3p_lo
 
     // run state
     m.x = (float*)m.dalloc((size_t)m.dim * 4);
+    m.x2 = (float*)m.dalloc((size_t)m.dim * 4);
     m.xb = (float*)m.dalloc((size_t)m.max_dim * 4);
     m.xb2 = (float*)m.dalloc((size_t)m.dim * 4);
     m.q = (float*)m.dalloc((size_t)m.q_dim * 4);
@@ -567,7 +568,25 @@ static GemvBatch one(const Mat& W, float* y, int epi) {
 static void layers_impl(l3p_ctx* c, bool with_logits) {
     Model& m = *c->model;
     hipStream_t s = c->stream;
-    const float eps = m.eps > 0 ? m.eps : 1e-5f;                 // c:3198
+    // Gemma's post norms (x += rmsnorm(y) . w, c:3364-3371 and c:3411-3417)
+    // run in the prologue of the next GEMV that reads x, which writes the
+    // updated residual to the other of two buffers: `cur` is the residual,
+    // `pending` the post norm not yet applied to it.
+    float* cur = m.x;
+    float* alt = m.x2;
+    const float* pend_y = nullptr;
+    const float* pend_w = nullptr;
+    auto fold = [&](GemvBatch& b) {
+        if (!pend_y) return;
+        b.post_y = pend_y;
+        b.post_w = pend_w;
+        b.post_out = alt;
+    };
+    auto folded = [&]() {
+        if (!pend_y) return;
+        std::swap(cur, alt);
+        pend_y = nullptr;
+    };
     for (int l = 0; l < m.n_layers; ++l) {
         const Layer& L = m.layers[l];
         // q, k, v = W . rmsnorm(x) (c:3211-3230), one launch when the three share a type
@@ -578,20 +597,28 @@ static void layers_impl(l3p_ctx* c, bool with_logits) {
             b.seg[2] = GemvSegment{L.wv.w, m.v, L.wv.rows};
             b.nseg = 3;
             b.epilogue = EPI_STORE;
-            gemv_batch(c, L.wq.type, b, m.dim, m.x, L.att_norm, "qkv");
+            fold(b);
+            gemv_batch(c, L.wq.type, b, m.dim, cur, L.att_norm, "qkv");
         } else {
-            gemv_batch(c, L.wq.type, one(L.wq, m.q, EPI_STORE), m.dim, m.x, L.att_norm, "q");
-            gemv_batch(c, L.wk.type, one(L.wk, m.k, EPI_STORE), m.dim, m.x, L.att_norm, "k");
-            gemv_batch(c, L.wv.type, one(L.wv, m.v, EPI_STORE), m.dim, m.x, L.att_norm, "v");
+            // each launch forms the same updated residual from `cur`
+            GemvBatch bq = one(L.wq, m.q, EPI_STORE), bk = one(L.wk, m.k, EPI_STORE), bv = one(L.wv, m.v, EPI_STORE);
+            fold(bq);
+            fold(bk);
+            fold(bv);
+            gemv_batch(c, L.wq.type, bq, m.dim, cur, L.att_norm, "q");
+            gemv_batch(c, L.wk.type, bk, m.dim, cur, L.att_norm, "k");
+            gemv_batch(c, L.wv.type, bv, m.dim, cur, L.att_norm, "v");
         }
+        folded();
         // QK-norm, RoPE, KV write, Q quantization and attention (c:3232-3359)
         launch_attention(m, l, m.xb, c->attn_per_head, s);
         // output projection + residual (c:3362-3371)
         if (m.is_gemma) {
             gemv_batch(c, L.wo.type, one(L.wo, m.xb2, EPI_STORE), m.q_dim, m.xb, nullptr, "wo");
-            launch_rmsnorm_add(m.xb2, L.post_att, m.dim, m.inv_dim, eps, m.x, s);
+            pend_y = m.xb2;
+            pend_w = L.post_att;
         } else {
-            gemv_batch(c, L.wo.type, one(L.wo, m.x, EPI_ADD), m.q_dim, m.xb, nullptr, "wo");
+            gemv_batch(c, L.wo.type, one(L.wo, cur, EPI_ADD), m.q_dim, m.xb, nullptr, "wo");
         }
         // FFN (c:3373-3417): gate/up with the norm and the activation fused
         {
@@ -601,18 +628,26 @@ static void layers_impl(l3p_ctx* c, bool with_logits) {
             b.nseg = 2;
             b.pair = 1;
             b.epilogue = m.is_gemma ? EPI_GEGLU : EPI_SWIGLU;
-            gemv_batch(c, L.w1.type, b, m.dim, m.x, L.ffn_norm, "gate|up");
+            fold(b);
+            gemv_batch(c, L.w1.type, b, m.dim, cur, L.ffn_norm, "gate|up");
+            folded();
         }
         if (m.is_gemma) {
             gemv_batch(c, L.w2.type, one(L.w2, m.xb, EPI_STORE), m.hidden, m.hb, nullptr, "down");
-            launch_rmsnorm_add(m.xb, L.post_ffn, m.dim, m.inv_dim, eps, m.x, s);
+            pend_y = m.xb;
+            pend_w = L.post_ffn;
         } else {
-            gemv_batch(c, L.w2.type, one(L.w2, m.x, EPI_ADD), m.hidden, m.hb, nullptr, "down");
+            gemv_batch(c, L.w2.type, one(L.w2, cur, EPI_ADD), m.hidden, m.hb, nullptr, "down");
         }
     }
-    // final rmsnorm (c:3420) fused into the classifier (c:3423-3433)
+    // final rmsnorm (c:3420) fused into the classifier (c:3423-3433).  Without
+    // logits the last post norm is dropped: the next step's embedding
+    // overwrites the residual.
     if (with_logits) {
-        gemv_batch(c, m.wcls.type, one(m.wcls, m.logits, EPI_STORE), m.dim, m.x, m.final_norm, "lm_head");
+        GemvBatch b = one(m.wcls, m.logits, EPI_STORE);
+        fold(b);
+        gemv_batch(c, m.wcls.type, b, m.dim, cur, m.final_norm, "lm_head");
+        folded();
         if (m.is_gemma && m.softcap > 0.0f) launch_softcap(m.logits, m.vocab, m.softcap, s);
     }
 }

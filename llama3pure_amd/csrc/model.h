@@ -35,7 +35,7 @@ struct Model {
     float *cos_d = nullptr, *sin_d = nullptr, *cos_s = nullptr, *sin_s = nullptr;
 
     // run state (RunState, c:281-343), device resident
-    float *x = nullptr, *xb = nullptr, *xb2 = nullptr, *q = nullptr, *k = nullptr, *v = nullptr;
+    float *x = nullptr, *x2 = nullptr, *xb = nullptr, *xb2 = nullptr, *q = nullptr, *k = nullptr, *v = nullptr;
     float *hb = nullptr, *hb2 = nullptr, *logits = nullptr;
     float* part_acc = nullptr;     // [n_heads][max_chunks][hs + 2] attention chunk partials
     int* step = nullptr;           // device {token, pos} of the step being computed
@@ -125,7 +125,6 @@ void gemv_plain(l3p_ctx* c, int type, const GemvBatch& b, int cols, const float*
 // x = embedding row of `token` (times `scale` when non-zero) and the device
 // step record {token, pos} that the layer kernels read.
 void launch_embed_step(const Mat& emb, int token, int pos, float scale, float* x, int* step, hipStream_t s);
-void launch_rmsnorm_add(const float* y, const float* w, int n, float inv_n, float eps, float* x, hipStream_t s);
 // QK-norm, RoPE, the K/V cache write and attention of one layer for the
 // step's position (c:3232-3359); out = [n_heads][head_dim].  The first form
 // reads the decode step's q, k, v and step record.
