@@ -15,6 +15,11 @@ MODELS = {
     "gemma_q8_0": dict(arch="gemma3", dim=512, hidden=1536, n_layers=7, n_heads=4, n_kv=2, head_dim=256,
                        vocab=2048, ctx=256, qtype=synth.Q8_0, seed=3, softcap=30.0, swa_window=16,
                        norm_jitter=0.1, tied=True),
+    # Gemma with Q6_K V rows next to Q4_K Q and K rows: q, k and v run as three
+    # GEMV launches, each applying the pending post-FFN norm to the residual
+    "gemma_q4_k_m": dict(arch="gemma3", dim=512, hidden=1536, n_layers=4, n_heads=4, n_kv=2, head_dim=256,
+                         vocab=2048, ctx=256, qtype=synth.Q4_K, seed=10, softcap=30.0, swa_window=16,
+                         norm_jitter=0.1, tied=True, qtypes={"ffn_down": synth.Q6_K, "attn_v": synth.Q6_K}),
     "llama_q4_k_m": dict(arch="llama", dim=512, hidden=1024, n_layers=4, n_heads=8, n_kv=2, vocab=2048, ctx=256,
                          qtype=synth.Q4_K, seed=4, norm_jitter=0.1,
                          qtypes={"ffn_down": synth.Q6_K, "attn_v": synth.Q6_K, "output": synth.Q6_K}),
