@@ -57,30 +57,6 @@ GEMMA2_2B = dict(arch="gemma3", dim=2304, hidden=9216, n_layers=26, n_heads=8, n
                  seed=4321)
 
 
-def gpu_q8_0_maker(ctx, torch, seed):
-    """make_mat for synth.synthetic_model: N(0, std) drawn on the GPU and
-    quantized to Q8_0 blocks by the library's quantizer."""
-    st = torch.cuda.ExternalStream(ctx.stream)
-    gen = torch.Generator(device="cuda")
-    gen.manual_seed(seed)
-    import llama3pure_amd as l3p
-
-    def make(qtype, rows, cols, std, view):
-        assert qtype == l3p.Q8_0
-        rb = cols // 32 * 34
-        step = max(1, (1 << 26) // cols)
-        with torch.cuda.stream(st):
-            for r0 in range(0, rows, step):
-                n = min(step, rows - r0)
-                w = torch.randn(n * cols, device="cuda", generator=gen) * std
-                q = torch.empty(n * rb, dtype=torch.uint8, device="cuda")
-                ctx.quantize_q8_0(w, n * cols, q)
-                view[r0 * rb:(r0 + n) * rb] = q.cpu().numpy()
-        return view
-
-    return make
-
-
 def time_gemv_shapes(ctx, torch, l3p, synth):
     """GB/s of single GEMV launches: at least 200 l3p_gemv calls over rotating
     weight copies (>= 1 GiB, so no launch finds its weights in a cache), each
@@ -145,7 +121,7 @@ def gemma_prompt_decode(np, torch, l3p, synth, prompt_len=512, steps=128, warmup
     configurations) with `warmup` decode steps after it, then timed; the
     decode steps then continue from the timed prompt."""
     ctx = l3p.Context(0)
-    img = synth.synthetic_model(qtype=synth.Q8_0, make_mat=gpu_q8_0_maker(ctx, torch, 77), **GEMMA2_2B)
+    img = synth.synthetic_model(qtype=synth.Q8_0, make_mat=synth.gpu_q8_0_maker(ctx, torch, 77), **GEMMA2_2B)
     mi = ctx.load_gguf(img)
     del img
     prompt = np.random.default_rng(6).integers(0, mi.vocab_size, prompt_len).astype(np.int32)
@@ -414,7 +390,7 @@ def main():
     ctx = l3p.Context(0)
     t0 = time.perf_counter()
     cfg = dict(LLAMA3_8B, n_layers=a.layers)
-    img = synth.synthetic_model(qtype=synth.Q8_0, make_mat=gpu_q8_0_maker(ctx, torch, 99), **cfg)
+    img = synth.synthetic_model(qtype=synth.Q8_0, make_mat=synth.gpu_q8_0_maker(ctx, torch, 99), **cfg)
     t_gen = time.perf_counter() - t0
     mi = ctx.load_gguf(img)
     print(f"[bench] model {img.nbytes / 1e9:.2f} GB generated in {t_gen:.1f} s, "

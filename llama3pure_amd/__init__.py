@@ -220,6 +220,15 @@ class Context:
         self._check(self.L.l3p_sample(self.h, _ptr(logits_dev), n, C.byref(s), C.byref(st), C.byref(out)))
         return out.value, st.value
 
+    def logits(self):
+        """The last forward's or decode's vocab logits, copied from the device."""
+        import numpy as np
+        d = C.c_void_p()
+        self._check(self.L.l3p_logits_device(self.h, C.byref(d)))
+        out = np.empty(self.model_info().vocab_size, np.float32)
+        self._check(self.L.l3p_download(self.h, out.ctypes.data, d, out.nbytes))
+        return out
+
     def copy_kv(self, layer: int, which_v: bool):
         import numpy as np
         mi = self.model_info()

@@ -546,3 +546,28 @@ def synthetic_model(arch: str = "llama", dim: int = 256, hidden: int = 512, n_la
 
     out = build_gguf(meta, specs, fill)
     return out if make_mat is not None else out.tobytes()
+
+
+def gpu_q8_0_maker(ctx, torch, seed: int):
+    """make_mat for synthetic_model that draws each matrix N(0, std) on the GPU
+    (torch's generator, seeded) and quantizes it to Q8_0 blocks with the
+    library's quantizer (l3p_quantize_q8_0), for multi-GB models that numpy
+    would take minutes to quantize.  ctx is an llama3pure_amd.Context."""
+    st = torch.cuda.ExternalStream(ctx.stream)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed)
+
+    def make(qtype, rows, cols, std, view):
+        assert qtype == Q8_0, "the GPU maker writes Q8_0 blocks only"
+        rb = cols // 32 * 34
+        step = max(1, (1 << 26) // cols)
+        with torch.cuda.stream(st):
+            for r0 in range(0, rows, step):
+                n = min(step, rows - r0)
+                w = torch.randn(n * cols, device="cuda", generator=gen) * std
+                q = torch.empty(n * rb, dtype=torch.uint8, device="cuda")
+                ctx.quantize_q8_0(w, n * cols, q)
+                view[r0 * rb:(r0 + n) * rb] = q.cpu().numpy()
+        return view
+
+    return make

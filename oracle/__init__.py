@@ -105,6 +105,7 @@ class CpuRef(_Lib):
         L.l3o_forward.argtypes = [_P, C.c_int, C.c_int, C.c_int, _P]
         L.l3o_prefill.argtypes = [_P, _P, C.c_int, C.c_int]
         L.l3o_copy_kv.argtypes = [_P, C.c_int, C.c_int, _P, C.c_size_t]
+        L.l3o_set_kv.argtypes = [_P, C.c_int, C.c_int, _P, C.c_size_t]
         L.l3o_copy_x.argtypes = [_P, _P]
         L.l3o_rope_row.argtypes = [_P, C.c_int, C.c_int, _P, _P]
 
@@ -201,7 +202,12 @@ class CpuModel:
 
     def __init__(self, ref: CpuRef, gguf: bytes, context_size: int):
         self.ref = ref
-        self._buf = np.frombuffer(gguf, dtype=np.uint8).copy()
+        # a uint8 array is borrowed as is (multi-GB images are not copied);
+        # bytes are copied into an array the model keeps alive
+        if isinstance(gguf, np.ndarray) and gguf.dtype == np.uint8 and gguf.flags.c_contiguous:
+            self._buf = gguf
+        else:
+            self._buf = np.frombuffer(gguf, dtype=np.uint8).copy()
         h = ref.lib.l3o_model_open(_vp(self._buf), self._buf.size, context_size)
         if not h:
             raise ValueError(ref.lib.l3o_last_error().decode())
@@ -230,6 +236,13 @@ class CpuModel:
         if self.ref.lib.l3o_copy_kv(self.h, layer, int(which_v), _vp(out), n) != 0:
             raise RuntimeError("copy_kv")
         return out
+
+    def set_kv(self, layer: int, which_v: bool, data: np.ndarray) -> None:
+        """Overwrite one layer's K or V cache (test support: installs a long
+        context without prefilling it in the oracle)."""
+        data = np.ascontiguousarray(data, np.uint8)
+        if self.ref.lib.l3o_set_kv(self.h, layer, int(which_v), _vp(data), data.size) != 0:
+            raise RuntimeError("set_kv")
 
     def rope_row(self, swa: bool, pos: int):
         c = np.empty(self.head_dim // 2, np.float32)
@@ -285,6 +298,7 @@ class Ref(_Lib):
         L.ref_forward.argtypes = [C.c_int, C.c_int, C.c_int, _P]
         L.ref_prefill.argtypes = [_P, C.c_int, C.c_int]
         L.ref_copy_kv.argtypes = [C.c_int, C.c_int, _P, C.c_size_t]
+        L.ref_set_kv.argtypes = [C.c_int, C.c_int, _P, C.c_size_t]
         L.ref_copy_x.argtypes = [_P]
         L.ref_rope_row.argtypes = [C.c_int, C.c_int, _P, _P]
         L.ref_generate_token.argtypes = [C.c_int, C.c_int, C.c_float, C.c_int, C.c_float, C.POINTER(C.c_ulonglong)]

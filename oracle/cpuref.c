@@ -491,65 +491,124 @@ static float dot_q8_0_q8_0(const uint8_t* xq, const uint8_t* w, int n) {
     return sum;
 }
 
+static int is_q8_act(int type) {   /* q8_func without a row dequantizer (c:2091-2133) */
+    return type == L3O_Q4_0 || type == L3O_Q4_1 || type == L3O_Q5_0 || type == L3O_Q5_1 || type == L3O_IQ4_NL;
+}
+
+static int is_float_type(int type) {
+    return type == L3O_F32 || type == L3O_F16 || type == L3O_BF16 || type == L3O_BF16_ALT;
+}
+
+/* Rows dequantized to fp32, then for each batch element b the sequential fp32
+ * dot y[b][r] = sum_j w[r][j] * x[b][j], j = 0, 1, ... in order: the per-row
+ * arithmetic of matmul_deq_4row / matmul_deq_batch_4row (c:2136-2273) and of
+ * the float dots vec_dot_f16/bf16/f32 (c:1467-1494; x*w and w*x round alike).
+ * Rows are taken kRowBlock at a time, each row its own accumulation chain, and
+ * the blocks are spread over OpenMP threads, as the reference spreads its row
+ * groups (c:2145, c:2189); no row's value depends on the thread count. */
+enum { kRowBlock = 8 };
+/* Eight fp32 lanes, one per row of a block: every operation on it is the
+ * lane-wise IEEE multiply or add, so lane r accumulates exactly the sequence
+ * s_r += w[r][j] * x[j] that a scalar loop over j would. */
+typedef float v8f __attribute__((vector_size(32)));
+
+static int deq_rows_dot(int type, const uint8_t* wb, size_t rb, int rows, int cols, const float* x, int batch,
+                        int ldx, float* y, int ldy) {
+    const int nblk = (rows + kRowBlock - 1) / kRowBlock;
+    int err = 0;
+#pragma omp parallel
+    {
+        /* the block's rows interleaved: wt[j] = {w[r0][j], .., w[r0 + 7][j]} */
+        v8f* wt = (v8f*)aligned_alloc(32, (size_t)cols * sizeof(v8f));
+        float* row = (float*)malloc((size_t)cols * sizeof(float));
+        if (!wt || !row) {
+#pragma omp atomic write
+            err = 1;
+        }
+#pragma omp for schedule(static)
+        for (int g = 0; g < nblk; g++) {
+            if (!wt || !row) continue;
+            const int r0 = g * kRowBlock;
+            const int nr = rows - r0 < kRowBlock ? rows - r0 : kRowBlock;
+            for (int r = 0; r < kRowBlock; r++) {
+                if (r < nr) {
+                    if (l3o_dequant_row(type, wb + (size_t)(r0 + r) * rb, row, cols) != 0) {
+#pragma omp atomic write
+                        err = 1;
+                    }
+                } else {
+                    memset(row, 0, (size_t)cols * sizeof(float));
+                }
+                for (int j = 0; j < cols; j++) wt[j][r] = row[j];
+            }
+            int b = 0;
+            for (; b + 1 < batch; b += 2) {   /* two independent chains per lane */
+                const float* x0 = x + (size_t)b * ldx;
+                const float* x1 = x0 + ldx;
+                v8f s0 = {0}, s1 = {0};
+                for (int j = 0; j < cols; j++) {
+                    s0 = s0 + wt[j] * x0[j];
+                    s1 = s1 + wt[j] * x1[j];
+                }
+                for (int r = 0; r < nr; r++) {
+                    y[(size_t)b * ldy + r0 + r] = s0[r];
+                    y[(size_t)(b + 1) * ldy + r0 + r] = s1[r];
+                }
+            }
+            if (b < batch) {
+                const float* x0 = x + (size_t)b * ldx;
+                v8f s0 = {0};
+                for (int j = 0; j < cols; j++) s0 = s0 + wt[j] * x0[j];
+                for (int r = 0; r < nr; r++) y[(size_t)b * ldy + r0 + r] = s0[r];
+            }
+        }
+        free(wt);
+        free(row);
+    }
+    return err ? -1 : 0;
+}
+
+/* The Q8_0-activation types: each batch element quantized to Q8_0 once, then
+ * the integer block dot of every row (c:2105-2116, c:2305-2318). */
+static int q8_rows_dot(int type, const uint8_t* wb, size_t rb, int rows, int cols, const float* x, int batch,
+                       int ldx, float* y, int ldy) {
+    float (*dot)(const uint8_t*, const uint8_t*, int) =
+        type == L3O_Q4_0 ? dot_q4_0_q8_0 : type == L3O_Q4_1 ? dot_q4_1_q8_0 :
+        type == L3O_Q5_0 ? dot_q5_0_q8_0 : type == L3O_Q5_1 ? dot_q5_1_q8_0 : dot_iq4_nl_q8_0;
+    const size_t qb = (size_t)(cols / 32) * 34;
+    uint8_t* xq = (uint8_t*)malloc(qb * (size_t)(batch > 0 ? batch : 1));
+    if (!xq) return -1;
+    for (int b = 0; b < batch; b++) l3o_quantize_q8_0(x + (size_t)b * ldx, xq + (size_t)b * qb, cols);
+#pragma omp parallel for schedule(static)
+    for (int r = 0; r < rows; r++)
+        for (int b = 0; b < batch; b++) y[(size_t)b * ldy + r] = dot(xq + (size_t)b * qb, wb + (size_t)r * rb, cols);
+    free(xq);
+    return 0;
+}
+
 /* matmul_quantized (c:2091-2133): rows with a row dequantizer (Q8_0, Q2_K
  * .. Q6_K) go through matmul_deq_4row (c:2136-2176): dequantize to fp32 then
  * a sequential fp32 dot `s += w[j]*x[j]`.  Q4_0, Q4_1, Q5_0, Q5_1 and IQ4_NL
  * quantize x to Q8_0 once and use their integer block dots.  F32/F16/BF16
  * take the float dot (sequential, c:1467-1494). */
 int l3o_matmul(int type, const void* w, int rows, int cols, const float* x, float* y) {
-    const uint8_t* wb = (const uint8_t*)w;
-    size_t rb = l3o_row_bytes(type, cols);
-    half_table_init();
-    if (has_row_dequant(type)) {
-        float* buf = (float*)malloc((size_t)cols * sizeof(float));
-        if (!buf) return -1;
-        for (int r = 0; r < rows; r++) {
-            if (l3o_dequant_row(type, wb + (size_t)r * rb, buf, cols) != 0) { free(buf); return -1; }
-            float s = 0.0f;
-            for (int j = 0; j < cols; j++) s += buf[j] * x[j];
-            y[r] = s;
-        }
-        free(buf);
-        return 0;
-    }
-    if (type == L3O_Q4_0 || type == L3O_Q4_1 || type == L3O_Q5_0 || type == L3O_Q5_1 || type == L3O_IQ4_NL) {
-        float (*dot)(const uint8_t*, const uint8_t*, int) =
-            type == L3O_Q4_0 ? dot_q4_0_q8_0 : type == L3O_Q4_1 ? dot_q4_1_q8_0 :
-            type == L3O_Q5_0 ? dot_q5_0_q8_0 : type == L3O_Q5_1 ? dot_q5_1_q8_0 : dot_iq4_nl_q8_0;
-        uint8_t* xq = (uint8_t*)malloc((size_t)(cols / 32) * 34);
-        if (!xq) return -1;
-        l3o_quantize_q8_0(x, xq, cols);
-        for (int r = 0; r < rows; r++) y[r] = dot(xq, wb + (size_t)r * rb, cols);
-        free(xq);
-        return 0;
-    }
-    if (type == L3O_F32 || type == L3O_F16 || type == L3O_BF16 || type == L3O_BF16_ALT) {
-        float* buf = (float*)malloc((size_t)cols * sizeof(float));
-        if (!buf) return -1;
-        for (int r = 0; r < rows; r++) {
-            l3o_dequant_row(type, wb + (size_t)r * rb, buf, cols);
-            float s = 0.0f;
-            for (int j = 0; j < cols; j++) s += x[j] * buf[j];
-            y[r] = s;
-        }
-        free(buf);
-        return 0;
-    }
-    return -1;
+    return l3o_matmul_batch(type, w, rows, cols, x, 1, cols, y, rows);
 }
 
 /* matmul_quantized_batch (c:2291-2331) computes, for every batch element,
- * exactly what matmul_quantized computes for that element alone. */
+ * exactly what matmul_quantized computes for that element alone; here every
+ * row is dequantized once for the whole batch, as matmul_deq_batch_4row
+ * does (c:2179-2273). */
 int l3o_matmul_batch(int type, const void* w, int rows, int cols, const float* x, int batch,
                      int in_stride, float* y, int out_stride) {
-    float* tmp = (float*)malloc((size_t)rows * sizeof(float));
-    if (!tmp) return -1;
-    for (int b = 0; b < batch; b++) {
-        if (l3o_matmul(type, w, rows, cols, x + (size_t)b * in_stride, tmp) != 0) { free(tmp); return -1; }
-        memcpy(y + (size_t)b * out_stride, tmp, (size_t)rows * sizeof(float));
-    }
-    free(tmp);
-    return 0;
+    const uint8_t* wb = (const uint8_t*)w;
+    const size_t rb = l3o_row_bytes(type, cols);
+    half_table_init();
+    if (rows <= 0 || batch <= 0) return rows < 0 || batch < 0 ? -1 : 0;
+    if (has_row_dequant(type) || is_float_type(type))
+        return deq_rows_dot(type, wb, rb, rows, cols, x, batch, in_stride, y, out_stride);
+    if (is_q8_act(type)) return q8_rows_dot(type, wb, rb, rows, cols, x, batch, in_stride, y, out_stride);
+    return -1;
 }
 
 /* ------------------------------------------------------------------------ */
@@ -1039,12 +1098,20 @@ static q8dot_t q8_dot_of(int type) {
     }
 }
 
-static int is_q8_class(int type) {   /* q8_func && !deq_func, c:3221 */
-    return type == L3O_Q4_0 || type == L3O_Q4_1 || type == L3O_Q5_0 || type == L3O_Q5_1 || type == L3O_IQ4_NL;
-}
+static int is_q8_class(int type) { return is_q8_act(type); }   /* q8_func && !deq_func, c:3221 */
 
 static int mm(const qt_t* q, const float* x, float* y) {
     return l3o_matmul(q->type, q->data, q->rows, q->cols, x, y);
+}
+
+/* matmul_quantized_preq8 (c:2275-2288): the rows of one matrix dotted with an
+ * activation already quantized to Q8_0, through the matrix's own q8 dot. */
+static int preq8_rows(const qt_t* w, const uint8_t* xq8, float* out) {
+    q8dot_t dot = q8_dot_of(w->type);
+    if (!dot) return -1;
+#pragma omp parallel for schedule(static)
+    for (int r = 0; r < w->rows; r++) out[r] = dot(xq8, w->data + (size_t)r * w->rb, w->cols);
+    return 0;
 }
 
 /* Q8_0 KV cache dot (c:1574-1597): sum += da*db*(float)isum per block. */
@@ -1134,6 +1201,9 @@ static void attend(l3o_model* m, int l, int pos, float* q, float* k, const float
         if (t0 < 0) t0 = 0;
     }
     int na = pos - t0 + 1;
+    /* query heads are independent (the reference spreads KV heads over
+     * threads, c:3328) */
+#pragma omp parallel for schedule(static)
     for (int h = 0; h < m->n_heads; h++) {
         int kh = h / m->kv_mul;
         const uint8_t* kb = m->kc + loff + kh * m->head_seq;
@@ -1171,17 +1241,9 @@ int l3o_forward(l3o_model* m, int token, int pos, int compute_logits, float* log
         if (is_q8_class(m->wq[l].type)) {
             /* one Q8_0 quantization shared by q/k/v (c:3221-3225) */
             l3o_quantize_q8_0(m->xb, m->xq8, m->wq[l].cols);
-            const qt_t* ws[3] = {&m->wq[l], &m->wk[l], &m->wv[l]};
-            float* outs[3] = {m->q, m->k, m->v};
-            for (int i = 0; i < 3; i++) {
-                const qt_t* w = ws[i];
-                for (int r = 0; r < w->rows; r++) {
-                    const uint8_t* row = w->data + (size_t)r * w->rb;
-                    q8dot_t dot = q8_dot_of(w->type);
-                    if (!dot) return -2;
-                    outs[i][r] = dot(m->xq8, row, w->cols);
-                }
-            }
+            if (preq8_rows(&m->wq[l], m->xq8, m->q) || preq8_rows(&m->wk[l], m->xq8, m->k) ||
+                preq8_rows(&m->wv[l], m->xq8, m->v))
+                return -2;
         } else {
             if (mm(&m->wq[l], m->xb, m->q) || mm(&m->wk[l], m->xb, m->k) || mm(&m->wv[l], m->xb, m->v)) return -2;
         }
@@ -1192,17 +1254,7 @@ int l3o_forward(l3o_model* m, int token, int pos, int compute_logits, float* log
         rmsnorm_inv(m->xb, x, m->ffn_norm + (size_t)l * dim, dim, m->inv_dim, eps);
         if (is_q8_class(m->w1[l].type)) {
             l3o_quantize_q8_0(m->xb, m->xq8, m->w1[l].cols);
-            const qt_t* ws[2] = {&m->w1[l], &m->w3[l]};
-            float* outs[2] = {m->hb, m->hb2};
-            for (int i = 0; i < 2; i++) {
-                const qt_t* w = ws[i];
-                for (int r = 0; r < w->rows; r++) {
-                    const uint8_t* row = w->data + (size_t)r * w->rb;
-                    q8dot_t dot = q8_dot_of(w->type);
-                    if (!dot) return -2;
-                    outs[i][r] = dot(m->xq8, row, w->cols);
-                }
-            }
+            if (preq8_rows(&m->w1[l], m->xq8, m->hb) || preq8_rows(&m->w3[l], m->xq8, m->hb2)) return -2;
         } else {
             if (mm(&m->w1[l], m->xb, m->hb) || mm(&m->w3[l], m->xb, m->hb2)) return -2;
         }
@@ -1292,6 +1344,15 @@ out:
 int l3o_copy_kv(const l3o_model* m, int layer, int which_v, void* dst, size_t cap) {
     if (layer < 0 || layer >= m->n_layers || cap < m->layer_kv) return -1;
     memcpy(dst, (which_v ? m->vc : m->kc) + (size_t)layer * m->layer_kv, m->layer_kv);
+    return 0;
+}
+
+/* Test support, no counterpart in the reference: overwrite one layer's K or
+ * V cache with n bytes (the layout l3o_copy_kv returns), so a long context
+ * can be installed without prefilling it here. */
+int l3o_set_kv(l3o_model* m, int layer, int which_v, const void* src, size_t n) {
+    if (layer < 0 || layer >= m->n_layers || n != m->layer_kv) return -1;
+    memcpy((which_v ? m->vc : m->kc) + (size_t)layer * m->layer_kv, src, n);
     return 0;
 }
 

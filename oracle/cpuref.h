@@ -78,6 +78,9 @@ int   l3o_forward(l3o_model* m, int token, int pos, int compute_logits, float* l
 int   l3o_prefill(l3o_model* m, const int* tokens, int start_pos, int batch);
 /* Copies one layer's Q8_0 key or value cache ([kv_head][seq][hd/32*34 B]). */
 int   l3o_copy_kv(const l3o_model* m, int layer, int which_v, void* dst, size_t cap);
+/* Test support (no counterpart in the reference): overwrites one layer's K or
+ * V cache with exactly layer_kv bytes in the l3o_copy_kv layout. */
+int   l3o_set_kv(l3o_model* m, int layer, int which_v, const void* src, size_t n);
 /* Row pos of the RoPE cos/sin tables (c:381-422); swa selects the
  * sliding-window tables of Gemma models. */
 int   l3o_rope_row(const l3o_model* m, int swa, int pos, float* cos_out, float* sin_out);

@@ -136,6 +136,15 @@ int ref_copy_kv(int layer, int which_v, void* dst, size_t cap) {
     return 0;
 }
 
+/* Harness-side test support (the engine has no such entry point): overwrite
+ * one layer's K or V cache with exactly kv_cache_layer_size bytes, so a long
+ * context written elsewhere can be installed before decode steps. */
+int ref_set_kv(int layer, int which_v, const void* src, size_t n) {
+    if (layer < 0 || layer >= config.n_layers || n != state.kv_cache_layer_size) return -1;
+    memcpy((which_v ? state.value_cache : state.key_cache) + (size_t)layer * n, src, n);
+    return 0;
+}
+
 void ref_rope_row(int swa, int p, float* c, float* s) {
     int half = state.head_size / 2;
     memcpy(c, (swa ? state.rope_cos_swa_all : state.rope_cos_all) + (size_t)p * half, half * sizeof(float));

@@ -12,7 +12,8 @@ reference differs from itself across its own supported builds.
 Needs oracle/_ref/libref_omp.so (``make -C oracle ref``).  One model per
 subprocess because the reference keeps its model in process globals.
 
-usage: python tests/golden/make_ref_drift.py        (rewrites ref_drift.json)
+usage: python tests/golden/make_ref_drift.py              (rewrites ref_drift.json)
+       python tests/golden/make_ref_drift.py --long-only  (refreshes its "long" section)
 """
 import json
 import os
@@ -97,7 +98,68 @@ def measure_single(case: str) -> list:
         os.unlink(path)
 
 
+def measure_long(case: str) -> dict:
+    """The long-context protocol of test_gpu_long_context.py: a prompt of
+    LONG_CASES[case]["prompt"] tokens (the reference's prefill batches of 32,
+    c:5277-5287), then LONG_STEPS teacher-forced decode steps; per step
+    max|dlogit|/rms of the reference's two builds, and the K/V quant
+    differences of every layer over all positions written."""
+    import oracle
+    from llama3pure_amd import synth
+    import model_cases as T
+
+    c = T.LONG_CASES[case]
+    g = synth.synthetic_model(**c["model"])
+    fd, path = tempfile.mkstemp(suffix=".gguf")
+    with os.fdopen(fd, "wb") as f:
+        f.write(g)
+    try:
+        ref = oracle.Ref(oracle.REF_OMP_SO)
+        assert ref.lib.ref_model_open(path.encode(), 0) == 0
+        m = oracle.CpuRef().open_model(g)
+        toks = T.long_prompt(case)
+        n = c["prompt"]
+        pos = 0
+        while pos < n:
+            bs = min(32, n - pos)
+            ref.lib.ref_prefill(oracle._vp(toks), pos, bs)
+            pos += bs
+        m.prefill(toks, 0, n)
+        tok = int(toks[n])
+        out = np.empty(m.vocab, np.float32)
+        rel = []
+        for _ in range(T.LONG_STEPS):
+            lo = m.forward(tok, pos)
+            ref.lib.ref_forward(tok, pos, 1, oracle._vp(out))
+            rel.append(float(np.abs(lo - out).max()) / T.rms(lo))
+            tok, pos = int(np.argmax(lo)), pos + 1
+        kv = {}
+        for layer in range(m.n_layers):
+            for wv in (0, 1):
+                b = m.kv(layer, bool(wv))
+                a = np.empty(b.size, np.uint8)
+                ref.lib.ref_copy_kv(layer, wv, oracle._vp(a), a.size)
+                d = T.kv_quant_diff(a, b, m, pos)
+                kv[f"{layer}/{'v' if wv else 'k'}"] = {"max": int(d.max()), "mean": float(d.mean())}
+        return {"max_rel": max(rel), "per_step": rel, "kv": kv}
+    finally:
+        os.unlink(path)
+
+
 def main():
+    if len(sys.argv) == 3 and sys.argv[1] == "--long":
+        print(json.dumps(measure_long(sys.argv[2])))
+        return
+    if len(sys.argv) == 2 and sys.argv[1] == "--long-only":
+        # refresh only the long-context section of an existing ref_drift.json
+        import model_cases as T
+        path = os.path.join(HERE, "ref_drift.json")
+        with open(path) as f:
+            out = json.load(f)
+        out["long"] = long_section(T)
+        with open(path, "w") as f:
+            json.dump(out, f, indent=1)
+        return
     if len(sys.argv) == 3 and sys.argv[1] == "--one":
         print(json.dumps(measure(sys.argv[2])))
         return
@@ -121,8 +183,22 @@ def main():
                            env=env)
         out["single_layer"][case] = json.loads(r.stdout.strip().splitlines()[-1])
         print(case, " ".join(f"{v:.1e}" for v in out["single_layer"][case]))
+    out["long"] = long_section(T)
     with open(os.path.join(HERE, "ref_drift.json"), "w") as f:
         json.dump(out, f, indent=1)
+
+
+def long_section(T) -> dict:
+    env = dict(os.environ, OMP_NUM_THREADS=os.environ.get("OMP_NUM_THREADS", "4"))
+    res = {}
+    for case in T.LONG_CASES:
+        r = subprocess.run([sys.executable, __file__, "--long", case], check=True, capture_output=True, text=True,
+                           env=env)
+        res[case] = json.loads(r.stdout.strip().splitlines()[-1])
+        print(case, f"{res[case]['max_rel']:.3e}",
+              "kv max", max(v["max"] for v in res[case]["kv"].values()),
+              "mean", f"{max(v['mean'] for v in res[case]['kv'].values()):.2e}")
+    return res
 
 
 if __name__ == "__main__":

@@ -104,6 +104,13 @@ def kv_quant_diff(a, b, m, pos):
     return np.abs(qa.astype(np.int32) - qb.astype(np.int32))
 
 
+def kv_rows_diff(a, b, n_kv, seq_len, p0, p1):
+    """|quant_a - quant_b| over the Q8_0 K or V cache blocks of positions [p0, p1)."""
+    qa = a.reshape(n_kv, seq_len, -1, 34)[:, p0:p1, :, 2:].view(np.int8)
+    qb = b.reshape(n_kv, seq_len, -1, 34)[:, p0:p1, :, 2:].view(np.int8)
+    return np.abs(qa.astype(np.int32) - qb.astype(np.int32))
+
+
 def _load_drift(key):
     p = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "ref_drift.json")
     if not os.path.exists(p):
@@ -117,3 +124,43 @@ def _load_drift(key):
 REF_DRIFT = _load_drift("models")
 # single-layer case -> max|dlogit|/rms(logits) per token of SINGLE_TOKENS at position 0
 SINGLE_DRIFT = _load_drift("single_layer")
+
+
+# Long contexts against the oracle (tests/test_gpu_long_context.py): a prompt
+# of `prompt` tokens through the batched prompt path (1024-row passes,
+# attn_prefill_kernel), then teacher-forced decode steps whose attention spans
+# the whole prompt (chunks + merge by default from 512 positions; the
+# per-head kernel forced for the later steps).  Small widths keep the oracle
+# fast; the head shapes, GQA groups and windows are the ones the kernels
+# specialise on.
+LONG_CASES = {
+    # head_dim 64, GQA 2, three prompt passes (2100 rows)
+    "llama_hs64_2100": dict(model=dict(arch="llama", dim=256, hidden=512, n_layers=2, n_heads=4, n_kv=2, vocab=512,
+                                       ctx=2304, qtype=synth.Q8_0, seed=51, norm_jitter=0.1), prompt=2100),
+    # head_dim 128 (136-byte cache rows), GQA 4, two passes
+    "llama_hs128_1100": dict(model=dict(arch="llama", dim=512, hidden=512, n_layers=2, n_heads=4, n_kv=1, vocab=512,
+                                        ctx=1280, qtype=synth.Q8_0, seed=52, norm_jitter=0.1), prompt=1100),
+    # Gemma head_dim 256 (32-position decode chunks), QK-norm, NEOX RoPE, a
+    # 257-position window on five of six layers: windows start mid-prompt
+    "gemma_hs256_swa_600": dict(model=dict(arch="gemma3", dim=512, hidden=512, n_layers=6, n_heads=2, n_kv=1,
+                                           head_dim=256, vocab=512, ctx=768, qtype=synth.Q8_0, seed=53,
+                                           softcap=30.0, swa_window=257, norm_jitter=0.1, tied=True), prompt=600),
+    # Gemma head_dim 128, GQA 2, a 1000-position window at 2100 positions
+    "gemma_hs128_swa_2100": dict(model=dict(arch="gemma3", dim=256, hidden=256, n_layers=6, n_heads=2, n_kv=1,
+                                            head_dim=128, vocab=512, ctx=2304, qtype=synth.Q8_0, seed=54,
+                                            softcap=30.0, swa_window=1000, norm_jitter=0.1, tied=True), prompt=2100),
+    # 4300 positions: 68 decode chunks of 64, so the merge takes two rounds;
+    # five prompt passes
+    "llama_hs64_4300": dict(model=dict(arch="llama", dim=256, hidden=256, n_layers=2, n_heads=4, n_kv=2, vocab=512,
+                                       ctx=4608, qtype=synth.Q8_0, seed=55, norm_jitter=0.1), prompt=4300),
+}
+LONG_STEPS = 4   # decode steps after the prompt (the last two on the per-head kernel)
+
+
+def long_prompt(case):
+    c = LONG_CASES[case]
+    return np.random.default_rng(c["model"]["seed"] + 100).integers(0, c["model"]["vocab"], c["prompt"] + 1).astype(
+        np.int32)
+
+
+LONG_DRIFT = _load_drift("long")
