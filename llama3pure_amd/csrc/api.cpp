@@ -50,9 +50,10 @@ int l3p_create(int device, l3p_ctx** out) {
             delete c;
             throw L3pError{L3P_E_HIP, std::string("hipStreamCreate: ") + hipGetErrorString(e)};
         }
-        const size_t ws_floats = (size_t)16 << 20;   // 64 MB of GEMM split-K partials
+        const size_t ws_floats = kGemmWsFloats;   // 64 MB of GEMM split-K partials
         e = hipMalloc(&c->gemm_ws, ws_floats * 4);
         if (e != hipSuccess) {
+            (void)hipGetLastError();
             hipStreamDestroy(c->stream);
             delete c;
             throw L3pError{L3P_E_HIP, std::string("hipMalloc: ") + hipGetErrorString(e)};
@@ -90,6 +91,7 @@ int l3p_malloc(l3p_ctx* c, size_t bytes, void** out) {
         L3P_REQUIRE(out, L3P_E_INVALID, "out is NULL");
         L3P_HIP(hipSetDevice(c->device));
         hipError_t e = hipMalloc(out, bytes ? bytes : 1);
+        if (e != hipSuccess) (void)hipGetLastError();   // consumed here: later launch checks must not see it
         if (e == hipErrorOutOfMemory) throw L3pError{L3P_E_NOMEM, "hipMalloc: out of device memory"};
         L3P_HIP(e);
     });
@@ -170,17 +172,28 @@ int l3p_stream_read(l3p_ctx* c, const void* buf, size_t bytes) {
     });
 }
 
+// Arguments of l3p_gemm; false when there is nothing to do.
+static bool gemm_args_ok(int type, const void* w, int rows, int cols, const float* x, int batch, int in_stride,
+                         const float* y, int out_stride) {
+    L3P_REQUIRE(rows >= 0 && cols > 0 && batch >= 0, L3P_E_INVALID, "gemm: bad shape %d x %d, batch %d", rows, cols,
+                batch);
+    L3P_REQUIRE(type_block_elems(type) > 0 && cols % type_block_elems(type) == 0, L3P_E_INVALID,
+                "gemm: cols=%d not a multiple of the block size of type %d", cols, type);
+    L3P_REQUIRE(in_stride >= cols && out_stride >= rows, L3P_E_INVALID, "gemm: bad strides %d, %d", in_stride,
+                out_stride);
+    L3P_REQUIRE(in_stride % 4 == 0, L3P_E_INVALID, "gemm: in_stride %d is not a multiple of 4", in_stride);
+    L3P_REQUIRE(gemv_supported(type, cols), L3P_E_UNSUPPORTED,
+                "gemm: type %d with %d columns not supported", type, cols);
+    if (rows == 0 || batch == 0) return false;
+    L3P_REQUIRE(w && x && y, L3P_E_INVALID, "gemm: null pointer");
+    return true;
+}
+
 int l3p_gemm(l3p_ctx* c, int type, const void* w, int rows, int cols, const float* x, int batch,
              int in_stride, float* y, int out_stride) {
     CHECK_CTX(c);
     return guard(c, [&] {
-        L3P_REQUIRE(batch >= 0 && in_stride >= cols && out_stride >= rows, L3P_E_INVALID,
-                    "gemm: bad batch/strides");
-        L3P_REQUIRE(in_stride % 4 == 0, L3P_E_INVALID, "gemm: in_stride %d is not a multiple of 4", in_stride);
-        L3P_REQUIRE(gemv_supported(type, cols), L3P_E_UNSUPPORTED,
-                    "gemm: type %d with %d columns not supported", type, cols);
-        if (rows == 0 || batch == 0) return;
-        L3P_REQUIRE(w && x && y, L3P_E_INVALID, "gemm: null pointer");
+        if (!gemm_args_ok(type, w, rows, cols, x, batch, in_stride, y, out_stride)) return;
         L3P_HIP(hipSetDevice(c->device));
         run_gemm(c, type, (const uint8_t*)w, rows, cols, x, batch, in_stride, y, out_stride);
     });

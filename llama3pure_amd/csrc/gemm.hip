@@ -240,8 +240,38 @@ bool gemm_mfma_supported(int type) {
     }
 }
 
+// The launch plan of a job: K splits and the partials they need (floats).
+GemmPlan gemm_plan(const GemmJob& j, size_t ws_floats) {
+    GemmPlan p;
+    int tiles = 0, ntot = 0;
+    for (int i = 0; i < j.nseg; ++i) {
+        tiles += (j.seg[i].n + kBN - 1) / kBN;
+        ntot += j.seg[i].n;
+    }
+    // K splits while the tiles give fewer than four workgroups per CU (the
+    // LDS of four fits a CU), each split at least eight K steps long
+    const int steps = (j.k + kBK - 1) / kBK;
+    const int mt = (j.m + kBM - 1) / kBM;
+    const int want = 4 * device_cus();
+    int split = 1;
+    if (ws_floats && j.m > 0 && (long)tiles * mt < want) {
+        split = std::min({(int)((want + (long)tiles * mt - 1) / ((long)tiles * mt)), steps / 8, 8});
+        while (split > 1 && (size_t)split * j.m * ntot > ws_floats) --split;
+        split = std::max(split, 1);
+    }
+    p.ksteps = (steps + split - 1) / split;
+    p.nsplit = p.ksteps > 0 ? (steps + p.ksteps - 1) / p.ksteps : 1;   // no empty split
+    p.partial_floats = p.nsplit > 1 ? (size_t)p.nsplit * j.m * ntot : 0;
+    return p;
+}
+
 void launch_gemm(const GemmJob& j, float* ws, size_t ws_floats, hipStream_t st) {
+    launch_gemm_planned(j, gemm_plan(j, ws ? ws_floats : 0), ws, st);
+}
+
+void launch_gemm_planned(const GemmJob& j, const GemmPlan& plan, float* ws, hipStream_t st) {
     L3P_REQUIRE(gemm_mfma_supported(j.type), L3P_E_UNSUPPORTED, "gemm: type %d has no MFMA path", j.type);
+    L3P_REQUIRE(plan.nsplit == 1 || ws, L3P_E_INVALID, "gemm: split-K plan without a workspace");
     L3P_REQUIRE(j.k % 32 == 0 && j.ldx % 4 == 0 && ((uintptr_t)j.x & 15) == 0, L3P_E_INVALID,
                 "gemm: x rows must be 16-byte aligned");
     L3P_REQUIRE(j.m <= 65535 * kBM, L3P_E_INVALID, "gemm: batch %d too large", j.m);
@@ -270,19 +300,8 @@ void launch_gemm(const GemmJob& j, float* ws, size_t ws_floats, hipStream_t st) 
     a.ldx = j.ldx;
     a.add = j.add ? 1 : 0;
     a.ntot = ntot;
-    // K splits while the tiles give fewer than four workgroups per CU (the
-    // LDS of four fits a CU), each split at least eight K steps long
-    const int steps = (j.k + kBK - 1) / kBK;
-    const int mt = (j.m + kBM - 1) / kBM;
-    const int want = 4 * device_cus();
-    int split = 1;
-    if (ws && (long)tiles * mt < want) {
-        split = std::min({(int)((want + (long)tiles * mt - 1) / ((long)tiles * mt)), steps / 8, 8});
-        while (split > 1 && (size_t)split * j.m * ntot > ws_floats) --split;
-        split = std::max(split, 1);
-    }
-    a.ksteps = (steps + split - 1) / split;
-    a.nsplit = (steps + a.ksteps - 1) / a.ksteps;   // no empty split
+    a.ksteps = plan.ksteps;
+    a.nsplit = plan.nsplit;
     a.part = a.nsplit > 1 ? ws : nullptr;
     switch (j.type) {
     case L3P_Q8_0: launch_typed<L3P_Q8_0>(a, st); break;

@@ -155,6 +155,16 @@ struct GemmJob {
 };
 bool gemm_mfma_supported(int type);
 void launch_gemm(const GemmJob& j, float* ws, size_t ws_floats, hipStream_t s);
+// K splits of a job and the fp32 partials they need, for a workspace of
+// ws_floats floats (0: no split)
+struct GemmPlan {
+    int nsplit = 1, ksteps = 0;
+    size_t partial_floats = 0;
+};
+GemmPlan gemm_plan(const GemmJob& j, size_t ws_floats);
+void launch_gemm_planned(const GemmJob& j, const GemmPlan& plan, float* ws, hipStream_t s);
+// split-K partials of a context (allocated with it): 64 MB
+constexpr size_t kGemmWsFloats = (size_t)16 << 20;
 // compute units of the current device
 int device_cus();
 // blocks.hip

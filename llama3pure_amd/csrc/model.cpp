@@ -21,6 +21,7 @@
 void* Model::dalloc(size_t bytes) {
     void* p = nullptr;
     hipError_t e = hipMalloc(&p, bytes ? bytes : 16);
+    if (e != hipSuccess) (void)hipGetLastError();   // consumed here: later launch checks must not see it
     if (e == hipErrorOutOfMemory) throw L3pError{L3P_E_NOMEM, "model: out of device memory"};
     L3P_HIP(e);
     allocs.push_back(p);
@@ -266,6 +267,7 @@ static Model* load_model(l3p_ctx* c, const void* bytes, size_t len, const l3p_lo
     if (const KV* tk = g.find("tokenizer.ggml.tokens"))   // vocab from the token list (c:5152-5157)
         if (tk->type == 9 && tk->atype == 8 && tk->alen > 0) m.vocab = (int)tk->alen;
     if (opts && opts->context_size > 0 && opts->context_size < m.seq_len) m.seq_len = opts->context_size;
+    L3P_REQUIRE(m.seq_len <= 262144, L3P_E_UNSUPPORTED, "context length %d exceeds 262144", m.seq_len);
 
     L3P_REQUIRE(m.dim > 0 && m.hidden > 0 && m.n_layers > 0 && m.vocab > 0 && m.seq_len > 0, L3P_E_FORMAT,
                 "GGUF: bad dimensions");
@@ -405,7 +407,6 @@ static Model* load_model(l3p_ctx* c, const void* bytes, size_t len, const l3p_lo
     // shorter chunks run in parallel)
     m.dec_tc = m.hs >= 192 ? 32 : 64;
     m.max_chunks = (m.seq_len + m.dec_tc - 1) / m.dec_tc;
-    L3P_REQUIRE(m.seq_len <= 262144, L3P_E_UNSUPPORTED, "context length %d exceeds 262144", m.seq_len);
     m.part_acc = (float*)m.dalloc((size_t)m.n_heads * m.max_chunks * (m.hs + 2) * 4);
     m.step = (int*)m.dalloc(4 * sizeof(int));
     const int ncand = std::max(256, sample_groups(m.vocab)) + sample_max_k();
@@ -1039,8 +1040,8 @@ int l3p_prefill(l3p_ctx* c, const int32_t* tokens, int n, int32_t start) {
     return mguard(c, true, [&] {
         const Model& m = *c->model;
         L3P_REQUIRE(n >= 0 && (n == 0 || tokens), L3P_E_INVALID, "prefill: bad token buffer");
-        L3P_REQUIRE(start >= 0 && start + n <= m.seq_len, L3P_E_INVALID, "prefill: positions [%d, %d) exceed %d", start,
-                    start + n, m.seq_len);
+        L3P_REQUIRE(start >= 0 && start <= m.seq_len && n <= m.seq_len - start, L3P_E_INVALID,
+                    "prefill: %d positions from %d exceed the context of %d", n, start, m.seq_len);
         for (int i = 0; i < n; ++i)
             L3P_REQUIRE(tokens[i] >= 0 && tokens[i] < m.vocab, L3P_E_INVALID, "prefill: token %d out of range",
                         tokens[i]);
