@@ -91,6 +91,19 @@ int l3p_gemv(l3p_ctx* ctx, int type, const void* w_dev, int rows, int cols, cons
 int l3p_gemm(l3p_ctx* ctx, int type, const void* w_dev, int rows, int cols, const float* x_dev,
              int batch, int in_stride, float* y_dev, int out_stride);
 
+/* l3p_gemm without a context and without any allocation.  No counterpart in
+ * the reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  The work is enqueued on `stream` (a hipStream_t; NULL: the
+ * null stream) of the current device.  Split-K partials go to a file-scope
+ * device array of 16 MB (4 Mi floats) that each GPU holds for the life of
+ * the process; the launch plan is l3p_gemm's, so results are l3p_gemm's, and
+ * a shape whose partials would exceed the array returns L3P_E_UNSUPPORTED.
+ * Every call on a GPU shares that GPU's array: calls that overlap on one GPU
+ * race.  Errors: the code, with the message in l3p_last_error(NULL). */
+int l3p_gemm_static(int type, const void* w_dev, int rows, int cols, const float* x_dev, int batch,
+                    int in_stride, float* y_dev, int out_stride, void* stream);
+
 /* ---- model -------------------------------------------------------------- */
 typedef struct {
     int context_size;   /* <=0: the model's context_length (c:5174-5178; js:4335)   */

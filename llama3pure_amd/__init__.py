@@ -27,7 +27,7 @@ EXPORTS = [
     "l3p_dequant", "l3p_quantize_q8_0", "l3p_gemv", "l3p_gemm",
     "l3p_load_gguf", "l3p_get_model_info", "l3p_forward", "l3p_prefill", "l3p_decode",
     "l3p_sample", "l3p_logits_device", "l3p_copy_kv", "l3p_rope_row",
-    "l3p_profile", "l3p_profile_read", "l3p_stream_read",
+    "l3p_profile", "l3p_profile_read", "l3p_stream_read", "l3p_gemm_static",
 ]
 
 
@@ -99,6 +99,7 @@ def lib() -> C.CDLL:
         "l3p_profile": (I, [P, I]),
         "l3p_profile_read": (I, [P, C.POINTER(KernelStat), I, C.POINTER(I)]),
         "l3p_stream_read": (I, [P, P, C.c_size_t]),
+        "l3p_gemm_static": (I, [I, P, I, I, P, I, I, P, I, P]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)

@@ -172,7 +172,7 @@ int l3p_stream_read(l3p_ctx* c, const void* buf, size_t bytes) {
     });
 }
 
-// Arguments of l3p_gemm; false when there is nothing to do.
+// Arguments of l3p_gemm / l3p_gemm_static; false when there is nothing to do.
 static bool gemm_args_ok(int type, const void* w, int rows, int cols, const float* x, int batch, int in_stride,
                          const float* y, int out_stride) {
     L3P_REQUIRE(rows >= 0 && cols > 0 && batch >= 0, L3P_E_INVALID, "gemm: bad shape %d x %d, batch %d", rows, cols,
@@ -196,6 +196,41 @@ int l3p_gemm(l3p_ctx* c, int type, const void* w, int rows, int cols, const floa
         if (!gemm_args_ok(type, w, rows, cols, x, batch, in_stride, y, out_stride)) return;
         L3P_HIP(hipSetDevice(c->device));
         run_gemm(c, type, (const uint8_t*)w, rows, cols, x, batch, in_stride, y, out_stride);
+    });
+}
+
+int l3p_gemm_static(int type, const void* w, int rows, int cols, const float* x, int batch, int in_stride,
+                    float* y, int out_stride, void* stream) {
+    return guard(nullptr, [&] {
+        if (!gemm_args_ok(type, w, rows, cols, x, batch, in_stride, y, out_stride)) return;
+        const hipStream_t st = static_cast<hipStream_t>(stream);
+        if (!gemm_mfma_supported(type)) {
+            // the Q8_0-activation types: the GEMV per batch row, as l3p_gemm
+            for (int b = 0; b < batch; ++b) {
+                GemvBatch gb{};
+                gb.seg[0] = GemvSegment{(const uint8_t*)w, y + (size_t)b * out_stride, rows};
+                gb.nseg = 1;
+                gb.epilogue = EPI_STORE;
+                launch_gemv(type, gb, cols, x + (size_t)b * in_stride, nullptr, 0.0f, st);
+            }
+            return;
+        }
+        GemmJob j{};
+        j.type = type;
+        j.seg[0] = GemmSegment{(const uint8_t*)w, rows, y, out_stride};
+        j.nseg = 1;
+        j.k = cols;
+        j.x = x;
+        j.m = batch;
+        j.ldx = in_stride;
+        // the plan l3p_gemm takes with its context workspace, so the values
+        // are l3p_gemm's; its partials must fit the file-scope array
+        const GemmPlan plan = gemm_plan(j, kGemmWsFloats);
+        L3P_REQUIRE(plan.partial_floats <= kGemmStaticScratchFloats, L3P_E_UNSUPPORTED,
+                    "gemm_static: %d x %d x batch %d needs %zu floats of split-K partials, more than the %zu of the "
+                    "static scratch; use l3p_gemm",
+                    rows, cols, batch, plan.partial_floats, kGemmStaticScratchFloats);
+        launch_gemm_planned(j, plan, plan.nsplit > 1 ? gemm_static_scratch() : nullptr, st);
     });
 }
 

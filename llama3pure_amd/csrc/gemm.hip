@@ -27,6 +27,7 @@
 // gemm_reduce_kernel adds the splits in split order, so results do not
 // depend on scheduling.
 #include <algorithm>
+#include <mutex>
 
 #include "dequant.h"
 #include "device_common.h"
@@ -315,4 +316,32 @@ void launch_gemm_planned(const GemmJob& j, const GemmPlan& plan, float* ws, hipS
     default: launch_typed<L3P_BF16>(a, st); break;
     }
     if (a.nsplit > 1) launch_kernel(gemm_reduce_kernel, dim3((ntot + 255) / 256, j.m), dim3(256), 0u, st, a);
+}
+
+// ---------------------------------------------------------------------------
+// The split-K partials of l3p_gemm_static: a file-scope device array instead
+// of a context workspace, so that entry point allocates nothing.  Each GPU
+// holds its own copy for the life of the process; host code uses the device
+// address that hipGetSymbolAddress returns for the current device (the
+// array's name is only a host-side stand-in).  Calls that overlap on one GPU
+// share it and race.
+// ---------------------------------------------------------------------------
+namespace {
+__device__ __align__(256) float scratch[kGemmStaticScratchFloats];
+constexpr int kMaxDevices = 64;
+}  // namespace
+
+float* gemm_static_scratch() {
+    static std::mutex mu;
+    static float* ptr[kMaxDevices] = {};
+    int dev = 0;
+    L3P_HIP(hipGetDevice(&dev));
+    L3P_REQUIRE(dev >= 0 && dev < kMaxDevices, L3P_E_UNSUPPORTED, "gemm_static: device %d", dev);
+    std::lock_guard<std::mutex> g(mu);
+    if (!ptr[dev]) {
+        void* p = nullptr;
+        L3P_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        ptr[dev] = static_cast<float*>(p);
+    }
+    return ptr[dev];
 }

@@ -165,6 +165,10 @@ GemmPlan gemm_plan(const GemmJob& j, size_t ws_floats);
 void launch_gemm_planned(const GemmJob& j, const GemmPlan& plan, float* ws, hipStream_t s);
 // split-K partials of a context (allocated with it): 64 MB
 constexpr size_t kGemmWsFloats = (size_t)16 << 20;
+// the file-scope partials array of l3p_gemm_static (16 MB per GPU) and its
+// device address on the current device
+constexpr size_t kGemmStaticScratchFloats = (size_t)4 << 20;
+float* gemm_static_scratch();
 // compute units of the current device
 int device_cus();
 // blocks.hip

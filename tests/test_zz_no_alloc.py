@@ -1,0 +1,64 @@
+"""l3p_gemm_static: the allocation-free l3p_gemm (file-scope split-K
+partials, no context), called through the C-ABI, against l3p_gemm on the same
+inputs: bit-identical outputs (the same kernels and the same launch plan), on
+two calls in a row, the second smaller, both splitting K so the file-scope
+partials are used; a shape whose partials exceed the array is rejected
+without a launch."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import llama3pure_amd as l3p
+from llama3pure_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+
+def _static(L, qt, w, rows, cols, x, batch, y, stream):
+    return L.l3p_gemm_static(qt, w.data_ptr(), rows, cols, x.data_ptr(), batch, cols, y.data_ptr(), rows, stream)
+
+
+@pytest.mark.parametrize("qt", [synth.Q8_0, synth.Q4_K, synth.Q4_0])
+def test_gemm_static_equals_gemm(torch_gpu, qt):
+    torch = torch_gpu
+    L = l3p.lib()
+    with l3p.Context(0) as ctx:
+        # rows x cols x batch: 64 output tiles of one 64-row tile, K split 8
+        # ways (partials of 8 x 8 x 4096 floats), then a smaller call split 4
+        # ways; for Q4_0 the GEMV per batch row
+        for rows, cols, batch in ((4096, 4096, 8), (1024, 2048, 3)):
+            w = torch.from_numpy(synth.random_blocks(qt, rows, cols, seed=rows + batch)).cuda()
+            x = torch.from_numpy(synth.random_x(cols, seed=cols, batch=batch)).cuda()
+            y_ref = torch.full((batch, rows), float("nan"), device="cuda")
+            y_st = torch.full((batch, rows), float("nan"), device="cuda")
+            torch.cuda.synchronize()
+            ctx.gemm(qt, w, rows, cols, x, batch, cols, y_ref, rows)
+            ctx.synchronize()
+            rc = _static(L, qt, w, rows, cols, x, batch, y_st, ctx.stream)
+            assert rc == l3p.OK, L.l3p_last_error(None).decode()
+            ctx.synchronize()
+            a, b = y_ref.cpu().numpy(), y_st.cpu().numpy()
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), (qt, rows, cols, batch)
+
+
+def test_gemm_static_rejects_oversized_partials(torch_gpu):
+    torch = torch_gpu
+    L = l3p.lib()
+    with l3p.Context(0) as ctx:
+        # 255 x 4 output tiles split twice: 2 x 256 x 16320 floats of
+        # partials, more than the 4 Mi of the file-scope array
+        rows, cols, batch = 16320, 1024, 256
+        w = torch.zeros(rows * synth.row_bytes(synth.Q8_0, cols), dtype=torch.uint8, device="cuda")
+        x = torch.zeros(batch * cols, device="cuda")
+        y = torch.zeros(batch * rows, device="cuda")
+        torch.cuda.synchronize()
+        rc = L.l3p_gemm_static(synth.Q8_0, w.data_ptr(), rows, cols, x.data_ptr(), batch, cols, y.data_ptr(), rows,
+                               ctx.stream)
+        assert rc == l3p.E_UNSUPPORTED
+        assert b"static scratch" in L.l3p_last_error(None)
+        # bad arguments are rejected before anything runs
+        assert L.l3p_gemm_static(synth.Q8_0, w.data_ptr(), -1, cols, x.data_ptr(), 1, cols, y.data_ptr(), rows,
+                                 ctx.stream) == l3p.E_INVALID
+        assert L.l3p_gemm_static(synth.Q8_0, w.data_ptr(), rows, 0, x.data_ptr(), 1, cols, y.data_ptr(), rows,
+                                 ctx.stream) == l3p.E_INVALID
