@@ -295,7 +295,7 @@ struct XBlock {
     float s;        //   fp32 value of the Q8_0 scale
     int sum8;       //   8 * sum of quants
     float xs;       // sum of the 32 values (Q4_K, Q5_K)
-    float xs0, xs1; // sums of values 0..15 and 16..31 (Q2_K, Q3_K, Q6_K)
+    float xs0, xs1; // sums of values 0..15 and 16..31 (Q6_K)
 };
 
 template <int QT>
@@ -645,8 +645,13 @@ __device__ __forceinline__ void ubyte_fma(uint32_t u, const float* x, float& s0,
 // at byte base = sh + 84*sb of the buffer (4-aligned).  Lane = 32-element
 // slice k = lane % 8 of super-block sb = lane / 8: groups 2k and 2k+1 of 16,
 // 2-bit codes at shift 2j of qs[32*half + l] (half = k / 4, j = k % 4), scale
-// byte scales[g] = (min << 4) | scale (dequantize_row_q2_K, c:748-784):
-//   (d*sc_a)*sum_a u x - (dmin*m_a)*sum_a x  +  the same for group b.
+// byte scales[g] = (min << 4) | scale (dequantize_row_q2_K, c:748-784).
+// Each weight is formed as the reference forms it, w = dl*u - ml with
+// dl = d*sc and ml = dmin*m (dl*u is exact: 11 + 4 + 2 bits, so fmaf gives
+// the reference's value), and the dot is sum w*x in fp32.  The factored form
+// dl*sum u x - ml*sum x cancels: with 2-bit codes the two terms are close,
+// and their rounding errors flip Q8_0 roundings of K and V that the
+// reference does not flip.
 template <>
 struct Lane<L3P_Q2_K> {
     uint32_t qs, sch, dd, sj;   // dword of the codes, halfword of the two scale bytes, dword of {d, dmin}, 2j
@@ -664,16 +669,20 @@ struct Lane<L3P_Q2_K> {
         for (int i = 0; i < 8; ++i) w[i] = buf[qs + i];
         const uint32_t scw = reinterpret_cast<const uint16_t*>(buf)[sch];
         const uint32_t dm = buf[dd];
-        float a0 = 0.0f, a1 = 0.0f, b0 = 0.0f, b1 = 0.0f;
+        const float d = h2f(dm), dmin = h2f(dm >> 16);
+        const float dl[2] = {d * (float)(scw & 15u), d * (float)((scw >> 8) & 15u)};
+        const float ml[2] = {dmin * (float)((scw >> 4) & 15u), dmin * (float)((scw >> 12) & 15u)};
+        float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const uint32_t u = (w[i] >> sj) & 0x03030303u;
-            if (i < 4) ubyte_fma(u, xb.x + 4 * i, a0, a1);
-            else ubyte_fma(u, xb.x + 4 * i, b0, b1);
+            const float a = dl[i >> 2], m = ml[i >> 2];
+            s0 = fmaf(fmaf(a, (float)(u & 0xffu), -m), xb.x[4 * i], s0);
+            s1 = fmaf(fmaf(a, (float)((u >> 8) & 0xffu), -m), xb.x[4 * i + 1], s1);
+            s2 = fmaf(fmaf(a, (float)((u >> 16) & 0xffu), -m), xb.x[4 * i + 2], s2);
+            s3 = fmaf(fmaf(a, (float)(u >> 24), -m), xb.x[4 * i + 3], s3);
         }
-        const float d = h2f(dm), dmin = h2f(dm >> 16);
-        return (d * (float)(scw & 15u)) * (a0 + a1) - (dmin * (float)((scw >> 4) & 15u)) * xb.xs0 +
-               ((d * (float)((scw >> 8) & 15u)) * (b0 + b1) - (dmin * (float)((scw >> 12) & 15u)) * xb.xs1);
+        return (s0 + s1) + (s2 + s3);
     }
 };
 
@@ -682,9 +691,10 @@ struct Lane<L3P_Q2_K> {
 // Q2_K; element l of group 2k + (l >= 16) has code v = u | h << 2 with u the
 // 2 bits at shift 2j of qs[32*half + l] and h bit 4*half + j of hmask[l],
 // value v - 4, and the 6-bit scale s_g (low 4 bits from byte g or the high
-// nibble of byte g - 8, high 2 bits from byte 8 + g%4 at bit 2*(g/4)):
-//   (d*(s_a - 32))*(sum_a v x - 4 sum_a x) + the same for group b
-// (dequantize_row_q3_K, c:786-832).
+// nibble of byte g - 8, high 2 bits from byte 8 + g%4 at bit 2*(g/4))
+// (dequantize_row_q3_K, c:786-832).  As for Q2_K, each weight is the
+// reference's exact value w = dl*(v - 4), dl = d*(s - 32) (11 + 6 + 3 bits),
+// formed as fmaf(dl, v, -4 dl), and the dot is sum w*x in fp32.
 template <>
 struct Lane<L3P_Q3_K> {
     uint32_t qpos, hpos, spos, dh;   // bit positions of qs, hmask, scales; halfword of d
@@ -716,14 +726,18 @@ struct Lane<L3P_Q3_K> {
         const uint32_t ol = olo & 31u, oh = ohi - 64u;
         const int sa = (int)(__builtin_amdgcn_ubfe(sl, ol, 4u) | (__builtin_amdgcn_ubfe(s2, oh, 2u) << 4)) - 32;
         const int sb = (int)(__builtin_amdgcn_ubfe(sl, ol + 8u, 4u) | (__builtin_amdgcn_ubfe(s2, oh + 8u, 2u) << 4)) - 32;
-        float a0 = 0.0f, a1 = 0.0f, b0 = 0.0f, b1 = 0.0f;
+        const float dl[2] = {d * (float)sa, d * (float)sb};
+        float t0 = 0.0f, t1 = 0.0f, t2 = 0.0f, t3 = 0.0f;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const uint32_t v = ((q[i] >> sj) & 0x03030303u) | (((h[i] >> hr) << hl) & 0x04040404u);
-            if (i < 4) ubyte_fma(v, xb.x + 4 * i, a0, a1);
-            else ubyte_fma(v, xb.x + 4 * i, b0, b1);
+            const float a = dl[i >> 2], m = -4.0f * dl[i >> 2];
+            t0 = fmaf(fmaf(a, (float)(v & 0xffu), m), xb.x[4 * i], t0);
+            t1 = fmaf(fmaf(a, (float)((v >> 8) & 0xffu), m), xb.x[4 * i + 1], t1);
+            t2 = fmaf(fmaf(a, (float)((v >> 16) & 0xffu), m), xb.x[4 * i + 2], t2);
+            t3 = fmaf(fmaf(a, (float)(v >> 24), m), xb.x[4 * i + 3], t3);
         }
-        return (d * (float)sa) * ((a0 + a1) - 4.0f * xb.xs0) + (d * (float)sb) * ((b0 + b1) - 4.0f * xb.xs1);
+        return (t0 + t1) + (t2 + t3);
     }
 };
 
