@@ -462,13 +462,16 @@ def synthetic_model(arch: str = "llama", dim: int = 256, hidden: int = 512, n_la
                     ctx: int = 256, qtype: int = Q8_0, std: float = 0.02, seed: int = 0,
                     rope_theta: float = 500000.0, eps: float = 1e-5, tied: bool = False,
                     softcap: float = 0.0, swa_window: int = 0, rope_theta_swa: float = 10000.0,
-                    norm_jitter: float = 0.0, qtypes: dict | None = None, make_mat=None):
+                    norm_jitter: float = 0.0, qtypes: dict | None = None, make_mat=None,
+                    mats: dict | None = None):
     """A random-init model in GGUF form.  arch 'llama' (Llama-3 layout) or
     'gemma3' (Gemma layout: QK-norm, post norms, NEOX RoPE, GeGLU).
     qtypes overrides the type per tensor-name suffix (e.g. {"ffn_down": Q4_0}).
     make_mat(qtype, rows, cols, std, view), when given, writes the quantized
     bytes of each matrix into view (e.g. generated on a GPU for multi-GB
-    models) and the image is returned as a uint8 array instead of bytes."""
+    models) and the image is returned as a uint8 array instead of bytes.
+    mats maps tensor names to fp32 [rows, cols] matrices that replace the
+    random ones (quantized to the tensor's type)."""
     rng = np.random.default_rng(seed)
     hd = head_dim or dim // n_heads
     qd, kvd = n_heads * hd, n_kv * hd
@@ -542,6 +545,8 @@ def synthetic_model(arch: str = "llama", dim: int = 256, hidden: int = 512, n_la
             make_mat(specs[i][1], rows, cols, std, view)
         else:
             w = rng.normal(0, std, (rows, cols)).astype(np.float32)
+            if mats and name in mats:
+                w = np.ascontiguousarray(mats[name], np.float32).reshape(rows, cols)
             view[:] = quantize(w, specs[i][1]).ravel()
 
     out = build_gguf(meta, specs, fill)
