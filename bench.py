@@ -22,8 +22,12 @@ Printed as one JSON line:
                the fp32-MFMA roofline of the dominant prefill GEMM class;
   cpu_baseline the reference C engine (oracle/_ref/libref_omp.so: its own
                source built with its Makefile's -Ofast -fopenmp line) decoding
-               the same GGUF on the host cores for a bounded sample; the
-               oracle (single-threaded C restatement) when that is not built.
+               the same GGUF on the host at positions 1024.. for a bounded
+               sample, with the threads this process is given
+               (OMP_NUM_THREADS, else its affinity mask; nproc and the lscpu
+               model are recorded), and its basic -O3 build on one thread
+               (single_thread_O3); the oracle (C restatement) when the
+               reference is not built.
 
 usage: python bench.py [--gpus 1] [--steps 128] [--warmup 8]
 """
@@ -272,18 +276,23 @@ def cpu_gemv(ref, synth) -> list:
     return out
 
 
-def cpu_leg(path: str, seconds: float, max_tokens: int, use_ref: bool) -> dict:
-    """Runs in a subprocess: the reference engine (or the oracle) decoding
-    greedily from position 0 on the GGUF at path, then (reference only) its
-    GEMV at the standalone GEMV shapes."""
+def cpu_leg(path: str, seconds: float, max_tokens: int, kind: str, start: int) -> dict:
+    """Runs in a subprocess: greedy decode steps at positions start, start+1,
+    ... on the GGUF at path, for about `seconds` (at least one step), by the
+    reference engine built with its Makefile's OpenMP line (kind "omp") or
+    its basic -O3 line (kind "o3"), or by the oracle ("port").  The steps
+    right after opening the model see a zero KV cache below `start`; a
+    step's cost (the weight stream and attention over start+1 positions)
+    does not depend on what the cache holds.  The "omp" leg then times the
+    reference's GEMV at the standalone GEMV shapes."""
     import ctypes
 
     import numpy as np
 
     import oracle
 
-    if use_ref:
-        ref = oracle.Ref(oracle.REF_OMP_SO)
+    if kind in ("omp", "o3"):
+        ref = oracle.Ref(oracle.REF_OMP_SO if kind == "omp" else oracle.REF_SO)
         t0 = time.perf_counter()
         if ref.lib.ref_model_open(path.encode(), 0) != 0:
             raise RuntimeError("reference failed to open the model")
@@ -291,56 +300,97 @@ def cpu_leg(path: str, seconds: float, max_tokens: int, use_ref: bool) -> dict:
         tok, n, seed = 1, 0, ctypes.c_ulonglong(42)
         t0 = time.perf_counter()
         while n < max_tokens and (n == 0 or time.perf_counter() - t0 < seconds):
-            tok = int(ref.lib.ref_generate_token(tok, n, 0.0, 40, 0.9, ctypes.byref(seed)))
+            tok = int(ref.lib.ref_generate_token(tok, start + n, 0.0, 40, 0.9, ctypes.byref(seed)))
             n += 1
         dt = time.perf_counter() - t0
-        from llama3pure_amd import synth
+        out = {"tokens": n, "seconds": dt, "load_seconds": load_s}
+        if kind == "omp":
+            from llama3pure_amd import synth
 
-        gemv = cpu_gemv(ref, synth)
-        return {"tokens": n, "seconds": dt, "load_seconds": load_s, "gemv": gemv}
-    else:
-        cr = oracle.CpuRef()
-        img = np.fromfile(path, np.uint8)
-        t0 = time.perf_counter()
-        m = cr.open_model(img.tobytes())
-        load_s = time.perf_counter() - t0
-        tok, n = 1, 0
-        t0 = time.perf_counter()
-        while n < max_tokens and (n == 0 or time.perf_counter() - t0 < seconds):
-            tok = int(np.argmax(m.forward(tok, n)))
-            n += 1
-        dt = time.perf_counter() - t0
+            out["gemv"] = cpu_gemv(ref, synth)
+        return out
+    cr = oracle.CpuRef()
+    img = np.fromfile(path, np.uint8)
+    t0 = time.perf_counter()
+    m = cr.open_model(img.tobytes())
+    load_s = time.perf_counter() - t0
+    tok, n = 1, 0
+    t0 = time.perf_counter()
+    while n < max_tokens and (n == 0 or time.perf_counter() - t0 < seconds):
+        tok = int(np.argmax(m.forward(tok, start + n)))
+        n += 1
+    dt = time.perf_counter() - t0
     return {"tokens": n, "seconds": dt, "load_seconds": load_s}
 
 
-def cpu_baseline(img, seconds: float) -> dict | None:
+def host_cpu() -> dict:
+    """nproc, the CPUs this process may run on, and the CPU model (lscpu)."""
+    model = ""
+    try:
+        r = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=20)
+        for line in r.stdout.splitlines():
+            if line.startswith("Model name:"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except (OSError, subprocess.SubprocessError):
+        pass
+    return {"nproc": os.cpu_count(), "affinity": len(os.sched_getaffinity(0)), "model": model}
+
+
+def run_cpu_leg(path: str, seconds: float, kind: str, threads: int, start: int) -> dict | None:
+    env = dict(os.environ, OMP_NUM_THREADS=str(threads))
+    r = subprocess.run([sys.executable, os.path.abspath(__file__), "--cpu-leg", path, "--cpu-seconds", str(seconds),
+                        "--cpu-kind", kind, "--cpu-start", str(start)], env=env, capture_output=True, text=True,
+                       timeout=900)
+    if r.returncode != 0:
+        print(r.stderr[-2000:], file=sys.stderr)
+        return None
+    # the reference prints each decoded token's text to stdout before the result line
+    return json.loads(r.stdout[r.stdout.rfind('{"tokens"'):].splitlines()[0])
+
+
+def cpu_baseline(img, seconds: float, start: int) -> dict | None:
+    """The reference on the GPU box's host, decoding at positions >= start of
+    the same GGUF: its OpenMP build with the threads this process is given
+    (OMP_NUM_THREADS when set, else every CPU of its affinity mask), and its
+    basic single-thread -O3 build."""
     import oracle
 
+    cpu = host_cpu()
     use_ref = oracle.have_ref() and os.path.exists(oracle.REF_OMP_SO)
-    cores = min(16, os.cpu_count() or 1) if use_ref else 1
+    env_threads = os.environ.get("OMP_NUM_THREADS", "")
+    threads = int(env_threads) if env_threads.isdigit() and int(env_threads) > 0 else cpu["affinity"]
     d = "/dev/shm" if os.path.isdir("/dev/shm") else None
     fd, path = tempfile.mkstemp(suffix=".gguf", dir=d)
     try:
         with os.fdopen(fd, "wb") as f:
             img.tofile(f)
-        env = dict(os.environ, OMP_NUM_THREADS=str(cores))
-        r = subprocess.run([sys.executable, os.path.abspath(__file__), "--cpu-leg", path, "--cpu-seconds",
-                            str(seconds), "--cpu-ref", str(int(use_ref))], env=env, capture_output=True, text=True,
-                           timeout=600)
-        if r.returncode != 0:
-            print(r.stderr[-2000:], file=sys.stderr)
-            return None
-        # the reference prints each decoded token's text to stdout before the result line
-        res = json.loads(r.stdout[r.stdout.rfind('{"tokens"'):].splitlines()[0])
+        res = run_cpu_leg(path, seconds, "omp" if use_ref else "port", threads if use_ref else 1, start)
+        single = run_cpu_leg(path, seconds, "o3", 1, start) if use_ref else None
     finally:
         os.unlink(path)
-    what = ("reference C engine built -Ofast -fopenmp (its Makefile OpenMP line)" if use_ref
-            else "oracle (C restatement of the reference, -O2, one thread)")
-    out = {"value": round(res["tokens"] / res["seconds"], 4), "unit": "tok/s", "cores": cores,
+    if res is None:
+        return None
+    where = (f"host: nproc {cpu['nproc']}, {cpu['affinity']} CPUs in this process's affinity mask, "
+             f"{cpu['model'] or 'CPU model unknown'}")
+    span = lambda r: f"positions {start}..{start + r['tokens'] - 1}"
+    if use_ref:
+        what = (f"reference C engine, its Makefile's OpenMP line (-Ofast -fopenmp), {threads} threads "
+                f"(OMP_NUM_THREADS={env_threads or 'unset'})")
+    else:
+        what = "oracle (C restatement of the reference), one thread"
+    out = {"value": round(res["tokens"] / res["seconds"], 4), "unit": "tok/s", "cores": threads if use_ref else 1,
            "kind": "reference" if use_ref else "port",
-           "sample": f"{what}: {res['tokens']} greedy decode tokens from position 0 of the same GGUF "
-                     f"({res['seconds']:.1f} s); per-token cost is the 8.0 GB weight stream, attention "
-                     f"over <= {res['tokens']} positions instead of 1024"}
+           "sample": f"{what}: {res['tokens']} greedy decode steps at {span(res)} of the same GGUF "
+                     f"({res['seconds']:.1f} s; the cache below {start} is zero, which does not change a "
+                     f"step's cost: the {img.nbytes / 1e9:.1f} GB weight stream and attention over the "
+                     f"positions); {where}",
+           "host": cpu}
+    if single:
+        out["single_thread_O3"] = {
+            "value": round(single["tokens"] / single["seconds"], 4), "unit": "tok/s", "cores": 1,
+            "sample": f"reference C engine, its Makefile's basic line (gcc -O3), one thread: {single['tokens']} "
+                      f"greedy decode steps at {span(single)} ({single['seconds']:.1f} s)"}
     if res.get("gemv"):
         out["gemv"] = res["gemv"]   # matmul_quantized at the standalone GEMV shapes, same blocks and x
     return out
@@ -364,11 +414,12 @@ def main():
                     help="only run both decode attentions at 65..3001 positions of the named attention shape "
                          "(for a kernel trace)")
     ap.add_argument("--cpu-leg", help=argparse.SUPPRESS)
-    ap.add_argument("--cpu-ref", type=int, default=1, help=argparse.SUPPRESS)
+    ap.add_argument("--cpu-kind", default="omp", choices=["omp", "o3", "port"], help=argparse.SUPPRESS)
+    ap.add_argument("--cpu-start", type=int, default=0, help=argparse.SUPPRESS)
     a = ap.parse_args()
 
     if a.cpu_leg:
-        print(json.dumps(cpu_leg(a.cpu_leg, a.cpu_seconds, 64, bool(a.cpu_ref))))
+        print(json.dumps(cpu_leg(a.cpu_leg, a.cpu_seconds, 64, a.cpu_kind, a.cpu_start)))
         return
     if a.calibrate_copy:
         calibrate_copy()
@@ -451,7 +502,7 @@ def main():
     if gemv:
         print(f"[bench] standalone GEMV: {json.dumps(gemv)}", file=sys.stderr, flush=True)
 
-    base = None if a.no_cpu else cpu_baseline(img, a.cpu_seconds)
+    base = None if a.no_cpu else cpu_baseline(img, a.cpu_seconds, a.prefill)
     del img
     ctx.close()
     gemma = None if a.no_gemma else gemma_prompt_decode(np, torch, l3p, synth)
