@@ -121,12 +121,14 @@ def prefill_summary(positions: int, seconds: float, stats: dict) -> dict:
 def gemma_prompt_decode(np, torch, l3p, synth, prompt_len=512, steps=128, warmup=4):
     """A 512-token prompt, then 128 sampled decode steps (temperature 0.9,
     top-k 40, top-p 0.9, fixed seed) on a random-init Gemma-2-2B-architecture
-    Q8_0 model.  The prompt is run once untimed (settling launch
-    configurations) with `warmup` decode steps after it, then timed; the
-    decode steps then continue from the timed prompt."""
+    Q8_0 model, loaded with Gemma-2's attention: alternating local/global
+    layers (swa_pattern 2, window 4096) and the attention score cap 50, next
+    to the final logit cap 30.  The prompt is run once untimed (settling
+    launch configurations) with `warmup` decode steps after it, then timed;
+    the decode steps then continue from the timed prompt."""
     ctx = l3p.Context(0)
     img = synth.synthetic_model(qtype=synth.Q8_0, make_mat=synth.gpu_q8_0_maker(ctx, torch, 77), **GEMMA2_2B)
-    mi = ctx.load_gguf(img)
+    mi = ctx.load_gguf(img, swa_pattern=2, attn_softcap=50.0)
     del img
     prompt = np.random.default_rng(6).integers(0, mi.vocab_size, prompt_len).astype(np.int32)
     sampler = dict(temperature=0.9, top_k=40, top_p=0.9)
@@ -155,7 +157,9 @@ def gemma_prompt_decode(np, torch, l3p, synth, prompt_len=512, steps=128, warmup
     ctx.close()
     pre = prefill_summary(prompt_len - 1, t_pre, pstats)
     return {"workload": "Gemma-2-2B architecture, all matrices Q8_0: 512-token prompt, then 128 decode steps "
-                        "sampled at temperature 0.9, top-k 40, top-p 0.9",
+                        "sampled at temperature 0.9, top-k 40, top-p 0.9; load options swa_pattern 2 "
+                        "(alternating local window-4096 / global layers) and attn_softcap 50, final logit "
+                        "soft-cap 30 from the GGUF",
             "layers": 26, "dim": 2304, "heads": 8, "kv_heads": 4, "head_dim": 256, "ffn": 9216, "vocab": 256000,
             "prefill": pre, "decode_steps": steps, "decode_ms": round(t_dec * 1e3, 2),
             "decode_tok_s": round(steps / t_dec, 1), "last_token": int(tok)}

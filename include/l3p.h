@@ -107,7 +107,19 @@ int l3p_gemm_static(int type, const void* w_dev, int rows, int cols, const float
 /* ---- model -------------------------------------------------------------- */
 typedef struct {
     int context_size;   /* <=0: the model's context_length (c:5174-5178; js:4335)   */
-    int reserved[7];
+    /* The two options below have no counterpart in the reference, which
+     * hard-codes Gemma's sliding-window pattern to 6 (c:5100) and has no
+     * attention score cap; they let Gemma-2 checkpoints run as trained.
+     * swa_pattern > 0: Gemma layer l uses the sliding window when
+     *   l % swa_pattern < swa_pattern - 1 (2: alternating local/global,
+     *   starting local); 0 keeps 6.  No effect on Llama models.
+     * attn_softcap > 0: every attention score s becomes
+     *   attn_softcap * tanhf(s / attn_softcap) before the softmax (Gemma-2's
+     *   attention logit soft-capping); 0: scores as they are.
+     * Negative values return L3P_E_INVALID. */
+    int swa_pattern;
+    float attn_softcap;
+    int reserved[5];
 } l3p_load_opts;
 
 typedef struct {
@@ -115,6 +127,8 @@ typedef struct {
     int is_gemma, swa_window, swa_pattern, weight_type;
     float rope_theta, rope_theta_swa, rms_eps, final_softcap;
     int64_t device_bytes;   /* HBM held by weights + KV cache + scratch */
+    float attn_softcap;     /* the load option in effect (0: none) */
+    int reserved;
 } l3p_model_info;
 
 /* Parse a GGUF image in host memory and copy every tensor, unchanged, into

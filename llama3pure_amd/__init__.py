@@ -38,7 +38,8 @@ class L3PError(RuntimeError):
 
 
 class LoadOpts(C.Structure):
-    _fields_ = [("context_size", C.c_int), ("reserved", C.c_int * 7)]
+    _fields_ = [("context_size", C.c_int), ("swa_pattern", C.c_int), ("attn_softcap", C.c_float),
+                ("reserved", C.c_int * 5)]
 
 
 class ModelInfo(C.Structure):
@@ -46,7 +47,7 @@ class ModelInfo(C.Structure):
                                        "vocab_size", "seq_len", "head_dim", "is_gemma", "swa_window",
                                        "swa_pattern", "weight_type")] + \
                [(n, C.c_float) for n in ("rope_theta", "rope_theta_swa", "rms_eps", "final_softcap")] + \
-               [("device_bytes", C.c_int64)]
+               [("device_bytes", C.c_int64), ("attn_softcap", C.c_float), ("reserved", C.c_int)]
 
 
 class KernelStat(C.Structure):
@@ -181,10 +182,10 @@ class Context:
         self._check(self.L.l3p_quantize_q8_0(self.h, _ptr(x), n, _ptr(dst)))
 
     # -- model --
-    def load_gguf(self, gguf, context_size: int = 0):
+    def load_gguf(self, gguf, context_size: int = 0, swa_pattern: int = 0, attn_softcap: float = 0.0):
         import numpy as np
         buf = gguf if isinstance(gguf, np.ndarray) else np.frombuffer(gguf, dtype=np.uint8)
-        opts = LoadOpts(context_size=context_size)
+        opts = LoadOpts(context_size=context_size, swa_pattern=swa_pattern, attn_softcap=attn_softcap)
         self._check(self.L.l3p_load_gguf(self.h, buf.ctypes.data, buf.nbytes, C.byref(opts)))
         return self.model_info()
 

@@ -143,7 +143,13 @@ struct AttnCArgs {
     // and its K/V rows are already in the cache (kv_ready, kv_rows_kernel).
     int q_stride, kv_stride, out_stride, kv_ready;
     size_t part_stride;
+    float softcap;   // > 0: scores s -> softcap * tanhf(s / softcap) (a load option; 0: none)
 };
+
+// A score after the optional cap (attention logit soft-capping).
+__device__ __forceinline__ float cap_score(float s, float cap) {
+    return cap > 0.0f ? cap * tanhf(s / cap) : s;
+}
 
 // The arguments of token z of a prompt batch (z = 0: a decode step).
 __device__ __forceinline__ AttnCArgs token_args(const AttnCArgs& a0, int z) {
@@ -393,7 +399,7 @@ __global__ void __launch_bounds__(1024) attn_chunk_kernel(AttnCArgs a0) {
             for (int k = 0; k < 8; ++k) isum = __builtin_amdgcn_sdot4(qw[8 * b + k], (int)kq[b][k], isum, false);
             sum += qd[w * 8 + b] * db[b] * (float)isum;
         }
-        sc = sum;
+        sc = cap_score(sum, a.softcap);
     }
     const float m = wave_max(sc);
     const float e = lane < cnt ? expf(sc - m) : 0.0f;
@@ -811,6 +817,7 @@ __global__ void __launch_bounds__(1024) attn_prefill_kernel(AttnCArgs a0, int nt
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int pa = p0 + st * 16 + 4 * gq + r;
+                sc[s2][r] = cap_score(sc[s2][r], a0.softcap);
                 if (my_pos < 0 || pa > my_pos || pa < my_beg) sc[s2][r] = -INFINITY;
             }
         }
@@ -1127,7 +1134,7 @@ __global__ void __launch_bounds__(1024) attn_head_kernel(AttnCArgs a) {
                 for (int e2 = 0; e2 < 8; ++e2) isum = __builtin_amdgcn_sdot4(qw[8 * b + e2], (int)kq[b][e2], isum, false);
                 sum += qs[b] * db[b] * (float)isum;
             }
-            sc = sum;
+            sc = cap_score(sum, a.softcap);
         }
         const float mn = fmaxf(m_run, wave_max(sc));
         const float alpha = expf(m_run - mn);   // 0 for the first chunk
@@ -1492,6 +1499,7 @@ static AttnCArgs attn_args(const Model& m, int l, const AttnIO& io) {
     a.attn_scale = m.attn_scale;
     a.eps = m.eps > 0 ? m.eps : 1e-5f;
     a.inv_hs = m.inv_hs;
+    a.softcap = m.attn_softcap;
     return a;
 }
 

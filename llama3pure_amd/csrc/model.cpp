@@ -267,6 +267,13 @@ static Model* load_model(l3p_ctx* c, const void* bytes, size_t len, const l3p_lo
     if (const KV* tk = g.find("tokenizer.ggml.tokens"))   // vocab from the token list (c:5152-5157)
         if (tk->type == 9 && tk->atype == 8 && tk->alen > 0) m.vocab = (int)tk->alen;
     if (opts && opts->context_size > 0 && opts->context_size < m.seq_len) m.seq_len = opts->context_size;
+    if (opts) {
+        L3P_REQUIRE(opts->swa_pattern >= 0 && opts->attn_softcap >= 0.0f, L3P_E_INVALID,
+                    "load: swa_pattern %d and attn_softcap %g must not be negative", opts->swa_pattern,
+                    (double)opts->attn_softcap);
+        if (opts->swa_pattern > 0) m.swa_pattern = opts->swa_pattern;
+        m.attn_softcap = opts->attn_softcap;
+    }
     L3P_REQUIRE(m.seq_len <= 262144, L3P_E_UNSUPPORTED, "context length %d exceeds 262144", m.seq_len);
 
     L3P_REQUIRE(m.dim > 0 && m.hidden > 0 && m.n_layers > 0 && m.vocab > 0 && m.seq_len > 0, L3P_E_FORMAT,
@@ -1020,6 +1027,7 @@ int l3p_get_model_info(l3p_ctx* c, l3p_model_info* o) {
         o->is_gemma = m.is_gemma; o->swa_window = m.swa_window; o->swa_pattern = m.swa_pattern;
         o->weight_type = m.weight_type; o->rope_theta = m.theta; o->rope_theta_swa = m.theta_swa;
         o->rms_eps = m.eps; o->final_softcap = m.softcap; o->device_bytes = m.device_bytes;
+        o->attn_softcap = m.attn_softcap;
     });
 }
 

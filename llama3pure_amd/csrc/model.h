@@ -22,6 +22,7 @@ struct Model {
     int hs = 0, kv_dim = 0, q_dim = 0, max_dim = 0, kv_mul = 0, hq8 = 0;
     int is_gemma = 0, swa_window = 0, swa_pattern = 6, weight_type = 0;
     float theta = 0, theta_swa = 0, eps = 0, softcap = 0;
+    float attn_softcap = 0;   // load option: attention score cap (0: none)
     float attn_scale = 0, embed_scale = 0, inv_dim = 0, inv_hs = 0;
     size_t head_seq = 0, layer_kv = 0;
 

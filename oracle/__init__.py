@@ -108,6 +108,8 @@ class CpuRef(_Lib):
         L.l3o_set_kv.argtypes = [_P, C.c_int, C.c_int, _P, C.c_size_t]
         L.l3o_copy_x.argtypes = [_P, _P]
         L.l3o_rope_row.argtypes = [_P, C.c_int, C.c_int, _P, _P]
+        L.l3o_set_attention.argtypes = [_P, C.c_int, C.c_float]
+        L.l3o_attend_head.argtypes = [_P, _P, _P, C.c_int, C.c_int, C.c_float, _P, _P]
 
     # -- primitives --
     def fp16_to_fp32(self, h: np.ndarray) -> np.ndarray:
@@ -182,6 +184,14 @@ class CpuRef(_Lib):
         self.lib.l3o_geglu(_vp(g), _vp(u), g.size)
         return g
 
+    def attend_head(self, q8, kc, vc, n, hs, cap):
+        """One head's attention over n Q8_0 cache rows: (weights, output)."""
+        q8, kc, vc = (np.ascontiguousarray(v, np.uint8) for v in (q8, kc, vc))
+        att = np.empty(n, np.float32)
+        out = np.zeros(hs, np.float32)
+        self.lib.l3o_attend_head(_vp(q8), _vp(kc), _vp(vc), n, hs, cap, _vp(att), _vp(out))
+        return att, out
+
     def sample(self, logits, temperature, top_k, top_p, seed):
         """Returns (token, new_seed)."""
         logits = np.ascontiguousarray(logits, np.float32)
@@ -236,6 +246,12 @@ class CpuModel:
         if self.ref.lib.l3o_copy_kv(self.h, layer, int(which_v), _vp(out), n) != 0:
             raise RuntimeError("copy_kv")
         return out
+
+    def set_attention(self, swa_pattern: int = 0, attn_softcap: float = 0.0) -> None:
+        """The load options the reference lacks: a sliding-window layer
+        pattern (0 keeps the model's) and an attention score cap (0: none)."""
+        if self.ref.lib.l3o_set_attention(self.h, swa_pattern, attn_softcap) != 0:
+            raise ValueError("set_attention")
 
     def set_kv(self, layer: int, which_v: bool, data: np.ndarray) -> None:
         """Overwrite one layer's K or V cache (test support: installs a long

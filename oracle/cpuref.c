@@ -766,6 +766,7 @@ struct l3o_model {
     int dim, hidden, n_layers, n_heads, n_kv, vocab, seq_len, head_dim, is_gemma;
     float theta, theta_swa, eps, softcap;
     int swa_window, swa_pattern;
+    float attn_softcap;   /* load option, no counterpart in the reference: 0 = off */
     /* weights (c:251-278) */
     qt_t emb;
     float *att_norm, *ffn_norm, *final_norm, *q_norm, *k_norm, *post_att_norm, *post_ffn_norm;
@@ -1138,6 +1139,29 @@ static void kv_accum(float* out, const uint8_t* c, float w, int n) {
     }
 }
 
+/* One head's attention over n cache rows (c:3323-3359): scores are the
+ * exact Q8_0 dots (dot_q8_0_q8_0_cache, c:1574-1597); with cap > 0 each
+ * becomes cap * tanhf(s / cap) (attention logit soft-capping, a load option
+ * the reference does not have); softmax (c:3167-3186) into att; out +=
+ * sum_t att[t] * V_t (accum_q8_0_cache, c:1600-1622). */
+void l3o_attend_head(const uint8_t* q8, const uint8_t* kc, const uint8_t* vc, int n, int hs, float cap,
+                     float* att, float* out) {
+    int hq8 = hs / 32 * 34;
+    for (int t = 0; t < n; t++) {
+        float sc = kv_dot(q8, kc + (size_t)t * hq8, hs);
+        att[t] = cap > 0.0f ? cap * tanhf(sc / cap) : sc;
+    }
+    l3o_softmax(att, n);
+    for (int t = 0; t < n; t++) kv_accum(out, vc + (size_t)t * hq8, att[t], hs);
+}
+
+int l3o_set_attention(l3o_model* m, int swa_pattern, float attn_softcap) {
+    if (swa_pattern < 0 || !(attn_softcap >= 0.0f)) return -1;
+    if (swa_pattern > 0) m->swa_pattern = swa_pattern;
+    m->attn_softcap = attn_softcap;
+    return 0;
+}
+
 static int swa_layer(const l3o_model* m, int l) {
     return m->swa_pattern > 0 && (l % m->swa_pattern < m->swa_pattern - 1);
 }
@@ -1209,9 +1233,8 @@ static void attend(l3o_model* m, int l, int pos, float* q, float* k, const float
         const uint8_t* kb = m->kc + loff + kh * m->head_seq;
         const uint8_t* vb = m->vc + loff + kh * m->head_seq;
         float* att = m->att + (size_t)h * m->seq_len;
-        for (int t = t0; t <= pos; t++) att[t - t0] = kv_dot(m->qq8 + h * m->hq8, kb + (size_t)t * m->hq8, hs);
-        l3o_softmax(att, na);
-        for (int t = t0; t <= pos; t++) kv_accum(out + h * hs, vb + (size_t)t * m->hq8, att[t - t0], hs);
+        l3o_attend_head(m->qq8 + h * m->hq8, kb + (size_t)t0 * m->hq8, vb + (size_t)t0 * m->hq8, na, hs,
+                        m->attn_softcap, att, out + h * hs);
     }
 }
 

@@ -86,6 +86,14 @@ int   l3o_set_kv(l3o_model* m, int layer, int which_v, const void* src, size_t n
 int   l3o_rope_row(const l3o_model* m, int swa, int pos, float* cos_out, float* sin_out);
 /* Residual stream x after the last forward (dim floats). */
 int   l3o_copy_x(const l3o_model* m, float* dst);
+/* Load options without a counterpart in the reference: swa_pattern > 0
+ * replaces the sliding-window layer pattern (layer l is local when
+ * l % p < p - 1; the reference hard-codes 6 for Gemma, c:5100), and
+ * attn_softcap > 0 caps every attention score s to cap * tanhf(s / cap). */
+int   l3o_set_attention(l3o_model* m, int swa_pattern, float attn_softcap);
+/* One head's capped attention over n Q8_0 cache rows (the forward's own). */
+void  l3o_attend_head(const uint8_t* q8, const uint8_t* kc, const uint8_t* vc, int n, int hs, float cap,
+                      float* att, float* out);
 
 #ifdef __cplusplus
 }

@@ -377,3 +377,49 @@ def test_attention_paths_agree(torch_gpu, monkeypatch, case):
                 qb = cc.copy_kv(layer, wv).reshape(mi.n_kv_heads, mi.seq_len, -1, 34)[:, :n_prompt + 6, :, 2:]
                 d = np.abs(qa.view(np.int8).astype(np.int32) - qb.view(np.int8).astype(np.int32))
                 assert d.max() <= 1, (case, layer, wv, int(d.max()))
+
+
+@pytest.mark.parametrize("cap", [0.0, 0.3])
+def test_attention_overrides_match_oracle(ctx, cpuref, monkeypatch, cap):
+    """The load options without a counterpart in the reference: Gemma-2's
+    alternating sliding-window layers (swa_pattern 2: layers 0, 2, 4, 6
+    local, the rest global) and its attention score cap cap * tanh(s / cap)
+    (the oracle's capped attention is pinned to that closed form in
+    test_oracle_primitives).  A 7-layer Gemma with a 16-position window: a
+    prefilled 40-token prompt, then 12 teacher-forced steps, the first six
+    on the per-head kernel and the rest on chunks + merge, against the
+    oracle with the same options; and the options must change the logits.
+    Scores of this random model stay within about 1, so a cap of 0.3 bites."""
+    kw = dict(MODELS["gemma_q8_0"])
+    g = synth.synthetic_model(**kw)
+    m = cpuref.open_model(g)
+    m.set_attention(2, cap)
+    ctx.load_gguf(g, swa_pattern=2, attn_softcap=cap)
+    mi = ctx.model_info()
+    assert mi.swa_pattern == 2 and abs(mi.attn_softcap - cap) < 1e-7
+    prompt = np.random.default_rng(11).integers(0, m.vocab, 41).astype(np.int32)
+    ctx.prefill(prompt[:-1], 0)
+    m.prefill(prompt[:-1], 0, len(prompt) - 1)
+    tok, pos = int(prompt[-1]), len(prompt) - 1
+    logits = []
+    for step in range(12):
+        monkeypatch.setenv("L3P_ATTN_HEAD", "1" if step < 6 else "0")
+        lo_ref = m.forward(tok, pos)
+        lo_gpu = ctx.forward(tok, pos)
+        tol = max(1e-2, 2.0 * REF_DRIFT["gemma_q8_0"]["max_rel"]) * rms(lo_ref)
+        err = float(np.max(np.abs(lo_gpu - lo_ref)))
+        assert err <= tol, f"step {step}: max |dlogit| {err:.3g} > {tol:.3g}"
+        logits.append(lo_ref)
+        tok, pos = int(np.argmax(lo_ref)), pos + 1
+    monkeypatch.delenv("L3P_ATTN_HEAD", raising=False)
+    m.close()
+    # the same steps without the options differ by far more than the tolerance
+    m0 = cpuref.open_model(g)
+    m0.prefill(prompt[:-1], 0, len(prompt) - 1)
+    tok, pos, moved = int(prompt[-1]), len(prompt) - 1, 0.0
+    for step in range(12):
+        lo = m0.forward(tok, pos)
+        moved = max(moved, float(np.max(np.abs(lo - logits[step]))) / rms(lo))
+        tok, pos = int(np.argmax(logits[step])), pos + 1
+    m0.close()
+    assert moved > 0.05, moved

@@ -434,3 +434,32 @@ def test_sampler_limits(cpuref):
     p = np.exp(lg2[:5] - 2.0)
     p /= p.sum()
     assert np.allclose(counts[:5] / counts.sum(), p, atol=0.015)
+
+
+@pytest.mark.parametrize("cap", [0.0, 50.0, 5.0])
+def test_attend_head_softcap_closed_form(cpuref, cap):
+    """One head's attention with the score cap, a load option the reference
+    does not have (Gemma-2's attention logit soft-capping): weights
+    softmax(cap * tanh(s / cap)) (cap 0: softmax(s)) and output sum w_t V_t,
+    with s the dot of the dequantized Q8_0 q and K rows, all in float64
+    here.  Scores reach +-150, so a cap of 50 or 5 moves every weight."""
+    rng = np.random.default_rng(21)
+    hs, n = 128, 40
+    q8 = cpuref.quantize_q8_0(rng.normal(0, 6, hs).astype(np.float32))
+    kc = cpuref.quantize_q8_0(rng.normal(0, 1.2, (n, hs)).astype(np.float32).ravel())
+    vc = cpuref.quantize_q8_0(rng.normal(0, 1, (n, hs)).astype(np.float32).ravel())
+    dq = cpuref.dequant(oracle.Q8_0, q8, hs).astype(np.float64)
+    dk = cpuref.dequant(oracle.Q8_0, kc, n * hs).astype(np.float64).reshape(n, hs)
+    dv = cpuref.dequant(oracle.Q8_0, vc, n * hs).astype(np.float64).reshape(n, hs)
+    s = dk @ dq
+    assert np.abs(s).max() > 60
+    z = cap * np.tanh(s / cap) if cap > 0 else s
+    w = np.exp(z - z.max())
+    w /= w.sum()
+    att, out = cpuref.attend_head(q8, kc, vc, n, hs, cap)
+    assert np.allclose(att, w, rtol=1e-4, atol=1e-7), np.abs(att - w).max()
+    assert np.allclose(out, w @ dv, rtol=0, atol=1e-4 * np.abs(w @ dv).max())
+    if cap > 0:   # the cap changes the weights: the check above would catch a dropped cap
+        raw = np.exp(s - s.max())
+        raw /= raw.sum()
+        assert np.abs(raw - w).max() > 0.05
