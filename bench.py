@@ -187,6 +187,29 @@ def read_ceiling(ctx, torch, nbytes: int) -> float:
     return nbytes / (p50 * 1e-3) / 1e9
 
 
+def gemv_shapes_only():
+    """The standalone GEMV lines, then the streaming-read ceiling at each
+    shape's weight bytes, in that order (a kernel trace takes the last 200
+    GEMV dispatches of each kernel and each block of stream_read_kernel
+    dispatches in turn)."""
+    import torch
+
+    import llama3pure_amd as l3p
+    from llama3pure_amd import synth
+
+    ctx = l3p.Context(0)
+    gemv = time_gemv_shapes(ctx, torch, l3p, synth)
+    for g in gemv:
+        name, shape = g["shape"].split()
+        rows, cols = (int(v) for v in shape.split("x"))
+        nbytes = rows * synth.row_bytes({"q8_0": l3p.Q8_0, "q4_0": l3p.Q4_0, "q4_k": l3p.Q4_K,
+                                         "q6_k": l3p.Q6_K}[name], cols)
+        g["read_ceiling_GBps"] = round(read_ceiling(ctx, torch, nbytes), 1)
+        g["frac_of_read_ceiling"] = round(g["GB/s"] / g["read_ceiling_GBps"], 4)
+        print(json.dumps(g), flush=True)
+    ctx.close()
+
+
 def measured_traffic(kernel: str):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE +
     WRITE_SIZE summary (a line "traffic <kernel>: <bytes>"), else None."""
@@ -414,6 +437,9 @@ def main():
                     help="layers of the model (32 = Llama-3-8B; fewer only for short counter-collection runs)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only copy 512 MiB device-to-device 5 times (scale for rocprofv3 FETCH_SIZE/WRITE_SIZE)")
+    ap.add_argument("--gemv-shapes", action="store_true",
+                    help="only the standalone GEMV shapes and the streaming-read ceiling at each shape's bytes "
+                         "(for a kernel trace or counters)")
     ap.add_argument("--attn-sweep", nargs="?", const="llama3-8b", choices=["llama3-8b", "gemma2b"],
                     help="only run both decode attentions at 65..3001 positions of the named attention shape "
                          "(for a kernel trace)")
@@ -430,6 +456,9 @@ def main():
         return
     if a.attn_sweep:
         attn_sweep(a.attn_sweep)
+        return
+    if a.gemv_shapes:
+        gemv_shapes_only()
         return
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the decode path runs on a single MI355X and has no multi-GPU "
