@@ -1288,7 +1288,11 @@ __global__ void argmax_final_kernel(const float* cv, const int* ci, int nc, int*
 // is one workgroup: waves 1..15 stream the logits and group maxima through
 // LDS in blocks of kScanBlock while wave 0, which holds the slots, scans the
 // previous block there, so a visited group costs an LDS read rather than a
-// dependent global load.
+// dependent global load.  For k <= 64 wave 0 also keeps the slots as a list
+// sorted by (value, slot), one entry per lane (NaN sorted as +inf: the
+// reference never takes a NaN slot as its minimum): the minimum is lane 0,
+// and a replacement drops it and inserts the new (value, slot) at its rank,
+// one ballot and a one-lane shift instead of a search over the slots.
 constexpr int kSlotsPerLane = 16;            // k <= 1024
 constexpr int kScanBlock = 16384;            // logits per LDS block (256 groups)
 
@@ -1360,6 +1364,10 @@ __global__ void __launch_bounds__(1024) topk_scan_kernel(const float* __restrict
         ms = slot;
     };
     auto lane_val = [](float v, int j) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), j)); };
+    // k <= 64: the sorted list (key, ks) by rank; sv[0], si[0] stay the slot
+    // values and indices by slot (lane = slot)
+    float key = INFINITY;
+    int ks = 64 + lane;   // lanes past k: sentinels after every slot
     if (w == 0) {
 #pragma unroll
         for (int j = 0; j < R; ++j) {
@@ -1367,8 +1375,61 @@ __global__ void __launch_bounds__(1024) topk_scan_kernel(const float* __restrict
             sv[j] = s < k ? l[s] : INFINITY;
             si[j] = s < k ? s : -1;
         }
-        find_min(cur, cur_slot);
+        if constexpr (R == 1) {
+            if (lane < k) {
+                key = sv[0] != sv[0] ? INFINITY : sv[0];
+                ks = lane;
+            }
+            // bitonic sort by (key, ks), ascending; the pairs are distinct
+            for (int size = 2; size <= 64; size <<= 1) {
+                for (int stride = size >> 1; stride > 0; stride >>= 1) {
+                    const float ok = __shfl_xor(key, stride, 64);
+                    const int os = __shfl_xor(ks, stride, 64);
+                    const bool other_less = ok < key || (ok == key && os < ks);
+                    const bool want_min = ((lane & stride) == 0) == ((lane & size) == 0);
+                    if (want_min ? other_less : !other_less) {
+                        key = ok;
+                        ks = os;
+                    }
+                }
+            }
+            // a NaN in slot 0 stays the reference's minimum: nothing is ever
+            // greater, so nothing is replaced
+            const float s0 = lane_val(sv[0], 0);
+            cur = s0 != s0 ? s0 : lane_val(key, 0);
+        } else {
+            find_min(cur, cur_slot);
+        }
     }
+    // logits[i] = bv > cur replaces the minimum slot
+    auto replace = [&](float bv, int i) {
+        if constexpr (R == 1) {
+            const int sh = __builtin_amdgcn_readlane(ks, 0);   // the minimum's slot
+            const bool before = lane >= 1 && lane < k && (key < bv || (key == bv && ks < sh));
+            const int r = __popcll(__ballot(before));
+            const float kn = __shfl_down(key, 1, 64);
+            const int sn = __shfl_down(ks, 1, 64);
+            if (lane < r) {
+                key = kn;
+                ks = sn;
+            } else if (lane == r) {
+                key = bv;
+                ks = sh;
+            }
+            if (lane == sh) {
+                sv[0] = bv;
+                si[0] = i;
+            }
+            cur = lane_val(key, 0);
+        } else {
+            if (lane == (cur_slot & 63)) {
+#pragma unroll
+                for (int jj = 0; jj < R; ++jj)
+                    if (jj == (cur_slot >> 6)) { sv[jj] = bv; si[jj] = i; }
+            }
+            find_min(cur, cur_slot);
+        }
+    };
     wait_vm<0>();
     __syncthreads();
     for (int b = 0; b < nblk; ++b) {
@@ -1389,19 +1450,14 @@ __global__ void __launch_bounds__(1024) topk_scan_kernel(const float* __restrict
                     const int base = b * kScanBlock + gofs;
                     const int i = base + lane;
                     const float v = (i >= k && i < n) ? lb[gofs + lane] : -INFINITY;
+                    // candidates in index order; after each replacement the
+                    // mask is narrowed to those still above the new minimum,
+                    // so every iteration replaces
                     uint64_t cand = __ballot(v > cur);
                     while (cand) {
                         const int c = __ffsll((unsigned long long)cand) - 1;
-                        cand &= cand - 1;
-                        const float bv = lane_val(v, c);
-                        if (bv > cur) {
-                            if (lane == (cur_slot & 63)) {
-#pragma unroll
-                                for (int jj = 0; jj < R; ++jj)
-                                    if (jj == (cur_slot >> 6)) { sv[jj] = bv; si[jj] = base + c; }
-                            }
-                            find_min(cur, cur_slot);
-                        }
+                        replace(lane_val(v, c), base + c);
+                        cand &= __ballot(v > cur) & ~((2ull << c) - 1ull);
                     }
                 }
             }

@@ -186,8 +186,9 @@ def test_sampler_matches_oracle(pair, ctx, cpuref, torch_gpu):
 def test_sampler_full_vocab(torch_gpu, cpuref, vocab):
     """Top-k/top-p over full-size vocabularies (several LDS blocks of the
     top-k scan) picks the oracle's token and RNG state: normal logits, logits
-    rounded to halves (many ties, so the lowest-slot rule decides), and
-    increasing logits (every index replaces a slot)."""
+    rounded to halves (many ties, so the lowest-slot rule decides),
+    increasing logits (every index replaces a slot), and NaN logits past
+    the initial slots."""
     g = synth.synthetic_model(arch="llama", dim=64, hidden=64, n_layers=1, n_heads=2, n_kv=1, vocab=vocab, ctx=32,
                               qtype=synth.Q8_0, seed=vocab % 1000)
     rng = np.random.default_rng(vocab)
@@ -200,6 +201,8 @@ def test_sampler_full_vocab(torch_gpu, cpuref, vocab):
                 lo = (np.round(lo * 2) / 2).astype(np.float32)
             elif trial % 3 == 2:
                 lo = np.sort(lo)
+            if trial in (1, 7, 9):   # NaN logits past the initial slots: never inserted
+                lo[rng.integers(1000, vocab, 50)] = np.nan
             k = [1, 40, 1000, 100, 200, 65][trial % 6]   # one to sixteen slot rows of 64
             p = [0.9, 1.0, 0.95, 0.5][trial % 4]
             t_gpu, s_gpu = c.sample(torch_gpu.from_numpy(lo).cuda(), vocab, temperature=0.9, top_k=k, top_p=p,
