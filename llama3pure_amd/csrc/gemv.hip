@@ -50,7 +50,8 @@
 // types use w[j] * x[j] and multiply each row total by r (the product is
 // linear in x), so no wave waits for the others before its first chunk.
 // The lane's x and norm loads are issued first, then the first weight
-// copies, so HBM is busy while the activation is prepared.
+// copies, and the prologue waits only for the loads, so the copies stay in
+// flight while the activation is prepared.
 #include "device_common.h"
 #include "internal.h"
 
@@ -136,6 +137,33 @@ __device__ __forceinline__ void wait_chunk(int younger) {
         if (younger >= J) wait_vm<J * CI>();
         else wait_chunk<J - 1, CI>(younger);
     }
+}
+
+// Prologue loads the compiler does not track.  Issued before the weight
+// copies and consumed after them, an ordinary load would be waited for with
+// vmcnt(0), since the compiler's wait counting leaves the LDS-DMA copies out,
+// and that also waits for every copy issued after it.  These loads are
+// waited for by wait_prologue, which leaves the copies in flight; pin8 then
+// orders each use after that wait.
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void load8_async(f32x4 (&q)[8], const float* p) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) asm volatile("global_load_dwordx4 %0, %1, off offset:%2" : "=v"(q[e]) : "v"(p), "i"(16 * e));
+}
+// vmcnt(min(younger, J) * CI): every load older than the last `younger`
+// chunk copies (CI instructions each) has landed
+template <int J, int CI>
+__device__ __forceinline__ void wait_prologue(int younger) {
+    if constexpr (J == 0) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    } else {
+        if (younger >= J) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(J * CI) : "memory");
+        else wait_prologue<J - 1, CI>(younger);
+    }
+}
+__device__ __forceinline__ void pin8(f32x4 (&q)[8]) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) asm volatile("" : "+v"(q[e]));
 }
 
 // Byte offsets this lane copies, from the copy base, for a chunk whose data
@@ -839,7 +867,7 @@ struct Lane<L3P_F32> {
 };
 
 template <int QT, int G, int NB, bool PAIR, bool UA, bool POST>
-__global__ void __launch_bounds__(1024) gemv_kernel(GemvArgs a) {
+__global__ void __launch_bounds__(POST ? 512 : 1024) gemv_kernel(GemvArgs a) {
     constexpr int CB = Fmt<QT>::kChunkBytes;
     constexpr int CDW = Fmt<QT>::kBufBytes / 4;
     constexpr int CI = Fmt<QT>::kCI;
@@ -880,45 +908,19 @@ __global__ void __launch_bounds__(1024) gemv_kernel(GemvArgs a) {
     float* ssy = ssred + nw;                                              // [nw] (post norm)
     float* out_lds = ssy + nw;                                            // [groups of this WG][NOUT]
 
-    // ---- this lane's activation block (and the norm weights), issued first:
-    // they come from L2 while the weight copies below are in flight
+    // ---- this lane's activation block, the norm weights and the residual
+    // update's inputs: issued before the weight copies, waited for after them
+    // without waiting for the copies (see load8_async).  Lanes past the row
+    // load the last block and drop it.
     const int blk = w * 64 + lane;
     const bool active = blk < nb;
-    float v[32];
-    float4 nv[8];
-    if (active) {
-        const float4* xp = reinterpret_cast<const float4*>(a.x + 32 * blk);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const float4 q = xp[e];
-            v[4 * e] = q.x; v[4 * e + 1] = q.y; v[4 * e + 2] = q.z; v[4 * e + 3] = q.w;
-        }
-        if (a.norm && !POST) {
-            const float4* np = reinterpret_cast<const float4*>(a.norm + 32 * blk);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) nv[e] = np[e];
-        }
-    } else {
-#pragma unroll
-        for (int j = 0; j < 32; ++j) v[j] = 0.0f;
-    }
-    // ---- optional residual update (rmsnorm_add_kernel's arithmetic): y is
-    // loaded here, ahead of the weight copies, in place of the norm weights,
-    // which are loaded with the post weights once the weight copies are
-    // issued (fewer live registers in the prologue)
-    float yv[32];
+    const int lblk = active ? blk : nb - 1;
+    f32x4 xq[8], nq[8], yq[8], pq[8];
+    load8_async(xq, a.x + 32 * lblk);
+    if (a.norm) load8_async(nq, a.norm + 32 * lblk);
     if (POST) {
-        if (active) {
-            const float4* yp = reinterpret_cast<const float4*>(a.post_y + 32 * blk);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const float4 q = yp[e];
-                yv[4 * e] = q.x; yv[4 * e + 1] = q.y; yv[4 * e + 2] = q.z; yv[4 * e + 3] = q.w;
-            }
-        } else {
-#pragma unroll
-            for (int j = 0; j < 32; ++j) yv[j] = 0.0f;
-        }
+        load8_async(yq, a.post_y + 32 * lblk);
+        load8_async(pq, a.post_w + 32 * lblk);
     }
 
     // ---- weight copies: the first NB-1 chunks of this workgroup's sequence,
@@ -929,13 +931,35 @@ __global__ void __launch_bounds__(1024) gemv_kernel(GemvArgs a) {
 #pragma unroll
     for (int b = 0; b < NB - 1; ++b)
         if (b < nk) issue(b, b);
+    wait_prologue<NB - 1, CI>(nk);
+    pin8(xq);
+    if (a.norm) pin8(nq);
+    if (POST) {
+        pin8(yq);
+        pin8(pq);
+    }
+    float v[32];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        v[4 * e] = active ? xq[e].x : 0.0f;
+        v[4 * e + 1] = active ? xq[e].y : 0.0f;
+        v[4 * e + 2] = active ? xq[e].z : 0.0f;
+        v[4 * e + 3] = active ? xq[e].w : 0.0f;
+    }
 
-    // x := x + post_w * (r_y * post_y), the same in every workgroup; the
-    // first workgroup stores it
+    // x := x + post_w * (r_y * post_y) (rmsnorm_add_kernel's arithmetic), the
+    // same in every workgroup; the first workgroup stores it
     if (POST) {
         float sy = 0.0f;
+        if (active) {
 #pragma unroll
-        for (int j = 0; j < 32; ++j) sy += yv[j] * yv[j];
+            for (int e = 0; e < 8; ++e) {
+                sy += yq[e].x * yq[e].x;
+                sy += yq[e].y * yq[e].y;
+                sy += yq[e].z * yq[e].z;
+                sy += yq[e].w * yq[e].w;
+            }
+        }
         sy = wave_sum(sy);
         if (lane == 0) ssy[w] = sy;
         lds_sync();
@@ -943,24 +967,17 @@ __global__ void __launch_bounds__(1024) gemv_kernel(GemvArgs a) {
         for (int i = 0; i < nw; ++i) sy += ssy[i];
         const float ry = 1.0f / sqrtf(sy * a.inv_n + a.eps);
         if (active) {
-            const float4* wp = reinterpret_cast<const float4*>(a.post_w + 32 * blk);
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                const float4 pw = wp[e];
-                v[4 * e] = v[4 * e] + pw.x * (ry * yv[4 * e]);
-                v[4 * e + 1] = v[4 * e + 1] + pw.y * (ry * yv[4 * e + 1]);
-                v[4 * e + 2] = v[4 * e + 2] + pw.z * (ry * yv[4 * e + 2]);
-                v[4 * e + 3] = v[4 * e + 3] + pw.w * (ry * yv[4 * e + 3]);
+                v[4 * e] = v[4 * e] + pq[e].x * (ry * yq[e].x);
+                v[4 * e + 1] = v[4 * e + 1] + pq[e].y * (ry * yq[e].y);
+                v[4 * e + 2] = v[4 * e + 2] + pq[e].z * (ry * yq[e].z);
+                v[4 * e + 3] = v[4 * e + 3] + pq[e].w * (ry * yq[e].w);
             }
             if (blockIdx.x == 0) {
                 float4* op = reinterpret_cast<float4*>(a.post_out + 32 * blk);
 #pragma unroll
                 for (int e = 0; e < 8; ++e) op[e] = make_float4(v[4 * e], v[4 * e + 1], v[4 * e + 2], v[4 * e + 3]);
-            }
-            if (a.norm) {
-                const float4* np = reinterpret_cast<const float4*>(a.norm + 32 * blk);
-#pragma unroll
-                for (int e = 0; e < 8; ++e) nv[e] = np[e];
             }
         }
     }
@@ -990,15 +1007,15 @@ __global__ void __launch_bounds__(1024) gemv_kernel(GemvArgs a) {
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 if (kLateScale) {
-                    v[4 * e] = nv[e].x * v[4 * e];
-                    v[4 * e + 1] = nv[e].y * v[4 * e + 1];
-                    v[4 * e + 2] = nv[e].z * v[4 * e + 2];
-                    v[4 * e + 3] = nv[e].w * v[4 * e + 3];
+                    v[4 * e] = nq[e].x * v[4 * e];
+                    v[4 * e + 1] = nq[e].y * v[4 * e + 1];
+                    v[4 * e + 2] = nq[e].z * v[4 * e + 2];
+                    v[4 * e + 3] = nq[e].w * v[4 * e + 3];
                 } else {
-                    v[4 * e] = nv[e].x * (r * v[4 * e]);
-                    v[4 * e + 1] = nv[e].y * (r * v[4 * e + 1]);
-                    v[4 * e + 2] = nv[e].z * (r * v[4 * e + 2]);
-                    v[4 * e + 3] = nv[e].w * (r * v[4 * e + 3]);
+                    v[4 * e] = nq[e].x * (r * v[4 * e]);
+                    v[4 * e + 1] = nq[e].y * (r * v[4 * e + 1]);
+                    v[4 * e + 2] = nq[e].z * (r * v[4 * e + 2]);
+                    v[4 * e + 3] = nq[e].w * (r * v[4 * e + 3]);
                 }
             }
         }
@@ -1122,8 +1139,14 @@ void launch_rows(GemvArgs a, hipStream_t st) {
     // fused), so workgroups per CU are also capped to keep that traffic near
     // 128 KB per CU: more workgroups than this only add x reads that compete
     // with the weight stream (measured on MI355X at the Llama-3-8B shapes).
+    // The residual update's two vectors count too when the launch is short
+    // (at most 4 row groups per workgroup at the plain cap), where they are a
+    // large share of a workgroup's reads (Gemma-2-2B's q|k|v and gate|up);
+    // long launches such as the LM head keep the plain cap.
     const int xbytes = a.cols * 4 * (a.norm ? 2 : 1);
-    const int per_cu = std::min(occupancy(kern, threads, lds_for(cus())), std::max(1, (128 << 10) / xbytes));
+    int xcap = std::max(1, (128 << 10) / xbytes);
+    if (a.post_y && a.ngroups <= 4 * xcap * cus()) xcap = std::max(1, (128 << 10) / (xbytes + a.cols * 8));
+    const int per_cu = std::min(occupancy(kern, threads, lds_for(cus())), xcap);
     const int cap = per_cu * cus();
     int grid = std::min(a.ngroups, cap);
     if (env_int("L3P_GEMV_BAL", 1)) {
@@ -1241,6 +1264,9 @@ void launch_gemv(int type, const GemvBatch& b, int cols, const float* x, const f
     L3P_REQUIRE(!b.post_y || (b.post_w && b.post_out && b.post_out != x && ((uintptr_t)b.post_y & 15) == 0 &&
                               ((uintptr_t)b.post_w & 15) == 0 && ((uintptr_t)b.post_out & 15) == 0),
                 L3P_E_INVALID, "gemv: bad residual update arguments");
+    // the residual-update kernels hold four activation vectors in registers
+    // and are built for at most 512 threads (8 chunk waves)
+    L3P_REQUIRE(!b.post_y || cols <= kMaxPostCols, L3P_E_UNSUPPORTED, "gemv: residual update over %d columns", cols);
     // Rows per group G: the largest of 16, 8, 4 that still gives about six
     // waves per CU (groups x column chunks); ring depth 3.  (Measured on
     // MI355X at the Llama-3-8B shapes.)

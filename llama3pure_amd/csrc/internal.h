@@ -125,6 +125,8 @@ struct GemvBatch {
     const float* post_w;
     float* post_out;
 };
+// Widest rows a GEMV with the residual update takes (8 column chunks).
+constexpr int kMaxPostCols = 16384;
 
 // gemv.hip: the decode GEMV over Q8_0 / Q4_0 / Q4_K / Q6_K rows, with an
 // optional RMSNorm of x fused into its prologue (norm != null).  Weights, x

@@ -586,6 +586,12 @@ static void layers_impl(l3p_ctx* c, bool with_logits) {
     const float* pend_w = nullptr;
     auto fold = [&](GemvBatch& b) {
         if (!pend_y) return;
+        if (m.dim > kMaxPostCols) {   // too wide for the fused update: apply it in place first
+            launch_rmsnorm_add_rows(pend_y, m.dim, pend_w, m.dim, m.inv_dim, m.eps > 0 ? m.eps : 1e-5f, cur, m.dim,
+                                    1, s);
+            pend_y = nullptr;
+            return;
+        }
         b.post_y = pend_y;
         b.post_w = pend_w;
         b.post_out = alt;
