@@ -90,3 +90,60 @@ def test_ref_drift_fixture_reproduces():
                        check=True, capture_output=True, text=True, timeout=600)
     got = json.loads(r.stdout.strip().splitlines()[-1])
     assert np.allclose(got["per_step"], want["per_step"], rtol=1e-6, atol=0)
+
+
+def _gemma_layers(rng, dim, hidden, qd, kvd):
+    w = lambda r, c: rng.normal(0, 0.05, (r, c)).astype(np.float32)
+    return {"attn_q": w(qd, dim), "attn_k": w(kvd, dim), "attn_v": w(kvd, dim), "attn_output": w(dim, qd),
+            "ffn_gate": w(hidden, dim), "ffn_up": w(hidden, dim), "ffn_down": w(dim, hidden)}
+
+
+@pytest.mark.skipif(not oracle.have_ref(), reason="oracle/_ref not built (make -C oracle ref)")
+@pytest.mark.parametrize("pattern,n_layers", [(2, 2), (3, 3), (2, 4)])
+def test_swa_pattern_option_against_reference(tmp_path, pattern, n_layers):
+    """The oracle's swa_pattern option (no counterpart in the reference, which
+    hard-codes every 6th layer global, c:5100) pinned against the reference
+    itself.  A Gemma layer whose matrices are all zero leaves the residual
+    bit-identical (its projections, post norms and GeGLU are all zero), so the
+    reference on a model with zero layers inserted where its fixed pattern
+    puts sliding-window layers runs the same computation as the oracle with
+    pattern p on the model without them: layers l with l % p < p - 1 local,
+    the others global with the global RoPE base.  Logits at every decode step
+    bit-identical, and the K/V caches of the mapped layers byte-identical."""
+    if not oracle.have_ref():
+        pytest.skip("oracle/_ref not built")
+    dim, hidden, heads, kv, hd, vocab = 128, 256, 2, 1, 64, 256
+    rng = np.random.default_rng(60 + 10 * pattern + n_layers)
+    layers = [_gemma_layers(rng, dim, hidden, heads * hd, kv * hd) for _ in range(n_layers)]
+    emb = rng.normal(0, 0.5, (vocab, dim)).astype(np.float32)
+    # reference layer of each oracle layer: the oracle's local layers fill
+    # the reference's local slots (l % 6 < 5) and its global layers the
+    # reference's global slots (l % 6 == 5), in order
+    ref_of, rl = [], 0
+    for l in range(n_layers):
+        glob = l % pattern == pattern - 1
+        while (rl % 6 == 5) != glob:
+            rl += 1
+        ref_of.append(rl)
+        rl += 1
+    n_ref = ref_of[-1] + 1
+    zero = {k: np.zeros_like(v) for k, v in layers[0].items()}
+
+    def model(n, at):
+        mats = {"token_embd.weight": emb}
+        for l in range(n):
+            src = layers[at.index(l)] if l in at else zero
+            mats.update({f"blk.{l}.{k}.weight": v for k, v in src.items()})
+        return synth.synthetic_model(arch="gemma3", dim=dim, hidden=hidden, n_layers=n, n_heads=heads, n_kv=kv,
+                                     head_dim=hd, vocab=vocab, ctx=64, qtype=synth.Q8_0, seed=0, tied=True,
+                                     softcap=30.0, swa_window=5, rope_theta=1e6, rope_theta_swa=1e4, mats=mats)
+
+    pr, po = tmp_path / "ref.gguf", tmp_path / "orc.gguf"
+    pr.write_bytes(model(n_ref, ref_of))
+    po.write_bytes(model(n_layers, list(range(n_layers))))
+    out = subprocess.run([sys.executable, os.path.join(HERE, "ref_swa_check.py"), str(pr), str(po), str(pattern),
+                          "20", "8", ",".join(map(str, ref_of))], capture_output=True, text=True, timeout=600)
+    i = out.stdout.rfind('{"ok"')
+    assert i >= 0, out.stdout[-2000:] + out.stderr[-2000:]
+    r = json.loads(out.stdout[i:].splitlines()[0])
+    assert r["ok"] and r["steps"] == 8 and r["kv_equal"], r
