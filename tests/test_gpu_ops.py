@@ -154,6 +154,14 @@ def _check_gemv(ctx, torch, cpuref, qtype, rows, cols, seed=0, sample_rows=None)
     # widths that leave a short last chunk column: 4160 columns (64 + 64 + 2
     # blocks), 2304 (64 + 8), 6400 (3 x 64 + 8)
     (l3p.Q8_0, 100, 4160),
+    # Q8_0 short last columns of 8, 16 or 32 lane slots are copied packed,
+    # several rows' short chunks per copy: rows per group G = 8 and 16 with a
+    # ragged last group, 16 lane slots, one wave of 32, three waves + 8
+    (l3p.Q8_0, 6150, 2304),
+    (l3p.Q8_0, 12289, 2304),
+    (l3p.Q8_0, 1001, 2560),
+    (l3p.Q8_0, 777, 1024),
+    (l3p.Q8_0, 500, 4352),
     (l3p.Q4_1, 300, 4160),
     (l3p.Q5_0, 200, 2304),
     (l3p.IQ4_NL, 257, 2304),
