@@ -1162,12 +1162,19 @@ void launch_rows(GemvArgs a, hipStream_t st) {
 }
 
 // Ring depth: 3 buffers per wave (deeper rings measured no faster on
-// MI355X); 2 for the 4 KB F16/BF16 and 8 KB F32 chunks of rows too wide for 3.
+// MI355X for Q8_0 and Q6_K); 4 for chunks of at most 1280 bytes; 2 for the
+// 4 KB F16/BF16 and 8 KB F32 chunks of rows too wide for 3.
 template <int QT, int G, bool PAIR, bool UA>
 void launch_nb(GemvArgs a, int nbuf, hipStream_t st) {
     if constexpr (Fmt<QT>::kBufBytes >= 4096) {
         if (nbuf == 2) {
             launch_rows<QT, G, 2, PAIR, UA>(a, st);
+            return;
+        }
+    }
+    if constexpr (Fmt<QT>::kChunkBytes <= 1280) {
+        if (nbuf == 4) {
+            launch_rows<QT, G, 4, PAIR, UA>(a, st);
             return;
         }
     }
@@ -1198,7 +1205,11 @@ void launch_type(GemvArgs a, bool pair, int G, hipStream_t st) {
     // three buffers per wave when they fit the 160 KB of LDS with room for
     // the result slots, else two (gemv_supported keeps F32 rows narrow enough)
     const int nw = (a.cols / 32 + 63) / 64;
-    const int nb = (size_t)nw * 3 * Fmt<QT>::kBufBytes + 16384 <= 160 * 1024 ? 3 : 2;
+    int nb = (size_t)nw * 3 * Fmt<QT>::kBufBytes + 16384 <= 160 * 1024 ? 3 : 2;
+    // chunks of at most 1280 bytes (Q4_0, Q4_1, IQ4_NL, Q2_K, Q3_K, Q4_K) keep
+    // three in flight: 5-6% faster at the Q4_0 and Q4_K FFN shapes, where
+    // a 2-deep ring leaves too few bytes in flight per CU (measured on MI355X)
+    if (Fmt<QT>::kChunkBytes <= 1280) nb = 4;
     if (row_bytes<QT>(a.cols) % 16 == 0) {
         launch_g<QT, false>(a, pair, G, nb, st);
     } else {
