@@ -208,6 +208,16 @@ __device__ __forceinline__ void v_accum(uint32_t dh, uint32_t q, float e, float 
     for (int i = 0; i < PER; ++i) acc[i] = fmaf((float)(int8_t)((q >> (8 * i)) & 0xffu), f, acc[i]);
 }
 
+// One 16-byte piece per lane into LDS (lane i of the instruction writes dst + 16 i).
+__device__ __forceinline__ void piece16(const uint8_t* src, uint32_t* dst) {
+    __builtin_amdgcn_global_load_lds(src, (lds_void*)dst, 16, 0, 0);
+}
+
+// Dwords of LDS for one chunk's K (or V) rows: TC rows of hq8 bytes copied
+// in 16-byte pieces from the 16-byte aligned address at or below the first
+// row (up to 15 bytes before it and 15 after the last row).
+__host__ __device__ constexpr int chunk_rows_dw(int tc, int hq8) { return 4 * ((tc * hq8 + 30) / 16 + 1); }
+
 template <int NB, int TC>
 __global__ void __launch_bounds__(1024) attn_chunk_kernel(AttnCArgs a0) {
     extern __shared__ __align__(16) float smem[];
@@ -245,13 +255,13 @@ __global__ void __launch_bounds__(1024) attn_chunk_kernel(AttnCArgs a0) {
 
     // LDS: [kv_mul][hs] q rows, [2][hs] k and v rows, [kv_mul][8][TC] V
     // factors, [kv_mul][hs] int8 q, [kv_mul][8] q scales, then the chunk's K
-    // rows and V rows (TC * hq8 bytes + 8 each, dword aligned)
+    // rows and V rows (chunk_rows_dw dwords each, 16-byte aligned)
     float* qh = smem;
     float* kvh = qh + km * hs;
     float* f = kvh + 2 * hs;
     int8_t* qq = reinterpret_cast<int8_t*>(f + km * 8 * TC);
     float* qd = reinterpret_cast<float*>(qq + km * hs);
-    const int rowdw = (TC * hq8 + 8 + 3) / 4;
+    const int rowdw = chunk_rows_dw(TC, hq8);
     uint32_t* krows = reinterpret_cast<uint32_t*>(qd + km * 8);
     uint32_t* vrows = krows + rowdw;
 
@@ -265,23 +275,25 @@ __global__ void __launch_bounds__(1024) attn_chunk_kernel(AttnCArgs a0) {
         sn[k] = p < half ? sinr[p] : 0.0f;
     }
 
-    // the chunk's K and V rows, HBM -> LDS (dword copies from the 4-byte
-    // aligned start; the row at the step's position is replaced below)
+    // the chunk's K and V rows, HBM -> LDS in 16-byte pieces from the 16-byte
+    // aligned address at or below the first row (the last piece ends inside
+    // the 16-byte granule of the last row's last byte; the row at the step's
+    // position is replaced below)
     const size_t start = (size_t)g * a.head_seq + (size_t)(sp.t0 + jbeg) * hq8;
-    const size_t s4 = start & ~(size_t)3;
-    const int nd = (int)((start + (size_t)cnt * hq8 - s4 + 3) >> 2);
+    const size_t s16 = start & ~(size_t)15;
+    const int np = (int)((start + (size_t)cnt * hq8 - s16 + 15) >> 4);
     {
-        const uint32_t* ks = reinterpret_cast<const uint32_t*>(a.kc) + (s4 >> 2);
-        const uint32_t* vs = reinterpret_cast<const uint32_t*>(a.vc) + (s4 >> 2);
+        const uint8_t* ks = a.kc + s16;
+        const uint8_t* vs = a.vc + s16;
         const int nw = nt >> 6;
-        for (int i = w; i * 64 < nd; i += nw) {
-            if (i * 64 + lane < nd) {
-                __builtin_amdgcn_global_load_lds(ks + i * 64 + lane, (lds_void*)(krows + i * 64), 4, 0, 0);
-                __builtin_amdgcn_global_load_lds(vs + i * 64 + lane, (lds_void*)(vrows + i * 64), 4, 0, 0);
+        for (int i = w; i * 64 < np; i += nw) {
+            if (i * 64 + lane < np) {
+                __builtin_amdgcn_global_load_lds(ks + 16 * (i * 64 + lane), (lds_void*)(krows + i * 256), 16, 0, 0);
+                __builtin_amdgcn_global_load_lds(vs + 16 * (i * 64 + lane), (lds_void*)(vrows + i * 256), 16, 0, 0);
             }
         }
     }
-    const uint32_t roff = (uint32_t)(start - s4);   // byte offset of row 0 in krows / vrows
+    const uint32_t roff = (uint32_t)(start - s16);   // byte offset of row 0 in krows / vrows
 
     // QK-norm + RoPE + Q8_0 of the group's query heads (and of K, V at pos)
 #pragma unroll
@@ -608,7 +620,7 @@ constexpr int kPV = kPP + 4;    // bytes per transposed V row in LDS
 typedef int int32x4 __attribute__((ext_vector_type(4)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-__host__ __device__ constexpr int prefill_raw_dwords(int hq8) { return (kPP * hq8 + 8) / 4 + 1; }
+__host__ __device__ constexpr int prefill_raw_dwords(int hq8) { return chunk_rows_dw(kPP, hq8); }
 
 // LDS bytes of attn_prefill_kernel
 __host__ __device__ constexpr size_t prefill_attn_lds(int nb, int km) {
@@ -742,24 +754,21 @@ __global__ void __launch_bounds__(1024) attn_prefill_kernel(AttnCArgs a0, int nt
 #pragma unroll
     for (int d = 0; d < ND; ++d) acc[d] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
     const size_t head_base = (size_t)g * a0.head_seq;
-    const uint32_t* kc4 = reinterpret_cast<const uint32_t*>(a0.kc);
-    const uint32_t* vc4 = reinterpret_cast<const uint32_t*>(a0.vc);
 
-    // the K and V rows of the step at p0 into raw buffer `buf`: dword pieces
-    // from the 4-byte aligned start (the copies of the next step are in
-    // flight while this step is computed)
+    // the K and V rows of the step at p0 into raw buffer `buf`: 16-byte
+    // pieces from the 16-byte aligned address at or below the first row (the
+    // copies of the next step are in flight while this step is computed)
     const int p_first = hi < 0 ? 0 : (lo & ~(kPP - 1));
     auto copy_rows = [&](int p0, int buf) {
         const int cnt = min(kPP, hi + 1 - p0);
         const size_t start = head_base + (size_t)p0 * hq8;
-        const size_t s4 = start & ~(size_t)3;
-        const int nd = (int)((start + (size_t)cnt * hq8 - s4 + 3) >> 2);
+        const size_t s16 = start & ~(size_t)15;
+        const int np = (int)((start + (size_t)cnt * hq8 - s16 + 15) >> 4);
         uint32_t* kr = raw + (size_t)buf * 2 * rawdw;
-        for (int i = w; i * 64 < nd; i += nw) {
-            if (i * 64 + lane < nd) {
-                __builtin_amdgcn_global_load_lds(kc4 + (s4 >> 2) + i * 64 + lane, (lds_void*)(kr + i * 64), 4, 0, 0);
-                __builtin_amdgcn_global_load_lds(vc4 + (s4 >> 2) + i * 64 + lane, (lds_void*)(kr + rawdw + i * 64), 4,
-                                                 0, 0);
+        for (int i = w; i * 64 < np; i += nw) {
+            if (i * 64 + lane < np) {
+                piece16(a0.kc + s16 + 16 * (i * 64 + lane), kr + i * 256);
+                piece16(a0.vc + s16 + 16 * (i * 64 + lane), kr + rawdw + i * 256);
             }
         }
     };
@@ -767,7 +776,7 @@ __global__ void __launch_bounds__(1024) attn_prefill_kernel(AttnCArgs a0, int nt
     int buf = 0;
     for (int p0 = p_first; p0 <= hi; p0 += kPP, buf ^= 1) {
         const int cnt = min(kPP, hi + 1 - p0);   // rows p0 .. p0 + cnt - 1
-        const uint32_t roff = (uint32_t)((head_base + (size_t)p0 * hq8) & 3);
+        const uint32_t roff = (uint32_t)((head_base + (size_t)p0 * hq8) & 15);
         const uint32_t* kraw = raw + (size_t)buf * 2 * rawdw;
         const uint32_t* vraw = kraw + rawdw;
         __builtin_amdgcn_s_waitcnt(0x0070);   // vmcnt(0) lgkmcnt(0): this wave's copies have landed
@@ -1574,7 +1583,7 @@ static void launch_chunk_kernel(dim3 grid, dim3 block, size_t lds, const AttnCAr
 // Chunk and merge launches for `tokens` tokens of up to `chunks` chunks each.
 static void launch_chunks(const Model& m, const AttnCArgs& a, int chunks, int tokens, hipStream_t s) {
     const int tc = a.tc;
-    const int rowdw = (tc * m.hq8 + 8 + 3) / 4;
+    const int rowdw = chunk_rows_dw(tc, m.hq8);
     const size_t lds = (size_t)m.kv_mul * m.hs * 4 + 2 * (size_t)m.hs * 4 + (size_t)m.kv_mul * 8 * tc * 4 +
                        (size_t)m.kv_mul * m.hs + (size_t)m.kv_mul * 8 * 4 + 2 * (size_t)rowdw * 4 + 16;
     const dim3 grid(m.n_kv, chunks, tokens), block(64 * m.kv_mul);
