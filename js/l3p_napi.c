@@ -138,6 +138,7 @@ static napi_value info_object(napi_env env, const l3p_model_info* mi) {
     SETI("weightType", mi->weight_type)
     SETF("ropeTheta", mi->rope_theta) SETF("rmsEps", mi->rms_eps) SETF("finalSoftcap", mi->final_softcap)
     SETF("deviceBytes", (double)mi->device_bytes)
+    SETI("swaPattern", mi->swa_pattern) SETF("attnSoftcap", mi->attn_softcap)
     napi_get_boolean(env, mi->is_gemma != 0, &v);
     napi_set_named_property(env, o, "isGemma", v);
 #undef SETI
@@ -145,10 +146,13 @@ static napi_value info_object(napi_env env, const l3p_model_info* mi) {
     return o;
 }
 
-/* loadGguf(engine, ArrayBuffer | TypedArray | Buffer, contextSize) -> info */
+/* loadGguf(engine, ArrayBuffer | TypedArray | Buffer, contextSize,
+ *          {swaPattern, attnSoftcap}?) -> info
+ * The options object is optional; absent or non-numeric fields are 0, the
+ * reference's behaviour (l3p_load_opts). */
 static napi_value js_load(napi_env env, napi_callback_info info) {
-    napi_value argv[3];
-    if (!get_args(env, info, 3, argv)) return NULL;
+    napi_value argv[4];
+    if (!get_args(env, info, 4, argv)) return NULL;
     Engine* e = engine_of(env, argv[0]);
     if (!e) return NULL;
     void* data = NULL;
@@ -174,6 +178,13 @@ static napi_value js_load(napi_env env, napi_callback_info info) {
     l3p_load_opts o;
     memset(&o, 0, sizeof o);
     o.context_size = i32_of(env, argv[2], 0);
+    napi_valuetype ot;
+    if (napi_typeof(env, argv[3], &ot) == napi_ok && ot == napi_object) {
+        napi_value v;
+        if (napi_get_named_property(env, argv[3], "swaPattern", &v) == napi_ok) o.swa_pattern = i32_of(env, v, 0);
+        if (napi_get_named_property(env, argv[3], "attnSoftcap", &v) == napi_ok)
+            o.attn_softcap = (float)f64_of(env, v, 0.0);
+    }
     L3P_CALL(env, e, l3p_load_gguf(e->ctx, data, len, &o));
     l3p_model_info mi;
     L3P_CALL(env, e, l3p_get_model_info(e->ctx, &mi));

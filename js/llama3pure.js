@@ -37,7 +37,10 @@
 //     sampler run on the device and only the token id comes back to JS;
 //   * sampling draws from the C engine's xorshift64* generator
 //     (llama3pure-c-engine.c:4266-4276), seeded by data.seed ([hi, lo]
-//     uint32 words) when given, where the reference calls Math.random().
+//     uint32 words) when given, where the reference calls Math.random();
+//   * two optional load fields the reference lacks, data.swaPattern (every
+//     swaPattern-th Gemma layer global instead of every 6th) and
+//     data.attnSoftcap (Gemma-2's attention score cap), off when absent.
 "use strict"
 
 var path = require("path")
@@ -111,7 +114,8 @@ function load(data) {
     engine = new Engine(0)
   }
   config = null
-  config = engine.load(new Uint8Array(data.model), opt.contextSize)
+  config = engine.load(new Uint8Array(data.model), opt.contextSize,
+                       { swaPattern: data.swaPattern, attnSoftcap: data.attnSoftcap })
   if (Array.isArray(data.seed)) {
     engine.setSeed(data.seed[0], data.seed[1])
   }

@@ -29,9 +29,12 @@ function Engine(device) {
 }
 
 // loadModel (js:4288-4584): the GGUF bytes are parsed and uploaded once;
-// the caller may drop the ArrayBuffer afterwards.
-Engine.prototype.load = function (model, contextSize) {
-  this.config = addon.loadGguf(this.h, model, contextSize || 0)
+// the caller may drop the ArrayBuffer afterwards.  options: {swaPattern,
+// attnSoftcap}, both optional and off by default (no counterpart in the
+// reference: every swaPattern-th Gemma layer global instead of every 6th, and
+// the attention score cap of Gemma-2).
+Engine.prototype.load = function (model, contextSize, options) {
+  this.config = addon.loadGguf(this.h, model, contextSize || 0, options || {})
   this.logits = null
   return this.config
 }

@@ -36,23 +36,32 @@ def test_addon_exports_and_error_mapping():
 
 @needs_node
 @pytest.mark.gpu
-@pytest.mark.parametrize("arch", ["llama", "gemma3"])
+@pytest.mark.parametrize("arch", ["llama", "gemma3", "gemma3_opts"])
 def test_js_generate_flow_matches_oracle(arch, tmp_path, cpuref):
     """Prefill + greedy steps through the JS boundary: the logits match the
-    oracle within the single-model tolerance and the tokens are the oracle's."""
-    extra = dict(head_dim=256, softcap=30.0, swa_window=16, tied=True) if arch == "gemma3" else {}
-    g = synth.synthetic_model(arch=arch, dim=512, hidden=1024, n_layers=2, n_heads=8, n_kv=2, vocab=2048, ctx=128,
-                              qtype=synth.Q8_0, seed=31, norm_jitter=0.1, **extra)
+    oracle within the single-model tolerance and the tokens are the oracle's.
+    gemma3_opts passes the load options swaPattern 2 and attnSoftcap 5 (a cap
+    low enough to change the scores) through Engine.load, and the oracle runs
+    with the same options."""
+    extra = dict(head_dim=256, softcap=30.0, swa_window=16, tied=True) if arch.startswith("gemma3") else {}
+    g = synth.synthetic_model(arch=arch.split("_")[0], dim=512, hidden=1024, n_layers=2, n_heads=8, n_kv=2,
+                              vocab=2048, ctx=128, qtype=synth.Q8_0, seed=31, norm_jitter=0.1, **extra)
     p = tmp_path / "m.gguf"
     p.write_bytes(g)
     prompt = np.random.default_rng(4).integers(0, 2048, 40).astype(np.int32)
     steps = 8
     out = tmp_path / "out.bin"
+    opts = ["2", "5.0"] if arch == "gemma3_opts" else []
     r = subprocess.run([NODE, os.path.join(ROOT, "tests", "js_run.js"), str(p), str(out),
-                        ",".join(map(str, prompt)), str(steps)], capture_output=True, text=True, timeout=300)
+                        ",".join(map(str, prompt)), str(steps)] + opts, capture_output=True, text=True, timeout=300)
     assert r.returncode == 0, r.stderr[-2000:]
+    info = json.loads(r.stdout.strip().splitlines()[-1])
+    if opts:
+        assert info["swaPattern"] == 2 and abs(info["attnSoftcap"] - 5.0) < 1e-6, info
     raw = np.fromfile(out, np.uint8).reshape(steps, 2048 * 4 + 4)
     m = cpuref.open_model(g)
+    if opts:
+        m.set_attention(2, 5.0)
     pos = 0
     while pos < len(prompt) - 1:
         bs = min(32, len(prompt) - 1 - pos)
