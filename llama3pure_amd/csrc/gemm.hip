@@ -8,11 +8,14 @@
 // activation, so the products are the reference's and only the fp32
 // summation order differs.
 //
-// Tiling.  A workgroup owns a 64 x 64 tile of Y and walks K in steps of 64:
-//   1. the 64 x 64 X tile (fp32, from L2) and the dequantized 64 x 64 W tile
+// Tiling.  A workgroup owns a 64 x BN tile of Y (BN = 64, or 128 for passes
+// of at least 16 row tiles whose 128-wide tiles give every CU two workgroups
+// without splitting K, so each X tile serves twice the outputs) and walks K
+// in steps of 64:
+//   1. the 64 x 64 X tile (fp32, from L2) and the dequantized BN x 64 W tile
 //      go to LDS, rows padded to 68 floats; their global loads were issued
 //      one step earlier, before that step's matrix work;
-//   2. four waves each compute a 32 x 32 quarter with v_mfma_f32_16x16x4_f32
+//   2. BN / 16 waves each compute a 32 x 32 block with v_mfma_f32_16x16x4_f32
 //      (2 x 2 tiles of 16 x 16).  The instruction contracts over 4 k-slots,
 //      slot g held by lanes 16g..16g+15; here slot g of step s is
 //      k = kk + 4g + s, the same for A (X) and B (W), so each lane fetches
@@ -27,6 +30,7 @@
 // gemm_reduce_kernel adds the splits in split order, so results do not
 // depend on scheduling.
 #include <algorithm>
+#include <cstdlib>
 #include <mutex>
 
 #include "dequant.h"
@@ -37,7 +41,7 @@ namespace {
 
 using namespace l3pd;
 
-constexpr int kBM = 64, kBN = 64, kBK = 64;
+constexpr int kBM = 64, kBK = 64;
 constexpr int kLDK = kBK + 4;   // LDS row stride in floats (b128 reads spread over the banks)
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
@@ -66,17 +70,18 @@ struct GemmArgs {
 // quants and block scale (t: row t/4, block (t/2)&1, half t&1).
 template <int QT>
 struct StepRegs {
-    float4 x[4];
+    float4 x[4];   // the first 1024 / threads of them are used
     uint4 q;         // Q8_0: the 16 quants as fetched (bytes in order)
     uint32_t d;      // Q8_0: fp16 scale bits
 };
 
-template <int QT>
+template <int QT, int BN>
 __device__ __forceinline__ void fetch_step(StepRegs<QT>& sr, const GemmArgs& a, const uint8_t* W, int N, int m0, int n0,
                                            int k0, int t) {
+    constexpr int NT = 4 * BN, XU = 1024 / NT;   // threads; float4 of the X tile per thread
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-        const int i = t + 256 * u, r = i >> 4, c = i & 15;
+    for (int u = 0; u < XU; ++u) {
+        const int i = t + NT * u, r = i >> 4, c = i & 15;
         const int m = m0 + r, kk = k0 + 4 * c;
         sr.x[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         if (m < a.m && kk < a.k) sr.x[u] = *reinterpret_cast<const float4*>(a.x + (size_t)m * a.ldx + kk);
@@ -102,12 +107,13 @@ __device__ __forceinline__ void fetch_step(StepRegs<QT>& sr, const GemmArgs& a, 
 // (float)q * d as dequantize_row_q8_0 (c:691-702); the other types go
 // element by element through the reference-exact dequantizer, reading the
 // weight bytes here.
-template <int QT>
+template <int QT, int BN>
 __device__ __forceinline__ void store_step(float* xs, float* ws, const StepRegs<QT>& sr, const GemmArgs& a,
                                            const uint8_t* W, int N, int n0, int k0, int t) {
+    constexpr int NT = 4 * BN, XU = 1024 / NT;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-        const int i = t + 256 * u, r = i >> 4, c = i & 15;
+    for (int u = 0; u < XU; ++u) {
+        const int i = t + NT * u, r = i >> 4, c = i & 15;
         *reinterpret_cast<float4*>(xs + r * kLDK + 4 * c) = sr.x[u];
     }
     if (QT == L3P_Q8_0) {
@@ -121,7 +127,7 @@ __device__ __forceinline__ void store_step(float* xs, float* ws, const StepRegs<
 #pragma unroll
         for (int j = 0; j < 4; ++j) dst[j] = make_float4(v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
     } else {
-        // 4096 values, 16 per thread: row t/4, columns 16*(t%4) .. +16
+        // BN x 64 values, 16 per thread: row t/4, columns 16*(t%4) .. +16
         const int r = t >> 2, c0 = 16 * (t & 3);
         const int n = n0 + r;
         const bool ok = n < N;
@@ -134,18 +140,19 @@ __device__ __forceinline__ void store_step(float* xs, float* ws, const StepRegs<
     }
 }
 
-template <int QT>
-__global__ void __launch_bounds__(256) gemm_kernel(GemmArgs a) {
+template <int QT, int BN>
+__global__ void __launch_bounds__(4 * BN) gemm_kernel(GemmArgs a) {
     __shared__ __align__(16) float xs[kBM * kLDK];
-    __shared__ __align__(16) float ws[kBN * kLDK];
+    __shared__ __align__(16) float ws[BN * kLDK];
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
     const int tile = blockIdx.x;
     const int sg = (a.nseg > 1 && tile >= a.tbeg[1]) ? ((a.nseg > 2 && tile >= a.tbeg[2]) ? 2 : 1) : 0;
     const uint8_t* W = a.w[sg];
     const int N = a.n[sg];
-    const int n0 = (tile - a.tbeg[sg]) * kBN, m0 = blockIdx.y * kBM;
+    const int n0 = (tile - a.tbeg[sg]) * BN, m0 = blockIdx.y * kBM;
     const int kbeg = blockIdx.z * a.ksteps * kBK, kend = min(a.k, kbeg + a.ksteps * kBK);
-    const int wm = w >> 1, wn = w & 1;      // this wave's 32 x 32 quarter
+    constexpr int WN = BN / 32;              // waves across N
+    const int wm = w / WN, wn = w % WN;      // this wave's 32 x 32 block of the 64 x BN tile
     const int g = lane >> 4, i16 = lane & 15;
     floatx4 acc[2][2];
 #pragma unroll
@@ -154,12 +161,12 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmArgs a) {
         for (int in = 0; in < 2; ++in) acc[im][in] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 
     StepRegs<QT> sr;
-    fetch_step<QT>(sr, a, W, N, m0, n0, kbeg, t);
+    fetch_step<QT, BN>(sr, a, W, N, m0, n0, kbeg, t);
     for (int k0 = kbeg; k0 < kend; k0 += kBK) {
-        store_step<QT>(xs, ws, sr, a, W, N, n0, k0, t);
+        store_step<QT, BN>(xs, ws, sr, a, W, N, n0, k0, t);
         __syncthreads();
         // the next step's loads go out before this step's matrix work
-        if (k0 + kBK < kend) fetch_step<QT>(sr, a, W, N, m0, n0, k0 + kBK, t);
+        if (k0 + kBK < kend) fetch_step<QT, BN>(sr, a, W, N, m0, n0, k0 + kBK, t);
 #pragma unroll
         for (int kk = 0; kk < kBK; kk += 16) {
             float4 af[2], bf[2];
@@ -223,9 +230,10 @@ __global__ void __launch_bounds__(256) gemm_reduce_kernel(GemmArgs a) {
 }
 
 template <int QT>
-void launch_typed(const GemmArgs& a, hipStream_t st) {
+void launch_typed(const GemmArgs& a, int bn, hipStream_t st) {
     const dim3 grid(a.tbeg[a.nseg], (a.m + kBM - 1) / kBM, a.nsplit);
-    launch_kernel(gemm_kernel<QT>, grid, dim3(256), 0u, st, a);
+    if (bn == 128) launch_kernel(gemm_kernel<QT, 128>, grid, dim3(512), 0u, st, a);
+    else launch_kernel(gemm_kernel<QT, 64>, grid, dim3(256), 0u, st, a);
 }
 
 }  // namespace
@@ -244,15 +252,27 @@ bool gemm_mfma_supported(int type) {
 // The launch plan of a job: K splits and the partials they need (floats).
 GemmPlan gemm_plan(const GemmJob& j, size_t ws_floats) {
     GemmPlan p;
-    int tiles = 0, ntot = 0;
+    int tiles = 0, tiles128 = 0, ntot = 0;
     for (int i = 0; i < j.nseg; ++i) {
-        tiles += (j.seg[i].n + kBN - 1) / kBN;
+        tiles += (j.seg[i].n + 63) / 64;
+        tiles128 += (j.seg[i].n + 127) / 128;
         ntot += j.seg[i].n;
+    }
+    const int steps = (j.k + kBK - 1) / kBK;
+    const int mt = (j.m + kBM - 1) / kBM;
+    // 64 x 128 tiles (eight waves, half the X reads per output) for passes of
+    // at least 16 row tiles whose 128-wide tiles give every CU two workgroups
+    // unsplit (Llama-3-8B's 1024-row projections: MFMA busy 75 -> 77%, prompt
+    // 130 -> 127 ms); otherwise 64 x 64 tiles (measured slower with 128 at
+    // Gemma-2-2B's 511 rows: 25.2 -> 25.7 ms)
+    if (mt >= 16 && (long)tiles128 * mt >= 2L * device_cus()) {
+        p.bn = 128;
+        p.ksteps = steps;
+        p.nsplit = 1;
+        return p;
     }
     // K splits while the tiles give fewer than four workgroups per CU (the
     // LDS of four fits a CU), each split at least eight K steps long
-    const int steps = (j.k + kBK - 1) / kBK;
-    const int mt = (j.m + kBM - 1) / kBM;
     const int want = 4 * device_cus();
     int split = 1;
     if (ws_floats && j.m > 0 && (long)tiles * mt < want) {
@@ -288,7 +308,7 @@ void launch_gemm_planned(const GemmJob& j, const GemmPlan& plan, float* ws, hipS
         a.n[a.nseg] = j.seg[i].n;
         a.noff[a.nseg] = ntot;
         a.tbeg[a.nseg] = tiles;
-        tiles += (j.seg[i].n + kBN - 1) / kBN;
+        tiles += (j.seg[i].n + plan.bn - 1) / plan.bn;
         ntot += j.seg[i].n;
         ++a.nseg;
     }
@@ -305,15 +325,15 @@ void launch_gemm_planned(const GemmJob& j, const GemmPlan& plan, float* ws, hipS
     a.nsplit = plan.nsplit;
     a.part = a.nsplit > 1 ? ws : nullptr;
     switch (j.type) {
-    case L3P_Q8_0: launch_typed<L3P_Q8_0>(a, st); break;
-    case L3P_Q2_K: launch_typed<L3P_Q2_K>(a, st); break;
-    case L3P_Q3_K: launch_typed<L3P_Q3_K>(a, st); break;
-    case L3P_Q4_K: launch_typed<L3P_Q4_K>(a, st); break;
-    case L3P_Q5_K: launch_typed<L3P_Q5_K>(a, st); break;
-    case L3P_Q6_K: launch_typed<L3P_Q6_K>(a, st); break;
-    case L3P_F16: launch_typed<L3P_F16>(a, st); break;
-    case L3P_F32: launch_typed<L3P_F32>(a, st); break;
-    default: launch_typed<L3P_BF16>(a, st); break;
+    case L3P_Q8_0: launch_typed<L3P_Q8_0>(a, plan.bn, st); break;
+    case L3P_Q2_K: launch_typed<L3P_Q2_K>(a, plan.bn, st); break;
+    case L3P_Q3_K: launch_typed<L3P_Q3_K>(a, plan.bn, st); break;
+    case L3P_Q4_K: launch_typed<L3P_Q4_K>(a, plan.bn, st); break;
+    case L3P_Q5_K: launch_typed<L3P_Q5_K>(a, plan.bn, st); break;
+    case L3P_Q6_K: launch_typed<L3P_Q6_K>(a, plan.bn, st); break;
+    case L3P_F16: launch_typed<L3P_F16>(a, plan.bn, st); break;
+    case L3P_F32: launch_typed<L3P_F32>(a, plan.bn, st); break;
+    default: launch_typed<L3P_BF16>(a, plan.bn, st); break;
     }
     if (a.nsplit > 1) launch_kernel(gemm_reduce_kernel, dim3((ntot + 255) / 256, j.m), dim3(256), 0u, st, a);
 }

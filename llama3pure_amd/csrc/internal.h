@@ -161,6 +161,7 @@ void launch_gemm(const GemmJob& j, float* ws, size_t ws_floats, hipStream_t s);
 // ws_floats floats (0: no split)
 struct GemmPlan {
     int nsplit = 1, ksteps = 0;
+    int bn = 64;   // output columns per tile: 64, or 128 when those tiles fill the CUs unsplit
     size_t partial_floats = 0;
 };
 GemmPlan gemm_plan(const GemmJob& j, size_t ws_floats);

@@ -10,7 +10,7 @@ where S bounds the magnitudes summed by either side:
     Q4_0, Q4_1, Q5_0, Q5_1, IQ4_NL:
            S = sum_blocks |dw dx isum| (+ |mw dx xsum|)   (integer block dots are exact)
     Q2_K, Q4_K, Q5_K:
-           S = sum_j (|d1 q_j| + |m1|) |x_j|   (kernel factors scale and min out of a group)
+           S = sum_j (|d1 q_j| + |m1|) |x_j|   (the Q4_K and Q5_K kernels factor scale and min out of a group)
     Q3_K:  S = sum_j |d s| (v_j + 4) |x_j|     (code v in 0..7, offset 4)
     Q6_K:  S = sum_j |d sc| (|q_j| + 32) |x_j| (kernel factors d sc, offset 32)
 and the oracle itself must satisfy the same bound.
@@ -154,9 +154,9 @@ def _check_gemv(ctx, torch, cpuref, qtype, rows, cols, seed=0, sample_rows=None)
     # widths that leave a short last chunk column: 4160 columns (64 + 64 + 2
     # blocks), 2304 (64 + 8), 6400 (3 x 64 + 8)
     (l3p.Q8_0, 100, 4160),
-    # Q8_0 short last columns of 8, 16 or 32 lane slots are copied packed,
-    # several rows' short chunks per copy: rows per group G = 8 and 16 with a
-    # ragged last group, 16 lane slots, one wave of 32, three waves + 8
+    # Q8_0 widths whose last chunk column holds 8, 16 or 32 lane slots: rows
+    # per group G = 8 and 16 with a ragged last group, 16 lane slots, one wave
+    # of 32, three waves + 8
     (l3p.Q8_0, 6150, 2304),
     (l3p.Q8_0, 12289, 2304),
     (l3p.Q8_0, 1001, 2560),
@@ -270,6 +270,11 @@ def _dequant_bound(cpuref, qtype, w, rows, cols):
     (l3p.F16, 130, 320, 5),
     (l3p.BF16, 257, 2048, 64),
     (l3p.F32, 100, 512, 70),
+    # jobs large enough for 64 x 128 tiles (eight waves): ragged N and M,
+    # the element-wise dequantizer path, rows that are not 16-byte multiples
+    (l3p.Q8_0, 8200, 512, 1000),
+    (l3p.Q4_K, 8192, 512, 1024),
+    (l3p.Q6_K, 8320, 256, 1000),
 ])
 def test_gemm_mfma_parity(ctx, torch_gpu, cpuref, qtype, rows, cols, batch):
     """MFMA GEMM against the float64 value of the reference's dequantize-then-

@@ -46,9 +46,10 @@ def test_gemm_static_rejects_oversized_partials(torch_gpu):
     torch = torch_gpu
     L = l3p.lib()
     with l3p.Context(0) as ctx:
-        # 255 x 4 output tiles split twice: 2 x 256 x 16320 floats of
-        # partials, more than the 4 Mi of the file-scope array
-        rows, cols, batch = 16320, 1024, 256
+        # 255 x 3 output tiles of 64 x 64 (too few 64 x 128 tiles to fill the
+        # CUs unsplit) split twice: 2 x 192 x 16320 floats of partials, more
+        # than the 4 Mi of the file-scope array
+        rows, cols, batch = 16320, 1024, 192
         w = torch.zeros(rows * synth.row_bytes(synth.Q8_0, cols), dtype=torch.uint8, device="cuda")
         x = torch.zeros(batch * cols, device="cuda")
         y = torch.zeros(batch * rows, device="cuda")
