@@ -13,26 +13,25 @@ __device__ __forceinline__ float h2f(uint32_t h) {
 }
 
 // fp16 -> fp32 exactly as the reference's table (c:547-582): NaN payloads are
-// kept without forcing the quiet bit.
+// kept without forcing the quiet bit.  A select, no branch.
 __device__ __forceinline__ float h2f_exact(uint32_t h) {
     h &= 0xffffu;
-    if (((h >> 10) & 31u) == 31u)
-        return __uint_as_float(((h & 0x8000u) << 16) | 0x7f800000u | ((h & 0x3ffu) << 13));
-    return h2f(h);
+    const float special = __uint_as_float(((h & 0x8000u) << 16) | 0x7f800000u | ((h & 0x3ffu) << 13));
+    return ((h >> 10) & 31u) == 31u ? special : h2f(h);
 }
 
-// Truncating fp32 -> fp16 (c:585-599).
+// Truncating fp32 -> fp16 (c:585-599), without branches: exponents e <= 0
+// give the subnormal (m | 0x400) >> (1 - e), which is 0 once the shift
+// passes the 11 bits (the reference's e < -10 case; the shift is capped at
+// 31), e >= 31 gives infinity, the rest e << 10 | m.
 __device__ __forceinline__ uint32_t f2h_trunc(float f) {
     const uint32_t b = __float_as_uint(f);
     const uint32_t sign = (b >> 16) & 0x8000u;
     const int e = (int)((b >> 23) & 0xffu) - 112;
     const uint32_t m = (b >> 13) & 0x3ffu;
-    if (e <= 0) {
-        if (e < -10) return sign;
-        return sign | ((m | 0x400u) >> (1 - e));
-    }
-    if (e >= 31) return sign | 0x7c00u;
-    return sign | ((uint32_t)e << 10) | m;
+    const uint32_t sub = (m | 0x400u) >> min(max(1 - e, 0), 31);
+    const uint32_t nrm = e >= 31 ? 0x7c00u : (((uint32_t)e << 10) | m);
+    return sign | (e <= 0 ? sub : nrm);
 }
 
 __device__ __forceinline__ uint32_t shr64(uint32_t lo, uint32_t hi, uint32_t sh) {

@@ -32,6 +32,49 @@ __device__ __forceinline__ int8_t quant_lane(float v, uint32_t& dh) {
     return (int8_t)qi;
 }
 
+// quant_lane on N values per lane at once (value k of lane l is element
+// l + 64 k of a row): the same arithmetic, with the N reductions and
+// divisions interleaved instead of run one after another.
+template <int N>
+__device__ __forceinline__ void quant_lanes(const float (&v)[N], int8_t (&q)[N], uint32_t (&dh)[N]) {
+    float a[N];
+#pragma unroll
+    for (int k = 0; k < N; ++k) a[k] = fabsf(v[k]);
+#pragma unroll
+    for (int k = 0; k < N; ++k) a[k] = fmaxf(a[k], lane_partner<16>(a[k]));
+#pragma unroll
+    for (int k = 0; k < N; ++k) a[k] = fmaxf(a[k], lane_partner<8>(a[k]));
+#pragma unroll
+    for (int k = 0; k < N; ++k) a[k] = fmaxf(a[k], lane_partner<4>(a[k]));
+#pragma unroll
+    for (int k = 0; k < N; ++k) a[k] = fmaxf(a[k], lane_partner<2>(a[k]));
+#pragma unroll
+    for (int k = 0; k < N; ++k) a[k] = fmaxf(a[k], lane_partner<1>(a[k]));
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+        const float d = a[k] / 127.0f;
+        const float id = d > 0.0f ? 127.0f / a[k] : 0.0f;
+        dh[k] = f2h_trunc(d);
+        int qi = (int)roundf(v[k] * id);
+        qi = qi > 127 ? 127 : (qi < -128 ? -128 : qi);
+        q[k] = (int8_t)qi;
+    }
+}
+
+// s_waitcnt vmcnt(n) for a wave-uniform n in [LO, HI], by binary search over
+// the immediate forms
+template <int LO, int HI>
+__device__ __forceinline__ void wait_vm_dyn(int n) {
+    if constexpr (LO == HI) {
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(LO) : "memory");
+    } else {
+        constexpr int MID = (LO + HI) / 2;
+        if (n <= MID) wait_vm_dyn<LO, MID>(n);
+        else wait_vm_dyn<MID + 1, HI>(n);
+    }
+}
+__device__ __forceinline__ void wait_vm_upto(int n) { wait_vm_dyn<0, 63>(n < 63 ? n : 63); }
+
 // Sum over the workgroup (any size that is a multiple of 64, <= 1024).
 __device__ float block_sum(float v, float* sh) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
@@ -131,7 +174,7 @@ struct AttnCArgs {
     const float *cos, *sin;          // RoPE tables [seq][hs/2]; the step's row is used
     uint8_t *kc, *vc;                // this layer's caches [n_kv][seq][hq8]
     const int* step;                 // device {token, pos}
-    float* part;                     // [n_heads][part_chunks][hs + 2]: chunk output, max, sum
+    float* part;                     // [n_heads][part_chunks][attn_part_row(hs)]: chunk output, max, sum
     int part_chunks;                 // chunk slots per head in part
     int tc;                          // positions per chunk (kTC or 32)
     float* out;                      // [n_heads][hs]
@@ -223,87 +266,97 @@ __global__ void __launch_bounds__(1024) attn_chunk_kernel(AttnCArgs a0) {
     extern __shared__ __align__(16) float smem[];
     const AttnCArgs a = token_args(a0, blockIdx.z);
     const int g = blockIdx.x, c = blockIdx.y;
-    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, nt = blockDim.x;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63, nt = blockDim.x;
     constexpr int hs = 32 * NB, half = hs / 2, hq8 = 34 * NB;
+    constexpr int NQ = (hs + 63) / 64;     // elements of a head row per lane
+    constexpr int NR = (half + 63) / 64;   // RoPE factors per lane
     constexpr int PER = NB <= 2 ? 1 : (NB <= 4 ? 2 : 4);   // V outputs per lane, inside one 32-block
     const int km = a.kv_mul;
     const int h = g * km + w;
 
-    // this step's q, k and v rows and the norm weights go to registers first:
-    // they do not depend on the step record, so they are issued before it
-    // arrives, and before the row copies below, so waiting for these loads
-    // never waits for the copies (hs <= 256)
-    float qv[4], kv2[8], cs[2], sn[2], qn[4], kn[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const int j = lane + 64 * k;
-        qv[k] = j < hs ? a.q[(size_t)h * hs + j] : 0.0f;
-        qn[k] = (a.q_norm && j < hs) ? a.q_norm[j] : 0.0f;
-        kn[k] = (a.k_norm && j < hs) ? a.k_norm[j] : 0.0f;
-    }
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {   // k then v over the workgroup (2*hs <= 8*64)
-        const int j = threadIdx.x + nt * k;
-        kv2[k] = j < 2 * hs ? (j < hs ? a.k[(size_t)g * hs + j] : a.v[(size_t)g * hs + j - hs]) : 0.0f;
-    }
-    const Span sp = span_of(a.step, a.window, a.tc);
-    if (c >= sp.n_chunks) return;   // the grid covers the longest context
-    const int jbeg = c * TC, jend = min(sp.na, jbeg + TC), cnt = jend - jbeg;
-    // the chunk holding the step's position forms and writes its K/V row,
-    // unless a prompt batch's kv_rows_kernel already wrote it
-    const bool has_pos = c == sp.n_chunks - 1 && !a.kv_ready;
-
     // LDS: [kv_mul][hs] q rows, [2][hs] k and v rows, [kv_mul][8][TC] V
-    // factors, [kv_mul][hs] int8 q, [kv_mul][8] q scales, then the chunk's K
-    // rows and V rows (chunk_rows_dw dwords each, 16-byte aligned)
+    // factors, [kv_mul][hs] int8 q, [kv_mul][8] q scales, [2][hs] q and k norm
+    // weights, [2][hs/2] RoPE cos and sin, then the chunk's K rows and V rows
+    // (chunk_rows_dw dwords each); every part starts 16-byte aligned
     float* qh = smem;
     float* kvh = qh + km * hs;
     float* f = kvh + 2 * hs;
     int8_t* qq = reinterpret_cast<int8_t*>(f + km * 8 * TC);
     float* qd = reinterpret_cast<float*>(qq + km * hs);
+    float* nrm = qd + km * 8;
+    float* rope = nrm + 2 * hs;
     const int rowdw = chunk_rows_dw(TC, hq8);
-    uint32_t* krows = reinterpret_cast<uint32_t*>(qd + km * 8);
+    uint32_t* krows = reinterpret_cast<uint32_t*>(rope + hs);
     uint32_t* vrows = krows + rowdw;
 
+    // this step's q, k and v rows and the norm weights, HBM -> LDS in 16-byte
+    // pieces: they do not depend on the step record, so they are issued before
+    // it arrives.  Wave w copies its query head's row, wave 0 the group's k
+    // and v rows and the norm weights.  Like the RoPE factors and the chunk's
+    // rows below they are LDS copies, all counted by vmcnt in issue order, so
+    // Q is prepared once all but the chunk's row copies have landed, while
+    // those stay in flight.
+    const bool row_lane = lane < hs / 4;
+    if (row_lane) {
+        piece16(reinterpret_cast<const uint8_t*>(a.q + (size_t)h * hs) + 16 * lane, reinterpret_cast<uint32_t*>(qh + w * hs));
+        if (w == 0) {
+            piece16(reinterpret_cast<const uint8_t*>(a.k + (size_t)g * hs) + 16 * lane, reinterpret_cast<uint32_t*>(kvh));
+            piece16(reinterpret_cast<const uint8_t*>(a.v + (size_t)g * hs) + 16 * lane,
+                    reinterpret_cast<uint32_t*>(kvh + hs));
+            if (a.q_norm) {
+                piece16(reinterpret_cast<const uint8_t*>(a.q_norm) + 16 * lane, reinterpret_cast<uint32_t*>(nrm));
+                piece16(reinterpret_cast<const uint8_t*>(a.k_norm) + 16 * lane, reinterpret_cast<uint32_t*>(nrm + hs));
+            }
+        }
+    }
+    const Span sp = span_of(a.step, a.window, a.tc);
+    if (c >= sp.n_chunks) {   // the grid covers the longest context
+        wait_vm_dyn<0, 0>(0);   // this workgroup's LDS copies land before it ends
+        return;
+    }
+    const int jbeg = c * TC, jend = min(sp.na, jbeg + TC), cnt = jend - jbeg;
+    // the chunk holding the step's position forms and writes its K/V row,
+    // unless a prompt batch's kv_rows_kernel already wrote it
+    const bool has_pos = c == sp.n_chunks - 1 && !a.kv_ready;
+
     // the RoPE factors of the step's position
-    const float* cosr = a.cos + (size_t)sp.pos * half;
-    const float* sinr = a.sin + (size_t)sp.pos * half;
-#pragma unroll
-    for (int k = 0; k < 2; ++k) {
-        const int p = lane + 64 * k;
-        cs[k] = p < half ? cosr[p] : 0.0f;
-        sn[k] = p < half ? sinr[p] : 0.0f;
+    if (w == 0 && lane < half / 4) {
+        piece16(reinterpret_cast<const uint8_t*>(a.cos + (size_t)sp.pos * half) + 16 * lane,
+                reinterpret_cast<uint32_t*>(rope));
+        piece16(reinterpret_cast<const uint8_t*>(a.sin + (size_t)sp.pos * half) + 16 * lane,
+                reinterpret_cast<uint32_t*>(rope + half));
     }
 
     // the chunk's K and V rows, HBM -> LDS in 16-byte pieces from the 16-byte
     // aligned address at or below the first row (the last piece ends inside
     // the 16-byte granule of the last row's last byte; the row at the step's
-    // position is replaced below)
+    // position is replaced below).  ncopy counts this wave's copy
+    // instructions (lane 0 takes part in every one, so none is skipped).
     const size_t start = (size_t)g * a.head_seq + (size_t)(sp.t0 + jbeg) * hq8;
     const size_t s16 = start & ~(size_t)15;
     const int np = (int)((start + (size_t)cnt * hq8 - s16 + 15) >> 4);
+    int ncopy = 0;
     {
         const uint8_t* ks = a.kc + s16;
         const uint8_t* vs = a.vc + s16;
         const int nw = nt >> 6;
         for (int i = w; i * 64 < np; i += nw) {
             if (i * 64 + lane < np) {
-                __builtin_amdgcn_global_load_lds(ks + 16 * (i * 64 + lane), (lds_void*)(krows + i * 256), 16, 0, 0);
-                __builtin_amdgcn_global_load_lds(vs + 16 * (i * 64 + lane), (lds_void*)(vrows + i * 256), 16, 0, 0);
+                piece16(ks + 16 * (i * 64 + lane), krows + i * 256);
+                piece16(vs + 16 * (i * 64 + lane), vrows + i * 256);
             }
+            ncopy += 2;
         }
     }
     const uint32_t roff = (uint32_t)(start - s16);   // byte offset of row 0 in krows / vrows
 
-    // QK-norm + RoPE + Q8_0 of the group's query heads (and of K, V at pos)
-#pragma unroll
-    for (int k = 0; k < 4; ++k)
-        if (lane + 64 * k < hs) qh[w * hs + lane + 64 * k] = qv[k];
-    if (has_pos)
-#pragma unroll
-        for (int k = 0; k < 8; ++k)
-            if (threadIdx.x + nt * k < 2 * hs) kvh[threadIdx.x + nt * k] = kv2[k];
-    __syncthreads();
+    // every wave's q, k, v, norm and RoPE copies have landed once at most its
+    // row copies are outstanding; the barrier makes the others' visible
+    wait_vm_upto(ncopy);
+    lds_sync();
+
+    // QK-norm + RoPE + Q8_0 of the group's query heads (and of K, V at pos);
+    // LDS-only barriers, so the row copies stay in flight
     if (a.q_norm) {   // per-head rmsnorm (c:3151-3165); every wave also forms K's factor
         float ssq = 0.0f, ssk = 0.0f;
         for (int j = lane; j < hs; j += 64) {
@@ -314,44 +367,49 @@ __global__ void __launch_bounds__(1024) attn_chunk_kernel(AttnCArgs a0) {
         ssk = wave_sum(ssk);
         const float rq = 1.0f / sqrtf(ssq * a.inv_hs + a.eps);
         const float rk = 1.0f / sqrtf(ssk * a.inv_hs + a.eps);
-        __syncthreads();
+        lds_sync();
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
+        for (int k = 0; k < NQ; ++k) {
             const int j = lane + 64 * k;
             if (j < hs) {
-                qh[w * hs + j] = qn[k] * (rq * qh[w * hs + j]);
-                if (has_pos && w == 0) kvh[j] = kn[k] * (rk * kvh[j]);
+                qh[w * hs + j] = nrm[j] * (rq * qh[w * hs + j]);
+                if (has_pos && w == 0) kvh[j] = nrm[hs + j] * (rk * kvh[j]);
             }
         }
-        __syncthreads();
+        lds_sync();
     }
 #pragma unroll
-    for (int k = 0; k < 2; ++k) {   // RoPE: NEOX (Gemma) or interleaved pairs
+    for (int k = 0; k < NR; ++k) {   // RoPE: NEOX (Gemma) or interleaved pairs
         const int p = lane + 64 * k;
         if (p < half) {
             const int i0 = a.neox ? p : 2 * p;
             const int i1 = a.neox ? p + half : 2 * p + 1;
+            const float cs = rope[p], sn = rope[half + p];
             const float v0 = qh[w * hs + i0], v1 = qh[w * hs + i1];
-            qh[w * hs + i0] = (v0 * cs[k] - v1 * sn[k]) * a.attn_scale;
-            qh[w * hs + i1] = (v0 * sn[k] + v1 * cs[k]) * a.attn_scale;
+            qh[w * hs + i0] = (v0 * cs - v1 * sn) * a.attn_scale;
+            qh[w * hs + i1] = (v0 * sn + v1 * cs) * a.attn_scale;
             if (has_pos && w == 0) {
                 const float k0 = kvh[i0], k1 = kvh[i1];
-                kvh[i0] = k0 * cs[k] - k1 * sn[k];
-                kvh[i1] = k0 * sn[k] + k1 * cs[k];
+                kvh[i0] = k0 * cs - k1 * sn;
+                kvh[i1] = k0 * sn + k1 * cs;
             }
         }
     }
-    __syncthreads();
-    // Q8_0 of the head's q, one value per lane (c:3311-3312)
+    lds_sync();
+    // Q8_0 of the head's q, one value per lane (c:3311-3312); all lanes take part
+    {
+        float v[NQ];
+        int8_t q8[NQ];
+        uint32_t dh[NQ];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const int j = lane + 64 * k;
-        if (k * 64 < hs) {
-            uint32_t dh;
-            const int8_t qv8 = quant_lane(j < hs ? qh[w * hs + j] : 0.0f, dh);   // all lanes take part
+        for (int k = 0; k < NQ; ++k) v[k] = lane + 64 * k < hs ? qh[w * hs + lane + 64 * k] : 0.0f;
+        quant_lanes<NQ>(v, q8, dh);
+#pragma unroll
+        for (int k = 0; k < NQ; ++k) {
+            const int j = lane + 64 * k;
             if (j < hs) {
-                qq[w * hs + j] = qv8;
-                if ((lane & 31) == 0) qd[w * 8 + (j >> 5)] = h2f_exact(dh);
+                qq[w * hs + j] = q8[k];
+                if ((lane & 31) == 0) qd[w * 8 + (j >> 5)] = h2f_exact(dh[k]);
             }
         }
     }
@@ -360,16 +418,22 @@ __global__ void __launch_bounds__(1024) attn_chunk_kernel(AttnCArgs a0) {
     // to the cache at the end of the kernel (c:3301-3308)
     const int kvsel = w == 0 ? 0 : (w == 1 ? 1 : -1);
     const bool kv_wave = has_pos && (kvsel >= 0 || km == 1);
-    uint32_t kvq[2][4], kvdh[2][4];
+    uint32_t kvq[2][NQ], kvdh[2][NQ];
     if (kv_wave) {
 #pragma unroll
         for (int sel = 0; sel < 2; ++sel) {
             if (km > 1 && sel != kvsel) continue;
+            float v[NQ];
+            int8_t q8[NQ];
+            uint32_t dh[NQ];
 #pragma unroll
-            for (int k = 0; k < 4; ++k)
-                if (k * 64 < hs)
-                    kvq[sel][k] = (uint8_t)quant_lane(lane + 64 * k < hs ? kvh[sel * hs + lane + 64 * k] : 0.0f,
-                                                      kvdh[sel][k]);
+            for (int k = 0; k < NQ; ++k) v[k] = lane + 64 * k < hs ? kvh[sel * hs + lane + 64 * k] : 0.0f;
+            quant_lanes<NQ>(v, q8, dh);
+#pragma unroll
+            for (int k = 0; k < NQ; ++k) {
+                kvq[sel][k] = (uint8_t)q8[k];
+                kvdh[sel][k] = dh[k];
+            }
         }
     }
     __builtin_amdgcn_s_waitcnt(0x0070);   // vmcnt(0) lgkmcnt(0): this wave's row copies have landed
@@ -380,7 +444,7 @@ __global__ void __launch_bounds__(1024) attn_chunk_kernel(AttnCArgs a0) {
             if (km > 1 && sel != kvsel) continue;
             uint8_t* rb = reinterpret_cast<uint8_t*>(sel ? vrows : krows) + roff + (size_t)(cnt - 1) * hq8;
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
+            for (int k = 0; k < NQ; ++k) {
                 const int j = lane + 64 * k;
                 if (j < hs) {
                     const int b = j >> 5;
@@ -457,7 +521,7 @@ __global__ void __launch_bounds__(1024) attn_chunk_kernel(AttnCArgs a0) {
             for (int e2 = 0; e2 < PER; ++e2) acc[e2] = fmaf((float)(int8_t)((q >> (8 * e2)) & 0xffu), fb[j], acc[e2]);
         }
     }
-    float* dst = a.part + ((size_t)h * a.part_chunks + c) * (hs + 2);
+    float* dst = a.part + ((size_t)h * a.part_chunks + c) * attn_part_row(hs);
     if (act)
 #pragma unroll
         for (int e2 = 0; e2 < PER; ++e2) dst[i0 + e2] = acc[e2];
@@ -471,7 +535,7 @@ __global__ void __launch_bounds__(1024) attn_chunk_kernel(AttnCArgs a0) {
             if (km > 1 && sel != kvsel) continue;
             uint8_t* cd = (sel ? a.vc : a.kc) + (size_t)g * a.head_seq + (size_t)sp.pos * hq8;
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
+            for (int k = 0; k < NQ; ++k) {
                 const int j = lane + 64 * k;
                 if (j < hs) {
                     const int b = j >> 5;
@@ -549,45 +613,89 @@ __global__ void __launch_bounds__(64) kv_rows_kernel(AttnCArgs a0) {
 // its output's chunk partials, and the weights expf(m_c - M) / S go through
 // LDS.  (Reading all chunk slots before the step record arrives was measured
 // slower: the extra loads cost more than the wait they save.)
-__global__ void __launch_bounds__(256) attn_merge_kernel(AttnCArgs a0) {
-    __shared__ float wc[64];
+// VPL consecutive floats at p (4, 2 or 1; p aligned to 4 * VPL bytes)
+template <int VPL>
+__device__ __forceinline__ void load_vec(const float* p, float (&v)[VPL]) {
+    if constexpr (VPL == 4) {
+        const float4 t = *reinterpret_cast<const float4*>(p);
+        v[0] = t.x;
+        v[1] = t.y;
+        v[2] = t.z;
+        v[3] = t.w;
+    } else if constexpr (VPL == 2) {
+        const float2 t = *reinterpret_cast<const float2*>(p);
+        v[0] = t.x;
+        v[1] = t.y;
+    } else {
+        v[0] = *p;
+    }
+}
+
+// K chunks' partials of the lane's outputs (pb: the first chunk's, PS floats
+// apart), loaded together with no branch (past the nb chunks of the batch
+// the last one is read again), then tot += partial * weight for the nb
+// chunks in order, chunk b0 + k's weight taken from lane b0 + k of wl.
+template <int K, int VPL, int PS>
+__device__ __forceinline__ void merge_batch(const float* pb, int nb, float wl, int b0, float (&tot)[VPL]) {
+    float pv[K][VPL];
+#pragma unroll
+    for (int k = 0; k < K; ++k) load_vec<VPL>(pb + (size_t)min(k, nb - 1) * PS, pv[k]);
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        if (k < nb) {
+            const float wk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wl), b0 + k));
+#pragma unroll
+            for (int e = 0; e < VPL; ++e) tot[e] += pv[k][e] * wk;
+        }
+    }
+}
+
+// One wave per head of hs = 32 NB: lane l owns outputs [VPL l, VPL l + VPL)
+// (VPL = 4, 2 or 1 for hs up to 256, 128, 64) and reads them from every
+// chunk's partial with one vector load, up to 32 chunks' loads issued
+// together.  Lane c < 64 first folds the statistics of chunks c, c + 64, ...
+// (running max and rescaled sum), then M and S are the wave's max and sum;
+// chunk c's weight expf(m_c - M) / S comes from its lane, and each output
+// sums its chunks' terms in chunk order.
+template <int NB>
+__global__ void __launch_bounds__(64) attn_merge_kernel(AttnCArgs a0) {
+    constexpr int hs = 32 * NB, ps = attn_part_row(hs);
+    constexpr int VPL = NB <= 2 ? 1 : (NB <= 4 ? 2 : 4);
     const AttnCArgs a = token_args(a0, blockIdx.y);
     const Span sp = span_of(a.step, a.window, a.tc);
-    const int h = blockIdx.x, hs = a.hs, nch = sp.n_chunks, t = threadIdx.x;
-    const int ps = hs + 2;
+    const int h = blockIdx.x, nch = sp.n_chunks, lane = threadIdx.x;
     const float* part = a.part + (size_t)h * a.part_chunks * ps;
+    // lanes past the row read the last outputs and drop them
+    const float* mine = part + min(VPL * lane, hs - VPL);
     float mx = -INFINITY, ssum = 0.0f, m0 = -INFINITY;
+    for (int c = lane; c < nch; c += 64) {
+        const float2 st = *reinterpret_cast<const float2*>(part + (size_t)c * ps + hs);
+        if (c == lane) m0 = st.x;
+        const float mn = fmaxf(mx, st.x);
+        ssum = ssum * expf(mx - mn) + st.y * expf(st.x - mn);
+        mx = mn;
+    }
+    const float M = wave_max(mx);
+    const float S = wave_sum(lane < nch ? ssum * expf(mx - M) : 0.0f);
+    float tot[VPL];
+#pragma unroll
+    for (int e = 0; e < VPL; ++e) tot[e] = 0.0f;
     for (int c0 = 0; c0 < nch; c0 += 64) {   // 64 chunks per round
         const int nc = min(64, nch - c0);
-        float pv[64];
-        const int i = t;   // this thread's output element (hs <= 256 = blockDim)
-#pragma unroll
-        for (int k = 0; k < 64; ++k) pv[k] = (k < nc && i < hs) ? part[(size_t)(c0 + k) * ps + i] : 0.0f;
-        if (t < 64) {
-            if (c0 == 0) {   // the statistics of every chunk, for M and S
-                for (int c = t; c < nch; c += 64) {
-                    const float mc = part[(size_t)c * ps + hs], lc = part[(size_t)c * ps + hs + 1];
-                    if (c == t) m0 = mc;
-                    const float mn = fmaxf(mx, mc);
-                    ssum = ssum * expf(mx - mn) + lc * expf(mc - mn);
-                    mx = mn;
-                }
-                const float M = wave_max(mx);
-                ssum = wave_sum(t < nch ? ssum * expf(mx - M) : 0.0f);
-                mx = M;
-            }
-            const float mc = c0 == 0 ? m0 : (t < nc ? part[(size_t)(c0 + t) * ps + hs] : -INFINITY);
-            if (t < nc) wc[t] = expf(mc - mx) * (1.0f / ssum);
+        const float mc = c0 == 0 ? m0 : (lane < nc ? part[(size_t)(c0 + lane) * ps + hs] : -INFINITY);
+        const float wl = lane < nc ? expf(mc - M) * (1.0f / S) : 0.0f;
+        for (int b0 = 0; b0 < nc; b0 += 32) {
+            const float* pb = mine + (size_t)(c0 + b0) * ps;
+            const int nb = min(32, nc - b0);
+            if (nb <= 8) merge_batch<8, VPL, ps>(pb, nb, wl, b0, tot);
+            else if (nb <= 16) merge_batch<16, VPL, ps>(pb, nb, wl, b0, tot);
+            else if (nb <= 24) merge_batch<24, VPL, ps>(pb, nb, wl, b0, tot);
+            else merge_batch<32, VPL, ps>(pb, nb, wl, b0, tot);
         }
-        __syncthreads();
-        if (i < hs) {
-            float tot = c0 == 0 ? 0.0f : a.out[(size_t)h * hs + i];
+    }
+    if (VPL * lane < hs) {
 #pragma unroll
-            for (int k = 0; k < 64; ++k)
-                if (k < nc) tot += pv[k] * wc[k];
-            a.out[(size_t)h * hs + i] = tot;
-        }
-        __syncthreads();
+        for (int e = 0; e < VPL; ++e) a.out[(size_t)h * hs + VPL * lane + e] = tot[e];
     }
 }
 
@@ -1585,7 +1693,8 @@ static void launch_chunks(const Model& m, const AttnCArgs& a, int chunks, int to
     const int tc = a.tc;
     const int rowdw = chunk_rows_dw(tc, m.hq8);
     const size_t lds = (size_t)m.kv_mul * m.hs * 4 + 2 * (size_t)m.hs * 4 + (size_t)m.kv_mul * 8 * tc * 4 +
-                       (size_t)m.kv_mul * m.hs + (size_t)m.kv_mul * 8 * 4 + 2 * (size_t)rowdw * 4 + 16;
+                       (size_t)m.kv_mul * m.hs + (size_t)m.kv_mul * 8 * 4 + 3 * (size_t)m.hs * 4 +
+                       2 * (size_t)rowdw * 4 + 16;
     const dim3 grid(m.n_kv, chunks, tokens), block(64 * m.kv_mul);
     L3P_REQUIRE(tc == kTC || (tc == 32 && m.hs >= 192), L3P_E_INVALID, "attention: chunk of %d positions", tc);
     switch (m.hs / 32) {
@@ -1607,7 +1716,17 @@ static void launch_chunks(const Model& m, const AttnCArgs& a, int chunks, int to
         else launch_chunk_kernel<8, kTC>(grid, block, lds, a, s);
         break;
     }
-    hipLaunchKernelGGL(attn_merge_kernel, dim3(m.n_heads, tokens), dim3((m.hs + 63) / 64 * 64), 0, s, a);
+    const dim3 mgrid(m.n_heads, tokens);
+    switch (m.hs / 32) {
+    case 1: hipLaunchKernelGGL(attn_merge_kernel<1>, mgrid, dim3(64), 0, s, a); break;
+    case 2: hipLaunchKernelGGL(attn_merge_kernel<2>, mgrid, dim3(64), 0, s, a); break;
+    case 3: hipLaunchKernelGGL(attn_merge_kernel<3>, mgrid, dim3(64), 0, s, a); break;
+    case 4: hipLaunchKernelGGL(attn_merge_kernel<4>, mgrid, dim3(64), 0, s, a); break;
+    case 5: hipLaunchKernelGGL(attn_merge_kernel<5>, mgrid, dim3(64), 0, s, a); break;
+    case 6: hipLaunchKernelGGL(attn_merge_kernel<6>, mgrid, dim3(64), 0, s, a); break;
+    case 7: hipLaunchKernelGGL(attn_merge_kernel<7>, mgrid, dim3(64), 0, s, a); break;
+    default: hipLaunchKernelGGL(attn_merge_kernel<8>, mgrid, dim3(64), 0, s, a); break;
+    }
     L3P_HIP(hipGetLastError());
 }
 
@@ -1691,7 +1810,7 @@ void launch_attention_rows(const Model& m, int l, const AttnIO& io, int q_stride
     a.kv_ready = 1;
     a.part = part;
     a.part_chunks = chunks;
-    a.part_stride = (size_t)m.n_heads * chunks * (m.hs + 2);
+    a.part_stride = (size_t)m.n_heads * chunks * attn_part_row(m.hs);
     L3P_REQUIRE(a.part_stride * tokens <= part_cap, L3P_E_INVALID, "attention: %d tokens exceed the partials buffer",
                 tokens);
     hipLaunchKernelGGL(kv_rows_kernel, dim3(m.n_kv, tokens), dim3(64), 0, s, a);

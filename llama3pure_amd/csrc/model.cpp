@@ -414,7 +414,7 @@ static Model* load_model(l3p_ctx* c, const void* bytes, size_t len, const l3p_lo
     // shorter chunks run in parallel)
     m.dec_tc = m.hs >= 192 ? 32 : 64;
     m.max_chunks = (m.seq_len + m.dec_tc - 1) / m.dec_tc;
-    m.part_acc = (float*)m.dalloc((size_t)m.n_heads * m.max_chunks * (m.hs + 2) * 4);
+    m.part_acc = (float*)m.dalloc((size_t)m.n_heads * m.max_chunks * attn_part_row(m.hs) * 4);
     m.step = (int*)m.dalloc(4 * sizeof(int));
     const int ncand = std::max(256, sample_groups(m.vocab)) + sample_max_k();
     m.cand_val = (float*)m.dalloc((size_t)ncand * 4);
@@ -690,7 +690,7 @@ static void ensure_prefill_rows(Model& m) {
     m.pf_tok = (int*)m.dalloc((size_t)R * 4);
     m.pf_steps = (int*)m.dalloc((size_t)R * 8);
     // partials for up to R tokens at the longest context, within 512 MB
-    const size_t per_token = (size_t)m.n_heads * m.max_chunks * (m.hs + 2);
+    const size_t per_token = (size_t)m.n_heads * m.max_chunks * attn_part_row(m.hs);
     m.pf_part_cap = std::max(per_token, std::min(per_token * R, (size_t)128 << 20));
     m.pf_part = (float*)m.dalloc(m.pf_part_cap * 4);
     m.pf_rows = R;
@@ -781,7 +781,7 @@ static void prefill_batched(l3p_ctx* c, const int32_t* tokens, int n, int start)
                       R, false, "q|k|v");
             // attention of the rows, as many tokens per launch as the partials hold
             const size_t per_token =
-                (size_t)m.n_heads * attention_chunks(m, l, start + b0 + R - 1) * (m.hs + 2);
+                (size_t)m.n_heads * attention_chunks(m, l, start + b0 + R - 1) * attn_part_row(m.hs);
             const int T = (int)std::max<size_t>(1, std::min<size_t>(R, m.pf_part_cap / per_token));
             for (int z0 = 0; z0 < R; z0 += T) {
                 const int nz = std::min(T, R - z0);

@@ -3,6 +3,10 @@
 
 #include "internal.h"
 
+// Floats per attention chunk partial: the chunk's hs outputs, its softmax
+// max and sum, padded so that every partial starts 16-byte aligned.
+constexpr int attn_part_row(int hs) { return hs + 4; }
+
 // One weight matrix in HBM, native GGUF block layout (QuantizedTensor, c:238-249).
 struct Mat {
     const uint8_t* w = nullptr;
@@ -38,7 +42,7 @@ struct Model {
     // run state (RunState, c:281-343), device resident
     float *x = nullptr, *x2 = nullptr, *xb = nullptr, *xb2 = nullptr, *q = nullptr, *k = nullptr, *v = nullptr;
     float *hb = nullptr, *hb2 = nullptr, *logits = nullptr;
-    float* part_acc = nullptr;     // [n_heads][max_chunks][hs + 2] attention chunk partials
+    float* part_acc = nullptr;     // [n_heads][max_chunks][attn_part_row(hs)] attention chunk partials
     int* step = nullptr;           // device {token, pos} of the step being computed
     // prompt-batch rows (transformer_prefill's batch_* arrays, c:326-343),
     // allocated at the first batched prefill for pf_rows tokens
