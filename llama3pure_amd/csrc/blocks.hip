@@ -35,10 +35,12 @@ __global__ void dequant_kernel(int type, const uint8_t* __restrict__ s, int64_t 
 
 // Embedding row (c:3204-3207), times a scale when non-zero (Gemma's sqrt(dim),
 // which the reference applies to x in place before the first norm,
-// c:3132-3140; x*scale rounds the same), and the step record {token, pos}
-// that the kernels of the step read.
+// c:3132-3140; x*scale rounds the same), the step record {token, pos} that
+// the kernels of the step read, and the RoPE table rows of pos (when
+// rope.rope_cur is set), so that attention need not wait for the record to
+// find them.
 __global__ void embed_step_kernel(int type, const uint8_t* __restrict__ s, int n, float scale, float* __restrict__ y,
-                                  int token, int pos, int* step) {
+                                  int token, int pos, int* step, RopeRows rope) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) {
         const float v = deq_elem(type, s, i);
@@ -47,6 +49,10 @@ __global__ void embed_step_kernel(int type, const uint8_t* __restrict__ s, int n
     if (i == 0) {
         step[0] = token;
         step[1] = pos;
+    }
+    if (rope.rope_cur && i < 4 * rope.half) {
+        const int t = i / rope.half, j = i - t * rope.half;
+        rope.rope_cur[i] = rope.tables[t][(size_t)pos * rope.half + j];
     }
 }
 
@@ -100,8 +106,11 @@ void launch_dequant(int type, const uint8_t* src, int64_t n, float* dst, hipStre
 }
 
 void launch_embed_row(int type, const uint8_t* row, int n, float scale, float* dst, int token, int pos, int* step,
-                      hipStream_t st) {
-    hipLaunchKernelGGL(embed_step_kernel, dim3((n + 255) / 256), dim3(256), 0, st, type, row, n, scale, dst, token,
-                       pos, step);
+                      const RopeRows* rope, hipStream_t st) {
+    RopeRows r{};
+    if (rope) r = *rope;
+    const int threads = std::max(n, r.rope_cur ? 4 * r.half : 0);
+    hipLaunchKernelGGL(embed_step_kernel, dim3((threads + 255) / 256), dim3(256), 0, st, type, row, n, scale, dst,
+                       token, pos, step, r);
     L3P_HIP(hipGetLastError());
 }

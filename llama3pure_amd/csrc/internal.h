@@ -180,5 +180,12 @@ void launch_dequant(int type, const uint8_t* src, int64_t n, float* dst, hipStre
 // a plain streaming read of bytes (a multiple of 16) from 16-byte aligned p;
 // out: 256 words of device scratch
 void launch_stream_read(const void* p, size_t bytes, uint32_t* out, hipStream_t s);
+// rope (may be null): copies the four RoPE table rows of pos (tables[t] +
+// pos * half, t = 0..3) into rope_cur[t * half ..]
+struct RopeRows {
+    const float* tables[4];
+    int half;
+    float* rope_cur;
+};
 void launch_embed_row(int type, const uint8_t* row, int n, float scale, float* dst, int token, int pos, int* step,
-                      hipStream_t s);
+                      const RopeRows* rope, hipStream_t s);

@@ -172,6 +172,7 @@ struct AttnCArgs {
     const float *q, *k, *v;          // this step's projections [heads][hs]
     const float *q_norm, *k_norm;    // Gemma QK-norm weights (null otherwise)
     const float *cos, *sin;          // RoPE tables [seq][hs/2]; the step's row is used
+    const float* rope;               // decode steps: the step's cos row then sin row (null: read the tables)
     uint8_t *kc, *vc;                // this layer's caches [n_kv][seq][hq8]
     const int* step;                 // device {token, pos}
     float* part;                     // [n_heads][part_chunks][attn_part_row(hs)]: chunk output, max, sum
@@ -210,14 +211,15 @@ __device__ __forceinline__ AttnCArgs token_args(const AttnCArgs& a0, int z) {
 struct Span {
     int pos, t0, na, n_chunks;
 };
-__device__ __forceinline__ Span span_of(const int* step, int window, int tc) {
+__device__ __forceinline__ Span span_at(int pos, int window, int tc) {
     Span s;
-    s.pos = step[1];
+    s.pos = pos;
     s.t0 = window > 0 ? max(0, s.pos - window + 1) : 0;
     s.na = s.pos - s.t0 + 1;
     s.n_chunks = (s.na + tc - 1) / tc;
     return s;
 }
+__device__ __forceinline__ Span span_of(const int* step, int window, int tc) { return span_at(step[1], window, tc); }
 
 // Q8_0 block `b` of a cache row starting at byte offset `off` of a dword
 // array (LDS here): fp16 scale and the 32 quants as eight dwords.
@@ -289,13 +291,11 @@ __global__ void __launch_bounds__(1024) attn_chunk_kernel(AttnCArgs a0) {
     uint32_t* krows = reinterpret_cast<uint32_t*>(rope + hs);
     uint32_t* vrows = krows + rowdw;
 
-    // this step's q, k and v rows and the norm weights, HBM -> LDS in 16-byte
-    // pieces: they do not depend on the step record, so they are issued before
-    // it arrives.  Wave w copies its query head's row, wave 0 the group's k
-    // and v rows and the norm weights.  Like the RoPE factors and the chunk's
-    // rows below they are LDS copies, all counted by vmcnt in issue order, so
-    // Q is prepared once all but the chunk's row copies have landed, while
-    // those stay in flight.
+    // this step's q, k and v rows, the norm weights and, for a decode step,
+    // the RoPE factors of its position, HBM -> LDS in 16-byte pieces, and the
+    // step record: none depends on another, so one wait covers them all.
+    // Wave w copies its query head's row, wave 0 the group's k and v rows,
+    // the norm weights and the RoPE factors.
     const bool row_lane = lane < hs / 4;
     if (row_lane) {
         piece16(reinterpret_cast<const uint8_t*>(a.q + (size_t)h * hs) + 16 * lane, reinterpret_cast<uint32_t*>(qh + w * hs));
@@ -309,18 +309,23 @@ __global__ void __launch_bounds__(1024) attn_chunk_kernel(AttnCArgs a0) {
             }
         }
     }
-    const Span sp = span_of(a.step, a.window, a.tc);
-    if (c >= sp.n_chunks) {   // the grid covers the longest context
-        wait_vm_dyn<0, 0>(0);   // this workgroup's LDS copies land before it ends
-        return;
+    const bool rope_lane = w == 0 && lane < half / 4;
+    if (a.rope && rope_lane) {
+        piece16(reinterpret_cast<const uint8_t*>(a.rope) + 16 * lane, reinterpret_cast<uint32_t*>(rope));
+        piece16(reinterpret_cast<const uint8_t*>(a.rope + half) + 16 * lane, reinterpret_cast<uint32_t*>(rope + half));
     }
+    const int pos = *reinterpret_cast<const volatile int*>(a.step + 1);   // issued here, before the wait
+    wait_vm_dyn<0, 0>(0);
+    lds_sync();
+    const Span sp = span_at(pos, a.window, a.tc);
+    if (c >= sp.n_chunks) return;   // the grid covers the longest context
     const int jbeg = c * TC, jend = min(sp.na, jbeg + TC), cnt = jend - jbeg;
     // the chunk holding the step's position forms and writes its K/V row,
     // unless a prompt batch's kv_rows_kernel already wrote it
     const bool has_pos = c == sp.n_chunks - 1 && !a.kv_ready;
 
-    // the RoPE factors of the step's position
-    if (w == 0 && lane < half / 4) {
+    // prompt batches: the RoPE factors of the token's position
+    if (!a.rope && rope_lane) {
         piece16(reinterpret_cast<const uint8_t*>(a.cos + (size_t)sp.pos * half) + 16 * lane,
                 reinterpret_cast<uint32_t*>(rope));
         piece16(reinterpret_cast<const uint8_t*>(a.sin + (size_t)sp.pos * half) + 16 * lane,
@@ -330,8 +335,9 @@ __global__ void __launch_bounds__(1024) attn_chunk_kernel(AttnCArgs a0) {
     // the chunk's K and V rows, HBM -> LDS in 16-byte pieces from the 16-byte
     // aligned address at or below the first row (the last piece ends inside
     // the 16-byte granule of the last row's last byte; the row at the step's
-    // position is replaced below).  ncopy counts this wave's copy
-    // instructions (lane 0 takes part in every one, so none is skipped).
+    // position is replaced below); they stay in flight while Q is prepared.
+    // ncopy counts this wave's copy instructions (lane 0 takes part in every
+    // one, so none is skipped).
     const size_t start = (size_t)g * a.head_seq + (size_t)(sp.t0 + jbeg) * hq8;
     const size_t s16 = start & ~(size_t)15;
     const int np = (int)((start + (size_t)cnt * hq8 - s16 + 15) >> 4);
@@ -349,11 +355,10 @@ __global__ void __launch_bounds__(1024) attn_chunk_kernel(AttnCArgs a0) {
         }
     }
     const uint32_t roff = (uint32_t)(start - s16);   // byte offset of row 0 in krows / vrows
-
-    // every wave's q, k, v, norm and RoPE copies have landed once at most its
-    // row copies are outstanding; the barrier makes the others' visible
-    wait_vm_upto(ncopy);
-    lds_sync();
+    if (!a.rope) {   // the RoPE factors have landed once at most the row copies are outstanding
+        wait_vm_upto(ncopy);
+        lds_sync();
+    }
 
     // QK-norm + RoPE + Q8_0 of the group's query heads (and of K, V at pos);
     // LDS-only barriers, so the row copies stay in flight
@@ -460,37 +465,79 @@ __global__ void __launch_bounds__(1024) attn_chunk_kernel(AttnCArgs a0) {
     __syncthreads();
 
     // scores of head h: lane = position (all of a row's blocks read first)
+    const int* qw = reinterpret_cast<const int*>(qq + w * hs);
+    const uint8_t* vbytes = reinterpret_cast<const uint8_t*>(vrows) + roff;
+    float* fw = f + (size_t)w * 8 * TC;
+    constexpr bool kSplit = TC == 32 && NB % 2 == 0;   // two lanes per position
     float sc = -INFINITY;
-    if (lane < cnt) {
-        const int* qw = reinterpret_cast<const int*>(qq + w * hs);
-        uint32_t kq[NB][8];
-        float db[NB];
+    if constexpr (kSplit) {
+        // lane p sums the first NB/2 block terms of position p, lane p + 32
+        // continues that sum over the rest: the reference's order, bit-exact
+        constexpr int HB = NB / 2;
+        const int pl = lane & 31, hb = (lane >> 5) * HB;
+        float t[HB];
+        if (pl < cnt) {
+            uint32_t kq[HB][8];
+            float db[HB];
 #pragma unroll
-        for (int b = 0; b < NB; ++b) db[b] = row_block(krows, roff + (uint32_t)lane * hq8 + 34u * b, kq[b]);
-        float sum = 0.0f;
+            for (int i = 0; i < HB; ++i) db[i] = row_block(krows, roff + (uint32_t)pl * hq8 + 34u * (hb + i), kq[i]);
 #pragma unroll
-        for (int b = 0; b < NB; ++b) {
-            int isum = 0;
+            for (int i = 0; i < HB; ++i) {
+                int isum = 0;
 #pragma unroll
-            for (int k = 0; k < 8; ++k) isum = __builtin_amdgcn_sdot4(qw[8 * b + k], (int)kq[b][k], isum, false);
-            sum += qd[w * 8 + b] * db[b] * (float)isum;
+                for (int k = 0; k < 8; ++k) isum = __builtin_amdgcn_sdot4(qw[8 * (hb + i) + k], (int)kq[i][k], isum, false);
+                t[i] = qd[w * 8 + hb + i] * db[i] * (float)isum;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < HB; ++i) t[i] = 0.0f;
         }
-        sc = cap_score(sum, a.softcap);
+        float lo = 0.0f;
+#pragma unroll
+        for (int i = 0; i < HB; ++i) lo += t[i];
+        float sum = lane_partner<32>(lo);   // upper lanes: the lower half's sum of the same position
+#pragma unroll
+        for (int i = 0; i < HB; ++i) sum += t[i];
+        const float up = lane_partner<32>(pl < cnt ? cap_score(sum, a.softcap) : -INFINITY);
+        if (lane < 32) sc = up;
+    } else {
+        if (lane < cnt) {
+            uint32_t kq[NB][8];
+            float db[NB];
+#pragma unroll
+            for (int b = 0; b < NB; ++b) db[b] = row_block(krows, roff + (uint32_t)lane * hq8 + 34u * b, kq[b]);
+            float sum = 0.0f;
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                int isum = 0;
+#pragma unroll
+                for (int k = 0; k < 8; ++k) isum = __builtin_amdgcn_sdot4(qw[8 * b + k], (int)kq[b][k], isum, false);
+                sum += qd[w * 8 + b] * db[b] * (float)isum;
+            }
+            sc = cap_score(sum, a.softcap);
+        }
     }
     const float m = wave_max(sc);
     const float e = lane < cnt ? expf(sc - m) : 0.0f;
     const float l = wave_sum(e);
 
-    // f[b][j] = d(V row j, block b) * e_j, 0 for skipped positions
-    const uint8_t* vbytes = reinterpret_cast<const uint8_t*>(vrows) + roff;
-    float* fw = f + (size_t)w * 8 * TC;
-    if (lane < cnt) {
-        const bool skip = e < 1e-8f;
-        uint32_t dv[NB];
+    // f[b][j] = d(V row j, block b) * e_j, 0 for skipped positions (two
+    // lanes per position, as for the scores, when they split them)
+    {
+        constexpr int FB = kSplit ? NB / 2 : NB;
+        const int pl = kSplit ? (lane & 31) : lane;
+        const int fb0 = kSplit ? (lane >> 5) * FB : 0;
+        const float ep = kSplit ? lane_partner<32>(e) : e;   // upper lanes: their position's e
+        const float ej = (kSplit && lane >= 32) ? ep : e;
+        if (pl < cnt) {
+            const bool skip = ej < 1e-8f;
+            uint32_t dv[FB];
 #pragma unroll
-        for (int bb = 0; bb < NB; ++bb) dv[bb] = *reinterpret_cast<const uint16_t*>(vbytes + (size_t)lane * hq8 + 34 * bb);
+            for (int i = 0; i < FB; ++i)
+                dv[i] = *reinterpret_cast<const uint16_t*>(vbytes + (size_t)pl * hq8 + 34 * (fb0 + i));
 #pragma unroll
-        for (int bb = 0; bb < NB; ++bb) fw[bb * TC + lane] = skip ? 0.0f : h2f(dv[bb]) * e;
+            for (int i = 0; i < FB; ++i) fw[(fb0 + i) * TC + pl] = skip ? 0.0f : h2f(dv[i]) * ej;
+        }
     }
     __syncthreads();
     // V: acc_i += q_ji * f_j over the chunk's rows, eight rows' loads at a time
@@ -1596,8 +1643,10 @@ __global__ void __launch_bounds__(1024) topk_scan_kernel(const float* __restrict
 // ---------------------------------------------------------------------------
 // launchers
 // ---------------------------------------------------------------------------
-void launch_embed_step(const Mat& emb, int token, int pos, float scale, float* x, int* step, hipStream_t s) {
-    launch_embed_row(emb.type, emb.w + (size_t)token * emb.rb, emb.cols, scale, x, token, pos, step, s);
+void launch_embed_step(const Model& m, int token, int pos, hipStream_t s) {
+    const RopeRows rope{{m.cos_d, m.sin_d, m.cos_s, m.sin_s}, m.hs / 2, m.rope_cur};
+    launch_embed_row(m.emb.type, m.emb.w + (size_t)token * m.emb.rb, m.emb.cols, m.is_gemma ? m.embed_scale : 0.0f,
+                     m.x, token, pos, m.step, &rope, s);
 }
 
 void launch_rmsnorm_add_rows(const float* y, int ldy, const float* w, int n, float inv_n, float eps, float* x,
@@ -1655,6 +1704,7 @@ static AttnCArgs attn_args(const Model& m, int l, const AttnIO& io) {
     a.k_norm = m.is_gemma ? L.k_norm : nullptr;
     a.cos = use_swa ? m.cos_s : m.cos_d;
     a.sin = use_swa ? m.sin_s : m.sin_d;
+    a.rope = m.rope_cur + (use_swa ? m.hs : 0);   // decode steps; prompt batches read the tables
     a.kc = m.kc + (size_t)l * m.layer_kv;
     a.vc = m.vc + (size_t)l * m.layer_kv;
     a.step = io.step;
@@ -1808,6 +1858,7 @@ void launch_attention_rows(const Model& m, int l, const AttnIO& io, int q_stride
     a.kv_stride = kv_stride;
     a.out_stride = out_stride;
     a.kv_ready = 1;
+    a.rope = nullptr;   // each token's RoPE rows come from the tables at its position
     a.part = part;
     a.part_chunks = chunks;
     a.part_stride = (size_t)m.n_heads * chunks * attn_part_row(m.hs);

@@ -396,6 +396,7 @@ static Model* load_model(l3p_ctx* c, const void* bytes, size_t len, const l3p_lo
             m.cos_s = m.cos_d;
             m.sin_s = m.sin_d;
         }
+        m.rope_cur = (float*)m.dalloc((size_t)2 * m.hs * 4);
     }
 
     // run state
@@ -843,7 +844,7 @@ static bool graphs_enabled() {
 static void forward_impl(l3p_ctx* c, int token, int pos, bool with_logits) {
     Model& m = *c->model;
     hipStream_t s = c->stream;
-    launch_embed_step(m.emb, token, pos, m.is_gemma ? m.embed_scale : 0.0f, m.x, m.step, s);
+    launch_embed_step(m, token, pos, s);
     c->attn_per_head = attention_per_head(m, pos);
     const int v = (with_logits ? 1 : 0) | (c->attn_per_head ? 2 : 0);
     if (c->prof.on || !graphs_enabled() || c->graph_runs[v]++ == 0) {

@@ -38,6 +38,7 @@ struct Model {
     std::vector<Layer> layers;
     uint8_t *kc = nullptr, *vc = nullptr;
     float *cos_d = nullptr, *sin_d = nullptr, *cos_s = nullptr, *sin_s = nullptr;
+    float* rope_cur = nullptr;     // [cos_d, sin_d, cos_s, sin_s][hs/2]: rows of the decode step's position
 
     // run state (RunState, c:281-343), device resident
     float *x = nullptr, *x2 = nullptr, *xb = nullptr, *xb2 = nullptr, *q = nullptr, *k = nullptr, *v = nullptr;
@@ -127,9 +128,9 @@ struct l3p_ctx {
 void gemv_plain(l3p_ctx* c, int type, const GemvBatch& b, int cols, const float* x);
 
 // layers.hip
-// x = embedding row of `token` (times `scale` when non-zero) and the device
-// step record {token, pos} that the layer kernels read.
-void launch_embed_step(const Mat& emb, int token, int pos, float scale, float* x, int* step, hipStream_t s);
+// m.x = embedding row of `token` (times Gemma's scale), the device step record
+// {token, pos} that the layer kernels read and the RoPE rows of pos (m.rope_cur).
+void launch_embed_step(const Model& m, int token, int pos, hipStream_t s);
 // QK-norm, RoPE, the K/V cache write and attention of one layer for the
 // step's position (c:3232-3359); out = [n_heads][head_dim].  The first form
 // reads the decode step's q, k, v and step record.
