@@ -1086,7 +1086,6 @@ __global__ void __launch_bounds__(1024) attn_prefill_kernel(AttnCArgs a0, int nt
 // blockIdx.x = head-in-group * n_kv + group: with n_kv a multiple of 8 the
 // heads of a group run on one XCD and share its L2.
 // ---------------------------------------------------------------------------
-constexpr int kHeadAutoPositions = 512;           // default: longer contexts use attn_chunk_kernel
 constexpr int kHW = 16;                           // waves per workgroup
 constexpr int kHCopies = 4;                       // dwordx4 copy instructions per slot
 constexpr int kHSlot = kHCopies * 1024;           // bytes per K or V slot
@@ -1682,13 +1681,19 @@ void launch_attention(const Model& m, int l, float* out, bool per_head, hipStrea
 }
 
 // L3P_ATTN_HEAD=1 / 0 forces one attention or the other; by default the
-// per-head kernel takes steps attending to fewer than kHeadAutoPositions
-// positions (at Llama-3-8B shapes on MI355X it is faster there: 6.5 us
-// against 11.1 us for chunks + merge at 64 positions, even at ~600).
-bool attention_per_head(const Model&, int pos) {
+// per-head kernel takes steps attending to fewer positions than
+// attention_head_limit, where it is the faster of the two on MI355X (its
+// time grows with the positions one CU streams, chunks + merge stay near
+// 9-11 us): about 450 positions at head_dim 128 (Llama-3-8B's 32/8 heads:
+// 7.5 against 9.0 us at 257, 10.1 against 9.6 us at 513) and 190 at
+// head_dim 256 (Gemma-2-2B's 8/4 heads: 7.9 against 10.2 us at 65, 11.8
+// against 10.4 us at 257).
+int attention_head_limit(const Model& m) { return m.hs >= 192 ? 192 : 448; }
+
+bool attention_per_head(const Model& m, int pos) {
     const char* e = getenv("L3P_ATTN_HEAD");
     if (e && *e) return atoi(e) != 0;
-    return pos < kHeadAutoPositions;
+    return pos < attention_head_limit(m);
 }
 
 // The attention arguments of layer l for the token whose rows io holds.

@@ -142,6 +142,8 @@ struct AttnIO {
 // per_head: one workgroup per query head (attention_per_head(m, pos) says
 // whether the step at pos may take it); else split-position chunks + merge.
 bool attention_per_head(const Model& m, int pos);
+// positions below which attention_per_head picks the per-head kernel
+int attention_head_limit(const Model& m);
 void launch_attention(const Model& m, int layer, float* out, bool per_head, hipStream_t s);
 void launch_attention(const Model& m, int layer, const AttnIO& io, bool per_head, hipStream_t s);
 // Attention of `tokens` consecutive prompt tokens of a batch in three

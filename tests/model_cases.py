@@ -129,10 +129,10 @@ SINGLE_DRIFT = _load_drift("single_layer")
 # Long contexts against the oracle (tests/test_gpu_long_context.py): a prompt
 # of `prompt` tokens through the batched prompt path (1024-row passes,
 # attn_prefill_kernel), then teacher-forced decode steps whose attention spans
-# the whole prompt (chunks + merge by default from 512 positions; the
-# per-head kernel forced for the later steps).  Small widths keep the oracle
-# fast; the head shapes, GQA groups and windows are the ones the kernels
-# specialise on.
+# the whole prompt (chunks + merge by default from 448 positions, from 192
+# at head_dim >= 192; the per-head kernel forced for the later steps).  Small
+# widths keep the oracle fast; the head shapes, GQA groups and windows are the
+# ones the kernels specialise on.
 LONG_CASES = {
     # head_dim 64, GQA 2, three prompt passes (2100 rows)
     "llama_hs64_2100": dict(model=dict(arch="llama", dim=256, hidden=512, n_layers=2, n_heads=4, n_kv=2, vocab=512,

@@ -349,9 +349,9 @@ def test_prompt_attention_paths_agree(torch_gpu, monkeypatch, case):
 @pytest.mark.parametrize("case", list(PATH_CASES))
 def test_attention_paths_agree(torch_gpu, monkeypatch, case):
     """The two decode attentions give the same steps: one workgroup per query
-    head (L3P_ATTN_HEAD=1; by default for steps attending to fewer than 512
-    positions) and split position chunks with a merge kernel
-    (L3P_ATTN_HEAD=0; by default from 512 positions on).  Both form the
+    head (L3P_ATTN_HEAD=1; by default for steps attending to fewer than 448
+    positions, 192 at head_dim >= 192) and split position chunks with a merge
+    kernel (L3P_ATTN_HEAD=0; by default from there on).  Both form the
     step's K/V rows with the same arithmetic, so the layer-0 cache (whose
     inputs are the embeddings) is bit-identical and deeper layers differ by
     at most one-step quant flips; the attention outputs differ only in fp32
