@@ -52,6 +52,12 @@
 // The lane's x and norm loads are issued first, then the first weight
 // copies, and the prologue waits only for the loads, so the copies stay in
 // flight while the activation is prepared.
+//
+// Normed residual hand-over (fp32-activation types): a residual-add GEMV
+// (EPI_ADD) may also write x' * w_next for its outputs x' and its
+// workgroup's sum of x'^2 in a fixed order; the next GEMV then loads that
+// vector and those sums (256 per load) instead of x and its norm weights,
+// and scales its row totals by r from the sums.
 #include "device_common.h"
 #include "internal.h"
 
@@ -256,6 +262,16 @@ struct GemvArgs {
     // + eps), written to post_out by workgroup 0 (post_y null: x as is)
     const float *post_y, *post_w;
     float* post_out;
+    // residual-add producers: also xw[i] = y[i] * xw_w[i], ssp[blockIdx.x] =
+    // the workgroup's sum of y[i]^2 (xw null: neither)
+    float* xw;
+    const float* xw_w;
+    float* ssp;
+    // consumers: x is the residual times the norm weights and the RMSNorm's
+    // sum of squares is the sum of ss[0..256 ss_loads) (ss null: no such
+    // norm; zero past the producer's sums)
+    const float* ss;
+    int ss_loads;
 };
 
 // Row `i` of the concatenated row space -> (segment, local row).
@@ -915,12 +931,28 @@ __global__ void __launch_bounds__(POST ? 512 : 1024) gemv_kernel(GemvArgs a) {
     const int blk = w * 64 + lane;
     const bool active = blk < nb;
     const int lblk = active ? blk : nb - 1;
-    f32x4 xq[8], nq[8], yq[8], pq[8];
+    f32x4 xq[8], nq[8], yq[8], pq[8], sq[4];
     load8_async(xq, a.x + 32 * lblk);
     if (a.norm) load8_async(nq, a.norm + 32 * lblk);
     if (POST) {
         load8_async(yq, a.post_y + 32 * lblk);
         load8_async(pq, a.post_w + 32 * lblk);
+    }
+    // the producer's partial sums of squares (zero past its workgroups), 256
+    // per load; a residual-add producer's norm weights for its first output
+    if (a.ss) {
+#pragma unroll
+        for (int i = 0; i < kMaxSsParts / 256; ++i)
+            if (i < a.ss_loads)
+                asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(sq[i]) : "v"(a.ss + 4 * lane + 256 * i));
+    }
+    const int nout_mine = (a.ngroups > (int)blockIdx.x
+                               ? (a.ngroups - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x
+                               : 0) * NOUT;
+    float wfirst = 0.0f;   // xw_w at this thread's first output row (the epilogue's j = t)
+    if (a.xw && t < nout_mine) {
+        const int gi = ((int)blockIdx.x) * G + t % NOUT + (t / NOUT) * (int)gridDim.x * G;
+        asm volatile("global_load_dword %0, %1, off" : "=v"(wfirst) : "v"(a.xw_w + min(gi, a.rows_total - 1)));
     }
 
     // ---- weight copies: the first NB-1 chunks of this workgroup's sequence,
@@ -937,6 +969,12 @@ __global__ void __launch_bounds__(POST ? 512 : 1024) gemv_kernel(GemvArgs a) {
     if (POST) {
         pin8(yq);
         pin8(pq);
+    }
+    asm volatile("" : "+v"(wfirst));
+    if (a.ss) {
+#pragma unroll
+        for (int i = 0; i < kMaxSsParts / 256; ++i)
+            if (i < a.ss_loads) asm volatile("" : "+v"(sq[i]));
     }
     float v[32];
 #pragma unroll
@@ -1021,6 +1059,7 @@ __global__ void __launch_bounds__(POST ? 512 : 1024) gemv_kernel(GemvArgs a) {
         }
     }
     float rscale = 1.0f;   // late RMSNorm scale of the row totals (threads t < NOUT)
+    float rss = 1.0f;      // the same from a producer's partial sums
     XBlock xb;
     prepare_block<QT>(v, xb);
     Lane<QT> ln;
@@ -1054,6 +1093,20 @@ __global__ void __launch_bounds__(POST ? 512 : 1024) gemv_kernel(GemvArgs a) {
             acc[i] = d;
         }
         // group done: wave totals -> LDS -> sum over the chunk waves in order
+        if (a.ss && gl == 0) {   // x arrived normed but for the scale: r from the partial sums, in a fixed order
+            float ss = 0.0f;
+#pragma unroll
+            for (int i = 0; i < kMaxSsParts / 256; ++i) {
+                if (i < a.ss_loads) {
+                    ss += sq[i].x;
+                    ss += sq[i].y;
+                    ss += sq[i].z;
+                    ss += sq[i].w;
+                }
+            }
+            ss = wave_sum(ss);
+            rss = 1.0f / sqrtf(ss * a.inv_n + a.eps);
+        }
         float* rd = red + (gl & 1) * nw * G;
         const float tot = xreduce<G>(acc, lane);
         if ((lane & ((64 / G) - 1)) == 0) rd[w * G + rowof<G>(lane)] = tot;
@@ -1064,6 +1117,7 @@ __global__ void __launch_bounds__(POST ? 512 : 1024) gemv_kernel(GemvArgs a) {
                 for (int i = 0; i < nw; ++i) ss += ssred[i];
                 rscale = 1.0f / sqrtf(ss * a.inv_n + a.eps);
             }
+            if (a.ss && gl == 0) rscale = rss;
             float s0 = 0.0f;
             for (int c = 0; c < nw; ++c) s0 += rd[c * G + t];
             s0 *= rscale;
@@ -1079,6 +1133,7 @@ __global__ void __launch_bounds__(POST ? 512 : 1024) gemv_kernel(GemvArgs a) {
     }
     // ---- results of this workgroup's groups (every copy has been waited for)
     lds_sync();
+    float ssq = 0.0f;   // this thread's sum of its new residuals' squares (xw set)
     for (int j = t; j < ngroups_mine * NOUT; j += blockDim.x) {
         const int gk = j / NOUT, i = j % NOUT;
         const int grp = blockIdx.x + gk * gridDim.x;
@@ -1091,8 +1146,33 @@ __global__ void __launch_bounds__(POST ? 512 : 1024) gemv_kernel(GemvArgs a) {
             int s, row;
             seg_of(a, gi, s, row);
             float* y = a.y[s] + row;
-            if (a.epilogue == EPI_ADD) *y += out_lds[j];
-            else *y = out_lds[j];
+            if (a.epilogue == EPI_ADD) {
+                const float nx = *y + out_lds[j];
+                *y = nx;
+                if (a.xw) {   // one segment: gi is the row
+                    a.xw[gi] = nx * (j == t ? wfirst : a.xw_w[gi]);
+                    ssq += nx * nx;
+                }
+            } else {
+                *y = out_lds[j];
+            }
+        }
+    }
+    if (a.xw) {   // the workgroup's sum: threads in order within waves, then waves in order
+        if (nout_mine <= 64) {   // every output is wave 0's: no barrier
+            if (w == 0) {
+                ssq = wave_sum(ssq);
+                if (lane == 0) a.ssp[blockIdx.x] = ssq;
+            }
+        } else {
+            ssq = wave_sum(ssq);
+            if (lane == 0) ssred[w] = ssq;
+            lds_sync();
+            if (t == 0) {
+                float tot = 0.0f;
+                for (int i = 0; i < nw; ++i) tot += ssred[i];
+                a.ssp[blockIdx.x] = tot;
+            }
         }
     }
 }
@@ -1125,7 +1205,7 @@ int env_int(const char* name, int dflt) {
 }
 
 template <int QT, int G, int NB, bool PAIR, bool UA>
-void launch_rows(GemvArgs a, hipStream_t st) {
+int launch_rows(GemvArgs a, hipStream_t st) {
     constexpr int NOUT = PAIR ? G / 2 : G;
     const int nb = a.cols / 32;
     const int nw = (nb + 63) / 64;
@@ -1158,47 +1238,42 @@ void launch_rows(GemvArgs a, hipStream_t st) {
     const size_t lds = lds_for(grid);
     if (lds > 65536)
         L3P_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    if (grid > kMaxSsParts) a.xw = nullptr;   // too many partial sums: the next GEMV takes its norm itself
     launch_kernel(kern, dim3(grid), dim3(threads), (uint32_t)lds, st, a);
+    return a.xw ? grid : 0;
 }
 
 // Ring depth: 3 buffers per wave (deeper rings measured no faster on
 // MI355X for Q8_0 and Q6_K); 4 for chunks of at most 1280 bytes; 2 for the
 // 4 KB F16/BF16 and 8 KB F32 chunks of rows too wide for 3.
 template <int QT, int G, bool PAIR, bool UA>
-void launch_nb(GemvArgs a, int nbuf, hipStream_t st) {
+int launch_nb(GemvArgs a, int nbuf, hipStream_t st) {
     if constexpr (Fmt<QT>::kBufBytes >= 4096) {
-        if (nbuf == 2) {
-            launch_rows<QT, G, 2, PAIR, UA>(a, st);
-            return;
-        }
+        if (nbuf == 2) return launch_rows<QT, G, 2, PAIR, UA>(a, st);
     }
     if constexpr (Fmt<QT>::kChunkBytes <= 1280) {
-        if (nbuf == 4) {
-            launch_rows<QT, G, 4, PAIR, UA>(a, st);
-            return;
-        }
+        if (nbuf == 4) return launch_rows<QT, G, 4, PAIR, UA>(a, st);
     }
-    launch_rows<QT, G, 3, PAIR, UA>(a, st);
+    return launch_rows<QT, G, 3, PAIR, UA>(a, st);
 }
 
 template <int QT, bool UA>
-void launch_g(GemvArgs a, bool pair, int G, int nbuf, hipStream_t st) {
+int launch_g(GemvArgs a, bool pair, int G, int nbuf, hipStream_t st) {
     if (pair) {   // G counts gate and up rows together: 2 or 4 output rows per group
         switch (G) {
-        case 4: launch_nb<QT, 4, true, UA>(a, nbuf, st); break;
-        default: launch_nb<QT, 8, true, UA>(a, nbuf, st); break;
+        case 4: return launch_nb<QT, 4, true, UA>(a, nbuf, st);
+        default: return launch_nb<QT, 8, true, UA>(a, nbuf, st);
         }
-    } else {
-        switch (G) {
-        case 4: launch_nb<QT, 4, false, UA>(a, nbuf, st); break;
-        case 16: launch_nb<QT, 16, false, UA>(a, nbuf, st); break;
-        default: launch_nb<QT, 8, false, UA>(a, nbuf, st); break;
-        }
+    }
+    switch (G) {
+    case 4: return launch_nb<QT, 4, false, UA>(a, nbuf, st);
+    case 16: return launch_nb<QT, 16, false, UA>(a, nbuf, st);
+    default: return launch_nb<QT, 8, false, UA>(a, nbuf, st);
     }
 }
 
 template <int QT>
-void launch_type(GemvArgs a, bool pair, int G, hipStream_t st) {
+int launch_type(GemvArgs a, bool pair, int G, hipStream_t st) {
     const int units = pair ? a.rows[0] : a.rows_total;
     const int per = pair ? G / 2 : G;
     a.ngroups = (units + per - 1) / per;
@@ -1210,12 +1285,10 @@ void launch_type(GemvArgs a, bool pair, int G, hipStream_t st) {
     // three in flight: 5-6% faster at the Q4_0 and Q4_K FFN shapes, where
     // a 2-deep ring leaves too few bytes in flight per CU (measured on MI355X)
     if (Fmt<QT>::kChunkBytes <= 1280) nb = 4;
-    if (row_bytes<QT>(a.cols) % 16 == 0) {
-        launch_g<QT, false>(a, pair, G, nb, st);
-    } else {
-        // Q4_K, Q5_K, F16, BF16 and F32 rows are always 16-byte multiples
-        if constexpr (!Fmt<QT>::kAligned) launch_g<QT, true>(a, pair, G, nb, st);
-    }
+    if (row_bytes<QT>(a.cols) % 16 == 0) return launch_g<QT, false>(a, pair, G, nb, st);
+    // Q4_K, Q5_K, F16, BF16 and F32 rows are always 16-byte multiples
+    if constexpr (!Fmt<QT>::kAligned) return launch_g<QT, true>(a, pair, G, nb, st);
+    return 0;
 }
 
 }  // namespace
@@ -1244,8 +1317,19 @@ bool gemv_supported(int type, int cols) {
     return cols > 0 && cols % unit == 0 && cols <= kMaxWaves * kChunkElems;
 }
 
-void launch_gemv(int type, const GemvBatch& b, int cols, const float* x, const float* norm, float eps,
-                 hipStream_t st) {
+bool gemv_fp32_activation(int type) {
+    switch (type) {
+    case L3P_Q4_0: return !q8_act<L3P_Q4_0>();
+    case L3P_Q4_1: return !q8_act<L3P_Q4_1>();
+    case L3P_Q5_0: return !q8_act<L3P_Q5_0>();
+    case L3P_Q5_1: return !q8_act<L3P_Q5_1>();
+    case L3P_IQ4_NL: return !q8_act<L3P_IQ4_NL>();
+    default: return true;
+    }
+}
+
+int launch_gemv(int type, const GemvBatch& b, int cols, const float* x, const float* norm, float eps,
+                hipStream_t st) {
     L3P_REQUIRE(gemv_supported(type, cols), L3P_E_UNSUPPORTED, "gemv: type %d with %d columns not supported",
                 type, cols);
     L3P_REQUIRE(((uintptr_t)x & 15) == 0 && ((uintptr_t)norm & 15) == 0, L3P_E_INVALID,
@@ -1264,7 +1348,7 @@ void launch_gemv(int type, const GemvBatch& b, int cols, const float* x, const f
     if (b.pair) a.rows_total = b.seg[0].rows;
     else
         for (int s = 0; s < b.nseg; ++s) a.rows_total += b.seg[s].rows;
-    if (a.rows_total == 0) return;
+    if (a.rows_total == 0) return 0;
     a.x = x;
     a.norm = norm;
     a.eps = eps;
@@ -1278,6 +1362,16 @@ void launch_gemv(int type, const GemvBatch& b, int cols, const float* x, const f
     // the residual-update kernels hold four activation vectors in registers
     // and are built for at most 512 threads (8 chunk waves)
     L3P_REQUIRE(!b.post_y || cols <= kMaxPostCols, L3P_E_UNSUPPORTED, "gemv: residual update over %d columns", cols);
+    L3P_REQUIRE(!b.xw || (b.epilogue == EPI_ADD && b.nseg == 1 && !b.pair && b.xw_w && b.ssp), L3P_E_INVALID,
+                "gemv: normed residual output needs one residual-add segment");
+    L3P_REQUIRE(!b.ss || (!norm && gemv_fp32_activation(type) && ((uintptr_t)b.ss & 15) == 0), L3P_E_INVALID,
+                "gemv: summed-square input needs fp32 activations and no norm");
+    a.xw = b.xw;
+    a.xw_w = b.xw_w;
+    a.ssp = b.ssp;
+    a.ss = b.ss;
+    a.ss_loads = (b.n_ss + 255) / 256;
+    L3P_REQUIRE(!b.ss || (b.n_ss > 0 && b.n_ss <= kMaxSsParts), L3P_E_INVALID, "gemv: %d sums of squares", b.n_ss);
     // Rows per group G: the largest of 16, 8, 4 that still gives about six
     // waves per CU (groups x column chunks); ring depth 3.  (Measured on
     // MI355X at the Llama-3-8B shapes.)
@@ -1297,19 +1391,19 @@ void launch_gemv(int type, const GemvBatch& b, int cols, const float* x, const f
     }
     const bool pr = b.pair != 0;
     switch (type) {
-    case L3P_Q8_0: launch_type<L3P_Q8_0>(a, pr, G, st); break;
-    case L3P_Q4_0: launch_type<L3P_Q4_0>(a, pr, G, st); break;
-    case L3P_Q4_1: launch_type<L3P_Q4_1>(a, pr, G, st); break;
-    case L3P_Q5_0: launch_type<L3P_Q5_0>(a, pr, G, st); break;
-    case L3P_Q5_1: launch_type<L3P_Q5_1>(a, pr, G, st); break;
-    case L3P_IQ4_NL: launch_type<L3P_IQ4_NL>(a, pr, G, st); break;
-    case L3P_Q2_K: launch_type<L3P_Q2_K>(a, pr, G, st); break;
-    case L3P_Q3_K: launch_type<L3P_Q3_K>(a, pr, G, st); break;
-    case L3P_Q4_K: launch_type<L3P_Q4_K>(a, pr, G, st); break;
-    case L3P_Q5_K: launch_type<L3P_Q5_K>(a, pr, G, st); break;
-    case L3P_Q6_K: launch_type<L3P_Q6_K>(a, pr, G, st); break;
-    case L3P_F16: launch_type<L3P_F16>(a, pr, G, st); break;
-    case L3P_F32: launch_type<L3P_F32>(a, pr, G, st); break;
-    default: launch_type<L3P_BF16>(a, pr, G, st); break;
+    case L3P_Q8_0: return launch_type<L3P_Q8_0>(a, pr, G, st);
+    case L3P_Q4_0: return launch_type<L3P_Q4_0>(a, pr, G, st);
+    case L3P_Q4_1: return launch_type<L3P_Q4_1>(a, pr, G, st);
+    case L3P_Q5_0: return launch_type<L3P_Q5_0>(a, pr, G, st);
+    case L3P_Q5_1: return launch_type<L3P_Q5_1>(a, pr, G, st);
+    case L3P_IQ4_NL: return launch_type<L3P_IQ4_NL>(a, pr, G, st);
+    case L3P_Q2_K: return launch_type<L3P_Q2_K>(a, pr, G, st);
+    case L3P_Q3_K: return launch_type<L3P_Q3_K>(a, pr, G, st);
+    case L3P_Q4_K: return launch_type<L3P_Q4_K>(a, pr, G, st);
+    case L3P_Q5_K: return launch_type<L3P_Q5_K>(a, pr, G, st);
+    case L3P_Q6_K: return launch_type<L3P_Q6_K>(a, pr, G, st);
+    case L3P_F16: return launch_type<L3P_F16>(a, pr, G, st);
+    case L3P_F32: return launch_type<L3P_F32>(a, pr, G, st);
+    default: return launch_type<L3P_BF16>(a, pr, G, st);
     }
 }

@@ -124,16 +124,35 @@ struct GemvBatch {
     const float* post_y;
     const float* post_w;
     float* post_out;
+    // Optional, for a residual add (EPI_ADD, one segment): every output i
+    // also goes to xw[i] as y[i] * xw_w[i] (the next RMSNorm's weights), and
+    // ssp[g] receives workgroup g's sum of y[i]^2 over its outputs, in a
+    // fixed order; ssp holds kMaxSsParts floats, zero past the written ones.
+    float* xw;
+    const float* xw_w;
+    float* ssp;
+    // Optional, for a GEMV whose weights take fp32 activations: x is already
+    // the residual times the norm weights (norm null), and its RMSNorm's sum
+    // of squares is the sum of the n_ss floats at ss (n_ss <= kMaxSsParts).
+    const float* ss;
+    int n_ss;
 };
 // Widest rows a GEMV with the residual update takes (8 column chunks).
 constexpr int kMaxPostCols = 16384;
+// Workgroups of a residual-add GEMV whose sums of squares a later GEMV reads.
+constexpr int kMaxSsParts = 1024;
 
 // gemv.hip: the decode GEMV over Q8_0 / Q4_0 / Q4_K / Q6_K rows, with an
 // optional RMSNorm of x fused into its prologue (norm != null).  Weights, x
 // and norm must be 16-byte aligned.
 bool gemv_supported(int type, int cols);
-void launch_gemv(int type, const GemvBatch& b, int cols, const float* x, const float* norm, float eps,
-                 hipStream_t s);
+// whether the type's GEMV takes the activation in fp32 (not as Q8_0 blocks)
+bool gemv_fp32_activation(int type);
+// returns the number of partial sums of squares written to b.ssp (0 without
+// b.xw, or when the launch has more than kMaxSsParts workgroups: then xw and
+// ssp are not written)
+int launch_gemv(int type, const GemvBatch& b, int cols, const float* x, const float* norm, float eps,
+                hipStream_t s);
 // gemm.hip: Y[m][n] (=|+=) W[n,:] . X[m,:] on the fp32 matrix cores, for the
 // types the reference dequantizes before its batched dot (Q8_0, the K-quants,
 // F16, BF16, F32).  x rows must be 16-byte aligned (ldx a multiple of 4).

@@ -402,6 +402,9 @@ static Model* load_model(l3p_ctx* c, const void* bytes, size_t len, const l3p_lo
     // run state
     m.x = (float*)m.dalloc((size_t)m.dim * 4);
     m.x2 = (float*)m.dalloc((size_t)m.dim * 4);
+    m.xw = (float*)m.dalloc((size_t)m.dim * 4);
+    m.ssp = (float*)m.dalloc((size_t)kMaxSsParts * 4);
+    L3P_HIP(hipMemsetAsync(m.ssp, 0, (size_t)kMaxSsParts * 4, s));
     m.xb = (float*)m.dalloc((size_t)m.max_dim * 4);
     m.xb2 = (float*)m.dalloc((size_t)m.dim * 4);
     m.q = (float*)m.dalloc((size_t)m.q_dim * 4);
@@ -544,8 +547,8 @@ static double gemv_bytes(int type, int rows, int cols, int out_rows) {
 
 // b's segments = W . rmsnorm(x) (norm != null) or W . x, all of one type,
 // in one launch of the streaming GEMV (the norm runs in its prologue).
-static void gemv_batch(l3p_ctx* c, int type, const GemvBatch& b, int cols, const float* x, const float* norm,
-                       const char* what) {
+static int gemv_batch(l3p_ctx* c, int type, const GemvBatch& b, int cols, const float* x, const float* norm,
+                      const char* what) {
     Model& m = *c->model;
     hipStream_t s = c->stream;
     const float eps = m.eps > 0 ? m.eps : 1e-5f;   // c:3198
@@ -553,7 +556,7 @@ static void gemv_batch(l3p_ctx* c, int type, const GemvBatch& b, int cols, const
     for (int i = 0; i < (b.pair ? 2 : b.nseg); ++i) rows += b.seg[i].rows;
     const int out_rows = b.pair ? b.seg[0].rows : rows;
     ProfRange r(c->prof, s, gemv_label(what, type, rows, cols), gemv_bytes(type, rows, cols, out_rows));
-    launch_gemv(type, b, cols, x, norm, eps, s);
+    return launch_gemv(type, b, cols, x, norm, eps, s);
 }
 
 void gemv_plain(l3p_ctx* c, int type, const GemvBatch& b, int cols, const float* x) {
@@ -602,6 +605,27 @@ static void layers_impl(l3p_ctx* c, bool with_logits) {
         std::swap(cur, alt);
         pend_y = nullptr;
     };
+    // Without post norms the FFN's residual add (down) also writes the
+    // residual times the next RMSNorm's weights (m.xw) and its workgroups'
+    // sums of squares (m.ssp), so that the next layer's q|k|v (or the
+    // classifier) reads one vector and a few sums instead of the residual and
+    // the weights; n_ss is the number of those sums (0: the next GEMV forms
+    // its norm itself).  (wo's residual add does not: its 1024 workgroups'
+    // sums cost gate|up more than the weights did.)
+    auto produce = [&](GemvBatch& b, const float* next_norm, int next_type, float* ssp) {
+        if (m.is_gemma || !gemv_fp32_activation(next_type)) return;
+        b.xw = m.xw;
+        b.xw_w = next_norm;
+        b.ssp = ssp;
+    };
+    auto consume = [&](GemvBatch& b, int n_ss, const float* ssp, const float*& x, const float*& norm) {
+        if (n_ss <= 0) return;
+        b.ss = ssp;
+        b.n_ss = n_ss;
+        x = m.xw;
+        norm = nullptr;
+    };
+    int n_ss = 0;   // sums in m.ssp for the next q|k|v (or the classifier)
     for (int l = 0; l < m.n_layers; ++l) {
         const Layer& L = m.layers[l];
         // q, k, v = W . rmsnorm(x) (c:3211-3230), one launch when the three share a type
@@ -613,7 +637,10 @@ static void layers_impl(l3p_ctx* c, bool with_logits) {
             b.nseg = 3;
             b.epilogue = EPI_STORE;
             fold(b);
-            gemv_batch(c, L.wq.type, b, m.dim, cur, L.att_norm, "qkv");
+            const float* x = cur;
+            const float* norm = L.att_norm;
+            consume(b, n_ss, m.ssp, x, norm);
+            gemv_batch(c, L.wq.type, b, m.dim, x, norm, "qkv");
         } else {
             // each launch forms the same updated residual from `cur`
             GemvBatch bq = one(L.wq, m.q, EPI_STORE), bk = one(L.wk, m.k, EPI_STORE), bv = one(L.wv, m.v, EPI_STORE);
@@ -652,7 +679,14 @@ static void layers_impl(l3p_ctx* c, bool with_logits) {
             pend_y = m.xb;
             pend_w = L.post_ffn;
         } else {
-            gemv_batch(c, L.w2.type, one(L.w2, cur, EPI_ADD), m.hidden, m.hb, nullptr, "down");
+            GemvBatch b = one(L.w2, cur, EPI_ADD);
+            const bool last = l + 1 == m.n_layers;
+            const Layer* N = last ? nullptr : &m.layers[l + 1];
+            // the next layer's q|k|v takes the sums only as one launch
+            const bool next_one = !last && N->wq.type == N->wk.type && N->wq.type == N->wv.type;
+            if (next_one || (last && with_logits))
+                produce(b, last ? m.final_norm : N->att_norm, last ? m.wcls.type : N->wq.type, m.ssp);
+            n_ss = gemv_batch(c, L.w2.type, b, m.hidden, m.hb, nullptr, "down");
         }
     }
     // final rmsnorm (c:3420) fused into the classifier (c:3423-3433).  Without
@@ -661,7 +695,10 @@ static void layers_impl(l3p_ctx* c, bool with_logits) {
     if (with_logits) {
         GemvBatch b = one(m.wcls, m.logits, EPI_STORE);
         fold(b);
-        gemv_batch(c, m.wcls.type, b, m.dim, cur, m.final_norm, "lm_head");
+        const float* x = cur;
+        const float* norm = m.final_norm;
+        consume(b, n_ss, m.ssp, x, norm);
+        gemv_batch(c, m.wcls.type, b, m.dim, x, norm, "lm_head");
         folded();
         if (m.is_gemma && m.softcap > 0.0f) launch_softcap(m.logits, m.vocab, m.softcap, s);
     }

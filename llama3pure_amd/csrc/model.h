@@ -42,6 +42,9 @@ struct Model {
 
     // run state (RunState, c:281-343), device resident
     float *x = nullptr, *x2 = nullptr, *xb = nullptr, *xb2 = nullptr, *q = nullptr, *k = nullptr, *v = nullptr;
+    // the residual times the next RMSNorm's weights and the sums of squares of
+    // the FFN residual add's workgroups (see layers_impl)
+    float *xw = nullptr, *ssp = nullptr;
     float *hb = nullptr, *hb2 = nullptr, *logits = nullptr;
     float* part_acc = nullptr;     // [n_heads][max_chunks][attn_part_row(hs)] attention chunk partials
     int* step = nullptr;           // device {token, pos} of the step being computed

@@ -1,7 +1,8 @@
 """The GEMV prologue's untracked loads, checked in the gfx950 assembly.
 
-gemv.hip issues the activation, norm and residual-update loads as inline-asm
-global_load_dwordx4, so that the compiler does not wait for them with
+gemv.hip issues the activation, norm, residual-update and partial-sum loads
+(and a residual-add producer's norm weights) as inline-asm global loads, so
+that the compiler does not wait for them with
 vmcnt(0) (which would also wait for the weight copies issued after them);
 the kernel waits with its own s_waitcnt.  That is only correct if no other
 instruction reads or writes a destination register of those loads before
@@ -49,7 +50,7 @@ def check_kernel(body):
             waited = True
             break
         toks = re.findall(r"v\[\d+:\d+\]|v\d+\b", s)
-        if in_asm and s.startswith("global_load_dwordx4"):
+        if in_asm and s.startswith("global_load_dword"):
             if vregs(toks[1]) & pending:
                 problems.append("address register of a pending load: " + s)
             pending |= vregs(toks[0])
