@@ -1568,17 +1568,15 @@ __global__ void __launch_bounds__(1024) topk_scan_kernel(const float* __restrict
     auto replace = [&](float bv, int i) {
         if constexpr (R == 1) {
             const int sh = __builtin_amdgcn_readlane(ks, 0);   // the minimum's slot
-            const bool before = lane >= 1 && lane < k && (key < bv || (key == bv && ks < sh));
+            // bitwise, not short-circuit: no exec-mask branches on this chain
+            const bool before = (lane >= 1) & (lane < k) & ((key < bv) | ((key == bv) & (ks < sh)));
             const int r = __popcll(__ballot(before));
-            const float kn = __shfl_down(key, 1, 64);
-            const int sn = __shfl_down(ks, 1, 64);
-            if (lane < r) {
-                key = kn;
-                ks = sn;
-            } else if (lane == r) {
-                key = bv;
-                ks = sh;
-            }
+            // lane + 1's entry (DPP wave_shl:1; lane 63 keeps its own, never used)
+            const float kn = __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(key), __float_as_int(key),
+                                                                        0x130, 0xF, 0xF, false));
+            const int sn = __builtin_amdgcn_update_dpp(ks, ks, 0x130, 0xF, 0xF, false);
+            key = lane < r ? kn : (lane == r ? bv : key);
+            ks = lane < r ? sn : (lane == r ? sh : ks);
             if (lane == sh) {
                 sv[0] = bv;
                 si[0] = i;
