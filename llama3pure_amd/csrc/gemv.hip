@@ -1229,7 +1229,12 @@ int launch_rows(GemvArgs a, hipStream_t st) {
     const int per_cu = std::min(occupancy(kern, threads, lds_for(cus())), xcap);
     const int cap = per_cu * cus();
     int grid = std::min(a.ngroups, cap);
-    if (env_int("L3P_GEMV_BAL", 1)) {
+    // Launches with the fused residual update keep the plain grid (cap
+    // workgroups, one group more for the first ones): measured faster on
+    // MI355X at Gemma-2-2B's q|k|v (9.56 -> 9.16 us) and LM head (117.1 ->
+    // 112.9 us), while the balanced grid is faster for the others
+    // (Llama-3-8B gate|up 24.9 -> 23.7 us).
+    if (env_int("L3P_GEMV_BAL", 1) && !a.post_y) {
         // the same number of groups (k, or k-1 for the last few) per workgroup
         const int k = (a.ngroups + cap - 1) / cap;
         grid = (a.ngroups + k - 1) / k;
