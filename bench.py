@@ -9,7 +9,11 @@ position 1024 of a 2048 context with uniform random token ids.
 
 Printed as one JSON line:
   value        decode tok/s over exactly --steps timed steps (weights, KV
-               cache and run state already resident in HBM);
+               cache and run state already resident in HBM), run as the
+               reference's greedy loop through l3p_generate_greedy (each
+               step's token read back while the next step runs);
+               per_call_decode times the same number of steps as one
+               synchronous l3p_decode call per token;
   roofline     the dominant GEMV launch class: algorithmic bytes per launch
                over its average kernel duration, from the HIP events each
                GEMV dispatch records at its own start and end
@@ -504,17 +508,32 @@ def main():
             pos += 1
         return tok, pos
 
-    assert a.prefill + a.warmup + 2 * a.steps <= mi.seq_len, "steps exceed the 2048-position context"
+    def run_queued(n, tok, pos):
+        toks = ctx.generate_greedy(tok, pos, n)
+        assert len(toks) == n, (len(toks), n)
+        return toks[-1], pos + n
+
+    assert a.prefill + a.warmup + 3 * a.steps <= mi.seq_len, "steps exceed the 2048-position context"
     tok, pos = run(a.warmup, int(prompt[-1]), a.prefill)
     ctx.synchronize()
     torch.cuda.synchronize()
+    # the timed steps: the reference's greedy loop as one l3p_generate_greedy
+    # call (each step's token read back while the next step runs)
     t0 = time.perf_counter()
-    tok, pos = run(a.steps, tok, pos)
+    tok, pos = run_queued(a.steps, tok, pos)
     ctx.synchronize()
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
     tps = a.steps / dt
     print(f"[bench] {a.steps} decode steps in {dt * 1e3:.1f} ms: {tps:.1f} tok/s", file=sys.stderr, flush=True)
+    # the same number of steps as one l3p_decode call per token from Python
+    t0 = time.perf_counter()
+    tok, pos = run(a.steps, tok, pos)
+    ctx.synchronize()
+    torch.cuda.synchronize()
+    dt_call = time.perf_counter() - t0
+    print(f"[bench] {a.steps} l3p_decode calls in {dt_call * 1e3:.1f} ms: {a.steps / dt_call:.1f} tok/s",
+          file=sys.stderr, flush=True)
 
     # second pass with per-kernel dispatch events: the roofline of the dominant GEMV class
     ctx.profile(True)
@@ -557,7 +576,10 @@ def main():
         "data": "synthetic: random-init weights N(0,0.02) quantized to Q8_0, uniform random token ids",
         "config": {"workload": "greedy decode, Llama-3-8B architecture, all matrices Q8_0, KV prefilled to "
                                f"{a.prefill} of 2048", "layers": a.layers, "dim": 4096, "heads": 32, "kv_heads": 8,
-                   "ffn": 14336, "vocab": 128256, "start_pos": a.prefill, "parallelism": "single GPU"},
+                   "ffn": 14336, "vocab": 128256, "start_pos": a.prefill, "parallelism": "single GPU",
+                   "decode_call": "l3p_generate_greedy (steps queued two ahead of the host's token reads)"},
+        "per_call_decode": {"call": "l3p_decode once per token from Python (synchronous)",
+                            "tok_s": round(a.steps / dt_call, 3), "ms_per_step": round(dt_call * 1e3 / a.steps, 4)},
         "roofline": {"bound": "hbm", "kernel": name, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(name),
                      "bytes_per_launch": int(bpl), "avg_launch_us": round(avg_us, 2), "launches": launches,

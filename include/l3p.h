@@ -164,6 +164,19 @@ typedef struct {
 int l3p_decode(l3p_ctx* ctx, int32_t token, int32_t pos, const l3p_sampler* s, uint64_t* rng,
                int32_t* out_token);
 
+/* Greedy generation: the reference's decode loop (c:5289-5309, each
+ * iteration generate_token at temperature 0, c:4766-4813) from (token, pos)
+ * for up to max_steps steps, never past the context: step i decodes position
+ * pos + i and writes its argmax token to out_tokens[i].  It stops after the
+ * first token found in stop_ids[0..n_stop) (the reference's eos/eot checks,
+ * c:5296-5303), which is written and counted.  *n_out = tokens written.  The
+ * tokens equal those of l3p_decode called step by step with temperature 0;
+ * the steps are queued on the device ahead of the host's reads, so no step
+ * waits for the host.  The repetition stop (c:4910-4918) is left to the
+ * caller, which can cut the returned tokens. */
+int l3p_generate_greedy(l3p_ctx* ctx, int32_t token, int32_t pos, int32_t max_steps, const int32_t* stop_ids,
+                        int32_t n_stop, int32_t* out_tokens, int32_t* n_out);
+
 /* Sample from vocab logits already on the device (the sampler alone). */
 int l3p_sample(l3p_ctx* ctx, const float* logits_dev, int n, const l3p_sampler* s, uint64_t* rng,
                int32_t* out_token);

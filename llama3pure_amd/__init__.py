@@ -25,7 +25,7 @@ EXPORTS = [
     "l3p_create", "l3p_destroy", "l3p_last_error", "l3p_stream", "l3p_synchronize",
     "l3p_malloc", "l3p_free", "l3p_upload", "l3p_download", "l3p_row_bytes",
     "l3p_dequant", "l3p_quantize_q8_0", "l3p_gemv", "l3p_gemm",
-    "l3p_load_gguf", "l3p_get_model_info", "l3p_forward", "l3p_prefill", "l3p_decode",
+    "l3p_load_gguf", "l3p_get_model_info", "l3p_forward", "l3p_prefill", "l3p_decode", "l3p_generate_greedy",
     "l3p_sample", "l3p_logits_device", "l3p_copy_kv", "l3p_rope_row",
     "l3p_profile", "l3p_profile_read", "l3p_stream_read", "l3p_gemm_static",
 ]
@@ -93,6 +93,7 @@ def lib() -> C.CDLL:
         "l3p_prefill": (I, [P, P, I, C.c_int32]),
         "l3p_decode": (I, [P, C.c_int32, C.c_int32, C.POINTER(Sampler), C.POINTER(C.c_uint64),
                            C.POINTER(C.c_int32)]),
+        "l3p_generate_greedy": (I, [P, C.c_int32, C.c_int32, C.c_int32, P, C.c_int32, P, C.POINTER(C.c_int32)]),
         "l3p_sample": (I, [P, P, I, C.POINTER(Sampler), C.POINTER(C.c_uint64), C.POINTER(C.c_int32)]),
         "l3p_logits_device": (I, [P, C.POINTER(P)]),
         "l3p_copy_kv": (I, [P, I, I, P, SZ]),
@@ -214,6 +215,17 @@ class Context:
         out = C.c_int32()
         self._check(self.L.l3p_decode(self.h, token, pos, C.byref(s), C.byref(st), C.byref(out)))
         return out.value, st.value
+
+    def generate_greedy(self, token: int, pos: int, max_steps: int, stop_ids=()):
+        """Greedy tokens of up to max_steps steps from (token, pos), ending
+        after the first stop id (included); queued ahead on the device."""
+        import numpy as np
+        stops = np.ascontiguousarray(stop_ids, np.int32)
+        out = np.zeros(max(1, max_steps), np.int32)
+        n = C.c_int32()
+        self._check(self.L.l3p_generate_greedy(self.h, token, pos, max_steps, stops.ctypes.data if stops.size else None,
+                                               stops.size, out.ctypes.data, C.byref(n)))
+        return out[:n.value].tolist()
 
     def sample(self, logits_dev, n, temperature=0.0, top_k=40, top_p=0.9, rng: int = 0):
         s = Sampler(temperature, top_k, top_p, 0)

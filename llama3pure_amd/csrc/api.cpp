@@ -72,6 +72,9 @@ void l3p_destroy(l3p_ctx* c) {
     c->model = nullptr;
     c->prof.release();
     if (c->gemm_ws) hipFree(c->gemm_ws);
+    if (c->gen_host) hipHostFree(c->gen_host);
+    for (hipEvent_t e : c->gen_ev)
+        if (e) hipEventDestroy(e);
     hipStreamDestroy(c->stream);
     delete c;
 }

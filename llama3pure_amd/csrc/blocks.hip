@@ -40,8 +40,12 @@ __global__ void dequant_kernel(int type, const uint8_t* __restrict__ s, int64_t 
 // rope.rope_cur is set), so that attention need not wait for the record to
 // find them.
 __global__ void embed_step_kernel(int type, const uint8_t* __restrict__ s, int n, float scale, float* __restrict__ y,
-                                  int token, int pos, int* step, RopeRows rope) {
+                                  int token, int pos, int* step, RopeRows rope, const int* dtok, size_t rb) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (dtok) {   // the token the previous step's sampler left on the device; s is row 0
+        token = *dtok;
+        s += (size_t)token * rb;
+    }
     if (i < n) {
         const float v = deq_elem(type, s, i);
         y[i] = scale != 0.0f ? v * scale : v;
@@ -106,11 +110,11 @@ void launch_dequant(int type, const uint8_t* src, int64_t n, float* dst, hipStre
 }
 
 void launch_embed_row(int type, const uint8_t* row, int n, float scale, float* dst, int token, int pos, int* step,
-                      const RopeRows* rope, hipStream_t st) {
+                      const RopeRows* rope, hipStream_t st, const int* dtok, size_t rb) {
     RopeRows r{};
     if (rope) r = *rope;
     const int threads = std::max(n, r.rope_cur ? 4 * r.half : 0);
     hipLaunchKernelGGL(embed_step_kernel, dim3((threads + 255) / 256), dim3(256), 0, st, type, row, n, scale, dst,
-                       token, pos, step, r);
+                       token, pos, step, r, dtok, rb);
     L3P_HIP(hipGetLastError());
 }

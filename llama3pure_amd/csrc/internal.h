@@ -206,5 +206,7 @@ struct RopeRows {
     int half;
     float* rope_cur;
 };
+// dtok: read the token from device memory instead (row is then row 0 and
+// rb the row stride in bytes)
 void launch_embed_row(int type, const uint8_t* row, int n, float scale, float* dst, int token, int pos, int* step,
-                      const RopeRows* rope, hipStream_t s);
+                      const RopeRows* rope, hipStream_t s, const int* dtok = nullptr, size_t rb = 0);

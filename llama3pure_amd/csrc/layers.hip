@@ -1640,10 +1640,10 @@ __global__ void __launch_bounds__(1024) topk_scan_kernel(const float* __restrict
 // ---------------------------------------------------------------------------
 // launchers
 // ---------------------------------------------------------------------------
-void launch_embed_step(const Model& m, int token, int pos, hipStream_t s) {
+void launch_embed_step(const Model& m, int token, int pos, hipStream_t s, const int* dtok) {
     const RopeRows rope{{m.cos_d, m.sin_d, m.cos_s, m.sin_s}, m.hs / 2, m.rope_cur};
-    launch_embed_row(m.emb.type, m.emb.w + (size_t)token * m.emb.rb, m.emb.cols, m.is_gemma ? m.embed_scale : 0.0f,
-                     m.x, token, pos, m.step, &rope, s);
+    launch_embed_row(m.emb.type, m.emb.w + (dtok ? 0 : (size_t)token * m.emb.rb), m.emb.cols,
+                     m.is_gemma ? m.embed_scale : 0.0f, m.x, token, pos, m.step, &rope, s, dtok, m.emb.rb);
 }
 
 void launch_rmsnorm_add_rows(const float* y, int ldy, const float* w, int n, float inv_n, float eps, float* x,

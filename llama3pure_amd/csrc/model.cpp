@@ -878,10 +878,10 @@ static bool graphs_enabled() {
 // record are written by an eager launch; the layers run as a replayed HIP
 // graph from the second step of each variant on (the first, eager, step also
 // settles every launch configuration).  Per-launch timing runs eagerly.
-static void forward_impl(l3p_ctx* c, int token, int pos, bool with_logits) {
+static void forward_impl(l3p_ctx* c, int token, int pos, bool with_logits, const int* dtok = nullptr) {
     Model& m = *c->model;
     hipStream_t s = c->stream;
-    launch_embed_step(m, token, pos, s);
+    launch_embed_step(m, token, pos, s, dtok);
     c->attn_per_head = attention_per_head(m, pos);
     const int v = (with_logits ? 1 : 0) | (c->attn_per_head ? 2 : 0);
     if (c->prof.on || !graphs_enabled() || c->graph_runs[v]++ == 0) {
@@ -890,6 +890,7 @@ static void forward_impl(l3p_ctx* c, int token, int pos, bool with_logits) {
     }
     if (!c->graph[v]) {
         hipGraph_t g = nullptr;
+        L3P_HIP(hipStreamSynchronize(s));   // capture from an idle stream (steps may be queued ahead)
         L3P_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
         try {
             layers_impl(c, with_logits);
@@ -1113,6 +1114,61 @@ int l3p_decode(l3p_ctx* c, int32_t token, int32_t pos, const l3p_sampler* sp, ui
         L3P_REQUIRE(pos >= 0 && pos < m.seq_len, L3P_E_INVALID, "pos %d out of range [0, %d)", pos, m.seq_len);
         forward_impl(c, token, pos, true);
         sample_impl(c, m.logits, m.vocab, sp, rng, out);
+        c->prof.collect();
+    });
+}
+
+// Greedy generation, the reference's decode loop (c:5289-5309) at temperature
+// 0: step i runs the forward at position pos + i and the argmax.  Step 0 takes
+// `token`; every later step's embedding reads the previous argmax from device
+// memory, so the host queues steps ahead of the token it is waiting for (two
+// in flight) and a step starts as soon as the previous one ends.  Each token
+// comes back through its own pinned slot and event.  After a stop token the
+// step already queued behind it still runs: it writes the K/V rows of the next
+// position for the token that a following decode call at that position would
+// write there anyway (greedy steps are deterministic).
+int l3p_generate_greedy(l3p_ctx* c, int32_t token, int32_t pos, int32_t max_steps, const int32_t* stop_ids,
+                        int32_t n_stop, int32_t* out_tokens, int32_t* n_out) {
+    return mguard(c, true, [&] {
+        const Model& m = *c->model;
+        L3P_REQUIRE(out_tokens && n_out, L3P_E_INVALID, "generate: null output");
+        *n_out = 0;
+        L3P_REQUIRE(max_steps >= 0 && n_stop >= 0 && (n_stop == 0 || stop_ids), L3P_E_INVALID,
+                    "generate: max_steps=%d, n_stop=%d", max_steps, n_stop);
+        L3P_REQUIRE(token >= 0 && token < m.vocab, L3P_E_INVALID, "token %d out of range [0, %d)", token, m.vocab);
+        L3P_REQUIRE(pos >= 0 && pos < m.seq_len, L3P_E_INVALID, "pos %d out of range [0, %d)", pos, m.seq_len);
+        const int steps = std::min(max_steps, m.seq_len - pos);   // the reference's pos < max_tokens bound
+        if (steps == 0) return;
+        hipStream_t s = c->stream;
+        if (!c->gen_host) {
+            L3P_HIP(hipHostMalloc((void**)&c->gen_host, l3p_ctx::kGenSlots * sizeof(int), hipHostMallocDefault));
+            for (hipEvent_t& e : c->gen_ev) L3P_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+        }
+        constexpr int kAhead = 2;
+        static_assert(kAhead < l3p_ctx::kGenSlots, "a slot is read before it is written again");
+        int issued = 0, done = 0;
+        auto issue = [&](int i) {
+            forward_impl(c, token, pos + i, true, i == 0 ? nullptr : m.out_token);
+            launch_argmax(m.logits, m.vocab, m.out_token, s, m.cand_val, m.cand_idx);
+            const int slot = i % l3p_ctx::kGenSlots;
+            L3P_HIP(hipMemcpyAsync(c->gen_host + slot, m.out_token, 4, hipMemcpyDeviceToHost, s));
+            L3P_HIP(hipEventRecord(c->gen_ev[slot], s));
+        };
+        try {
+            while (done < steps) {
+                while (issued < steps && issued < done + kAhead) issue(issued++);
+                const int slot = done % l3p_ctx::kGenSlots;
+                L3P_HIP(hipEventSynchronize(c->gen_ev[slot]));
+                const int t = c->gen_host[slot];
+                out_tokens[done++] = t;
+                *n_out = done;
+                if (std::find(stop_ids, stop_ids + n_stop, t) != stop_ids + n_stop) break;
+            }
+        } catch (...) {
+            (void)hipStreamSynchronize(s);
+            throw;
+        }
+        L3P_HIP(hipStreamSynchronize(s));   // the steps queued past a stop
         c->prof.collect();
     });
 }

@@ -124,6 +124,10 @@ struct l3p_ctx {
     // no GEMM call allocates)
     float* gemm_ws = nullptr;
     size_t gemm_ws_floats = 0;
+    // l3p_generate_greedy: pinned token slots and their events (made on first use)
+    static constexpr int kGenSlots = 4;
+    int* gen_host = nullptr;
+    hipEvent_t gen_ev[kGenSlots] = {};
     void drop_graphs();
 };
 
@@ -133,7 +137,8 @@ void gemv_plain(l3p_ctx* c, int type, const GemvBatch& b, int cols, const float*
 // layers.hip
 // m.x = embedding row of `token` (times Gemma's scale), the device step record
 // {token, pos} that the layer kernels read and the RoPE rows of pos (m.rope_cur).
-void launch_embed_step(const Model& m, int token, int pos, hipStream_t s);
+// With dtok the token is read from device memory when the kernel runs.
+void launch_embed_step(const Model& m, int token, int pos, hipStream_t s, const int* dtok = nullptr);
 // QK-norm, RoPE, the K/V cache write and attention of one layer for the
 // step's position (c:3232-3359); out = [n_heads][head_dim].  The first form
 // reads the decode step's q, k, v and step record.
