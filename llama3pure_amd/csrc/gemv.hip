@@ -1393,6 +1393,11 @@ int launch_gemv(int type, const GemvBatch& b, int cols, const float* x, const fl
                 G = g;
                 break;
             }
+        // rows of at most two chunk columns keep 8 rows per group down to
+        // four waves per CU (Llama-3-8B wo, 4096 x 4096: 7.56 -> 7.24 us),
+        // except with the residual update (Gemma-2-2B's 4096 x 2304 q|k|v:
+        // 9.20 us at 4 rows, 9.24 at 8)
+        if (G == 4 && nw <= 2 && !a.post_y && waves(8) >= 4L * cus()) G = 8;
     }
     const bool pr = b.pair != 0;
     switch (type) {
