@@ -63,6 +63,9 @@ LLAMA3_8B = dict(arch="llama", dim=4096, hidden=14336, n_layers=32, n_heads=32, 
 GEMMA2_2B = dict(arch="gemma3", dim=2304, hidden=9216, n_layers=26, n_heads=8, n_kv=4, head_dim=256, vocab=256000,
                  ctx=1024, softcap=30.0, swa_window=4096, tied=True, rope_theta=10000.0, eps=1e-6, std=0.02,
                  seed=4321)
+# the workload's Gemma-2 attention: alternating local/global layers and the
+# attention score cap 50 (load options; see gemma_prompt_decode)
+GEMMA2_2B_LOAD = dict(swa_pattern=2, attn_softcap=50.0)
 
 
 def time_gemv_shapes(ctx, torch, l3p, synth):
@@ -132,7 +135,7 @@ def gemma_prompt_decode(np, torch, l3p, synth, prompt_len=512, steps=128, warmup
     the decode steps then continue from the timed prompt."""
     ctx = l3p.Context(0)
     img = synth.synthetic_model(qtype=synth.Q8_0, make_mat=synth.gpu_q8_0_maker(ctx, torch, 77), **GEMMA2_2B)
-    mi = ctx.load_gguf(img, swa_pattern=2, attn_softcap=50.0)
+    mi = ctx.load_gguf(img, **GEMMA2_2B_LOAD)
     del img
     prompt = np.random.default_rng(6).integers(0, mi.vocab_size, prompt_len).astype(np.int32)
     sampler = dict(temperature=0.9, top_k=40, top_p=0.9)
@@ -322,8 +325,8 @@ def cpu_leg(path: str, seconds: float, max_tokens: int, kind: str, start: int) -
 
     import oracle
 
-    if kind in ("omp", "o3"):
-        ref = oracle.Ref(oracle.REF_OMP_SO if kind == "omp" else oracle.REF_SO)
+    if kind in ("omp", "omp_v4", "o3"):
+        ref = oracle.Ref({"omp": oracle.REF_OMP_SO, "omp_v4": oracle.REF_OMP_V4_SO, "o3": oracle.REF_SO}[kind])
         t0 = time.perf_counter()
         if ref.lib.ref_model_open(path.encode(), 0) != 0:
             raise RuntimeError("reference failed to open the model")
@@ -335,7 +338,7 @@ def cpu_leg(path: str, seconds: float, max_tokens: int, kind: str, start: int) -
             n += 1
         dt = time.perf_counter() - t0
         out = {"tokens": n, "seconds": dt, "load_seconds": load_s}
-        if kind == "omp":
+        if kind.startswith("omp"):
             from llama3pure_amd import synth
 
             out["gemv"] = cpu_gemv(ref, synth)
@@ -368,6 +371,19 @@ def host_cpu() -> dict:
     return {"nproc": os.cpu_count(), "affinity": len(os.sched_getaffinity(0)), "model": model}
 
 
+def host_has_avx512() -> bool:
+    """Whether the host runs x86-64-v4 code (AVX-512 F, BW, CD, DQ, VL)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("flags"):
+                    flags = set(line.split(":", 1)[1].split())
+                    return {"avx512f", "avx512bw", "avx512cd", "avx512dq", "avx512vl"} <= flags
+    except OSError:
+        pass
+    return False
+
+
 def run_cpu_leg(path: str, seconds: float, kind: str, threads: int, start: int) -> dict | None:
     env = dict(os.environ, OMP_NUM_THREADS=str(threads))
     r = subprocess.run([sys.executable, os.path.abspath(__file__), "--cpu-leg", path, "--cpu-seconds", str(seconds),
@@ -389,6 +405,10 @@ def cpu_baseline(img, seconds: float, start: int) -> dict | None:
 
     cpu = host_cpu()
     use_ref = oracle.have_ref() and os.path.exists(oracle.REF_OMP_SO)
+    # the Makefile's -march=native, approximated by the widest ISA level the
+    # host runs that a library built elsewhere can target
+    v4 = use_ref and os.path.exists(oracle.REF_OMP_V4_SO) and host_has_avx512()
+    march = "x86-64-v4" if v4 else "x86-64-v3"
     env_threads = os.environ.get("OMP_NUM_THREADS", "")
     threads = int(env_threads) if env_threads.isdigit() and int(env_threads) > 0 else cpu["affinity"]
     d = "/dev/shm" if os.path.isdir("/dev/shm") else None
@@ -396,7 +416,8 @@ def cpu_baseline(img, seconds: float, start: int) -> dict | None:
     try:
         with os.fdopen(fd, "wb") as f:
             img.tofile(f)
-        res = run_cpu_leg(path, seconds, "omp" if use_ref else "port", threads if use_ref else 1, start)
+        res = run_cpu_leg(path, seconds, ("omp_v4" if v4 else "omp") if use_ref else "port",
+                          threads if use_ref else 1, start)
         single = run_cpu_leg(path, seconds, "o3", 1, start) if use_ref else None
     finally:
         os.unlink(path)
@@ -406,8 +427,8 @@ def cpu_baseline(img, seconds: float, start: int) -> dict | None:
              f"{cpu['model'] or 'CPU model unknown'}")
     span = lambda r: f"positions {start}..{start + r['tokens'] - 1}"
     if use_ref:
-        what = (f"reference C engine, its Makefile's OpenMP line (-Ofast -fopenmp), {threads} threads "
-                f"(OMP_NUM_THREADS={env_threads or 'unset'})")
+        what = (f"reference C engine, its Makefile's OpenMP line with -march={march} for -march=native "
+                f"(-Ofast -fopenmp -march={march}), {threads} threads (OMP_NUM_THREADS={env_threads or 'unset'})")
     else:
         what = "oracle (C restatement of the reference), one thread"
     out = {"value": round(res["tokens"] / res["seconds"], 4), "unit": "tok/s", "cores": threads if use_ref else 1,

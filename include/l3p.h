@@ -116,7 +116,7 @@ typedef struct {
      * attn_softcap > 0: every attention score s becomes
      *   attn_softcap * tanhf(s / attn_softcap) before the softmax (Gemma-2's
      *   attention logit soft-capping); 0: scores as they are.
-     * Negative values return L3P_E_INVALID. */
+     * Negative values, an infinite or NaN cap return L3P_E_INVALID. */
     int swa_pattern;
     float attn_softcap;
     int reserved[5];
@@ -173,7 +173,10 @@ int l3p_decode(l3p_ctx* ctx, int32_t token, int32_t pos, const l3p_sampler* s, u
  * tokens equal those of l3p_decode called step by step with temperature 0;
  * the steps are queued on the device ahead of the host's reads, so no step
  * waits for the host.  The repetition stop (c:4910-4918) is left to the
- * caller, which can cut the returned tokens. */
+ * caller, which can cut the returned tokens.  A step already queued behind
+ * a stop still runs (the queue is two steps ahead): it writes the K/V rows
+ * of position pos + *n_out and leaves its logits (l3p_logits_device) for a
+ * token that is not returned. */
 int l3p_generate_greedy(l3p_ctx* ctx, int32_t token, int32_t pos, int32_t max_steps, const int32_t* stop_ids,
                         int32_t n_stop, int32_t* out_tokens, int32_t* n_out);
 
@@ -181,7 +184,9 @@ int l3p_generate_greedy(l3p_ctx* ctx, int32_t token, int32_t pos, int32_t max_st
 int l3p_sample(l3p_ctx* ctx, const float* logits_dev, int n, const l3p_sampler* s, uint64_t* rng,
                int32_t* out_token);
 
-/* Device pointer of the last forward's logits (vocab_size floats). */
+/* Device pointer of the logits of the last step run (vocab_size floats).
+ * After l3p_generate_greedy stopped on a stop id, that is the queued step past
+ * the stop, whose token was not returned. */
 int l3p_logits_device(l3p_ctx* ctx, const float** out_dev);
 
 /* Copy one layer's K or V cache in the reference layout

@@ -235,7 +235,8 @@ class Context:
         return out.value, st.value
 
     def logits(self):
-        """The last forward's or decode's vocab logits, copied from the device."""
+        """The vocab logits of the last step run (forward, decode, or the step
+        generate_greedy queued past a stop), copied from the device."""
         import numpy as np
         d = C.c_void_p()
         self._check(self.L.l3p_logits_device(self.h, C.byref(d)))

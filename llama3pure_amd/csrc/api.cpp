@@ -18,6 +18,7 @@ static int guard(l3p_ctx* c, F&& f) {
         return e.code;
     } catch (const std::bad_alloc&) {
         if (c) c->err = "host allocation failed";
+        else g_create_error = "host allocation failed";
         return L3P_E_NOMEM;
     }
 }

@@ -268,10 +268,12 @@ struct GemvArgs {
     const float* xw_w;
     float* ssp;
     // consumers: x is the residual times the norm weights and the RMSNorm's
-    // sum of squares is the sum of ss[0..256 ss_loads) (ss null: no such
-    // norm; zero past the producer's sums)
+    // sum of squares is the sum of ss[0..n_ss), read 256 per load over
+    // ss_loads loads (ss null: no such norm).  Entries past n_ss are never
+    // counted: they may hold an earlier producer's sums from a larger grid.
     const float* ss;
     int ss_loads;
+    int n_ss;
 };
 
 // Row `i` of the concatenated row space -> (segment, local row).
@@ -888,6 +890,11 @@ __global__ void __launch_bounds__(POST ? 512 : 1024) gemv_kernel(GemvArgs a) {
     constexpr int CDW = Fmt<QT>::kBufBytes / 4;
     constexpr int CI = Fmt<QT>::kCI;
     constexpr int NOUT = PAIR ? G / 2 : G;
+    // the normed residual hand-over (xw / ssp out, ss in) is for one-segment
+    // GEMVs without the residual update; launch_gemv rejects other mixes, and
+    // leaving its registers out of the pair and residual-update kernels keeps
+    // their prologue loads clear of the register allocator
+    constexpr bool kHandOver = !PAIR && !POST;
     extern __shared__ __align__(16) uint32_t lds[];
     const int t = threadIdx.x, lane = t & 63, nw = blockDim.x >> 6;
     const int w = __builtin_amdgcn_readfirstlane(t >> 6);
@@ -940,7 +947,7 @@ __global__ void __launch_bounds__(POST ? 512 : 1024) gemv_kernel(GemvArgs a) {
     }
     // the producer's partial sums of squares (zero past its workgroups), 256
     // per load; a residual-add producer's norm weights for its first output
-    if (a.ss) {
+    if (kHandOver && a.ss) {
 #pragma unroll
         for (int i = 0; i < kMaxSsParts / 256; ++i)
             if (i < a.ss_loads)
@@ -950,7 +957,7 @@ __global__ void __launch_bounds__(POST ? 512 : 1024) gemv_kernel(GemvArgs a) {
                                ? (a.ngroups - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x
                                : 0) * NOUT;
     float wfirst = 0.0f;   // xw_w at this thread's first output row (the epilogue's j = t)
-    if (a.xw && t < nout_mine) {
+    if (kHandOver && a.xw && t < nout_mine) {
         const int gi = ((int)blockIdx.x) * G + t % NOUT + (t / NOUT) * (int)gridDim.x * G;
         asm volatile("global_load_dword %0, %1, off" : "=v"(wfirst) : "v"(a.xw_w + min(gi, a.rows_total - 1)));
     }
@@ -971,7 +978,7 @@ __global__ void __launch_bounds__(POST ? 512 : 1024) gemv_kernel(GemvArgs a) {
         pin8(pq);
     }
     asm volatile("" : "+v"(wfirst));
-    if (a.ss) {
+    if (kHandOver && a.ss) {
 #pragma unroll
         for (int i = 0; i < kMaxSsParts / 256; ++i)
             if (i < a.ss_loads) asm volatile("" : "+v"(sq[i]));
@@ -1093,15 +1100,16 @@ __global__ void __launch_bounds__(POST ? 512 : 1024) gemv_kernel(GemvArgs a) {
             acc[i] = d;
         }
         // group done: wave totals -> LDS -> sum over the chunk waves in order
-        if (a.ss && gl == 0) {   // x arrived normed but for the scale: r from the partial sums, in a fixed order
+        if (kHandOver && a.ss && gl == 0) {   // x arrived normed but for the scale: r from the partial sums, in a fixed order
             float ss = 0.0f;
 #pragma unroll
             for (int i = 0; i < kMaxSsParts / 256; ++i) {
                 if (i < a.ss_loads) {
-                    ss += sq[i].x;
-                    ss += sq[i].y;
-                    ss += sq[i].z;
-                    ss += sq[i].w;
+                    const int e = 256 * i + 4 * lane;
+                    ss += e < a.n_ss ? sq[i].x : 0.0f;
+                    ss += e + 1 < a.n_ss ? sq[i].y : 0.0f;
+                    ss += e + 2 < a.n_ss ? sq[i].z : 0.0f;
+                    ss += e + 3 < a.n_ss ? sq[i].w : 0.0f;
                 }
             }
             ss = wave_sum(ss);
@@ -1117,7 +1125,7 @@ __global__ void __launch_bounds__(POST ? 512 : 1024) gemv_kernel(GemvArgs a) {
                 for (int i = 0; i < nw; ++i) ss += ssred[i];
                 rscale = 1.0f / sqrtf(ss * a.inv_n + a.eps);
             }
-            if (a.ss && gl == 0) rscale = rss;
+            if (kHandOver && a.ss && gl == 0) rscale = rss;
             float s0 = 0.0f;
             for (int c = 0; c < nw; ++c) s0 += rd[c * G + t];
             s0 *= rscale;
@@ -1149,7 +1157,7 @@ __global__ void __launch_bounds__(POST ? 512 : 1024) gemv_kernel(GemvArgs a) {
             if (a.epilogue == EPI_ADD) {
                 const float nx = *y + out_lds[j];
                 *y = nx;
-                if (a.xw) {   // one segment: gi is the row
+                if (kHandOver && a.xw) {   // one segment: gi is the row
                     a.xw[gi] = nx * (j == t ? wfirst : a.xw_w[gi]);
                     ssq += nx * nx;
                 }
@@ -1158,7 +1166,7 @@ __global__ void __launch_bounds__(POST ? 512 : 1024) gemv_kernel(GemvArgs a) {
             }
         }
     }
-    if (a.xw) {   // the workgroup's sum: threads in order within waves, then waves in order
+    if (kHandOver && a.xw) {   // the workgroup's sum: threads in order within waves, then waves in order
         if (nout_mine <= 64) {   // every output is wave 0's: no barrier
             if (w == 0) {
                 ssq = wave_sum(ssq);
@@ -1371,11 +1379,14 @@ int launch_gemv(int type, const GemvBatch& b, int cols, const float* x, const fl
                 "gemv: normed residual output needs one residual-add segment");
     L3P_REQUIRE(!b.ss || (!norm && gemv_fp32_activation(type) && ((uintptr_t)b.ss & 15) == 0), L3P_E_INVALID,
                 "gemv: summed-square input needs fp32 activations and no norm");
+    L3P_REQUIRE(!(b.ss || b.xw) || (!b.post_y && !b.pair), L3P_E_INVALID,
+                "gemv: the normed residual hand-over takes one-segment launches without a residual update");
     a.xw = b.xw;
     a.xw_w = b.xw_w;
     a.ssp = b.ssp;
     a.ss = b.ss;
     a.ss_loads = (b.n_ss + 255) / 256;
+    a.n_ss = b.n_ss;
     L3P_REQUIRE(!b.ss || (b.n_ss > 0 && b.n_ss <= kMaxSsParts), L3P_E_INVALID, "gemv: %d sums of squares", b.n_ss);
     // Rows per group G: the largest of 16, 8, 4 that still gives about six
     // waves per CU (groups x column chunks); ring depth 3.  (Measured on

@@ -127,7 +127,9 @@ struct GemvBatch {
     // Optional, for a residual add (EPI_ADD, one segment): every output i
     // also goes to xw[i] as y[i] * xw_w[i] (the next RMSNorm's weights), and
     // ssp[g] receives workgroup g's sum of y[i]^2 over its outputs, in a
-    // fixed order; ssp holds kMaxSsParts floats, zero past the written ones.
+    // fixed order; ssp holds kMaxSsParts floats, and entries past this
+    // launch's grid keep whatever an earlier, larger grid wrote (consumers
+    // read only the first n_ss).
     float* xw;
     const float* xw_w;
     float* ssp;

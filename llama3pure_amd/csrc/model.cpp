@@ -268,9 +268,9 @@ static Model* load_model(l3p_ctx* c, const void* bytes, size_t len, const l3p_lo
         if (tk->type == 9 && tk->atype == 8 && tk->alen > 0) m.vocab = (int)tk->alen;
     if (opts && opts->context_size > 0 && opts->context_size < m.seq_len) m.seq_len = opts->context_size;
     if (opts) {
-        L3P_REQUIRE(opts->swa_pattern >= 0 && opts->attn_softcap >= 0.0f, L3P_E_INVALID,
-                    "load: swa_pattern %d and attn_softcap %g must not be negative", opts->swa_pattern,
-                    (double)opts->attn_softcap);
+        L3P_REQUIRE(opts->swa_pattern >= 0 && opts->attn_softcap >= 0.0f && std::isfinite(opts->attn_softcap),
+                    L3P_E_INVALID, "load: swa_pattern %d and attn_softcap %g must be finite and not negative",
+                    opts->swa_pattern, (double)opts->attn_softcap);
         if (opts->swa_pattern > 0) m.swa_pattern = opts->swa_pattern;
         m.attn_softcap = opts->attn_softcap;
     }

@@ -22,7 +22,8 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 CPUREF_SO = os.path.join(HERE, "_build", "libcpuref.so")
 REF_SO = os.path.join(HERE, "_ref", "libref.so")
-REF_OMP_SO = os.path.join(HERE, "_ref", "libref_omp.so")
+REF_OMP_SO = os.path.join(HERE, "_ref", "libref_omp.so")          # -Ofast -fopenmp -march=x86-64-v3
+REF_OMP_V4_SO = os.path.join(HERE, "_ref", "libref_omp_v4.so")    # the same with -march=x86-64-v4 (AVX-512)
 REF_SRC = "/root/reference/llama3pure-c-engine.c"
 
 # GGML type ids (llama3pure-c-engine.c:95-113)

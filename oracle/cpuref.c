@@ -1156,7 +1156,7 @@ void l3o_attend_head(const uint8_t* q8, const uint8_t* kc, const uint8_t* vc, in
 }
 
 int l3o_set_attention(l3o_model* m, int swa_pattern, float attn_softcap) {
-    if (swa_pattern < 0 || !(attn_softcap >= 0.0f)) return -1;
+    if (swa_pattern < 0 || !(attn_softcap >= 0.0f) || isinf(attn_softcap)) return -1;
     if (swa_pattern > 0) m->swa_pattern = swa_pattern;
     m->attn_softcap = attn_softcap;
     return 0;

@@ -23,6 +23,13 @@ MODELS = {
     "llama_q4_k_m": dict(arch="llama", dim=512, hidden=1024, n_layers=4, n_heads=8, n_kv=2, vocab=2048, ctx=256,
                          qtype=synth.Q4_K, seed=4, norm_jitter=0.1,
                          qtypes={"ffn_down": synth.Q6_K, "attn_v": synth.Q6_K, "output": synth.Q6_K}),
+    # Q4_K_M's per-layer mix: ffn_down Q6_K in layers 0 and 2 and Q4_K in
+    # layers 1 and 3, so consecutive down GEMVs (each handing its sums of
+    # squares to the next q|k|v) run different kernels and launch plans
+    "llama_q4_k_m_alt": dict(arch="llama", dim=512, hidden=1024, n_layers=4, n_heads=8, n_kv=2, vocab=2048,
+                             ctx=256, qtype=synth.Q4_K, seed=14, norm_jitter=0.1,
+                             qtypes={"blk.0.ffn_down": synth.Q6_K, "blk.2.ffn_down": synth.Q6_K,
+                                     "attn_v": synth.Q6_K, "output": synth.Q6_K}),
     # Q5_K_M-, Q3_K_M- and Q2_K-style mixes
     "llama_q5_k_m": dict(arch="llama", dim=512, hidden=1024, n_layers=4, n_heads=8, n_kv=2, vocab=2048, ctx=256,
                          qtype=synth.Q5_K, seed=5, norm_jitter=0.1,

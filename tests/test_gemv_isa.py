@@ -6,8 +6,11 @@ that the compiler does not wait for them with
 vmcnt(0) (which would also wait for the weight copies issued after them);
 the kernel waits with its own s_waitcnt.  That is only correct if no other
 instruction reads or writes a destination register of those loads before
-the wait: the compiler does not know the loads are in flight.  This test
-compiles gemv.hip to assembly and checks every gemv_kernel instantiation.
+the wait: the compiler does not know the loads are in flight.  The wait
+also counts on the loads being older than every weight copy
+(global_load_lds) issued before it, so a load the compiler moved after a
+copy would make the wait too weak.  This test compiles gemv.hip to assembly
+and checks both for every gemv_kernel instantiation.
 """
 import os
 import re
@@ -31,10 +34,12 @@ def vregs(tok):
 
 def check_kernel(body):
     """Problems in one kernel's text: a pending load's register used before
-    the first inline-asm s_waitcnt vmcnt, or no such loads / wait at all."""
+    the first inline-asm s_waitcnt vmcnt, a pending load issued after a weight
+    copy, or no such loads / wait at all."""
     pending = set()
     in_asm = False
     waited = False
+    copied = False
     problems = []
     for line in body.split("\n"):
         s = line.strip()
@@ -50,7 +55,11 @@ def check_kernel(body):
             waited = True
             break
         toks = re.findall(r"v\[\d+:\d+\]|v\d+\b", s)
+        if not in_asm and s.startswith("global_load_lds"):
+            copied = True
         if in_asm and s.startswith("global_load_dword"):
+            if copied:
+                problems.append("prologue load after a weight copy: " + s)
             if vregs(toks[1]) & pending:
                 problems.append("address register of a pending load: " + s)
             pending |= vregs(toks[0])
@@ -82,8 +91,9 @@ def test_gemv_prologue_loads_untouched_until_waited(tmp_path):
 
 def test_checker_flags_early_use():
     """The checker itself: a read of a pending register before the wait, an
-    address register overwritten by an earlier pending load, and a missing
-    wait are reported; a clean sequence is not."""
+    address register overwritten by an earlier pending load, a prologue load
+    after a weight copy and a missing wait are reported; a clean sequence is
+    not."""
     load = ";;#ASMSTART\n\tglobal_load_dwordx4 v[10:13], v[2:3], off offset:0\n;;#ASMEND\n"
     wait = ";;#ASMSTART\n\ts_waitcnt vmcnt(6)\n;;#ASMEND\n"
     clean = load + "\tv_add_u32 v20, v21, v22\n\tglobal_load_lds_dwordx4 v[30:31], off nt\n" + wait + "\tv_mov_b32 v1, v11\n"
@@ -93,3 +103,5 @@ def test_checker_flags_early_use():
     clobbered = load + ";;#ASMSTART\n\tglobal_load_dwordx4 v[14:17], v[10:11], off offset:16\n;;#ASMEND\n" + wait
     assert any("address register" in p for p in check_kernel(clobbered))
     assert "no prologue wait found" in check_kernel(load + "\tv_mov_b32 v1, v2\n")
+    late = load + "\tglobal_load_lds_dwordx4 v[30:31], off nt\n" + load.replace("v[10:13]", "v[40:43]") + wait
+    assert any("after a weight copy" in p for p in check_kernel(late))

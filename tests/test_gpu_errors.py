@@ -73,6 +73,19 @@ def test_context_option(ctx, good):
     assert e.value.code == l3p.E_INVALID
 
 
+def test_attention_option_ranges(ctx, good):
+    """swa_pattern and attn_softcap (options without a counterpart in the
+    reference) must be finite and not negative: a negative value, an infinite
+    cap (cap * tanh(s / cap) would be inf * 0 = NaN for every score) and a NaN
+    cap are refused with L3P_E_INVALID, and the context then loads normally."""
+    for opts in (dict(swa_pattern=-1), dict(attn_softcap=-1.0), dict(attn_softcap=float("inf")),
+                 dict(attn_softcap=float("nan"))):
+        with pytest.raises(l3p.L3PError) as e:
+            ctx.load_gguf(good, **opts)
+        assert e.value.code == l3p.E_INVALID, opts
+    assert ctx.load_gguf(good, attn_softcap=50.0).attn_softcap == 50.0
+
+
 def test_out_of_memory_context(torch_gpu):
     """A context whose K/V cache cannot fit the GPU (40 layers x 64 KV heads
     of 256 x 262144 positions: 365 GB) fails with L3P_E_NOMEM after freeing

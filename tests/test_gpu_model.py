@@ -26,7 +26,8 @@ scale by one fp16 ulp (2^-10 relative).  The stated tolerances:
     many later quants; the reference's builds show the same spread);
   * greedy tokens identical for 32 free-running steps, or until a step whose
     oracle top-2 margin is within 2 * tolerance (a near-tie that the
-    reference's own builds may also resolve either way).
+    reference's own builds may also resolve either way), and in any case
+    for at least the first GREEDY_MIN_SAME steps.
 
 Norm weights are jittered around 1.0 as in trained models; with all-ones
 norms and Q4_0 embeddings the activations fall exactly on Q8_0 rounding ties,
@@ -42,6 +43,10 @@ from model_cases import (MODELS, REF_DRIFT, SINGLE_DRIFT, SINGLE_LAYER, SINGLE_T
                          single_layer_model, teacher_prompt)
 
 pytestmark = pytest.mark.gpu
+
+# free-running greedy steps that must be identical before a near-tie may end
+# the comparison (every case ran 32 of 32 when this was set)
+GREEDY_MIN_SAME = 16
 
 
 def tol_of(lo, name):
@@ -140,7 +145,8 @@ def test_teacher_forced_logits_and_kv(pair, ctx):
 
 
 def test_greedy_decode_identical(pair, ctx):
-    """Free-running greedy decode: same tokens as the oracle for 32 steps."""
+    """Free-running greedy decode: same tokens as the oracle for 32 steps,
+    or up to a near-tie after at least GREEDY_MIN_SAME identical steps."""
     name, g, m = pair
     rng = np.random.default_rng(12)
     prompt = rng.integers(0, m.vocab, 12).astype(np.int32)
@@ -156,6 +162,8 @@ def test_greedy_decode_identical(pair, ctx):
         if t_gpu != t_ref:
             assert margin(lo) <= 2 * tol_of(lo, name), \
                 f"{name} step {step}: token {t_gpu} != {t_ref} with top-2 margin {margin(lo):.3g}"
+            assert step >= GREEDY_MIN_SAME, \
+                f"{name}: tokens differ at step {step}, before {GREEDY_MIN_SAME} identical steps (a near-tie)"
             break
         same += 1
         pos += 1

@@ -29,6 +29,11 @@ CASES = {
     "llama_q4_k_m": dict(arch="llama", dim=256, hidden=512, n_layers=2, n_heads=8, n_kv=2, vocab=512, ctx=128,
                          qtype=synth.Q4_K, seed=4, norm_jitter=0.1,
                          qtypes={"ffn_down": synth.Q6_K, "attn_v": synth.Q6_K, "output": synth.Q6_K}),
+    # Q4_K_M's per-layer mix: ffn_down Q6_K in layers 0 and 2, Q4_K in 1 and 3
+    "llama_q4_k_m_alt": dict(arch="llama", dim=256, hidden=512, n_layers=4, n_heads=8, n_kv=2, vocab=512, ctx=128,
+                             qtype=synth.Q4_K, seed=14, norm_jitter=0.1,
+                             qtypes={"blk.0.ffn_down": synth.Q6_K, "blk.2.ffn_down": synth.Q6_K,
+                                     "attn_v": synth.Q6_K, "output": synth.Q6_K}),
     # the other K-quants: Q5_K_M-, Q3_K_M- and Q2_K-style mixes
     "llama_q5_k_m": dict(arch="llama", dim=256, hidden=512, n_layers=2, n_heads=8, n_kv=2, vocab=512, ctx=128,
                          qtype=synth.Q5_K, seed=5, norm_jitter=0.1,
@@ -78,6 +83,21 @@ def test_sampler_bit_identical(tmp_path):
     r = run(tmp_path, CASES["llama_q8_0"], n_pre=8, n_dec=16, sample=(0.9, 40, 0.9))
     assert r["ok"], r
     assert len(set(r["sampled"])) > 1   # genuinely sampling, not argmax
+
+
+def test_attention_options_refused_out_of_range(cpuref):
+    """The oracle's set_attention takes the library's option ranges: negative
+    swa_pattern or attn_softcap, an infinite cap (inf * tanh(s / inf) is NaN)
+    and a NaN cap are refused; 0 and finite caps are taken."""
+    m = cpuref.open_model(synth.synthetic_model(**CASES["gemma_swa"]))
+    try:
+        for pat, cap in ((-1, 0.0), (2, -1.0), (2, float("inf")), (2, float("nan"))):
+            with pytest.raises(ValueError):
+                m.set_attention(pat, cap)
+        m.set_attention(2, 50.0)
+        m.set_attention(0, 0.0)
+    finally:
+        m.close()
 
 
 @pytest.mark.skipif(not oracle.have_ref(), reason="oracle/_ref not built (make -C oracle ref)")

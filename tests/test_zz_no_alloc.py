@@ -2,8 +2,8 @@
 partials, no context), called through the C-ABI, against l3p_gemm on the same
 inputs: bit-identical outputs (the same kernels and the same launch plan), on
 two calls in a row, the second smaller, both splitting K so the file-scope
-partials are used; a shape whose partials exceed the array is rejected
-without a launch."""
+partials are used; the same call captured into a HIP graph and replayed; a
+shape whose partials exceed the array is rejected without a launch."""
 import ctypes as C
 
 import numpy as np
@@ -42,14 +42,55 @@ def test_gemm_static_equals_gemm(torch_gpu, qt):
             assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), (qt, rows, cols, batch)
 
 
+@pytest.mark.parametrize("qt", [synth.Q8_0, synth.Q4_0])
+def test_gemm_static_in_graph(torch_gpu, qt):
+    """For callers under graph capture: after one warm call (which looks up
+    the array's address and the launch plan), l3p_gemm_static is captured on
+    a stream into a graph; every replay, with eager work and synchronizations
+    between replays, equals l3p_gemm bit for bit.  4096 x 4096 x batch 8
+    splits K 8 ways (Q8_0), so the replays use the file-scope partials; Q4_0
+    runs the GEMV per batch row."""
+    torch = torch_gpu
+    L = l3p.lib()
+    rows, cols, batch = 4096, 4096, 8
+    with l3p.Context(0) as ctx:
+        w = torch.from_numpy(synth.random_blocks(qt, rows, cols, seed=11)).cuda()
+        x = torch.from_numpy(synth.random_x(cols, seed=12, batch=batch)).cuda()
+        y_ref = torch.full((batch, rows), float("nan"), device="cuda")
+        y_st = torch.full((batch, rows), float("nan"), device="cuda")
+        torch.cuda.synchronize()
+        ctx.gemm(qt, w, rows, cols, x, batch, cols, y_ref, rows)
+        ctx.synchronize()
+        ref = y_ref.cpu().numpy().view(np.uint32)
+        s = torch.cuda.Stream()
+        with torch.cuda.stream(s):
+            assert _static(L, qt, w, rows, cols, x, batch, y_st, s.cuda_stream) == l3p.OK   # warm
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            rc = _static(L, qt, w, rows, cols, x, batch, y_st, s.cuda_stream)
+        assert rc == l3p.OK, L.l3p_last_error(None).decode()
+        for rep in range(3):
+            y_st.fill_(float("nan"))
+            x.mul_(1.0)                 # eager work on the inputs between replays
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            assert np.array_equal(y_st.cpu().numpy().view(np.uint32), ref), (qt, rep)
+
+
 def test_gemm_static_rejects_oversized_partials(torch_gpu):
     torch = torch_gpu
     L = l3p.lib()
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    # T x 3 output tiles of 64 x 64 with 3 T below four workgroups per CU (so
+    # the plan splits K, here twice over 16 K steps): 2 x 192 x 64 T floats of
+    # partials, more than the 4 Mi of the file-scope array once T > 170
+    tiles = min(341, (4 * cus + 2) // 3 - 1)
+    if tiles <= 171:
+        pytest.skip(f"{cus} CUs: no shape of this form splits with partials past the array")
     with l3p.Context(0) as ctx:
-        # 255 x 3 output tiles of 64 x 64 (too few 64 x 128 tiles to fill the
-        # CUs unsplit) split twice: 2 x 192 x 16320 floats of partials, more
-        # than the 4 Mi of the file-scope array
-        rows, cols, batch = 16320, 1024, 192
+        rows, cols, batch = 64 * tiles, 1024, 192
         w = torch.zeros(rows * synth.row_bytes(synth.Q8_0, cols), dtype=torch.uint8, device="cuda")
         x = torch.zeros(batch * cols, device="cuda")
         y = torch.zeros(batch * rows, device="cuda")
