@@ -132,7 +132,11 @@ def gemma_prompt_decode(np, torch, l3p, synth, prompt_len=512, steps=128, warmup
     layers (swa_pattern 2, window 4096) and the attention score cap 50, next
     to the final logit cap 30.  The prompt is run once untimed (settling
     launch configurations) with `warmup` decode steps after it, then timed;
-    the decode steps then continue from the timed prompt."""
+    the decode steps then continue from the timed prompt as one
+    l3p_generate_sampled call (steps queued on the device ahead of the host,
+    which finishes each step's sampler in the reference's arithmetic and hands
+    the token back through pinned memory); `per_call_decode` times the same
+    steps as one synchronous l3p_decode call per token."""
     ctx = l3p.Context(0)
     img = synth.synthetic_model(qtype=synth.Q8_0, make_mat=synth.gpu_q8_0_maker(ctx, torch, 77), **GEMMA2_2B)
     mi = ctx.load_gguf(img, **GEMMA2_2B_LOAD)
@@ -148,15 +152,22 @@ def gemma_prompt_decode(np, torch, l3p, synth, prompt_len=512, steps=128, warmup
 
     ctx.prefill(prompt[:-1], 0)
     run(warmup, int(prompt[-1]), prompt_len - 1, 42)
+    ctx.generate_sampled(int(prompt[-1]), prompt_len - 1, warmup, rng=42, **sampler)
     ctx.synchronize()
     t0 = time.perf_counter()
     ctx.prefill(prompt[:-1], 0)
     ctx.synchronize()
     t_pre = time.perf_counter() - t0
     t0 = time.perf_counter()
-    tok, pos, rng = run(steps, int(prompt[-1]), prompt_len - 1, 42)
+    toks, rng = ctx.generate_sampled(int(prompt[-1]), prompt_len - 1, steps, rng=42, **sampler)
     ctx.synchronize()
     t_dec = time.perf_counter() - t0
+    tok = toks[-1]
+    t0 = time.perf_counter()
+    tok_c, _, rng_c = run(steps, int(prompt[-1]), prompt_len - 1, 42)
+    ctx.synchronize()
+    t_call = time.perf_counter() - t0
+    assert (tok_c, rng_c) == (tok, rng), "queued and per-call sampled decode disagree"
     ctx.profile(True)
     ctx.prefill(prompt[:-1], 0)
     pstats = ctx.profile_read()
@@ -169,7 +180,9 @@ def gemma_prompt_decode(np, torch, l3p, synth, prompt_len=512, steps=128, warmup
                         "soft-cap 30 from the GGUF",
             "layers": 26, "dim": 2304, "heads": 8, "kv_heads": 4, "head_dim": 256, "ffn": 9216, "vocab": 256000,
             "prefill": pre, "decode_steps": steps, "decode_ms": round(t_dec * 1e3, 2),
-            "decode_tok_s": round(steps / t_dec, 1), "last_token": int(tok)}
+            "decode_tok_s": round(steps / t_dec, 1), "last_token": int(tok),
+            "per_call_decode": {"call": "l3p_decode once per token from Python (synchronous)",
+                                "tok_s": round(steps / t_call, 1)}}
 
 
 def read_ceiling(ctx, torch, nbytes: int) -> float:

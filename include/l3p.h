@@ -180,6 +180,26 @@ int l3p_decode(l3p_ctx* ctx, int32_t token, int32_t pos, const l3p_sampler* s, u
 int l3p_generate_greedy(l3p_ctx* ctx, int32_t token, int32_t pos, int32_t max_steps, const int32_t* stop_ids,
                         int32_t n_stop, int32_t* out_tokens, int32_t* n_out);
 
+/* Sampled generation: the reference's decode loop (c:5289-5309) with
+ * generate_token at temperature > 0 (c:4766-4907) from (token, pos) for up
+ * to max_steps steps, never past the context.  Step i decodes position
+ * pos + i and writes its sampled token to out_tokens[i]; *rng is the
+ * xorshift64* state (c:4266-4276), advanced by one draw per step; it stops
+ * after the first token found in stop_ids[0..n_stop), which is written and
+ * counted (*n_out = tokens written).  The tokens and the final RNG state equal
+ * those of l3p_decode called step by step with the same sampler.  The top-k
+ * slots run on the device and the sampler's last part (c:4850-4907: expf,
+ * sort, top-p cut, draw) on the host in the reference's arithmetic; the steps
+ * are queued on the device ahead of the host, each step's embedding waiting
+ * on the device for the token the host hands over through pinned memory, so
+ * no launch waits for the host.  A step already queued behind a stop still
+ * runs with the stop token (the K/V rows of position pos + *n_out; its
+ * logits, l3p_logits_device, belong to no returned token).  temperature must
+ * be > 0 (0 is l3p_generate_greedy) and top_k in [1, 1024]. */
+int l3p_generate_sampled(l3p_ctx* ctx, int32_t token, int32_t pos, int32_t max_steps, const l3p_sampler* s,
+                         uint64_t* rng, const int32_t* stop_ids, int32_t n_stop, int32_t* out_tokens,
+                         int32_t* n_out);
+
 /* Sample from vocab logits already on the device (the sampler alone). */
 int l3p_sample(l3p_ctx* ctx, const float* logits_dev, int n, const l3p_sampler* s, uint64_t* rng,
                int32_t* out_token);

@@ -27,7 +27,7 @@ EXPORTS = [
     "l3p_dequant", "l3p_quantize_q8_0", "l3p_gemv", "l3p_gemm",
     "l3p_load_gguf", "l3p_get_model_info", "l3p_forward", "l3p_prefill", "l3p_decode", "l3p_generate_greedy",
     "l3p_sample", "l3p_logits_device", "l3p_copy_kv", "l3p_rope_row",
-    "l3p_profile", "l3p_profile_read", "l3p_stream_read", "l3p_gemm_static",
+    "l3p_profile", "l3p_profile_read", "l3p_stream_read", "l3p_gemm_static", "l3p_generate_sampled",
 ]
 
 
@@ -102,6 +102,8 @@ def lib() -> C.CDLL:
         "l3p_profile_read": (I, [P, C.POINTER(KernelStat), I, C.POINTER(I)]),
         "l3p_stream_read": (I, [P, P, C.c_size_t]),
         "l3p_gemm_static": (I, [I, P, I, I, P, I, I, P, I, P]),
+        "l3p_generate_sampled": (I, [P, C.c_int32, C.c_int32, C.c_int32, C.POINTER(Sampler), C.POINTER(C.c_uint64),
+                                     P, C.c_int32, P, C.POINTER(C.c_int32)]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)
@@ -226,6 +228,22 @@ class Context:
         self._check(self.L.l3p_generate_greedy(self.h, token, pos, max_steps, stops.ctypes.data if stops.size else None,
                                                stops.size, out.ctypes.data, C.byref(n)))
         return out[:n.value].tolist()
+
+    def generate_sampled(self, token: int, pos: int, max_steps: int, temperature=0.9, top_k=40, top_p=0.9,
+                         rng: int = 0, stop_ids=()):
+        """Sampled tokens of up to max_steps steps from (token, pos), ending
+        after the first stop id (included), and the final RNG state; queued
+        ahead on the device, the sampler finished on the host per step."""
+        import numpy as np
+        stops = np.ascontiguousarray(stop_ids, np.int32)
+        out = np.zeros(max(1, max_steps), np.int32)
+        n = C.c_int32()
+        s = Sampler(temperature, top_k, top_p, 0)
+        st = C.c_uint64(rng)
+        self._check(self.L.l3p_generate_sampled(self.h, token, pos, max_steps, C.byref(s), C.byref(st),
+                                                stops.ctypes.data if stops.size else None, stops.size,
+                                                out.ctypes.data, C.byref(n)))
+        return out[:n.value].tolist(), st.value
 
     def sample(self, logits_dev, n, temperature=0.0, top_k=40, top_p=0.9, rng: int = 0):
         s = Sampler(temperature, top_k, top_p, 0)

@@ -74,8 +74,11 @@ void l3p_destroy(l3p_ctx* c) {
     c->prof.release();
     if (c->gemm_ws) hipFree(c->gemm_ws);
     if (c->gen_host) hipHostFree(c->gen_host);
+    for (void* p : {(void*)c->smp_v, (void*)c->smp_i, (void*)c->smp_seq, (void*)c->smp_tok, (void*)c->smp_fail})
+        if (p) hipHostFree(p);
     for (hipEvent_t e : c->gen_ev)
         if (e) hipEventDestroy(e);
+    if (c->cap_stream) hipStreamDestroy(c->cap_stream);
     hipStreamDestroy(c->stream);
     delete c;
 }

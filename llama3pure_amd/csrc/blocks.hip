@@ -40,10 +40,35 @@ __global__ void dequant_kernel(int type, const uint8_t* __restrict__ s, int64_t 
 // rope.rope_cur is set), so that attention need not wait for the record to
 // find them.
 __global__ void embed_step_kernel(int type, const uint8_t* __restrict__ s, int n, float scale, float* __restrict__ y,
-                                  int token, int pos, int* step, RopeRows rope, const int* dtok, size_t rb) {
+                                  int token, int pos, int* step, RopeRows rope, const int* dtok, size_t rb,
+                                  HostToken ht) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (dtok) {   // the token the previous step's sampler left on the device; s is row 0
         token = *dtok;
+        s += (size_t)token * rb;
+    } else if (ht.word) {   // the token the host's sampler finish hands over; s is row 0
+        __shared__ int tok_s;
+        if (threadIdx.x == 0) {
+            const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+            uint64_t w = __hip_atomic_load(ht.word, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM);
+            while ((uint32_t)(w >> 32) != ht.seq) {
+                if (__builtin_amdgcn_s_memrealtime() - t0 > kHostWaitTicks) {   // the host never answered
+                    __hip_atomic_store(ht.fail, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                    w = 0;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(2);
+                w = __hip_atomic_load(ht.word, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM);
+            }
+            int t = (int)(uint32_t)w;
+            if (t < 0 || t >= ht.vocab) {
+                __hip_atomic_store(ht.fail, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                t = 0;
+            }
+            tok_s = t;
+        }
+        __syncthreads();
+        token = tok_s;
         s += (size_t)token * rb;
     }
     if (i < n) {
@@ -110,11 +135,11 @@ void launch_dequant(int type, const uint8_t* src, int64_t n, float* dst, hipStre
 }
 
 void launch_embed_row(int type, const uint8_t* row, int n, float scale, float* dst, int token, int pos, int* step,
-                      const RopeRows* rope, hipStream_t st, const int* dtok, size_t rb) {
+                      const RopeRows* rope, hipStream_t st, const int* dtok, size_t rb, HostToken ht) {
     RopeRows r{};
     if (rope) r = *rope;
     const int threads = std::max(n, r.rope_cur ? 4 * r.half : 0);
     hipLaunchKernelGGL(embed_step_kernel, dim3((threads + 255) / 256), dim3(256), 0, st, type, row, n, scale, dst,
-                       token, pos, step, r, dtok, rb);
+                       token, pos, step, r, dtok, rb, ht);
     L3P_HIP(hipGetLastError());
 }

@@ -894,7 +894,8 @@ __global__ void __launch_bounds__(POST ? 512 : 1024) gemv_kernel(GemvArgs a) {
     // GEMVs without the residual update; launch_gemv rejects other mixes, and
     // leaving its registers out of the pair and residual-update kernels keeps
     // their prologue loads clear of the register allocator
-    constexpr bool kHandOver = !PAIR && !POST;
+    constexpr bool kConsume = !PAIR && !POST;
+    constexpr bool kProduce = !PAIR && !POST;
     extern __shared__ __align__(16) uint32_t lds[];
     const int t = threadIdx.x, lane = t & 63, nw = blockDim.x >> 6;
     const int w = __builtin_amdgcn_readfirstlane(t >> 6);
@@ -947,7 +948,7 @@ __global__ void __launch_bounds__(POST ? 512 : 1024) gemv_kernel(GemvArgs a) {
     }
     // the producer's partial sums of squares (zero past its workgroups), 256
     // per load; a residual-add producer's norm weights for its first output
-    if (kHandOver && a.ss) {
+    if (kConsume && a.ss) {
 #pragma unroll
         for (int i = 0; i < kMaxSsParts / 256; ++i)
             if (i < a.ss_loads)
@@ -957,7 +958,7 @@ __global__ void __launch_bounds__(POST ? 512 : 1024) gemv_kernel(GemvArgs a) {
                                ? (a.ngroups - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x
                                : 0) * NOUT;
     float wfirst = 0.0f;   // xw_w at this thread's first output row (the epilogue's j = t)
-    if (kHandOver && a.xw && t < nout_mine) {
+    if (kProduce && a.xw && t < nout_mine) {
         const int gi = ((int)blockIdx.x) * G + t % NOUT + (t / NOUT) * (int)gridDim.x * G;
         asm volatile("global_load_dword %0, %1, off" : "=v"(wfirst) : "v"(a.xw_w + min(gi, a.rows_total - 1)));
     }
@@ -978,7 +979,7 @@ __global__ void __launch_bounds__(POST ? 512 : 1024) gemv_kernel(GemvArgs a) {
         pin8(pq);
     }
     asm volatile("" : "+v"(wfirst));
-    if (kHandOver && a.ss) {
+    if (kConsume && a.ss) {
 #pragma unroll
         for (int i = 0; i < kMaxSsParts / 256; ++i)
             if (i < a.ss_loads) asm volatile("" : "+v"(sq[i]));
@@ -1100,7 +1101,7 @@ __global__ void __launch_bounds__(POST ? 512 : 1024) gemv_kernel(GemvArgs a) {
             acc[i] = d;
         }
         // group done: wave totals -> LDS -> sum over the chunk waves in order
-        if (kHandOver && a.ss && gl == 0) {   // x arrived normed but for the scale: r from the partial sums, in a fixed order
+        if (kConsume && a.ss && gl == 0) {   // x arrived normed but for the scale: r from the partial sums, in a fixed order
             float ss = 0.0f;
 #pragma unroll
             for (int i = 0; i < kMaxSsParts / 256; ++i) {
@@ -1125,7 +1126,7 @@ __global__ void __launch_bounds__(POST ? 512 : 1024) gemv_kernel(GemvArgs a) {
                 for (int i = 0; i < nw; ++i) ss += ssred[i];
                 rscale = 1.0f / sqrtf(ss * a.inv_n + a.eps);
             }
-            if (kHandOver && a.ss && gl == 0) rscale = rss;
+            if (kConsume && a.ss && gl == 0) rscale = rss;
             float s0 = 0.0f;
             for (int c = 0; c < nw; ++c) s0 += rd[c * G + t];
             s0 *= rscale;
@@ -1157,7 +1158,7 @@ __global__ void __launch_bounds__(POST ? 512 : 1024) gemv_kernel(GemvArgs a) {
             if (a.epilogue == EPI_ADD) {
                 const float nx = *y + out_lds[j];
                 *y = nx;
-                if (kHandOver && a.xw) {   // one segment: gi is the row
+                if (kProduce && a.xw) {   // one segment: gi is the row
                     a.xw[gi] = nx * (j == t ? wfirst : a.xw_w[gi]);
                     ssq += nx * nx;
                 }
@@ -1166,7 +1167,7 @@ __global__ void __launch_bounds__(POST ? 512 : 1024) gemv_kernel(GemvArgs a) {
             }
         }
     }
-    if (kHandOver && a.xw) {   // the workgroup's sum: threads in order within waves, then waves in order
+    if (kProduce && a.xw) {   // the workgroup's sum: threads in order within waves, then waves in order
         if (nout_mine <= 64) {   // every output is wave 0's: no barrier
             if (w == 0) {
                 ssq = wave_sum(ssq);

@@ -208,7 +208,29 @@ struct RopeRows {
     int half;
     float* rope_cur;
 };
+// A token handed over by the host through coherent pinned memory: the step
+// waits until *word holds (seq << 32) | token (word null: no such wait).  The
+// wait is bounded (kHostWaitTicks of the 100 MHz realtime counter): past it,
+// or for a token outside [0, vocab), the step runs with token 0 and sets
+// *fail, which the host reports.
+struct HostToken {
+    const uint64_t* word;
+    uint32_t seq;
+    uint32_t* fail;
+    int vocab;
+};
+constexpr uint64_t kHostWaitTicks = 1000000000ull;   // 10 s
 // dtok: read the token from device memory instead (row is then row 0 and
-// rb the row stride in bytes)
+// rb the row stride in bytes); ht.word: wait for it from the host (likewise)
 void launch_embed_row(int type, const uint8_t* row, int n, float scale, float* dst, int token, int pos, int* step,
-                      const RopeRows* rope, hipStream_t s, const int* dtok = nullptr, size_t rb = 0);
+                      const RopeRows* rope, hipStream_t s, const int* dtok = nullptr, size_t rb = 0,
+                      HostToken ht = HostToken{});
+// Top-k slots published to coherent pinned host memory by the scan kernel:
+// the k values and indices, then *seq_word = seq once they are visible
+// (v null: not published).
+struct HostSlots {
+    float* v;
+    int* i;
+    uint32_t* seq_word;
+    uint32_t seq;
+};

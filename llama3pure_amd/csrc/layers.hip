@@ -1474,7 +1474,7 @@ __global__ void __launch_bounds__(1024) topk_groupmax_kernel(const float* __rest
 template <int R>
 __global__ void __launch_bounds__(1024) topk_scan_kernel(const float* __restrict__ l, int n, int k,
                                                          const float* __restrict__ gmax, int ng, float* out_v,
-                                                         int* out_i) {
+                                                         int* out_i, HostSlots pub) {
     static_assert(R >= 1 && R <= kSlotsPerLane, "slot rows");
     extern __shared__ __align__(16) float tl[];   // [2][kScanBlock] logits, then [2][256] group maxima
     float* tg = tl + 2 * kScanBlock;
@@ -1632,6 +1632,18 @@ __global__ void __launch_bounds__(1024) topk_scan_kernel(const float* __restrict
             const int s = lane + 64 * j;
             if (s < k) { out_v[s] = sv[j]; out_i[s] = si[j]; }
         }
+        if (pub.v) {   // the slots to the host, then the sequence word once they are visible there
+#pragma unroll
+            for (int j = 0; j < R; ++j) {
+                const int s = lane + 64 * j;
+                if (s < k) {
+                    __hip_atomic_store(pub.v + s, sv[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                    __hip_atomic_store(pub.i + s, si[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                }
+            }
+            __threadfence_system();
+            if (lane == 0) __hip_atomic_store(pub.seq_word, pub.seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+        }
     }
 }
 
@@ -1640,10 +1652,11 @@ __global__ void __launch_bounds__(1024) topk_scan_kernel(const float* __restrict
 // ---------------------------------------------------------------------------
 // launchers
 // ---------------------------------------------------------------------------
-void launch_embed_step(const Model& m, int token, int pos, hipStream_t s, const int* dtok) {
+void launch_embed_step(const Model& m, int token, int pos, hipStream_t s, const int* dtok, HostToken ht) {
     const RopeRows rope{{m.cos_d, m.sin_d, m.cos_s, m.sin_s}, m.hs / 2, m.rope_cur};
-    launch_embed_row(m.emb.type, m.emb.w + (dtok ? 0 : (size_t)token * m.emb.rb), m.emb.cols,
-                     m.is_gemma ? m.embed_scale : 0.0f, m.x, token, pos, m.step, &rope, s, dtok, m.emb.rb);
+    const bool later = dtok || ht.word;   // the token is read when the kernel runs
+    launch_embed_row(m.emb.type, m.emb.w + (later ? 0 : (size_t)token * m.emb.rb), m.emb.cols,
+                     m.is_gemma ? m.embed_scale : 0.0f, m.x, token, pos, m.step, &rope, s, dtok, m.emb.rb, ht);
 }
 
 void launch_rmsnorm_add_rows(const float* y, int ldy, const float* w, int n, float inv_n, float eps, float* x,
@@ -1903,7 +1916,7 @@ void launch_argmax(const float* l, int n, int* out, hipStream_t s, float* cv, in
 
 template <int R>
 static void launch_topk_scan(const float* l, int n, int k, const float* gmax, int ng, float* out_v, int* out_i,
-                             hipStream_t s) {
+                             hipStream_t s, HostSlots pub) {
     const size_t lds = (2 * (size_t)kScanBlock + 2 * 256) * 4;
     static bool lds_set = false;   // dynamic LDS above 64 KB must be allowed first
     if (!lds_set) {
@@ -1911,19 +1924,20 @@ static void launch_topk_scan(const float* l, int n, int k, const float* gmax, in
                                     (int)lds));
         lds_set = true;
     }
-    hipLaunchKernelGGL(topk_scan_kernel<R>, dim3(1), dim3(1024), lds, s, l, n, k, gmax, ng, out_v, out_i);
+    hipLaunchKernelGGL(topk_scan_kernel<R>, dim3(1), dim3(1024), lds, s, l, n, k, gmax, ng, out_v, out_i, pub);
     L3P_HIP(hipGetLastError());
 }
 
-void launch_topk_slots(const float* l, int n, int k, float* gmax, float* out_v, int* out_i, hipStream_t s) {
+void launch_topk_slots(const float* l, int n, int k, float* gmax, float* out_v, int* out_i, hipStream_t s,
+                       HostSlots pub) {
     L3P_REQUIRE(k >= 1 && k <= 64 * kSlotsPerLane && k <= n, L3P_E_UNSUPPORTED, "sampler: top_k=%d outside [1, %d]",
                 k, 64 * kSlotsPerLane);
     const int ng = sample_groups(n);
     hipLaunchKernelGGL(topk_groupmax_kernel, dim3((ng + 15) / 16), dim3(1024), 0, s, l, n, k, ng, gmax);
     L3P_HIP(hipGetLastError());
     const int rows = (k + 63) / 64;
-    if (rows <= 1) launch_topk_scan<1>(l, n, k, gmax, ng, out_v, out_i, s);
-    else if (rows <= 2) launch_topk_scan<2>(l, n, k, gmax, ng, out_v, out_i, s);
-    else if (rows <= 4) launch_topk_scan<4>(l, n, k, gmax, ng, out_v, out_i, s);
-    else launch_topk_scan<kSlotsPerLane>(l, n, k, gmax, ng, out_v, out_i, s);
+    if (rows <= 1) launch_topk_scan<1>(l, n, k, gmax, ng, out_v, out_i, s, pub);
+    else if (rows <= 2) launch_topk_scan<2>(l, n, k, gmax, ng, out_v, out_i, s, pub);
+    else if (rows <= 4) launch_topk_scan<4>(l, n, k, gmax, ng, out_v, out_i, s, pub);
+    else launch_topk_scan<kSlotsPerLane>(l, n, k, gmax, ng, out_v, out_i, s, pub);
 }

@@ -8,6 +8,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <chrono>
 #include <initializer_list>
 #include <memory>
 #include <new>
@@ -878,10 +879,11 @@ static bool graphs_enabled() {
 // record are written by an eager launch; the layers run as a replayed HIP
 // graph from the second step of each variant on (the first, eager, step also
 // settles every launch configuration).  Per-launch timing runs eagerly.
-static void forward_impl(l3p_ctx* c, int token, int pos, bool with_logits, const int* dtok = nullptr) {
+static void forward_impl(l3p_ctx* c, int token, int pos, bool with_logits, const int* dtok = nullptr,
+                         HostToken ht = HostToken{}) {
     Model& m = *c->model;
     hipStream_t s = c->stream;
-    launch_embed_step(m, token, pos, s, dtok);
+    launch_embed_step(m, token, pos, s, dtok, ht);
     c->attn_per_head = attention_per_head(m, pos);
     const int v = (with_logits ? 1 : 0) | (c->attn_per_head ? 2 : 0);
     if (c->prof.on || !graphs_enabled() || c->graph_runs[v]++ == 0) {
@@ -889,17 +891,24 @@ static void forward_impl(l3p_ctx* c, int token, int pos, bool with_logits, const
         return;
     }
     if (!c->graph[v]) {
+        // captured on an idle stream of its own, so that steps queued on the
+        // context stream (which may wait for the host) need not drain first;
+        // the layer launches take c->stream, which points there meanwhile
+        if (!c->cap_stream) L3P_HIP(hipStreamCreateWithFlags(&c->cap_stream, hipStreamNonBlocking));
+        hipStream_t cs = c->cap_stream;
         hipGraph_t g = nullptr;
-        L3P_HIP(hipStreamSynchronize(s));   // capture from an idle stream (steps may be queued ahead)
-        L3P_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+        L3P_HIP(hipStreamBeginCapture(cs, hipStreamCaptureModeThreadLocal));
+        c->stream = cs;
         try {
             layers_impl(c, with_logits);
         } catch (...) {
-            hipStreamEndCapture(s, &g);
+            c->stream = s;
+            hipStreamEndCapture(cs, &g);
             if (g) hipGraphDestroy(g);
             throw;
         }
-        L3P_HIP(hipStreamEndCapture(s, &g));
+        c->stream = s;
+        L3P_HIP(hipStreamEndCapture(cs, &g));
         hipError_t e = hipGraphInstantiate(&c->graph[v], g, nullptr, nullptr, 0);
         hipGraphDestroy(g);
         L3P_HIP(e);
@@ -1169,6 +1178,107 @@ int l3p_generate_greedy(l3p_ctx* c, int32_t token, int32_t pos, int32_t max_step
             throw;
         }
         L3P_HIP(hipStreamSynchronize(s));   // the steps queued past a stop
+        c->prof.collect();
+    });
+}
+
+// Sampled generation, the reference's decode loop (c:5289-5309) with
+// generate_token at temperature > 0 (c:4766-4907).  The host finishes each
+// step's sampler (sample_slots: the reference's expf, sort, cut and draw), so
+// a step's token is known only on the host; the device runs ahead anyway:
+// steps are queued two ahead, each step's top-k scan writes its k slots into
+// coherent pinned memory followed by a sequence word, the host spins on that
+// word, samples, and writes (seq << 32) | token into the pinned word that the
+// next step's embedding kernel is polling.  The only host round trip left on
+// the critical path is that handshake; no launch waits for the host.
+// Sequence numbers grow across calls, so a word left by an earlier call never
+// matches.  After a stop token the step already queued behind it runs with
+// that token (K/V rows of the next position, its logits and slots unused).
+int l3p_generate_sampled(l3p_ctx* c, int32_t token, int32_t pos, int32_t max_steps, const l3p_sampler* sp,
+                         uint64_t* rng, const int32_t* stop_ids, int32_t n_stop, int32_t* out_tokens,
+                         int32_t* n_out) {
+    return mguard(c, true, [&] {
+        Model& m = *c->model;
+        L3P_REQUIRE(out_tokens && n_out && sp && rng, L3P_E_INVALID, "generate: null argument");
+        *n_out = 0;
+        L3P_REQUIRE(max_steps >= 0 && n_stop >= 0 && (n_stop == 0 || stop_ids), L3P_E_INVALID,
+                    "generate: max_steps=%d, n_stop=%d", max_steps, n_stop);
+        L3P_REQUIRE(sp->temperature > 0.0f, L3P_E_INVALID, "generate_sampled: temperature %g (0 is greedy)",
+                    (double)sp->temperature);
+        L3P_REQUIRE(sp->top_k >= 1, L3P_E_INVALID, "sampler: top_k=%d", sp->top_k);
+        L3P_REQUIRE(token >= 0 && token < m.vocab, L3P_E_INVALID, "token %d out of range [0, %d)", token, m.vocab);
+        L3P_REQUIRE(pos >= 0 && pos < m.seq_len, L3P_E_INVALID, "pos %d out of range [0, %d)", pos, m.seq_len);
+        const int steps = std::min(max_steps, m.seq_len - pos);   // the reference's pos < max_tokens bound
+        if (steps == 0) return;
+        const int k = std::min(sp->top_k, m.vocab);                // c:4815-4816
+        L3P_REQUIRE(k <= sample_max_k(), L3P_E_UNSUPPORTED, "sampler: top_k=%d above %d", k, sample_max_k());
+        hipStream_t s = c->stream;
+        constexpr int S = l3p_ctx::kGenSlots;
+        if (!c->smp_v) {
+            const size_t kmax = (size_t)sample_max_k();
+            L3P_HIP(hipHostMalloc((void**)&c->smp_v, S * kmax * 4, hipHostMallocCoherent));
+            L3P_HIP(hipHostMalloc((void**)&c->smp_i, S * kmax * 4, hipHostMallocCoherent));
+            L3P_HIP(hipHostMalloc((void**)&c->smp_seq, S * 4, hipHostMallocCoherent));
+            L3P_HIP(hipHostMalloc((void**)&c->smp_tok, S * 8, hipHostMallocCoherent));
+            L3P_HIP(hipHostMalloc((void**)&c->smp_fail, 4, hipHostMallocCoherent));
+            for (int i = 0; i < S; ++i) {
+                c->smp_seq[i] = 0;
+                c->smp_tok[i] = 0;
+            }
+        }
+        L3P_HIP(hipStreamSynchronize(s));   // nothing of an earlier call still reads the words
+        *(volatile uint32_t*)c->smp_fail = 0;
+        const uint32_t base = c->smp_next;
+        c->smp_next += (uint32_t)steps + 1;
+        if (c->smp_next < base) c->smp_next = 1;   // wrapped (after ~4e9 steps): restart above 0
+        const int ng = std::max(256, sample_groups(m.vocab));
+        const size_t kmax = (size_t)sample_max_k();
+        constexpr int kAhead = 2;
+        static_assert(kAhead < S, "a slot is read before it is written again");
+        int issued = 0, done = 0;
+        auto seq = [&](int i) { return base + (uint32_t)i; };
+        auto publish = [&](int i, int t) {   // the token of step i, for step i + 1's embedding
+            __atomic_store_n(&c->smp_tok[i % S], ((uint64_t)seq(i) << 32) | (uint32_t)t, __ATOMIC_RELEASE);
+        };
+        auto issue = [&](int i) {
+            HostToken ht{};
+            if (i > 0) ht = HostToken{c->smp_tok + (i - 1) % S, seq(i - 1), c->smp_fail, m.vocab};
+            forward_impl(c, token, pos + i, true, nullptr, ht);
+            const int slot = i % S;
+            launch_topk_slots(m.logits, m.vocab, k, m.cand_val, m.cand_val + ng, m.cand_idx, s,
+                              HostSlots{c->smp_v + slot * kmax, c->smp_i + slot * kmax, c->smp_seq + slot, seq(i)});
+        };
+        try {
+            while (done < steps) {
+                while (issued < steps && issued < done + kAhead) issue(issued++);
+                const int slot = done % S;
+                const auto t0 = std::chrono::steady_clock::now();
+                while (__atomic_load_n(&c->smp_seq[slot], __ATOMIC_ACQUIRE) != seq(done)) {
+                    L3P_REQUIRE(__atomic_load_n(c->smp_fail, __ATOMIC_RELAXED) == 0, L3P_E_HIP,
+                                "generate_sampled: a step's token wait failed on the device");
+                    if (std::chrono::steady_clock::now() - t0 > std::chrono::seconds(10)) {
+                        const hipError_t q = hipStreamQuery(s);
+                        if (q != hipSuccess && q != hipErrorNotReady) L3P_HIP(q);
+                        throw L3pError{L3P_E_HIP, "generate_sampled: no top-k slots from the device in 10 s"};
+                    }
+                    __builtin_ia32_pause();
+                }
+                const int t = sample_slots(c->smp_v + slot * kmax, c->smp_i + slot * kmax, k, sp->temperature,
+                                           sp->top_p, rng);
+                publish(done, t);
+                out_tokens[done++] = t;
+                *n_out = done;
+                if (std::find(stop_ids, stop_ids + n_stop, t) != stop_ids + n_stop) break;
+            }
+        } catch (...) {
+            // release every queued step still waiting for a token, then drain
+            for (int i = done; i + 1 < issued; ++i) publish(i, 0);
+            (void)hipStreamSynchronize(s);
+            throw;
+        }
+        L3P_HIP(hipStreamSynchronize(s));   // the step queued past a stop
+        L3P_REQUIRE(__atomic_load_n(c->smp_fail, __ATOMIC_RELAXED) == 0, L3P_E_HIP,
+                    "generate_sampled: a step's token wait failed on the device");
         c->prof.collect();
     });
 }

@@ -118,6 +118,7 @@ struct l3p_ctx {
     // (index: with logits) and replayed; dropped when the model changes
     // decode graphs by variant: bit 0 logits, bit 1 per-head attention
     hipGraphExec_t graph[4] = {nullptr, nullptr, nullptr, nullptr};
+    hipStream_t cap_stream = nullptr;   // idle stream the graphs are captured on (made on first use)
     int graph_runs[4] = {0, 0, 0, 0};
     bool attn_per_head = false;   // the attention of the step being recorded
     // split-K partials of the prefill GEMM (allocated with the context, so
@@ -128,6 +129,16 @@ struct l3p_ctx {
     static constexpr int kGenSlots = 4;
     int* gen_host = nullptr;
     hipEvent_t gen_ev[kGenSlots] = {};
+    // l3p_generate_sampled: coherent pinned memory (made on first use) for
+    // the top-k slots each step publishes ([kGenSlots][max k] values and
+    // indices, then a sequence word per slot), the tokens the host hands back
+    // ((seq << 32) | token per slot) and the device's wait-failure word
+    float* smp_v = nullptr;
+    int* smp_i = nullptr;
+    uint32_t* smp_seq = nullptr;
+    uint64_t* smp_tok = nullptr;
+    uint32_t* smp_fail = nullptr;
+    uint32_t smp_next = 1;   // next sequence number (never 0: the words start at 0)
     void drop_graphs();
 };
 
@@ -138,7 +149,9 @@ void gemv_plain(l3p_ctx* c, int type, const GemvBatch& b, int cols, const float*
 // m.x = embedding row of `token` (times Gemma's scale), the device step record
 // {token, pos} that the layer kernels read and the RoPE rows of pos (m.rope_cur).
 // With dtok the token is read from device memory when the kernel runs.
-void launch_embed_step(const Model& m, int token, int pos, hipStream_t s, const int* dtok = nullptr);
+// With ht.word the token is the host's, waited for on the device (HostToken).
+void launch_embed_step(const Model& m, int token, int pos, hipStream_t s, const int* dtok = nullptr,
+                       HostToken ht = HostToken{});
 // QK-norm, RoPE, the K/V cache write and attention of one layer for the
 // step's position (c:3232-3359); out = [n_heads][head_dim].  The first form
 // reads the decode step's q, k, v and step record.
@@ -172,7 +185,9 @@ void launch_rmsnorm_rows(const float* x, int ldx, const float* w, int n, float i
 void launch_act_rows(float* h, const float* h2, int64_t n, bool gelu, hipStream_t s);
 void launch_softcap(float* logits, int n, float cap, hipStream_t s);
 void launch_argmax(const float* logits, int n, int* out, hipStream_t s, float* cv, int* ci);
-void launch_topk_slots(const float* logits, int n, int k, float* gmax, float* out_v, int* out_i, hipStream_t s);
+// with pub.v the slots also go to pinned host memory (HostSlots)
+void launch_topk_slots(const float* logits, int n, int k, float* gmax, float* out_v, int* out_i, hipStream_t s,
+                       HostSlots pub = HostSlots{});
 int sample_groups(int n);
 int sample_max_k();
 

@@ -1,8 +1,11 @@
-"""l3p_generate_greedy: the reference's greedy decode loop (c:5289-5309) with
-the steps queued on the device ahead of the host's token reads.  Its tokens
-must equal l3p_decode called step by step, which the model tests compare with
-the oracle; stop ids end the run after the stop token, and a run continued
-after a stop equals the uninterrupted one."""
+"""l3p_generate_greedy and l3p_generate_sampled: the reference's decode loop
+(c:5289-5309) with the steps queued on the device ahead of the host.  Greedy
+steps read the previous argmax from device memory; sampled steps wait on the
+device for the token the host's sampler finish hands over through pinned
+memory.  Their tokens (and, sampled, the final RNG state) must equal
+l3p_decode called step by step, which the model tests compare with the
+oracle; stop ids end the run after the stop token, and a run continued after
+a stop equals the uninterrupted one."""
 import numpy as np
 import pytest
 
@@ -19,6 +22,19 @@ def step_by_step(c, tok, pos, n):
         out.append(tok)
         pos += 1
     return out
+
+
+def sampled_step_by_step(c, tok, pos, n, rng, **smp):
+    out = []
+    for _ in range(n):
+        tok, rng = c.decode(tok, pos, rng=rng, **smp)
+        out.append(tok)
+        pos += 1
+    return out, rng
+
+
+SAMPLERS = [dict(temperature=0.9, top_k=40, top_p=0.9), dict(temperature=1.3, top_k=200, top_p=1.0),
+            dict(temperature=0.5, top_k=1, top_p=0.5)]
 
 
 @pytest.fixture(scope="module", params=["llama", "gemma3"])
@@ -80,3 +96,48 @@ def test_generate_bounds(model_ctx):
         with pytest.raises(l3p.L3PError) as e:
             c.generate_greedy(bad["token"], bad["pos"], bad["max_steps"])
         assert e.value.code == l3p.E_INVALID
+
+
+@pytest.mark.parametrize("smp", SAMPLERS, ids=["t0.9_k40_p0.9", "t1.3_k200_p1", "t0.5_k1"])
+def test_sampled_equals_step_by_step(model_ctx, smp):
+    """Queued sampled steps give l3p_decode's tokens and final RNG state; the
+    second half of the run crosses the attention-path switch at 448
+    positions, and a second call (later sequence numbers) repeats the first."""
+    arch, c, tok, pos = model_ctx
+    for p0 in (pos, 420):
+        gen, rng_g = c.generate_sampled(tok, p0, 48, rng=0x9E3779B97F4A7C15, **smp)
+        ref, rng_r = sampled_step_by_step(c, tok, p0, 48, 0x9E3779B97F4A7C15, **smp)
+        assert (gen, rng_g) == (ref, rng_r), (arch, p0, smp)
+        again, rng_a = c.generate_sampled(tok, p0, 48, rng=0x9E3779B97F4A7C15, **smp)
+        assert (again, rng_a) == (gen, rng_g)
+    print(f"[generate] {arch} sampled {smp}: first {gen[:6]}", flush=True)
+
+
+def test_sampled_stop_and_continue(model_ctx):
+    arch, c, tok, pos = model_ctx
+    smp = SAMPLERS[0]
+    full, rng_full = sampled_step_by_step(c, tok, pos, 30, 12345, **smp)
+    stop = full[9]
+    first = full.index(stop)
+    part, rng_p = c.generate_sampled(tok, pos, 30, rng=12345, stop_ids=[100000, stop], **smp)
+    assert part == full[:first + 1]
+    rest, rng_r = c.generate_sampled(part[-1], pos + len(part), 30 - len(part), rng=rng_p, **smp)
+    assert part + rest == full and rng_r == rng_full
+
+
+def test_sampled_bounds(model_ctx):
+    arch, c, tok, _ = model_ctx
+    seq = c.model_info().seq_len
+    assert len(c.generate_sampled(tok, seq - 3, 10, rng=7)[0]) == 3   # never past the context
+    assert c.generate_sampled(tok, 5, 0, rng=7) == ([], 7)
+    for bad in [dict(token=-1, pos=5, max_steps=4), dict(token=tok, pos=seq, max_steps=4),
+                dict(token=tok, pos=5, max_steps=-1), dict(token=tok, pos=5, max_steps=4, temperature=0.0),
+                dict(token=tok, pos=5, max_steps=4, top_k=0)]:
+        kw = dict(bad)
+        with pytest.raises(l3p.L3PError) as e:
+            c.generate_sampled(kw.pop("token"), kw.pop("pos"), kw.pop("max_steps"), rng=7, **kw)
+        assert e.value.code == l3p.E_INVALID, bad
+    # the context still works after the refused calls; top_k above the
+    # vocabulary keeps every logit (c:4815-4816)
+    smp = dict(temperature=0.9, top_k=600, top_p=0.95)
+    assert c.generate_sampled(tok, 5, 4, rng=7, **smp) == sampled_step_by_step(c, tok, 5, 4, 7, **smp)
