@@ -256,6 +256,58 @@ def calibrate_copy():
     print(json.dumps({"calibrate_copy_bytes": a.numel() * 4, "copies": 5}), flush=True)
 
 
+def copy_ceiling():
+    """An independent check of the streaming-read ceiling: at each size (the
+    Q8_0 4096 x 4096 weights, the 4-bit FFN shapes' weights, the Llama-3-8B
+    gate|up pair's, and 512 MiB) the runtime's device-to-device copy and
+    l3p_stream_read, each over buffers rotated through >= 1 GiB so the 256 MB
+    last-level cache serves none of them, each launch timed by its own
+    events; the median of >= 40 launches.  The copy reads N and writes N
+    bytes: its read side runs at N / t (the counters FETCH_SIZE and
+    WRITE_SIZE of the same run give the bytes each copy dispatch moves)."""
+    import torch
+
+    import llama3pure_amd as l3p
+
+    ctx = l3p.Context(0)
+    sizes = [("q8_0 4096x4096 weights", 4096 * 4352), ("q4_0 14336x4096 weights", 14336 * 2304),
+             ("q8_0 gate|up 28672x4096 weights", 28672 * 4352), ("512 MiB", 512 << 20)]
+    for name, nbytes in sizes:
+        nbytes = nbytes // 16 * 16
+        copies = max(2, -(-(1 << 30) // nbytes))
+        src = [torch.ones(nbytes // 4, dtype=torch.float32, device="cuda") for _ in range(copies)]
+        dst = [torch.empty_like(src[0]) for _ in range(2)]
+        torch.cuda.synchronize()
+        st = torch.cuda.current_stream()
+        ts = []
+        for i in range(max(40, 2 * copies) + copies):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(st)
+            dst[i % 2].copy_(src[i % copies])
+            b.record(st)
+            ts.append((a, b))
+        torch.cuda.synchronize()
+        us = sorted(a.elapsed_time(b) * 1e3 for a, b in ts[copies:])
+        t_copy = us[len(us) // 2]
+        del dst
+        for b in src:
+            ctx.stream_read(b, nbytes)
+        ctx.synchronize()
+        ctx.profile(True)
+        for i in range(max(40, 2 * copies)):
+            ctx.stream_read(src[i % copies], nbytes)
+        t_read = next(iter(ctx.profile_percentiles().values()))[1] * 1e3
+        ctx.profile(False)
+        del src
+        torch.cuda.empty_cache()
+        print(json.dumps({"bytes": nbytes, "what": name, "copy_us": round(t_copy, 2),
+                          "copy_read_side_GBps": round(nbytes / t_copy / 1e3, 1),
+                          "copy_total_GBps": round(2 * nbytes / t_copy / 1e3, 1),
+                          "stream_read_us": round(t_read, 2), "stream_read_GBps": round(nbytes / t_read / 1e3, 1)}),
+              flush=True)
+    ctx.close()
+
+
 def attn_sweep(shape: str):
     """Both decode attentions at several context lengths, for a kernel trace:
     a 2-layer model with the attention of Llama-3-8B (32 query / 8 KV heads,
@@ -473,6 +525,9 @@ def main():
     ap.add_argument("--no-gemma", action="store_true", help="skip the Gemma-2-2B prompt + sampled decode run")
     ap.add_argument("--layers", type=int, default=32,
                     help="layers of the model (32 = Llama-3-8B; fewer only for short counter-collection runs)")
+    ap.add_argument("--copy-ceiling", action="store_true",
+                    help="only the runtime's device-to-device copy and l3p_stream_read at the GEMV byte sizes "
+                         "(an independent check of the streaming-read ceiling)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only copy 512 MiB device-to-device 5 times (scale for rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     ap.add_argument("--gemv-shapes", action="store_true",
@@ -491,6 +546,9 @@ def main():
         return
     if a.calibrate_copy:
         calibrate_copy()
+        return
+    if a.copy_ceiling:
+        copy_ceiling()
         return
     if a.attn_sweep:
         attn_sweep(a.attn_sweep)

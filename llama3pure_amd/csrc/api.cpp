@@ -165,6 +165,7 @@ int l3p_gemv(l3p_ctx* c, int type, const void* w, int rows, int cols, const floa
         b.seg[0] = GemvSegment{(const uint8_t*)w, y, rows};
         b.nseg = 1;
         b.epilogue = EPI_STORE;
+        b.standalone = 1;
         gemv_plain(c, type, b, cols, x);
     });
 }

@@ -1257,16 +1257,19 @@ int launch_rows(GemvArgs a, hipStream_t st) {
     return a.xw ? grid : 0;
 }
 
-// Ring depth: 3 buffers per wave (deeper rings measured no faster on
-// MI355X for Q8_0 and Q6_K); 4 for chunks of at most 1280 bytes; 2 for the
-// 4 KB F16/BF16 and 8 KB F32 chunks of rows too wide for 3.
+// Ring depth: 3 buffers per wave, 4 and 5 for Q8_0 and Q6_K launches with
+// few waves per CU (see launch_type); 4 for chunks of at most 1280 bytes; 2
+// for the 4 KB F16/BF16 and 8 KB F32 chunks of rows too wide for 3.
 template <int QT, int G, bool PAIR, bool UA>
 int launch_nb(GemvArgs a, int nbuf, hipStream_t st) {
     if constexpr (Fmt<QT>::kBufBytes >= 4096) {
         if (nbuf == 2) return launch_rows<QT, G, 2, PAIR, UA>(a, st);
     }
-    if constexpr (Fmt<QT>::kChunkBytes <= 1280) {
+    if constexpr (Fmt<QT>::kChunkBytes <= 1280 || QT == L3P_Q8_0 || QT == L3P_Q6_K) {
         if (nbuf == 4) return launch_rows<QT, G, 4, PAIR, UA>(a, st);
+    }
+    if constexpr (QT == L3P_Q8_0 || QT == L3P_Q6_K) {
+        if (nbuf == 5) return launch_rows<QT, G, 5, PAIR, UA>(a, st);
     }
     return launch_rows<QT, G, 3, PAIR, UA>(a, st);
 }
@@ -1287,7 +1290,7 @@ int launch_g(GemvArgs a, bool pair, int G, int nbuf, hipStream_t st) {
 }
 
 template <int QT>
-int launch_type(GemvArgs a, bool pair, int G, hipStream_t st) {
+int launch_type(GemvArgs a, bool pair, int G, bool standalone, hipStream_t st) {
     const int units = pair ? a.rows[0] : a.rows_total;
     const int per = pair ? G / 2 : G;
     a.ngroups = (units + per - 1) / per;
@@ -1299,6 +1302,22 @@ int launch_type(GemvArgs a, bool pair, int G, hipStream_t st) {
     // three in flight: 5-6% faster at the Q4_0 and Q4_K FFN shapes, where
     // a 2-deep ring leaves too few bytes in flight per CU (measured on MI355X)
     if (Fmt<QT>::kChunkBytes <= 1280) nb = 4;
+    // A CU's stream runs at the bytes it has in flight over the ~0.6 us load
+    // latency, up to about 40 GB/s a CU (measured on MI355X): standalone Q8_0
+    // and Q6_K launches with few waves per CU (the 4096 x 4096 Q8_0 GEMV: 4
+    // waves a CU, two 2176-byte chunks each in flight) take a deeper ring,
+    // until about 28 KB per CU are in flight (4096 x 4096: 7.64 -> 6.85 us
+    // mean).  Inside the decode step the same rings were slower (the output
+    // projection 6.92 -> 7.36 us, q|k|v 8.08 -> 8.20 us), so it keeps three.
+    // The waves count the row's chunk columns as fractions (a 256-column
+    // last column is an eighth of a chunk).
+    if constexpr (QT == L3P_Q8_0 || QT == L3P_Q6_K) {
+        const double kb = standalone ? env_int("L3P_GEMV_INFLIGHT_KB", 28) : 0;
+        const double wpc = (double)std::min(a.ngroups, 4 * cus()) * a.cols / kChunkElems / cus();
+        while (nb < 5 && wpc * (nb - 1) * Fmt<QT>::kChunkBytes < kb * 1024 &&
+               (size_t)nw * (nb + 1) * Fmt<QT>::kBufBytes + 16384 <= 160 * 1024)
+            ++nb;
+    }
     if (row_bytes<QT>(a.cols) % 16 == 0) return launch_g<QT, false>(a, pair, G, nb, st);
     // Q4_K, Q5_K, F16, BF16 and F32 rows are always 16-byte multiples
     if constexpr (!Fmt<QT>::kAligned) return launch_g<QT, true>(a, pair, G, nb, st);
@@ -1412,20 +1431,21 @@ int launch_gemv(int type, const GemvBatch& b, int cols, const float* x, const fl
         if (G == 4 && nw <= 2 && !a.post_y && waves(8) >= 4L * cus()) G = 8;
     }
     const bool pr = b.pair != 0;
+    const bool sa = b.standalone != 0;
     switch (type) {
-    case L3P_Q8_0: return launch_type<L3P_Q8_0>(a, pr, G, st);
-    case L3P_Q4_0: return launch_type<L3P_Q4_0>(a, pr, G, st);
-    case L3P_Q4_1: return launch_type<L3P_Q4_1>(a, pr, G, st);
-    case L3P_Q5_0: return launch_type<L3P_Q5_0>(a, pr, G, st);
-    case L3P_Q5_1: return launch_type<L3P_Q5_1>(a, pr, G, st);
-    case L3P_IQ4_NL: return launch_type<L3P_IQ4_NL>(a, pr, G, st);
-    case L3P_Q2_K: return launch_type<L3P_Q2_K>(a, pr, G, st);
-    case L3P_Q3_K: return launch_type<L3P_Q3_K>(a, pr, G, st);
-    case L3P_Q4_K: return launch_type<L3P_Q4_K>(a, pr, G, st);
-    case L3P_Q5_K: return launch_type<L3P_Q5_K>(a, pr, G, st);
-    case L3P_Q6_K: return launch_type<L3P_Q6_K>(a, pr, G, st);
-    case L3P_F16: return launch_type<L3P_F16>(a, pr, G, st);
-    case L3P_F32: return launch_type<L3P_F32>(a, pr, G, st);
-    default: return launch_type<L3P_BF16>(a, pr, G, st);
+    case L3P_Q8_0: return launch_type<L3P_Q8_0>(a, pr, G, sa, st);
+    case L3P_Q4_0: return launch_type<L3P_Q4_0>(a, pr, G, sa, st);
+    case L3P_Q4_1: return launch_type<L3P_Q4_1>(a, pr, G, sa, st);
+    case L3P_Q5_0: return launch_type<L3P_Q5_0>(a, pr, G, sa, st);
+    case L3P_Q5_1: return launch_type<L3P_Q5_1>(a, pr, G, sa, st);
+    case L3P_IQ4_NL: return launch_type<L3P_IQ4_NL>(a, pr, G, sa, st);
+    case L3P_Q2_K: return launch_type<L3P_Q2_K>(a, pr, G, sa, st);
+    case L3P_Q3_K: return launch_type<L3P_Q3_K>(a, pr, G, sa, st);
+    case L3P_Q4_K: return launch_type<L3P_Q4_K>(a, pr, G, sa, st);
+    case L3P_Q5_K: return launch_type<L3P_Q5_K>(a, pr, G, sa, st);
+    case L3P_Q6_K: return launch_type<L3P_Q6_K>(a, pr, G, sa, st);
+    case L3P_F16: return launch_type<L3P_F16>(a, pr, G, sa, st);
+    case L3P_F32: return launch_type<L3P_F32>(a, pr, G, sa, st);
+    default: return launch_type<L3P_BF16>(a, pr, G, sa, st);
     }
 }

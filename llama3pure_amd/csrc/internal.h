@@ -117,6 +117,10 @@ struct GemvBatch {
     int nseg;
     int pair;      // 1: seg[0] and seg[1] are (gate, up) processed together
     int epilogue;  // GemvEpilogue
+    // 1: a launch on its own (l3p_gemv), not inside a decode step: Q8_0 and
+    // Q6_K rows then take a copy ring deep enough for the launch's waves per
+    // CU (measured faster there, slower inside the decode step)
+    int standalone;
     // Optional residual update before the GEMV's own norm (Gemma's post
     // norms): x := x + post_w * rmsnorm(post_y) with the GEMV's eps and width,
     // the updated x written to post_out (not x: the launch's workgroups all
