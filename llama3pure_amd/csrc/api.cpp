@@ -238,7 +238,7 @@ int l3p_gemm_static(int type, const void* w, int rows, int cols, const float* x,
                     "gemm_static: %d x %d x batch %d needs %zu floats of split-K partials, more than the %zu of the "
                     "static scratch; use l3p_gemm",
                     rows, cols, batch, plan.partial_floats, kGemmStaticScratchFloats);
-        launch_gemm_planned(j, plan, plan.nsplit > 1 ? gemm_static_scratch() : nullptr, st);
+        launch_gemm_planned(j, plan, plan.nsplit > 1 || plan.streamk ? gemm_static_scratch() : nullptr, st);
     });
 }
 

@@ -25,10 +25,16 @@
 //
 // One launch covers up to three matrices with the same K and X (q|k|v,
 // gate|up): blockIdx.x runs over the N tiles of the segments in order.  When
-// the tiles cannot give every CU four workgroups, K is split over blockIdx.z:
-// each split writes its fp32 partial tile to a workspace and
-// gemm_reduce_kernel adds the splits in split order, so results do not
-// depend on scheduling.
+// the tiles cannot give every CU four workgroups, the launch is stream-K:
+// the (tile, K step) pairs, tile by tile, are cut into P equal runs for P
+// resident workgroups, so every CU gets the same number of K steps (whole
+// splits of K did not divide evenly: Gemma-2-2B's output and down
+// projections gave 1152 workgroups of 8 and 36 steps for 1024 resident
+// slots).  Each run writes its fp32 partial of each tile it touches to
+// workspace slot j, j = its rank among the runs that share the tile, and
+// gemm_reduce_kernel adds the slots in order, so results do not depend on
+// scheduling.  (Splitting K over blockIdx.z, the same partials with equal
+// splits, remains for workspaces too small for the stream-K slots.)
 #include <algorithm>
 #include <cstdlib>
 #include <mutex>
@@ -62,7 +68,16 @@ struct GemmArgs {
     int nsplit, ksteps;    // K splits and kBK-steps per split
     float* part;           // [nsplit][m][ntot] partials when nsplit > 1
     int ntot;
+    int streamk;           // > 0: stream-K over that many workgroups (grid.x), nsplit = most slots of a tile
+    int kst;               // stream-K: kBK steps of a whole tile
 };
+
+// Stream-K bookkeeping: the runs of P workgroups cut the tile-major sequence
+// of W (tile, K step) pairs at floor(p W / P); the run holding pair x is
+// ((x + 1) P - 1) / W.
+__host__ __device__ __forceinline__ int sk_owner(long x, long W, int P) {
+    return (int)(((x + 1) * (long)P - 1) / W);
+}
 
 // The global data of one K step, held in registers from the step before so
 // that its loads are in flight while the matrix cores work on the current
@@ -140,33 +155,42 @@ __device__ __forceinline__ void store_step(float* xs, float* ws, const StepRegs<
     }
 }
 
+// The output tile a workgroup works on: segment, its weights and output
+// features, first output feature and first batch row.
+struct TileRef {
+    int sg, N, n0, m0;
+    const uint8_t* W;
+};
+template <int BN>
+__device__ __forceinline__ TileRef tile_ref(const GemmArgs& a, int tile, int mtile) {
+    TileRef r;
+    r.sg = (a.nseg > 1 && tile >= a.tbeg[1]) ? ((a.nseg > 2 && tile >= a.tbeg[2]) ? 2 : 1) : 0;
+    r.W = a.w[r.sg];
+    r.N = a.n[r.sg];
+    r.n0 = (tile - a.tbeg[r.sg]) * BN;
+    r.m0 = mtile * kBM;
+    return r;
+}
+
+// acc := this wave's 32 x 32 block of the tile's sum over K [kbeg, kend)
 template <int QT, int BN>
-__global__ void __launch_bounds__(4 * BN) gemm_kernel(GemmArgs a) {
-    __shared__ __align__(16) float xs[kBM * kLDK];
-    __shared__ __align__(16) float ws[BN * kLDK];
+__device__ __forceinline__ void tile_mma(const GemmArgs& a, const TileRef& tr, int kbeg, int kend, float* xs,
+                                         float* ws, floatx4 (&acc)[2][2]) {
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-    const int tile = blockIdx.x;
-    const int sg = (a.nseg > 1 && tile >= a.tbeg[1]) ? ((a.nseg > 2 && tile >= a.tbeg[2]) ? 2 : 1) : 0;
-    const uint8_t* W = a.w[sg];
-    const int N = a.n[sg];
-    const int n0 = (tile - a.tbeg[sg]) * BN, m0 = blockIdx.y * kBM;
-    const int kbeg = blockIdx.z * a.ksteps * kBK, kend = min(a.k, kbeg + a.ksteps * kBK);
     constexpr int WN = BN / 32;              // waves across N
     const int wm = w / WN, wn = w % WN;      // this wave's 32 x 32 block of the 64 x BN tile
     const int g = lane >> 4, i16 = lane & 15;
-    floatx4 acc[2][2];
 #pragma unroll
     for (int im = 0; im < 2; ++im)
 #pragma unroll
         for (int in = 0; in < 2; ++in) acc[im][in] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-
     StepRegs<QT> sr;
-    fetch_step<QT, BN>(sr, a, W, N, m0, n0, kbeg, t);
+    fetch_step<QT, BN>(sr, a, tr.W, tr.N, tr.m0, tr.n0, kbeg, t);
     for (int k0 = kbeg; k0 < kend; k0 += kBK) {
-        store_step<QT, BN>(xs, ws, sr, a, W, N, n0, k0, t);
+        store_step<QT, BN>(xs, ws, sr, a, tr.W, tr.N, tr.n0, k0, t);
         __syncthreads();
         // the next step's loads go out before this step's matrix work
-        if (k0 + kBK < kend) fetch_step<QT, BN>(sr, a, W, N, m0, n0, k0 + kBK, t);
+        if (k0 + kBK < kend) fetch_step<QT, BN>(sr, a, tr.W, tr.N, tr.m0, tr.n0, k0 + kBK, t);
 #pragma unroll
         for (int kk = 0; kk < kBK; kk += 16) {
             float4 af[2], bf[2];
@@ -190,21 +214,30 @@ __global__ void __launch_bounds__(4 * BN) gemm_kernel(GemmArgs a) {
         }
         __syncthreads();
     }
+}
+
+// The tile's results: to Y (slot < 0) or to partial slot `slot`.
+template <int BN>
+__device__ __forceinline__ void tile_store(const GemmArgs& a, const TileRef& tr, int slot, const floatx4 (&acc)[2][2]) {
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    constexpr int WN = BN / 32;
+    const int wm = w / WN, wn = w % WN;
+    const int g = lane >> 4, i16 = lane & 15;
     // D layout of the 16 x 16 tile: lane (g, i16) holds rows 4g..4g+3 of column i16
-    float* const Y = a.y[sg];
-    const int ldy = a.ldy[sg];
-    float* const P = a.nsplit > 1 ? a.part + (size_t)blockIdx.z * a.m * a.ntot + a.noff[sg] : nullptr;
+    float* const Y = a.y[tr.sg];
+    const int ldy = a.ldy[tr.sg];
+    float* const P = slot >= 0 ? a.part + (size_t)slot * a.m * a.ntot + a.noff[tr.sg] : nullptr;
 #pragma unroll
     for (int im = 0; im < 2; ++im)
 #pragma unroll
         for (int in = 0; in < 2; ++in) {
-            const int n = n0 + 32 * wn + 16 * in + i16;
+            const int n = tr.n0 + 32 * wn + 16 * in + i16;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int m = m0 + 32 * wm + 16 * im + 4 * g + r;
-                if (m < a.m && n < N) {
+                const int m = tr.m0 + 32 * wm + 16 * im + 4 * g + r;
+                if (m < a.m && n < tr.N) {
                     const float v = acc[im][in][r];
-                    if (a.nsplit > 1) {
+                    if (slot >= 0) {
                         P[(size_t)m * a.ntot + n] = v;
                     } else {
                         float* p = Y + (size_t)m * ldy + n;
@@ -215,23 +248,57 @@ __global__ void __launch_bounds__(4 * BN) gemm_kernel(GemmArgs a) {
         }
 }
 
-// Y (=|+=) the sum of the K splits' partials, in split order: one thread per
-// output, blockIdx.y = batch row.
+template <int QT, int BN>
+__global__ void __launch_bounds__(4 * BN) gemm_kernel(GemmArgs a) {
+    __shared__ __align__(16) float xs[kBM * kLDK];
+    __shared__ __align__(16) float ws[BN * kLDK];
+    floatx4 acc[2][2];
+    if (a.streamk) {
+        // this workgroup's run [s0, s1) of the tile-major (tile, K step) pairs
+        const int NT = a.tbeg[a.nseg], S = a.kst, P = (int)gridDim.x;
+        const long W = (long)NT * ((a.m + kBM - 1) / kBM) * S;
+        const long s1 = ((long)blockIdx.x + 1) * W / P;
+        for (long s = (long)blockIdx.x * W / P; s < s1;) {
+            const int tt = (int)(s / S), kb = (int)(s % S);
+            const int ke = (int)min((long)S, kb + (s1 - s));
+            const TileRef tr = tile_ref<BN>(a, tt % NT, tt / NT);
+            tile_mma<QT, BN>(a, tr, kb * kBK, min(a.k, ke * kBK), xs, ws, acc);
+            tile_store<BN>(a, tr, (int)blockIdx.x - sk_owner((long)tt * S, W, P), acc);
+            s += ke - kb;
+        }
+        return;
+    }
+    const TileRef tr = tile_ref<BN>(a, blockIdx.x, blockIdx.y);
+    const int kbeg = blockIdx.z * a.ksteps * kBK, kend = min(a.k, kbeg + a.ksteps * kBK);
+    tile_mma<QT, BN>(a, tr, kbeg, kend, xs, ws, acc);
+    tile_store<BN>(a, tr, a.nsplit > 1 ? (int)blockIdx.z : -1, acc);
+}
+
+// Y (=|+=) the sum of the K splits' partials, in split order (stream-K: the
+// slots of the output's tile, in slot order): one thread per output,
+// blockIdx.y = batch row.
 __global__ void __launch_bounds__(256) gemm_reduce_kernel(GemmArgs a) {
     const int c = blockIdx.x * 256 + threadIdx.x, m = blockIdx.y;
     if (c >= a.ntot) return;
     const int sg = (a.nseg > 1 && c >= a.noff[1]) ? ((a.nseg > 2 && c >= a.noff[2]) ? 2 : 1) : 0;
+    int nslot = a.nsplit;
+    if (a.streamk) {   // 64-wide tiles
+        const int NT = a.tbeg[a.nseg], S = a.kst;
+        const long W = (long)NT * ((a.m + kBM - 1) / kBM) * S;
+        const long tt = (long)(m / kBM) * NT + a.tbeg[sg] + (c - a.noff[sg]) / 64;
+        nslot = sk_owner((tt + 1) * S - 1, W, a.streamk) - sk_owner(tt * S, W, a.streamk) + 1;
+    }
     const float* p = a.part + (size_t)m * a.ntot + c;
     const size_t zs = (size_t)a.m * a.ntot;
     float v = p[0];
-    for (int z = 1; z < a.nsplit; ++z) v += p[z * zs];
+    for (int z = 1; z < nslot; ++z) v += p[z * zs];
     float* y = a.y[sg] + (size_t)m * a.ldy[sg] + (c - a.noff[sg]);
     *y = a.add ? *y + v : v;
 }
 
 template <int QT>
 void launch_typed(const GemmArgs& a, int bn, hipStream_t st) {
-    const dim3 grid(a.tbeg[a.nseg], (a.m + kBM - 1) / kBM, a.nsplit);
+    const dim3 grid = a.streamk ? dim3(a.streamk) : dim3(a.tbeg[a.nseg], (a.m + kBM - 1) / kBM, a.nsplit);
     if (bn == 128) launch_kernel(gemm_kernel<QT, 128>, grid, dim3(512), 0u, st, a);
     else launch_kernel(gemm_kernel<QT, 64>, grid, dim3(256), 0u, st, a);
 }
@@ -271,9 +338,27 @@ GemmPlan gemm_plan(const GemmJob& j, size_t ws_floats) {
         p.nsplit = 1;
         return p;
     }
-    // K splits while the tiles give fewer than four workgroups per CU (the
-    // LDS of four fits a CU), each split at least eight K steps long
+    // Stream-K while the tiles give fewer than four workgroups per CU (the
+    // LDS of four fits a CU): as many workgroups as fit at once, each run at
+    // least eight K steps long, when the workspace holds the slots
     const int want = 4 * device_cus();
+    if (ws_floats && j.m > 0 && (long)tiles * mt < want) {
+        const long W = (long)tiles * mt * steps;
+        const int P = (int)std::min<long>(want, W / 8);
+        if (P > tiles * mt / 2 && P > 1) {   // fewer runs than tiles: plain tiles do as well
+            int slots = 1;
+            for (long tt = 0; tt < (long)tiles * mt; ++tt)
+                slots = std::max(slots, sk_owner((tt + 1) * steps - 1, W, P) - sk_owner(tt * steps, W, P) + 1);
+            if ((size_t)slots * j.m * ntot <= ws_floats) {
+                p.streamk = P;
+                p.ksteps = steps;
+                p.nsplit = slots;
+                p.partial_floats = (size_t)slots * j.m * ntot;
+                return p;
+            }
+        }
+    }
+    // otherwise K splits, each at least eight K steps long
     int split = 1;
     if (ws_floats && j.m > 0 && (long)tiles * mt < want) {
         split = std::min({(int)((want + (long)tiles * mt - 1) / ((long)tiles * mt)), steps / 8, 8});
@@ -323,7 +408,10 @@ void launch_gemm_planned(const GemmJob& j, const GemmPlan& plan, float* ws, hipS
     a.ntot = ntot;
     a.ksteps = plan.ksteps;
     a.nsplit = plan.nsplit;
-    a.part = a.nsplit > 1 ? ws : nullptr;
+    a.streamk = plan.streamk;
+    a.kst = plan.ksteps;
+    a.part = (a.nsplit > 1 || a.streamk) ? ws : nullptr;
+    L3P_REQUIRE(!a.streamk || (plan.bn == 64 && ws), L3P_E_INVALID, "gemm: stream-K plan without a workspace");
     switch (j.type) {
     case L3P_Q8_0: launch_typed<L3P_Q8_0>(a, plan.bn, st); break;
     case L3P_Q2_K: launch_typed<L3P_Q2_K>(a, plan.bn, st); break;
@@ -335,7 +423,8 @@ void launch_gemm_planned(const GemmJob& j, const GemmPlan& plan, float* ws, hipS
     case L3P_F32: launch_typed<L3P_F32>(a, plan.bn, st); break;
     default: launch_typed<L3P_BF16>(a, plan.bn, st); break;
     }
-    if (a.nsplit > 1) launch_kernel(gemm_reduce_kernel, dim3((ntot + 255) / 256, j.m), dim3(256), 0u, st, a);
+    if (a.nsplit > 1 || a.streamk)
+        launch_kernel(gemm_reduce_kernel, dim3((ntot + 255) / 256, j.m), dim3(256), 0u, st, a);
 }
 
 // ---------------------------------------------------------------------------

@@ -61,9 +61,11 @@
 #include "device_common.h"
 #include "internal.h"
 
+#include <algorithm>
 #include <map>
 #include <mutex>
 #include <tuple>
+#include <vector>
 
 namespace {
 
@@ -274,6 +276,10 @@ struct GemvArgs {
     const float* ss;
     int ss_loads;
     int n_ss;
+    // > 0 (not pair mode): workgroup b takes the rows [b * rpw, (b + 1) *
+    // rpw) in groups of G, the last group cut short; 0: the groups b, b +
+    // gridDim.x, b + 2 * gridDim.x, ... of G consecutive rows each
+    int rpw;
 };
 
 // Row `i` of the concatenated row space -> (segment, local row).
@@ -294,6 +300,7 @@ __device__ __forceinline__ void seg_of(const GemvArgs& a, int i, int& s, int& r)
 struct Cursor {
     const uint8_t *w0, *w1, *w2;
     int rows0, rows1, rows_total, ngroups, bid, gdim;
+    int rbeg, nmine;  // row ranges (rpw > 0): first row and rows of this workgroup, else nmine = -1
     uint32_t rb;      // row bytes
     uint32_t coff;    // byte offset of this wave's chunk column in a row
 };
@@ -310,7 +317,18 @@ __device__ __forceinline__ bool chunk_src(const Cursor& cc, int k, const uint8_t
     const uint8_t* base = cc.w0;
     int r;
     bool ok = j < cc.ngroups;
-    if (PAIR) {
+    if (!PAIR && cc.nmine >= 0) {   // row ranges: chunk k is row rbeg + k
+        r = cc.rbeg + k;
+        ok = k < cc.nmine;
+        if (ok && r >= cc.rows0) {
+            r -= cc.rows0;
+            base = cc.w1;
+            if (r >= cc.rows1) {
+                r -= cc.rows1;
+                base = cc.w2;
+            }
+        }
+    } else if (PAIR) {
         r = j * (G / 2) + (i % (G / 2));
         if (i >= G / 2) base = cc.w1;
         ok = ok && r < cc.rows0;
@@ -912,6 +930,10 @@ __global__ void __launch_bounds__(POST ? 512 : 1024) gemv_kernel(GemvArgs a) {
     cc.ngroups = a.ngroups;
     cc.bid = blockIdx.x;
     cc.gdim = gridDim.x;
+    // row ranges (rpw > 0, never in pair mode): this workgroup's rows
+    const bool ranges = !PAIR && a.rpw > 0;
+    cc.rbeg = (int)blockIdx.x * a.rpw;
+    cc.nmine = ranges ? max(0, min(a.rpw, a.rows_total - cc.rbeg)) : -1;
     cc.rb = rb;
     cc.coff = (uint32_t)w * (uint32_t)CB;
     const int nbytes = (int)min((uint32_t)CB, rb - cc.coff);   // this wave's chunk length
@@ -954,20 +976,21 @@ __global__ void __launch_bounds__(POST ? 512 : 1024) gemv_kernel(GemvArgs a) {
             if (i < a.ss_loads)
                 asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(sq[i]) : "v"(a.ss + 4 * lane + 256 * i));
     }
-    const int nout_mine = (a.ngroups > (int)blockIdx.x
-                               ? (a.ngroups - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x
-                               : 0) * NOUT;
+    const int ngroups_mine =
+        ranges ? (cc.nmine + G - 1) / G
+               : (a.ngroups > (int)blockIdx.x ? (a.ngroups - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x : 0);
+    const int nout_mine = ranges ? cc.nmine : ngroups_mine * NOUT;   // output rows of this workgroup
     float wfirst = 0.0f;   // xw_w at this thread's first output row (the epilogue's j = t)
     if (kProduce && a.xw && t < nout_mine) {
-        const int gi = ((int)blockIdx.x) * G + t % NOUT + (t / NOUT) * (int)gridDim.x * G;
+        const int gi = ranges ? cc.rbeg + t : ((int)blockIdx.x) * G + t % NOUT + (t / NOUT) * (int)gridDim.x * G;
         asm volatile("global_load_dword %0, %1, off" : "=v"(wfirst) : "v"(a.xw_w + min(gi, a.rows_total - 1)));
     }
 
     // ---- weight copies: the first NB-1 chunks of this workgroup's sequence,
-    // CI instructions each.  nk = number of row-chunks this wave processes.
-    const int ngroups_mine =
-        a.ngroups > (int)blockIdx.x ? (a.ngroups - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x : 0;
-    const int nk = ngroups_mine * G;
+    // CI instructions each.  nk = number of row-chunks this wave copies; with
+    // row ranges the slots of the last group past nk are neither copied nor
+    // waited for (their dots read a stale buffer and are dropped).
+    const int nk = ranges ? cc.nmine : ngroups_mine * G;
 #pragma unroll
     for (int b = 0; b < NB - 1; ++b)
         if (b < nk) issue(b, b);
@@ -1143,14 +1166,14 @@ __global__ void __launch_bounds__(POST ? 512 : 1024) gemv_kernel(GemvArgs a) {
     // ---- results of this workgroup's groups (every copy has been waited for)
     lds_sync();
     float ssq = 0.0f;   // this thread's sum of its new residuals' squares (xw set)
-    for (int j = t; j < ngroups_mine * NOUT; j += blockDim.x) {
+    for (int j = t; j < nout_mine; j += blockDim.x) {
         const int gk = j / NOUT, i = j % NOUT;
         const int grp = blockIdx.x + gk * gridDim.x;
         if (PAIR) {
             const int row = grp * NOUT + i;
             if (row < a.rows[0]) a.y[0][row] = out_lds[j];
         } else {
-            const int gi = grp * G + i;
+            const int gi = ranges ? cc.rbeg + j : grp * G + i;
             if (gi >= a.rows_total) continue;
             int s, row;
             seg_of(a, gi, s, row);
@@ -1249,7 +1272,41 @@ int launch_rows(GemvArgs a, hipStream_t st) {
         grid = (a.ngroups + k - 1) / k;
     }
     grid = std::max(grid, (a.ngroups * NOUT + kMaxOut - 1) / kMaxOut);
-    const size_t lds = lds_for(grid);
+    // Row ranges when they spread the rows at least 10% more evenly over the
+    // CUs.  The dispatcher places workgroup b on CU b mod CUs while every
+    // workgroup of the launch is resident (breadth first), so a grid that is
+    // not a multiple of the CUs loads some CUs with one workgroup more, and
+    // the launch ends with them: Gemma-2-2B's 2304-row GEMVs in groups of 4
+    // rows put 8 or 12 rows on a CU at 576 workgroups, 9 on every CU as 768
+    // ranges of 3 rows (output projection 4.02 -> 3.70 us, down projection
+    // 9.37 -> 8.76 us, measured on MI355X).  Small gains are left alone:
+    // ranges spread the workgroups' streams over the whole matrix instead of
+    // one band of it at a time, which made Gemma-2-2B's 590 MB LM head
+    // slower (112 -> 122 us) for 0.6% fewer rows on its busiest CU; rows
+    // dealt one by one over the workgroups kept the band but were no faster
+    // at the small shapes (4.04 and 9.11 us).
+    a.rpw = 0;
+    size_t lds = lds_for(grid);
+    if (!PAIR && env_int("L3P_GEMV_RANGES", 1)) {
+        const int n = cus();
+        auto worst_cu = [&](int g, int rpw) {   // most rows on one CU
+            std::vector<int> per(n, 0);
+            for (int b = 0; b < g; ++b)
+                per[b % n] += rpw ? std::max(0, std::min(rpw, a.rows_total - b * rpw))
+                                  : (a.ngroups - b + g - 1) / g * G;
+            return *std::max_element(per.begin(), per.end());
+        };
+        const int m = (grid + n - 1) / n;   // <= the workgroups per CU that fit (grid <= their count)
+        const int rpw = (a.rows_total + m * n - 1) / (m * n);
+        const int grid_r = (a.rows_total + rpw - 1) / rpw;
+        const size_t lds_r = base + (size_t)((rpw + G - 1) / G) * G * 4;
+        if ((rpw + G - 1) / G * G <= kMaxOut && lds_r <= lds_for(cus()) &&
+            10 * worst_cu(grid_r, rpw) <= 9 * worst_cu(grid, 0)) {
+            a.rpw = rpw;
+            grid = grid_r;
+            lds = lds_r;
+        }
+    }
     if (lds > 65536)
         L3P_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     if (grid > kMaxSsParts) a.xw = nullptr;   // too many partial sums: the next GEMV takes its norm itself

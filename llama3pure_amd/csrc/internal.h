@@ -185,8 +185,9 @@ void launch_gemm(const GemmJob& j, float* ws, size_t ws_floats, hipStream_t s);
 // K splits of a job and the fp32 partials they need, for a workspace of
 // ws_floats floats (0: no split)
 struct GemmPlan {
-    int nsplit = 1, ksteps = 0;
+    int nsplit = 1, ksteps = 0;   // stream-K: nsplit = most partial slots of a tile, ksteps = K steps of a tile
     int bn = 64;   // output columns per tile: 64, or 128 when those tiles fill the CUs unsplit
+    int streamk = 0;   // > 0: stream-K over that many workgroups
     size_t partial_floats = 0;
 };
 GemmPlan gemm_plan(const GemmJob& j, size_t ws_floats);

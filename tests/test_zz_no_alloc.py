@@ -1,8 +1,8 @@
 """l3p_gemm_static: the allocation-free l3p_gemm (file-scope split-K
 partials, no context), called through the C-ABI, against l3p_gemm on the same
 inputs: bit-identical outputs (the same kernels and the same launch plan), on
-two calls in a row, the second smaller, both splitting K so the file-scope
-partials are used; the same call captured into a HIP graph and replayed; a
+two calls in a row, the second smaller, both cutting K over several
+workgroups (stream-K) so the file-scope partials are used; the same call captured into a HIP graph and replayed; a
 shape whose partials exceed the array is rejected without a launch."""
 import ctypes as C
 
@@ -24,9 +24,9 @@ def test_gemm_static_equals_gemm(torch_gpu, qt):
     torch = torch_gpu
     L = l3p.lib()
     with l3p.Context(0) as ctx:
-        # rows x cols x batch: 64 output tiles of one 64-row tile, K split 8
-        # ways (partials of 8 x 8 x 4096 floats), then a smaller call split 4
-        # ways; for Q4_0 the GEMV per batch row
+        # rows x cols x batch: 64 output tiles of one 64-row tile whose K is
+        # cut over 8 workgroups each (partials of 8 x 8 x 4096 floats), then a
+        # smaller call cut over 4; for Q4_0 the GEMV per batch row
         for rows, cols, batch in ((4096, 4096, 8), (1024, 2048, 3)):
             w = torch.from_numpy(synth.random_blocks(qt, rows, cols, seed=rows + batch)).cuda()
             x = torch.from_numpy(synth.random_x(cols, seed=cols, batch=batch)).cuda()
@@ -48,8 +48,8 @@ def test_gemm_static_in_graph(torch_gpu, qt):
     the array's address and the launch plan), l3p_gemm_static is captured on
     a stream into a graph; every replay, with eager work and synchronizations
     between replays, equals l3p_gemm bit for bit.  4096 x 4096 x batch 8
-    splits K 8 ways (Q8_0), so the replays use the file-scope partials; Q4_0
-    runs the GEMV per batch row."""
+    cuts K over 8 workgroups per tile (Q8_0), so the replays use the
+    file-scope partials; Q4_0 runs the GEMV per batch row."""
     torch = torch_gpu
     L = l3p.lib()
     rows, cols, batch = 4096, 4096, 8
@@ -84,8 +84,9 @@ def test_gemm_static_rejects_oversized_partials(torch_gpu):
     L = l3p.lib()
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     # T x 3 output tiles of 64 x 64 with 3 T below four workgroups per CU (so
-    # the plan splits K, here twice over 16 K steps): 2 x 192 x 64 T floats of
-    # partials, more than the 4 Mi of the file-scope array once T > 170
+    # the plan cuts K over at least two workgroups per tile of 16 K steps):
+    # at least 2 x 192 x 64 T floats of partials, more than the 4 Mi of the
+    # file-scope array once T > 170
     tiles = min(341, (4 * cus + 2) // 3 - 1)
     if tiles <= 171:
         pytest.skip(f"{cus} CUs: no shape of this form splits with partials past the array")
