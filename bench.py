@@ -537,7 +537,7 @@ def main():
                     help="only run both decode attentions at 65..3001 positions of the named attention shape "
                          "(for a kernel trace)")
     ap.add_argument("--cpu-leg", help=argparse.SUPPRESS)
-    ap.add_argument("--cpu-kind", default="omp", choices=["omp", "o3", "port"], help=argparse.SUPPRESS)
+    ap.add_argument("--cpu-kind", default="omp", choices=["omp", "omp_v4", "o3", "port"], help=argparse.SUPPRESS)
     ap.add_argument("--cpu-start", type=int, default=0, help=argparse.SUPPRESS)
     a = ap.parse_args()
 
