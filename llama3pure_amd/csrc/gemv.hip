@@ -1210,6 +1210,222 @@ __global__ void __launch_bounds__(POST ? 512 : 1024) gemv_kernel(GemvArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// Q8_0 rows of 2048 < cols <= 2560 columns, cols = 256 J (Gemma-2-2B's 2304):
+// whole rows per wave.  The chunk-column kernel above gives such a row a
+// second wave for its last 256 or 512 columns, and that wave issues a whole
+// activation's worth of prologue loads (8 per vector, whatever few lanes
+// carry data) and copies its short chunk with as many instructions as a full
+// one.  Here one wave streams whole rows, RB = 272 J bytes each, copied with
+// kWideCI dwordx4 instructions into a private ring of NB buffers, and lane l
+// owns the columns 256 j + 4 l .. 256 j + 4 l + 3 for j < J: an activation
+// vector is J coalesced 16-byte loads per lane, a row's dot needs no
+// cross-wave sum (there is no barrier in the kernel), and the residual update
+// and the RMSNorm of the prologue reduce over the wave alone.  A workgroup is
+// one wave, persistent over groups of G rows as in gemv_kernel.
+//
+// Lane l's four columns of group j lie in block b = 8 j + l / 8, at quant
+// bytes 4 (l % 8) .. + 3, i.e. at byte 34 b + 2 + 4 (l % 8) of the row:
+// dword-aligned when b is odd and 2 bytes into a dword when b is even (b has
+// the parity of l / 8), so one alignbyte of two buffer dwords gives the four
+// quants.  The lane's term for the group is d_b * sum q x over its four
+// columns (gemv_kernel's d * sum q_j x_j, over four columns instead of 32).
+// ---------------------------------------------------------------------------
+constexpr int kWideCI = 3;                // copy instructions per row: RB <= 3 KB
+constexpr int kWideBufBytes = kWideCI * 1024;
+
+bool wide_cols(int cols) { return cols > kChunkElems && cols <= 2560 && cols % 256 == 0; }
+
+// Lane offsets of a row copy: piece i*64 + lane of the row's RB/16 pieces,
+// clamped to the last piece (clamped lanes re-read it and write it past RB in
+// the buffer), so every row is exactly kWideCI instructions.
+struct WideDma {
+    int o[kWideCI];
+};
+__device__ __forceinline__ WideDma wide_dma(int lane, uint32_t rb) {
+    const int last = (int)(rb >> 4) - 1;
+    WideDma d;
+#pragma unroll
+    for (int i = 0; i < kWideCI; ++i) d.o[i] = 16 * min(64 * i + lane, last);
+    return d;
+}
+__device__ __forceinline__ void wide_copy(uint32_t* dst, const uint8_t* src, const WideDma& d) {
+#pragma unroll
+    for (int i = 0; i < kWideCI; ++i) __builtin_amdgcn_global_load_lds(src + d.o[i], (lds_void*)(dst + 256 * i), 16, 0, 2);
+}
+
+// J untracked 16-byte loads per lane, 256 floats apart (see load8_async)
+template <int J>
+__device__ __forceinline__ void loadj_async(f32x4 (&q)[J], const float* p) {
+#pragma unroll
+    for (int j = 0; j < J; ++j) asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(q[j]) : "v"(p + 256 * j));
+}
+template <int J>
+__device__ __forceinline__ void pinj(f32x4 (&q)[J]) {
+#pragma unroll
+    for (int j = 0; j < J; ++j) asm volatile("" : "+v"(q[j]));
+}
+
+template <int J, int G, int NB, bool PAIR, bool POST>
+__global__ void __launch_bounds__(64) gemv_wide_kernel(GemvArgs a) {
+    constexpr int NOUT = PAIR ? G / 2 : G;
+    constexpr int BDW = kWideBufBytes / 4;
+    extern __shared__ __align__(16) uint32_t lds[];
+    float* xch = reinterpret_cast<float*>(lds + NB * BDW);   // [G] row totals of a group (pair epilogue)
+    const int lane = threadIdx.x;
+    const uint32_t rb = 272u * J;
+    Cursor cc;
+    cc.w0 = a.w[0];
+    cc.w1 = a.w[1];
+    cc.w2 = a.w[2];
+    cc.rows0 = a.rows[0];
+    cc.rows1 = a.rows[1];
+    cc.rows_total = a.rows_total;
+    cc.ngroups = a.ngroups;
+    cc.bid = blockIdx.x;
+    cc.gdim = gridDim.x;
+    cc.rbeg = 0;
+    cc.nmine = -1;
+    cc.rb = rb;
+    cc.coff = 0;
+    const WideDma dl = wide_dma(lane, rb);
+    auto issue = [&](int k, int slot) {
+        const uint8_t* src;
+        chunk_src<G, PAIR>(cc, k, src);
+        wide_copy(lds + slot * BDW, src, dl);
+    };
+
+    // ---- the lane's activation columns, norm weights and residual-update
+    // inputs, issued before the weight copies and waited for without them
+    f32x4 xq[J], nq[J], yq[J], pq[J];
+    loadj_async<J>(xq, a.x + 4 * lane);
+    if (a.norm) loadj_async<J>(nq, a.norm + 4 * lane);
+    if (POST) {
+        loadj_async<J>(yq, a.post_y + 4 * lane);
+        loadj_async<J>(pq, a.post_w + 4 * lane);
+    }
+    const int ngroups_mine =
+        a.ngroups > (int)blockIdx.x ? (a.ngroups - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x : 0;
+    const int nk = ngroups_mine * G;   // rows this wave copies
+#pragma unroll
+    for (int b = 0; b < NB - 1; ++b)
+        if (b < nk) issue(b, b);
+    wait_prologue<NB - 1, kWideCI>(nk);
+    pinj<J>(xq);
+    if (a.norm) pinj<J>(nq);
+    if (POST) {
+        pinj<J>(yq);
+        pinj<J>(pq);
+    }
+    float v[4 * J];   // v[4j + e] = x[256 j + 4 lane + e]
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        v[4 * j] = xq[j].x;
+        v[4 * j + 1] = xq[j].y;
+        v[4 * j + 2] = xq[j].z;
+        v[4 * j + 3] = xq[j].w;
+    }
+    // x := x + post_w * (r_y * post_y) (rmsnorm_add_kernel's arithmetic); the
+    // first workgroup stores it
+    if (POST) {
+        float sy = 0.0f;
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            sy += yq[j].x * yq[j].x;
+            sy += yq[j].y * yq[j].y;
+            sy += yq[j].z * yq[j].z;
+            sy += yq[j].w * yq[j].w;
+        }
+        sy = wave_sum(sy);
+        const float ry = 1.0f / sqrtf(sy * a.inv_n + a.eps);
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            v[4 * j] = v[4 * j] + pq[j].x * (ry * yq[j].x);
+            v[4 * j + 1] = v[4 * j + 1] + pq[j].y * (ry * yq[j].y);
+            v[4 * j + 2] = v[4 * j + 2] + pq[j].z * (ry * yq[j].z);
+            v[4 * j + 3] = v[4 * j + 3] + pq[j].w * (ry * yq[j].w);
+        }
+        if (blockIdx.x == 0) {
+#pragma unroll
+            for (int j = 0; j < J; ++j)
+                *reinterpret_cast<float4*>(a.post_out + 256 * j + 4 * lane) =
+                    make_float4(v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
+        }
+    }
+    // RMSNorm: the lanes take w[i] * x[i], and the row totals are scaled by
+    // r (the GEMV is linear in x)
+    float rscale = 1.0f;
+    if (a.norm) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4 * J; ++i) ss += v[i] * v[i];
+        ss = wave_sum(ss);
+        rscale = 1.0f / sqrtf(ss * a.inv_n + a.eps);
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            v[4 * j] = nq[j].x * v[4 * j];
+            v[4 * j + 1] = nq[j].y * v[4 * j + 1];
+            v[4 * j + 2] = nq[j].z * v[4 * j + 2];
+            v[4 * j + 3] = nq[j].w * v[4 * j + 3];
+        }
+    }
+    // lane geometry in a row buffer: the quant dword and byte shift, and the
+    // scale's halfword, of group 0 (group j: + 68 j dwords, + 136 j halfwords)
+    const uint32_t bl = (uint32_t)lane >> 3;
+    const uint32_t qb = 34u * bl + 2u + 4u * ((uint32_t)lane & 7u);
+    const uint32_t qdw = qb >> 2, sft = qb & 3u, sh = 17u * bl;
+
+    for (int gl = 0; gl < ngroups_mine; ++gl) {
+        float acc[G];
+#pragma unroll
+        for (int i = 0; i < G; ++i) {
+            const int k = gl * G + i;
+            const int kn = k + NB - 1;
+            if (kn < nk) issue(kn, kn % NB);
+            wait_chunk<NB - 1, kWideCI>(nk - 1 - k);
+            const uint8_t* src;
+            const bool real = chunk_src<G, PAIR>(cc, k, src);
+            const uint32_t* buf = lds + (k % NB) * BDW;
+            const uint16_t* hw = reinterpret_cast<const uint16_t*>(buf);
+            float dv = 0.0f;
+#pragma unroll
+            for (int j = 0; j < J; ++j) {
+                const uint32_t q = __builtin_amdgcn_alignbyte(buf[qdw + 68 * j + 1], buf[qdw + 68 * j], sft);
+                const float d = h2f(hw[sh + 136 * j]);
+                float s = (float)(int8_t)(q & 0xffu) * v[4 * j];
+                s = fmaf((float)(int8_t)((q >> 8) & 0xffu), v[4 * j + 1], s);
+                s = fmaf((float)(int8_t)((q >> 16) & 0xffu), v[4 * j + 2], s);
+                s = fmaf((float)(int8_t)(q >> 24), v[4 * j + 3], s);
+                dv = fmaf(s, d, dv);
+            }
+            asm volatile("" : "+v"(dv));
+            acc[i] = real ? dv : 0.0f;
+            wait_lgkm();   // this row's LDS reads are done before its buffer is refilled
+        }
+        const float tot = xreduce<G>(acc, lane) * rscale;
+        const int ri = rowof<G>(lane);
+        const bool lead = (lane & ((64 / G) - 1)) == 0;
+        const int grp = (int)blockIdx.x + gl * (int)gridDim.x;
+        if (PAIR) {
+            if (lead) xch[ri] = tot;
+            if (lane < NOUT) {
+                const int row = grp * NOUT + lane;
+                const float g = xch[lane], u = xch[lane + NOUT];
+                if (row < a.rows[0]) a.y[0][row] = a.epilogue == EPI_GEGLU ? ref_geglu(g, u) : ref_swiglu(g, u);
+            }
+        } else if (lead) {
+            const int gi = grp * G + ri;
+            if (gi < a.rows_total) {
+                int s, row;
+                seg_of(a, gi, s, row);
+                float* y = a.y[s] + row;
+                if (a.epilogue == EPI_ADD) *y = *y + tot;
+                else *y = tot;
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // launch
 // ---------------------------------------------------------------------------
 int cus() { return device_cus(); }
@@ -1346,6 +1562,59 @@ int launch_g(GemvArgs a, bool pair, int G, int nbuf, hipStream_t st) {
     }
 }
 
+// Whole-row launches (gemv_wide_kernel): one wave per workgroup, at most
+// eight per CU, the same number of row groups per workgroup.
+template <int J, int G, int NB, bool PAIR>
+int launch_wide_rows(GemvArgs a, int wpc, hipStream_t st) {
+    auto kern = a.post_y ? gemv_wide_kernel<J, G, NB, PAIR, true> : gemv_wide_kernel<J, G, NB, PAIR, false>;
+    const size_t lds = (size_t)NB * kWideBufBytes + (size_t)G * 4;
+    const int cap = std::min(occupancy(kern, 64, lds), wpc) * cus();
+    const int k = (a.ngroups + cap - 1) / cap;
+    const int grid = (a.ngroups + k - 1) / k;
+    launch_kernel(kern, dim3(grid), dim3(64), (uint32_t)lds, st, a);
+    return 0;
+}
+template <int J, int G, bool PAIR>
+int launch_wide_nb(GemvArgs a, int wpc, int nb, hipStream_t st) {
+    switch (nb) {
+    case 3: return launch_wide_rows<J, G, 3, PAIR>(a, wpc, st);
+    case 5: return launch_wide_rows<J, G, 5, PAIR>(a, wpc, st);
+    default: return launch_wide_rows<J, G, 4, PAIR>(a, wpc, st);
+    }
+}
+template <int J>
+int launch_wide_g(GemvArgs a, bool pair, int G, int wpc, int nb, hipStream_t st) {
+    if (pair) return G == 4 ? launch_wide_nb<J, 4, true>(a, wpc, nb, st) : launch_wide_nb<J, 8, true>(a, wpc, nb, st);
+    switch (G) {
+    case 2: return launch_wide_nb<J, 2, false>(a, wpc, nb, st);
+    case 4: return launch_wide_nb<J, 4, false>(a, wpc, nb, st);
+    case 16: return launch_wide_nb<J, 16, false>(a, wpc, nb, st);
+    default: return launch_wide_nb<J, 8, false>(a, wpc, nb, st);
+    }
+}
+// Four rows per group (two gate and two up rows for a pair) and up to eight
+// waves per CU, measured on MI355X at Gemma-2-2B's 2304 columns (rocprof
+// medians in the decode step, with the residual update fused): gate|up
+// 12.9-13.1 us at six and eight waves per CU (14.6 at four, 13.8 at ten;
+// 13.2 with eight rows per group at ten), q|k|v 5.7 us (6.7 and 6.9 with two
+// and eight rows per group), the 256000-row LM head 102 us at eight (145,
+// 123, 107 and 105 at four, six, ten and twelve), against 17.8, 9.0 and
+// 115 us for the chunk-column kernel; ring depths 3 and 5 were slower than 4.
+int launch_wide(GemvArgs a, bool pair, hipStream_t st) {
+    const int units = pair ? a.rows[0] : a.rows_total;
+    int wpc = env_int("L3P_GEMV_WIDE_WPC", 0);
+    if (wpc <= 0) wpc = 8;
+    int G = env_int("L3P_GEMV_WIDE_G", 0);
+    if (G != 2 && G != 4 && G != 8 && G != 16) G = 4;
+    if (pair && G == 16) G = 8;
+    if (pair && G == 2) G = 4;
+    const int per = pair ? G / 2 : G;
+    a.ngroups = (units + per - 1) / per;
+    const int nb = env_int("L3P_GEMV_WIDE_NB", 4);
+    if (a.cols == 2304) return launch_wide_g<9>(a, pair, G, wpc, nb, st);
+    return launch_wide_g<10>(a, pair, G, wpc, nb, st);
+}
+
 template <int QT>
 int launch_type(GemvArgs a, bool pair, int G, bool standalone, hipStream_t st) {
     const int units = pair ? a.rows[0] : a.rows_total;
@@ -1465,6 +1734,9 @@ int launch_gemv(int type, const GemvBatch& b, int cols, const float* x, const fl
     a.ss_loads = (b.n_ss + 255) / 256;
     a.n_ss = b.n_ss;
     L3P_REQUIRE(!b.ss || (b.n_ss > 0 && b.n_ss <= kMaxSsParts), L3P_E_INVALID, "gemv: %d sums of squares", b.n_ss);
+    // Q8_0 rows of 2304 or 2560 columns stream whole rows per wave
+    if (type == L3P_Q8_0 && wide_cols(cols) && !b.xw && !b.ss && env_int("L3P_GEMV_WIDE", 1))
+        return launch_wide(a, b.pair != 0, st);
     // Rows per group G: the largest of 16, 8, 4 that still gives about six
     // waves per CU (groups x column chunks); ring depth 3.  (Measured on
     // MI355X at the Llama-3-8B shapes.)

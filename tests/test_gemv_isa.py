@@ -10,7 +10,7 @@ the wait: the compiler does not know the loads are in flight.  The wait
 also counts on the loads being older than every weight copy
 (global_load_lds) issued before it, so a load the compiler moved after a
 copy would make the wait too weak.  This test compiles gemv.hip to assembly
-and checks both for every gemv_kernel instantiation.
+and checks both for every gemv_kernel and gemv_wide_kernel instantiation.
 """
 import os
 import re
@@ -83,7 +83,7 @@ def test_gemv_prologue_loads_untouched_until_waited(tmp_path):
     r = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
     assert r.returncode == 0, r.stderr[-2000:]
     src = out.read_text()
-    kernels = re.findall(r"^(_ZN\S*gemv_kernel\S+):[^\n]*\n(.*?)s_endpgm", src, re.S | re.M)
+    kernels = re.findall(r"^(_ZN\S*gemv_(?:wide_)?kernel\S+):[^\n]*\n(.*?)s_endpgm", src, re.S | re.M)
     assert len(kernels) >= 100, len(kernels)
     bad = {name: p for name, body in kernels if (p := check_kernel(body))}
     assert not bad, {k: v[:3] for k, v in list(bad.items())[:5]}

@@ -318,6 +318,47 @@ PATH_CASES = {
 }
 
 
+def test_wide_gemv_matches_chunk_columns(torch_gpu, cpuref, monkeypatch):
+    """Gemma-2-2B widths: the decode step's Q8_0 GEMVs over 2304 columns
+    (q|k|v and gate|up with the fused post-norm update, the LM head with the
+    last post norm and the final norm) stream whole rows per wave by default
+    (gemv_wide_kernel); L3P_GEMV_WIDE=0 takes the chunk-column kernel.  Each
+    context captures its step graph with its own setting.  The two kernels
+    sum every row in another order, so logits agree to 1e-3 * rms and the
+    K/V caches within one quant step; against the oracle the whole-row
+    logits are within the full-model tolerance, with the same greedy token
+    wherever the oracle's top-2 margin is clear of it."""
+    g = synth.synthetic_model(arch="gemma3", dim=2304, hidden=9216, n_layers=3, n_heads=8, n_kv=4, head_dim=256,
+                              vocab=2048, ctx=64, qtype=synth.Q8_0, seed=31, softcap=30.0, swa_window=16,
+                              norm_jitter=0.1, tied=True)
+    toks = np.random.default_rng(31).integers(0, 2048, 12).astype(np.int32)
+    m = cpuref.open_model(g)
+    with l3p.Context(0) as cw, l3p.Context(0) as cc:
+        for c, wide in ((cw, "1"), (cc, "0")):
+            monkeypatch.setenv("L3P_GEMV_WIDE", wide)
+            c.load_gguf(g)
+            c.prefill(toks[:8], 0)
+            c.forward(int(toks[8]), 8)   # captures the step graph with this setting
+        monkeypatch.delenv("L3P_GEMV_WIDE", raising=False)
+        m.prefill(toks[:8], 0, 8)
+        m.forward(int(toks[8]), 8)
+        tok = int(toks[9])
+        for pos in range(9, 13):
+            a = cw.forward(tok, pos)
+            b = cc.forward(tok, pos)
+            r = m.forward(tok, pos)
+            assert float(np.max(np.abs(a - b))) <= 1e-3 * rms(b), pos
+            assert float(np.max(np.abs(a - r))) <= 1e-2 * rms(r), pos
+            if margin(r) > 2e-2 * rms(r):
+                assert int(np.argmax(a)) == int(np.argmax(r)), pos
+            tok = int(np.argmax(r))
+        for layer in range(m.n_layers):
+            for wv in (False, True):
+                d = kv_quant_diff(cw.copy_kv(layer, wv), cc.copy_kv(layer, wv), m, 13)
+                assert d.max() <= 1, (layer, wv, int(d.max()))
+    m.close()
+
+
 @pytest.mark.parametrize("case", list(PATH_CASES))
 def test_prompt_attention_paths_agree(torch_gpu, monkeypatch, case):
     """A prompt through attn_prefill_kernel (the default) and through chunks +

@@ -200,6 +200,20 @@ def test_gemv_ragged_rows(ctx, torch_gpu, cpuref, qtype, rows):
     _check_gemv(ctx, torch_gpu, cpuref, qtype, rows, cols, seed=rows)
 
 
+@pytest.mark.parametrize("cols", [2304, 2560])
+@pytest.mark.parametrize("rows", [1, 2, 3, 5, 7, 9, 4097])
+def test_gemv_wide_rows_ragged(ctx, torch_gpu, cpuref, monkeypatch, rows, cols):
+    """Q8_0 rows of 2304 and 2560 columns stream whole rows per wave
+    (gemv_wide_kernel, four rows per group): ragged last groups against the
+    oracle's bound, and the chunk-column kernel (L3P_GEMV_WIDE=0) on the
+    same inputs within the same bound."""
+    got = _check_gemv(ctx, torch_gpu, cpuref, l3p.Q8_0, rows, cols, seed=rows + cols)
+    monkeypatch.setenv("L3P_GEMV_WIDE", "0")
+    old = _check_gemv(ctx, torch_gpu, cpuref, l3p.Q8_0, rows, cols, seed=rows + cols)
+    if rows > 4096:   # different summation orders: some of 4097 row totals differ in their last bits
+        assert not np.array_equal(got, old), "both runs took the same kernel"
+
+
 def test_gemv_zero_rows_and_errors(ctx, torch_gpu):
     x = empty_f32(torch_gpu, 512)
     y = empty_f32(torch_gpu, 8)
