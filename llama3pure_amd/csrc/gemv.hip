@@ -1216,7 +1216,7 @@ __global__ void __launch_bounds__(POST ? 512 : 1024) gemv_kernel(GemvArgs a) {
 // activation's worth of prologue loads (8 per vector, whatever few lanes
 // carry data) and copies its short chunk with as many instructions as a full
 // one.  Here one wave streams whole rows, RB = 272 J bytes each, copied with
-// kWideCI dwordx4 instructions into a private ring of NB buffers, and lane l
+// ceil(RB / 1024) dwordx4 instructions into a private ring of NB buffers, and lane l
 // owns the columns 256 j + 4 l .. 256 j + 4 l + 3 for j < J: an activation
 // vector is J coalesced 16-byte loads per lane, a row's dot needs no
 // cross-wave sum (there is no barrier in the kernel), and the residual update
@@ -1230,27 +1230,34 @@ __global__ void __launch_bounds__(POST ? 512 : 1024) gemv_kernel(GemvArgs a) {
 // quants.  The lane's term for the group is d_b * sum q x over its four
 // columns (gemv_kernel's d * sum q_j x_j, over four columns instead of 32).
 // ---------------------------------------------------------------------------
-constexpr int kWideCI = 3;                // copy instructions per row: RB <= 3 KB
-constexpr int kWideBufBytes = kWideCI * 1024;
+// dwordx4 copy instructions of a row of J 256-column groups (272 J bytes)
+template <int J>
+constexpr int wide_ci() { return (17 * J + 63) / 64; }
 
+// Rows of 2304 and 2560 columns.  At 4096 columns, where the chunk-column
+// kernel's two waves both carry full chunks, whole rows were slower (Llama-3-8B
+// gate|up 23.2 -> 25.3 us, wo 8.1 -> 8.4 us in the decode step on MI355X).
 bool wide_cols(int cols) { return cols > kChunkElems && cols <= 2560 && cols % 256 == 0; }
 
 // Lane offsets of a row copy: piece i*64 + lane of the row's RB/16 pieces,
 // clamped to the last piece (clamped lanes re-read it and write it past RB in
-// the buffer), so every row is exactly kWideCI instructions.
+// the buffer), so every row is exactly CI instructions.
 struct WideDma {
-    int o[kWideCI];
+    int o[8];   // CI <= 8 (rows of up to 30 groups)
 };
+template <int CI>
 __device__ __forceinline__ WideDma wide_dma(int lane, uint32_t rb) {
+    static_assert(CI <= 8, "at most eight copy instructions per row");
     const int last = (int)(rb >> 4) - 1;
     WideDma d;
 #pragma unroll
-    for (int i = 0; i < kWideCI; ++i) d.o[i] = 16 * min(64 * i + lane, last);
+    for (int i = 0; i < CI; ++i) d.o[i] = 16 * min(64 * i + lane, last);
     return d;
 }
+template <int CI>
 __device__ __forceinline__ void wide_copy(uint32_t* dst, const uint8_t* src, const WideDma& d) {
 #pragma unroll
-    for (int i = 0; i < kWideCI; ++i) __builtin_amdgcn_global_load_lds(src + d.o[i], (lds_void*)(dst + 256 * i), 16, 0, 2);
+    for (int i = 0; i < CI; ++i) __builtin_amdgcn_global_load_lds(src + d.o[i], (lds_void*)(dst + 256 * i), 16, 0, 2);
 }
 
 // J untracked 16-byte loads per lane, 256 floats apart (see load8_async)
@@ -1268,7 +1275,8 @@ __device__ __forceinline__ void pinj(f32x4 (&q)[J]) {
 template <int J, int G, int NB, bool PAIR, bool POST>
 __global__ void __launch_bounds__(64) gemv_wide_kernel(GemvArgs a) {
     constexpr int NOUT = PAIR ? G / 2 : G;
-    constexpr int BDW = kWideBufBytes / 4;
+    constexpr int CI = wide_ci<J>();
+    constexpr int BDW = CI * 256;   // dwords per ring buffer
     extern __shared__ __align__(16) uint32_t lds[];
     float* xch = reinterpret_cast<float*>(lds + NB * BDW);   // [G] row totals of a group (pair epilogue)
     const int lane = threadIdx.x;
@@ -1287,11 +1295,11 @@ __global__ void __launch_bounds__(64) gemv_wide_kernel(GemvArgs a) {
     cc.nmine = -1;
     cc.rb = rb;
     cc.coff = 0;
-    const WideDma dl = wide_dma(lane, rb);
+    const WideDma dl = wide_dma<CI>(lane, rb);
     auto issue = [&](int k, int slot) {
         const uint8_t* src;
         chunk_src<G, PAIR>(cc, k, src);
-        wide_copy(lds + slot * BDW, src, dl);
+        wide_copy<CI>(lds + slot * BDW, src, dl);
     };
 
     // ---- the lane's activation columns, norm weights and residual-update
@@ -1309,7 +1317,7 @@ __global__ void __launch_bounds__(64) gemv_wide_kernel(GemvArgs a) {
 #pragma unroll
     for (int b = 0; b < NB - 1; ++b)
         if (b < nk) issue(b, b);
-    wait_prologue<NB - 1, kWideCI>(nk);
+    wait_prologue<NB - 1, CI>(nk);
     pinj<J>(xq);
     if (a.norm) pinj<J>(nq);
     if (POST) {
@@ -1381,7 +1389,7 @@ __global__ void __launch_bounds__(64) gemv_wide_kernel(GemvArgs a) {
             const int k = gl * G + i;
             const int kn = k + NB - 1;
             if (kn < nk) issue(kn, kn % NB);
-            wait_chunk<NB - 1, kWideCI>(nk - 1 - k);
+            wait_chunk<NB - 1, CI>(nk - 1 - k);
             const uint8_t* src;
             const bool real = chunk_src<G, PAIR>(cc, k, src);
             const uint32_t* buf = lds + (k % NB) * BDW;
@@ -1567,7 +1575,7 @@ int launch_g(GemvArgs a, bool pair, int G, int nbuf, hipStream_t st) {
 template <int J, int G, int NB, bool PAIR>
 int launch_wide_rows(GemvArgs a, int wpc, hipStream_t st) {
     auto kern = a.post_y ? gemv_wide_kernel<J, G, NB, PAIR, true> : gemv_wide_kernel<J, G, NB, PAIR, false>;
-    const size_t lds = (size_t)NB * kWideBufBytes + (size_t)G * 4;
+    const size_t lds = (size_t)NB * wide_ci<J>() * 1024 + (size_t)G * 4;
     const int cap = std::min(occupancy(kern, 64, lds), wpc) * cus();
     const int k = (a.ngroups + cap - 1) / cap;
     const int grid = (a.ngroups + k - 1) / k;
