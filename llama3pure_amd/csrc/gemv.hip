@@ -1496,8 +1496,8 @@ int launch_rows(GemvArgs a, hipStream_t st) {
         grid = (a.ngroups + k - 1) / k;
     }
     grid = std::max(grid, (a.ngroups * NOUT + kMaxOut - 1) / kMaxOut);
-    // Row ranges when they spread the rows at least 10% more evenly over the
-    // CUs.  The dispatcher places workgroup b on CU b mod CUs while every
+    // Row ranges when they take at least 20% of the rows off the busiest
+    // CU.  The dispatcher places workgroup b on CU b mod CUs while every
     // workgroup of the launch is resident (breadth first), so a grid that is
     // not a multiple of the CUs loads some CUs with one workgroup more, and
     // the launch ends with them: Gemma-2-2B's 2304-row GEMVs in groups of 4
@@ -1508,7 +1508,9 @@ int launch_rows(GemvArgs a, hipStream_t st) {
     // one band of it at a time, which made Gemma-2-2B's 590 MB LM head
     // slower (112 -> 122 us) for 0.6% fewer rows on its busiest CU; rows
     // dealt one by one over the workgroups kept the band but were no faster
-    // at the small shapes (4.04 and 9.11 us).
+    // at the small shapes (4.04 and 9.11 us).  At 12.5% (the 14336-row Q4_0
+    // and Q4_K GEMVs: 64 -> 56 rows) ranges were 2-3% slower (p50 10.4-10.6
+    // -> 10.7 us and 11.0-11.1 -> 11.2-11.4 us, alternating runs on one box).
     a.rpw = 0;
     size_t lds = lds_for(grid);
     if (!PAIR && env_int("L3P_GEMV_RANGES", 1)) {
@@ -1525,7 +1527,7 @@ int launch_rows(GemvArgs a, hipStream_t st) {
         const int grid_r = (a.rows_total + rpw - 1) / rpw;
         const size_t lds_r = base + (size_t)((rpw + G - 1) / G) * G * 4;
         if ((rpw + G - 1) / G * G <= kMaxOut && lds_r <= lds_for(cus()) &&
-            10 * worst_cu(grid_r, rpw) <= 9 * worst_cu(grid, 0)) {
+            5 * worst_cu(grid_r, rpw) <= 4 * worst_cu(grid, 0)) {
             a.rpw = rpw;
             grid = grid_r;
             lds = lds_r;
