@@ -309,15 +309,16 @@ struct Cursor {
 // gridDim.x, row slot i = k % G.  Pair mode: slots [0, G/2) are gate rows,
 // [G/2, G) the matching up rows.  Sets src to the chunk and returns true for
 // a real row; past the end it returns false with src at the same chunk column
-// of the first row (a valid dummy copy of the same size).
-template <int G, bool PAIR>
+// of the first row (a valid dummy copy of the same size).  RG: the kernel
+// supports row ranges (see gemv_kernel).
+template <int G, bool PAIR, bool RG = false>
 __device__ __forceinline__ bool chunk_src(const Cursor& cc, int k, const uint8_t*& src) {
     const int j = cc.bid + (k / G) * cc.gdim;
     const int i = k % G;
     const uint8_t* base = cc.w0;
     int r;
     bool ok = j < cc.ngroups;
-    if (!PAIR && cc.nmine >= 0) {   // row ranges: chunk k is row rbeg + k
+    if (RG && !PAIR && cc.nmine >= 0) {   // row ranges: chunk k is row rbeg + k
         r = cc.rbeg + k;
         ok = k < cc.nmine;
         if (ok && r >= cc.rows0) {
@@ -902,7 +903,10 @@ struct Lane<L3P_F32> {
     }
 };
 
-template <int QT, int G, int NB, bool PAIR, bool UA, bool POST>
+// RG: built with row ranges (a.rpw > 0); kernels without them carry none of
+// their per-chunk branches (measured 3-5% faster at the standalone C1-C3
+// shapes and 0.7% on the Llama-3-8B decode step on MI355X).
+template <int QT, int G, int NB, bool PAIR, bool UA, bool POST, bool RG = false>
 __global__ void __launch_bounds__(POST ? 512 : 1024) gemv_kernel(GemvArgs a) {
     constexpr int CB = Fmt<QT>::kChunkBytes;
     constexpr int CDW = Fmt<QT>::kBufBytes / 4;
@@ -931,7 +935,7 @@ __global__ void __launch_bounds__(POST ? 512 : 1024) gemv_kernel(GemvArgs a) {
     cc.bid = blockIdx.x;
     cc.gdim = gridDim.x;
     // row ranges (rpw > 0, never in pair mode): this workgroup's rows
-    const bool ranges = !PAIR && a.rpw > 0;
+    const bool ranges = RG && !PAIR && a.rpw > 0;
     cc.rbeg = (int)blockIdx.x * a.rpw;
     cc.nmine = ranges ? max(0, min(a.rpw, a.rows_total - cc.rbeg)) : -1;
     cc.rb = rb;
@@ -941,7 +945,7 @@ __global__ void __launch_bounds__(POST ? 512 : 1024) gemv_kernel(GemvArgs a) {
     // copy row-chunk k of the sequence into ring slot `slot`
     auto issue = [&](int k, int slot) {
         const uint8_t* src;
-        chunk_src<G, PAIR>(cc, k, src);
+        chunk_src<G, PAIR, RG>(cc, k, src);
         if (UA) {
             const uint32_t sh = (uint32_t)(uintptr_t)src & 15u;
             chunk_dma<QT>(ring + slot * CDW, src - sh, dma_lane<QT>(lane, (int)sh + nbytes));
@@ -1111,7 +1115,7 @@ __global__ void __launch_bounds__(POST ? 512 : 1024) gemv_kernel(GemvArgs a) {
             // NB-1 of them in steady state, fewer near the end of the sequence
             wait_chunk<NB - 1, CI>(nk - 1 - k);
             const uint8_t* src;
-            const bool real = chunk_src<G, PAIR>(cc, k, src);
+            const bool real = chunk_src<G, PAIR, RG>(cc, k, src);
             if (UA) ln.at(lane, (uint32_t)(uintptr_t)src & 15u);
             // every lane reads inside the buffer, so the dot runs unconditionally
             // and lanes past the row or rows past the matrix drop their value
@@ -1511,9 +1515,12 @@ int launch_rows(GemvArgs a, hipStream_t st) {
     // at the small shapes (4.04 and 9.11 us).  At 12.5% (the 14336-row Q4_0
     // and Q4_K GEMVs: 64 -> 56 rows) ranges were 2-3% slower (p50 10.4-10.6
     // -> 10.7 us and 11.0-11.1 -> 11.2-11.4 us, alternating runs on one box).
+    // Row ranges are built into the Q8_0 kernels without the residual update
+    // (Gemma-2-2B's 2304-row output and down projections), where they gained.
+    constexpr bool kRG = QT == L3P_Q8_0 && !PAIR;
     a.rpw = 0;
     size_t lds = lds_for(grid);
-    if (!PAIR && env_int("L3P_GEMV_RANGES", 1)) {
+    if (kRG && !a.post_y && env_int("L3P_GEMV_RANGES", 1)) {
         const int n = cus();
         auto worst_cu = [&](int g, int rpw) {   // most rows on one CU
             std::vector<int> per(n, 0);
@@ -1532,6 +1539,9 @@ int launch_rows(GemvArgs a, hipStream_t st) {
             grid = grid_r;
             lds = lds_r;
         }
+    }
+    if constexpr (kRG) {
+        if (a.rpw > 0) kern = gemv_kernel<QT, G, NB, PAIR, UA, false, true>;
     }
     if (lds > 65536)
         L3P_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
