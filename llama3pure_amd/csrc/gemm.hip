@@ -70,6 +70,7 @@ struct GemmArgs {
     int ntot;
     int streamk;           // > 0: stream-K over that many workgroups (grid.x), nsplit = most slots of a tile
     int kst;               // stream-K: kBK steps of a whole tile
+    int bn;                // output columns per tile
 };
 
 // Stream-K bookkeeping: the runs of P workgroups cut the tile-major sequence
@@ -191,8 +192,17 @@ __device__ __forceinline__ void tile_mma(const GemmArgs& a, const TileRef& tr, i
         __syncthreads();
         // the next step's loads go out before this step's matrix work
         if (k0 + kBK < kend) fetch_step<QT, BN>(sr, a, tr.W, tr.N, tr.m0, tr.n0, k0 + kBK, t);
+        // 128-wide tiles raise the wave's issue priority for its matrix work,
+        // so that waves in their load and dequantization phase fill the gaps
+        // (Llama-3-8B wo 4096 x 4096 at 1024 rows: 300 -> 274 us; at 64-wide
+        // tiles it was slower); LLVM's MFMA / LDS-read interleaving strategy
+        // 1 for 128-wide tiles and 0 for 64-wide ones (Gemma-2-2B down at 511
+        // rows: 204 -> 197 us).  Neither changes an operation or its order.
+        if (BN == 128) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int kk = 0; kk < kBK; kk += 16) {
+            if constexpr (BN == 128) __builtin_amdgcn_iglp_opt(1);
+            else __builtin_amdgcn_iglp_opt(0);
             float4 af[2], bf[2];
 #pragma unroll
             for (int im = 0; im < 2; ++im)
@@ -212,6 +222,7 @@ __device__ __forceinline__ void tile_mma(const GemmArgs& a, const TileRef& tr, i
                 acc[1][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1[s], b1[s], acc[1][1], 0, 0, 0);
             }
         }
+        if (BN == 128) __builtin_amdgcn_s_setprio(0);
         __syncthreads();
     }
 }
@@ -282,10 +293,10 @@ __global__ void __launch_bounds__(256) gemm_reduce_kernel(GemmArgs a) {
     if (c >= a.ntot) return;
     const int sg = (a.nseg > 1 && c >= a.noff[1]) ? ((a.nseg > 2 && c >= a.noff[2]) ? 2 : 1) : 0;
     int nslot = a.nsplit;
-    if (a.streamk) {   // 64-wide tiles
+    if (a.streamk) {
         const int NT = a.tbeg[a.nseg], S = a.kst;
         const long W = (long)NT * ((a.m + kBM - 1) / kBM) * S;
-        const long tt = (long)(m / kBM) * NT + a.tbeg[sg] + (c - a.noff[sg]) / 64;
+        const long tt = (long)(m / kBM) * NT + a.tbeg[sg] + (c - a.noff[sg]) / a.bn;
         nslot = sk_owner((tt + 1) * S - 1, W, a.streamk) - sk_owner(tt * S, W, a.streamk) + 1;
     }
     const float* p = a.part + (size_t)m * a.ntot + c;
@@ -316,6 +327,11 @@ bool gemm_mfma_supported(int type) {
     }
 }
 
+static int gemm_env(const char* name, int dflt) {
+    const char* e = getenv(name);
+    return e ? std::max(1, atoi(e)) : dflt;
+}
+
 // The launch plan of a job: K splits and the partials they need (floats).
 GemmPlan gemm_plan(const GemmJob& j, size_t ws_floats) {
     GemmPlan p;
@@ -341,15 +357,22 @@ GemmPlan gemm_plan(const GemmJob& j, size_t ws_floats) {
     // Stream-K while the tiles give fewer than four workgroups per CU (the
     // LDS of four fits a CU): as many workgroups as fit at once, each run at
     // least eight K steps long, when the workspace holds the slots
+    // (L3P_GEMM_SK_BN = 128, L3P_GEMM_SK_WPC and L3P_GEMM_SK_MIN override the
+    // tile width, the workgroups per CU and the shortest run, for measurement:
+    // at Gemma-2-2B's 511 rows none of them was faster than these defaults)
     const int want = 4 * device_cus();
     if (ws_floats && j.m > 0 && (long)tiles * mt < want) {
-        const long W = (long)tiles * mt * steps;
-        const int P = (int)std::min<long>(want, W / 8);
-        if (P > tiles * mt / 2 && P > 1) {   // fewer runs than tiles: plain tiles do as well
+        const int skbn = gemm_env("L3P_GEMM_SK_BN", 64) == 128 ? 128 : 64;
+        const int skt = skbn == 128 ? tiles128 : tiles;
+        const long W = (long)skt * mt * steps;
+        const int P = (int)std::min<long>((long)gemm_env("L3P_GEMM_SK_WPC", skbn == 128 ? 3 : 4) * device_cus(),
+                                          W / gemm_env("L3P_GEMM_SK_MIN", 8));
+        if (P > skt * mt / 2 && P > 1) {   // fewer runs than tiles: plain tiles do as well
             int slots = 1;
-            for (long tt = 0; tt < (long)tiles * mt; ++tt)
+            for (long tt = 0; tt < (long)skt * mt; ++tt)
                 slots = std::max(slots, sk_owner((tt + 1) * steps - 1, W, P) - sk_owner(tt * steps, W, P) + 1);
             if ((size_t)slots * j.m * ntot <= ws_floats) {
+                p.bn = skbn;
                 p.streamk = P;
                 p.ksteps = steps;
                 p.nsplit = slots;
@@ -410,8 +433,9 @@ void launch_gemm_planned(const GemmJob& j, const GemmPlan& plan, float* ws, hipS
     a.nsplit = plan.nsplit;
     a.streamk = plan.streamk;
     a.kst = plan.ksteps;
+    a.bn = plan.bn;
     a.part = (a.nsplit > 1 || a.streamk) ? ws : nullptr;
-    L3P_REQUIRE(!a.streamk || (plan.bn == 64 && ws), L3P_E_INVALID, "gemm: stream-K plan without a workspace");
+    L3P_REQUIRE(!a.streamk || ws, L3P_E_INVALID, "gemm: stream-K plan without a workspace");
     switch (j.type) {
     case L3P_Q8_0: launch_typed<L3P_Q8_0>(a, plan.bn, st); break;
     case L3P_Q2_K: launch_typed<L3P_Q2_K>(a, plan.bn, st); break;
