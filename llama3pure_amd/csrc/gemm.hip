@@ -80,19 +80,158 @@ __host__ __device__ __forceinline__ int sk_owner(long x, long W, int P) {
     return (int)(((x + 1) * (long)P - 1) / W);
 }
 
+// One thread's slice of a step's W tile: row t / 4 of the tile, elements
+// e0 .. e0 + 15 of that row with e0 = k0 + 16 (t % 4).  Sixteen consecutive
+// elements lie in one Q8_0 block or one scale group of a K-quant, so the
+// slice needs at most three 16-byte pieces and a few header words, which are
+// fetched one step ahead like the X tile.
+struct WRaw {
+    uint4 a, b, c, d;       // quant bytes / header / F32 values, by type
+    uint32_t h0, h1, h2;    // scale words and scale bytes, by type
+};
+
+__device__ __forceinline__ uint32_t byte_of(const uint4& u, int i) {   // byte i (0..15, not constant)
+    const uint32_t w = i < 4 ? u.x : (i < 8 ? u.y : (i < 12 ? u.z : u.w));
+    return (w >> (8 * (i & 3))) & 0xffu;
+}
+__device__ __forceinline__ uint32_t byte_c(const uint4& u, int j) {     // byte j (constant after unrolling)
+    const uint32_t w = (j >> 2) == 0 ? u.x : ((j >> 2) == 1 ? u.y : ((j >> 2) == 2 ? u.z : u.w));
+    return (w >> (8 * (j & 3))) & 0xffu;
+}
+
+template <int QT>
+__device__ __forceinline__ void fetch_slice(WRaw& r, const uint8_t* row, int e0) {
+    if constexpr (QT == L3P_Q8_0) {   // 34-byte blocks: d, 32 quants
+        const uint8_t* b = row + (size_t)(e0 >> 5) * 34;
+        r.h0 = *reinterpret_cast<const uint16_t*>(b);
+        // 2-byte aligned: one unaligned 16-byte load, left untouched until
+        // store_step so that nothing waits for it here
+        __builtin_memcpy(&r.a, b + 2 + 16 * ((e0 >> 4) & 1), 16);
+    } else if constexpr (QT == L3P_Q4_K) {   // 144 bytes: d, dmin, 12 scale bytes, 128 nibble pairs
+        const uint8_t* b = row + (size_t)(e0 >> 8) * 144;
+        const int e = e0 & 255;
+        __builtin_memcpy(&r.b, b, 16);
+        __builtin_memcpy(&r.a, b + 16 + 32 * (e >> 6) + (e & 31), 16);
+    } else if constexpr (QT == L3P_Q5_K) {   // 176 bytes: d, dmin, 12 scale bytes, 32 high-bit bytes, 128 nibble pairs
+        const uint8_t* b = row + (size_t)(e0 >> 8) * 176;
+        const int e = e0 & 255;
+        __builtin_memcpy(&r.c, b, 16);
+        __builtin_memcpy(&r.b, b + 16 + (e & 31), 16);
+        __builtin_memcpy(&r.a, b + 48 + 32 * (e >> 6) + (e & 31), 16);
+    } else if constexpr (QT == L3P_Q6_K) {   // 210 bytes: ql[128], qh[64], 16 int8 scales, d
+        const uint8_t* b = row + (size_t)(e0 >> 8) * 210;
+        const int e = e0 & 255, half = e >> 7, g = (e & 127) >> 5, l0 = e & 31;
+        __builtin_memcpy(&r.a, b + 64 * half + 32 * (g & 1) + l0, 16);
+        __builtin_memcpy(&r.b, b + 128 + 32 * half + l0, 16);
+        r.h0 = *reinterpret_cast<const uint16_t*>(b + 208);
+        r.h1 = b[192 + 8 * half + (l0 >> 4) + 2 * g];
+    } else if constexpr (QT == L3P_Q3_K) {   // 110 bytes: hmask[32], qs[64], 12 scale bytes, d
+        const uint8_t* b = row + (size_t)(e0 >> 8) * 110;
+        const int g = (e0 & 255) >> 4, half = g >> 3, second = g & 1;
+        __builtin_memcpy(&r.a, b + 32 + 32 * half + 16 * second, 16);
+        __builtin_memcpy(&r.b, b + 16 * second, 16);
+        r.h0 = *reinterpret_cast<const uint16_t*>(b + 108);
+        r.h1 = b[96 + (g & 7)];
+        r.h2 = b[104 + (g & 3)];
+    } else if constexpr (QT == L3P_Q2_K) {   // 84 bytes: 16 scale bytes, qs[64], d, dmin
+        const uint8_t* b = row + (size_t)(e0 >> 8) * 84;
+        const int g = (e0 & 255) >> 4, half = g >> 3, second = g & 1;
+        __builtin_memcpy(&r.a, b + 16 + 32 * half + 16 * second, 16);
+        __builtin_memcpy(&r.h0, b + 80, 4);
+        r.h1 = b[g];
+    } else if constexpr (QT == L3P_F16 || QT == L3P_BF16) {
+        const uint4* p = reinterpret_cast<const uint4*>(row + 2 * (size_t)e0);
+        r.a = p[0];
+        r.b = p[1];
+    } else {   // F32
+        const uint4* p = reinterpret_cast<const uint4*>(row + 4 * (size_t)e0);
+        r.a = p[0];
+        r.b = p[1];
+        r.c = p[2];
+        r.d = p[3];
+    }
+}
+
+// The slice's 16 values, each formed exactly as dequantize_row_* forms it
+// (c:611-934; the expressions of deq_elem), from the fetched bytes.
+template <int QT>
+__device__ __forceinline__ void decode_slice(const WRaw& r, int e0, float (&v)[16]) {
+    if constexpr (QT == L3P_Q8_0) {
+        const float d = h2f_exact(r.h0);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) v[j] = (float)(int8_t)byte_c(r.a, j) * d;
+    } else if constexpr (QT == L3P_Q4_K || QT == L3P_Q5_K) {
+        // sub-block js = e / 32 of the super-block: its 6-bit scale and min
+        const uint4& hd = QT == L3P_Q4_K ? r.b : r.c;
+        const int e = e0 & 255, js = e >> 5;
+        int scv, mnv;
+        if (js < 4) {
+            scv = (int)(byte_of(hd, 4 + js) & 63u);
+            mnv = (int)(byte_of(hd, 8 + js) & 63u);
+        } else {
+            scv = (int)((byte_of(hd, 8 + js) & 0x0fu) | ((byte_of(hd, js) >> 6) << 4));
+            mnv = (int)((byte_of(hd, 8 + js) >> 4) | ((byte_of(hd, 4 + js) >> 6) << 4));
+        }
+        const float d1 = h2f_exact(hd.x & 0xffffu) * (float)scv, m1 = h2f_exact(hd.x >> 16) * (float)mnv;
+        const int sh = QT == L3P_Q4_K ? 4 * ((e >> 5) & 1) : 4 * (js & 1);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            int q = (int)((byte_c(r.a, j) >> sh) & 0x0fu);
+            if constexpr (QT == L3P_Q5_K) q += ((byte_c(r.b, j) >> js) & 1u) ? 16 : 0;
+            v[j] = d1 * (float)q - m1;
+        }
+    } else if constexpr (QT == L3P_Q6_K) {
+        const int g = (e0 & 127) >> 5;
+        const float ds = h2f_exact(r.h0) * (float)(int8_t)r.h1;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const int lo = (int)byte_c(r.a, j);
+            const int nib = (g & 2) ? (lo >> 4) : (lo & 0x0f);
+            const int q = (nib | (int)(((byte_c(r.b, j) >> (2 * g)) & 3u) << 4)) - 32;
+            v[j] = ds * (float)q;
+        }
+    } else if constexpr (QT == L3P_Q3_K) {
+        const int g = (e0 & 255) >> 4, half = g >> 3, j4 = (g >> 1) & 3;
+        const int lo = g < 8 ? (int)(r.h1 & 0x0fu) : (int)(r.h1 >> 4);
+        const int sg = (lo | (int)(((r.h2 >> (2 * (g >> 2))) & 3u) << 4)) - 32;
+        const float ds = h2f_exact(r.h0) * (float)sg;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const int u = (int)((byte_c(r.a, j) >> (2 * j4)) & 3u);
+            const int h = (int)((byte_c(r.b, j) >> (4 * half + j4)) & 1u);
+            v[j] = ds * (float)(u - (h ? 0 : 4));
+        }
+    } else if constexpr (QT == L3P_Q2_K) {
+        const int j4 = (((e0 & 255) >> 4) >> 1) & 3;
+        const float dl = h2f_exact(r.h0 & 0xffffu) * (float)(r.h1 & 0x0fu);
+        const float ml = h2f_exact(r.h0 >> 16) * (float)(r.h1 >> 4);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) v[j] = dl * (float)((byte_c(r.a, j) >> (2 * j4)) & 3u) - ml;
+    } else if constexpr (QT == L3P_F16 || QT == L3P_BF16) {
+        const uint32_t hw[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const uint32_t h = (hw[j >> 1] >> (16 * (j & 1))) & 0xffffu;
+            v[j] = QT == L3P_F16 ? h2f_exact(h) : __uint_as_float(h << 16);
+        }
+    } else {   // F32
+        const uint32_t fw[16] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w,
+                                 r.c.x, r.c.y, r.c.z, r.c.w, r.d.x, r.d.y, r.d.z, r.d.w};
+#pragma unroll
+        for (int j = 0; j < 16; ++j) v[j] = __uint_as_float(fw[j]);
+    }
+}
+
 // The global data of one K step, held in registers from the step before so
 // that its loads are in flight while the matrix cores work on the current
-// step: the X tile (4 float4 per thread) and, for Q8_0, this thread's 16
-// quants and block scale (t: row t/4, block (t/2)&1, half t&1).
-template <int QT>
+// step: the X tile (4 float4 per thread) and this thread's W slice.
 struct StepRegs {
     float4 x[4];   // the first 1024 / threads of them are used
-    uint4 q;         // Q8_0: the 16 quants as fetched (bytes in order)
-    uint32_t d;      // Q8_0: fp16 scale bits
+    WRaw w;
 };
 
 template <int QT, int BN>
-__device__ __forceinline__ void fetch_step(StepRegs<QT>& sr, const GemmArgs& a, const uint8_t* W, int N, int m0, int n0,
+__device__ __forceinline__ void fetch_step(StepRegs& sr, const GemmArgs& a, const uint8_t* W, int N, int m0, int n0,
                                            int k0, int t) {
     constexpr int NT = 4 * BN, XU = 1024 / NT;   // threads; float4 of the X tile per thread
 #pragma unroll
@@ -102,58 +241,28 @@ __device__ __forceinline__ void fetch_step(StepRegs<QT>& sr, const GemmArgs& a, 
         sr.x[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         if (m < a.m && kk < a.k) sr.x[u] = *reinterpret_cast<const float4*>(a.x + (size_t)m * a.ldx + kk);
     }
-    if (QT == L3P_Q8_0) {
-        const int r = t >> 2, blk = (t >> 1) & 1, half = t & 1;
-        const int n = n0 + r, kb = (k0 >> 5) + blk;
-        if (n < N && 32 * kb < a.k) {
-            const uint8_t* b = W + (size_t)n * a.rb + (size_t)kb * 34;
-            sr.d = *reinterpret_cast<const uint16_t*>(b);
-            // 2-byte aligned: one unaligned 16-byte load, left untouched until
-            // store_step so that nothing waits for it here
-            __builtin_memcpy(&sr.q, b + 2 + 16 * half, 16);
-        } else {
-            sr.d = 0u;
-            sr.q = make_uint4(0u, 0u, 0u, 0u);
-        }
-    }
+    const int n = n0 + (t >> 2), e0 = k0 + 16 * (t & 3);
+    sr.w = WRaw{};
+    if (n < N && e0 < a.k) fetch_slice<QT>(sr.w, W + (size_t)n * a.rb, e0);
 }
 
 // The step's tiles into LDS, rows padded to kLDK floats: X as fetched, W rows
-// [n0, n0+64) x columns [k0, k0+64) dequantized exactly.  Q8_0 expands
-// (float)q * d as dequantize_row_q8_0 (c:691-702); the other types go
-// element by element through the reference-exact dequantizer, reading the
-// weight bytes here.
+// [n0, n0 + BN) x columns [k0, k0 + 64) dequantized exactly (slices past the
+// matrix are zero bytes, whose values only meet zero X columns or rows that
+// are not stored).
 template <int QT, int BN>
-__device__ __forceinline__ void store_step(float* xs, float* ws, const StepRegs<QT>& sr, const GemmArgs& a,
-                                           const uint8_t* W, int N, int n0, int k0, int t) {
+__device__ __forceinline__ void store_step(float* xs, float* ws, const StepRegs& sr, int k0, int t) {
     constexpr int NT = 4 * BN, XU = 1024 / NT;
 #pragma unroll
     for (int u = 0; u < XU; ++u) {
         const int i = t + NT * u, r = i >> 4, c = i & 15;
         *reinterpret_cast<float4*>(xs + r * kLDK + 4 * c) = sr.x[u];
     }
-    if (QT == L3P_Q8_0) {
-        const int r = t >> 2, blk = (t >> 1) & 1, half = t & 1;
-        const float d = h2f_exact(sr.d);
-        const uint32_t qw[4] = {sr.q.x, sr.q.y, sr.q.z, sr.q.w};
-        float v[16];
+    float v[16];
+    decode_slice<QT>(sr.w, k0 + 16 * (t & 3), v);
+    float4* dst = reinterpret_cast<float4*>(ws + (t >> 2) * kLDK + 16 * (t & 3));
 #pragma unroll
-        for (int j = 0; j < 16; ++j) v[j] = (float)(int8_t)((qw[j >> 2] >> (8 * (j & 3))) & 0xffu) * d;
-        float4* dst = reinterpret_cast<float4*>(ws + r * kLDK + 32 * blk + 16 * half);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) dst[j] = make_float4(v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
-    } else {
-        // BN x 64 values, 16 per thread: row t/4, columns 16*(t%4) .. +16
-        const int r = t >> 2, c0 = 16 * (t & 3);
-        const int n = n0 + r;
-        const bool ok = n < N;
-        const uint8_t* row = W + (size_t)(ok ? n : 0) * a.rb;
-#pragma unroll 4
-        for (int j = 0; j < 16; ++j) {
-            const int kk = k0 + c0 + j;
-            ws[r * kLDK + c0 + j] = (ok && kk < a.k) ? deq_elem(QT, row, kk) : 0.0f;
-        }
-    }
+    for (int j = 0; j < 4; ++j) dst[j] = make_float4(v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
 }
 
 // The output tile a workgroup works on: segment, its weights and output
@@ -185,10 +294,10 @@ __device__ __forceinline__ void tile_mma(const GemmArgs& a, const TileRef& tr, i
     for (int im = 0; im < 2; ++im)
 #pragma unroll
         for (int in = 0; in < 2; ++in) acc[im][in] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-    StepRegs<QT> sr;
+    StepRegs sr;
     fetch_step<QT, BN>(sr, a, tr.W, tr.N, tr.m0, tr.n0, kbeg, t);
     for (int k0 = kbeg; k0 < kend; k0 += kBK) {
-        store_step<QT, BN>(xs, ws, sr, a, tr.W, tr.N, tr.n0, k0, t);
+        store_step<QT, BN>(xs, ws, sr, k0, t);
         __syncthreads();
         // the next step's loads go out before this step's matrix work
         if (k0 + kBK < kend) fetch_step<QT, BN>(sr, a, tr.W, tr.N, tr.m0, tr.n0, k0 + kBK, t);
@@ -316,9 +425,9 @@ void launch_typed(const GemmArgs& a, int bn, hipStream_t st) {
 
 }  // namespace
 
-// The types the reference multiplies as fp32 (a row dequantizer or a float
-// dot, c:2291-2331); Q4_0, Q4_1, Q5_0, Q5_1 and IQ4_NL take the Q8_0
-// activation path instead.
+// The types the reference dequantizes before its batched dot
+// (matmul_deq_batch_4row, c:2179-2273); Q4_0, Q4_1, Q5_0, Q5_1 and IQ4_NL
+// take the Q8_0 activation path instead (exact integer block dots per row).
 bool gemm_mfma_supported(int type) {
     switch (type) {
     case L3P_Q8_0: case L3P_Q2_K: case L3P_Q3_K: case L3P_Q4_K: case L3P_Q5_K: case L3P_Q6_K:

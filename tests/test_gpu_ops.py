@@ -260,6 +260,29 @@ def test_gemm_q8_activation_equals_gemv_rows(ctx, torch_gpu, qtype):
     assert torch_gpu.equal(y.view(batch, rows), torch_gpu.stack(ys))
 
 
+GEMM_TYPES = (l3p.F32, l3p.F16, l3p.BF16, l3p.Q8_0, l3p.Q2_K, l3p.Q3_K, l3p.Q4_K, l3p.Q5_K, l3p.Q6_K)
+
+
+@pytest.mark.parametrize("qtype", GEMM_TYPES)
+def test_gemm_weight_tiles_exact(ctx, torch_gpu, cpuref, qtype):
+    """The GEMM's weight tiles bit for bit: with unit activation rows
+    (x_b = e_b) every output is one product w[n][b] * 1 plus exact zeros, so
+    y[b][n] must be the reference's dequantized weight (dequantize_row_*,
+    c:611-934).  512 columns hold every element position of two
+    super-blocks; 200 rows leave a ragged row tile."""
+    rows, cols = 200, 512
+    w = synth.random_blocks(qtype, rows, cols, seed=7)
+    eye = np.eye(cols, dtype=np.float32)
+    y = torch_gpu.full((cols * rows,), float("nan"), dtype=torch_gpu.float32, device="cuda")
+    ctx.gemm(qtype, dev(torch_gpu, w), rows, cols, dev(torch_gpu, eye), cols, cols, y, rows)
+    ctx.synchronize()
+    got = y.cpu().numpy().reshape(cols, rows)
+    want = np.stack([cpuref.dequant(qtype, w[r], cols) for r in range(rows)]).T   # the reference's values
+    bad = np.argwhere(got != want)
+    assert bad.size == 0, f"{len(bad)} outputs differ, first (b, n) {tuple(bad[0])}: {got[tuple(bad[0])]!r} vs " \
+                          f"{want[tuple(bad[0])]!r}"
+
+
 def _dequant_bound(cpuref, qtype, w, rows, cols):
     """(W, A): the exact dequantized weights in float64 and the per-element
     magnitudes whose products with |x| bound either side's fp32 sums (module
@@ -285,7 +308,7 @@ def _dequant_bound(cpuref, qtype, w, rows, cols):
     (l3p.BF16, 257, 2048, 64),
     (l3p.F32, 100, 512, 70),
     # jobs large enough for 64 x 128 tiles (eight waves): ragged N and M,
-    # the element-wise dequantizer path, rows that are not 16-byte multiples
+    # K-quant slices, rows that are not 16-byte multiples
     (l3p.Q8_0, 8200, 512, 1000),
     (l3p.Q4_K, 8192, 512, 1024),
     (l3p.Q6_K, 8320, 256, 1000),
