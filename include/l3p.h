@@ -85,9 +85,10 @@ int l3p_gemv(l3p_ctx* ctx, int type, const void* w_dev, int rows, int cols, cons
  * for b < batch.  Replaces matmul_quantized_batch (c:2291-2331; js:3159-3845).
  * Q8_0, the K-quants, F16, BF16 and F32 run on the fp32-MFMA GEMM (weights
  * dequantized exactly, as matmul_deq_batch_4row, c:2179-2273); Q4_0 Q4_1
- * Q5_0 Q5_1 IQ4_NL run the GEMV per batch row (the reference's
- * Q8_0-activation integer dots, c:2305-2318).  in_stride must be a multiple
- * of 4 and x_dev 16-byte aligned. */
+ * Q5_0 Q5_1 IQ4_NL on the int8 matrix cores as the reference's
+ * Q8_0-activation dots (c:2305-2318): every batch row quantized to Q8_0,
+ * exact integer block dots, each output's block terms added in block order.
+ * in_stride must be a multiple of 4 and x_dev 16-byte aligned. */
 int l3p_gemm(l3p_ctx* ctx, int type, const void* w_dev, int rows, int cols, const float* x_dev,
              int batch, int in_stride, float* y_dev, int out_stride);
 
@@ -99,6 +100,8 @@ int l3p_gemm(l3p_ctx* ctx, int type, const void* w_dev, int rows, int cols, cons
  * device array of 16 MB (4 Mi floats) that each GPU holds for the life of
  * the process; the launch plan is l3p_gemm's, so results are l3p_gemm's, and
  * a shape whose partials would exceed the array returns L3P_E_UNSUPPORTED.
+ * (Q4_0 Q4_1 Q5_0 Q5_1 IQ4_NL keep their Q8_0-quantized x rows there
+ * instead, as many rows per launch as fit.)
  * Every call on a GPU shares that GPU's array: calls that overlap on one GPU
  * race.  Errors: the code, with the message in l3p_last_error(NULL). */
 int l3p_gemm_static(int type, const void* w_dev, int rows, int cols, const float* x_dev, int batch,

@@ -212,17 +212,6 @@ int l3p_gemm_static(int type, const void* w, int rows, int cols, const float* x,
     return guard(nullptr, [&] {
         if (!gemm_args_ok(type, w, rows, cols, x, batch, in_stride, y, out_stride)) return;
         const hipStream_t st = static_cast<hipStream_t>(stream);
-        if (!gemm_mfma_supported(type)) {
-            // the Q8_0-activation types: the GEMV per batch row, as l3p_gemm
-            for (int b = 0; b < batch; ++b) {
-                GemvBatch gb{};
-                gb.seg[0] = GemvSegment{(const uint8_t*)w, y + (size_t)b * out_stride, rows};
-                gb.nseg = 1;
-                gb.epilogue = EPI_STORE;
-                launch_gemv(type, gb, cols, x + (size_t)b * in_stride, nullptr, 0.0f, st);
-            }
-            return;
-        }
         GemmJob j{};
         j.type = type;
         j.seg[0] = GemmSegment{(const uint8_t*)w, rows, y, out_stride};
@@ -231,6 +220,14 @@ int l3p_gemm_static(int type, const void* w, int rows, int cols, const float* x,
         j.x = x;
         j.m = batch;
         j.ldx = in_stride;
+        if (gemm_q8_activation(type)) {
+            // the int8 path of l3p_gemm (no partials; each output's blocks in
+            // order, so the rows per launch do not change a value), with the
+            // quantized activation rows in the file-scope array
+            launch_gemm_q8a(j, gemm_static_scratch(), kGemmStaticScratchFloats, st);
+            return;
+        }
+        L3P_REQUIRE(gemm_mfma_supported(type), L3P_E_UNSUPPORTED, "gemm_static: type %d", type);
         // the plan l3p_gemm takes with its context workspace, so the values
         // are l3p_gemm's; its partials must fit the file-scope array
         const GemmPlan plan = gemm_plan(j, kGemmWsFloats);

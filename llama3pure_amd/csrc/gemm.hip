@@ -51,6 +51,7 @@ constexpr int kBM = 64, kBK = 64;
 constexpr int kLDK = kBK + 4;   // LDS row stride in floats (b128 reads spread over the banks)
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef int int32x4 __attribute__((ext_vector_type(4)));
 
 struct GemmArgs {
     const uint8_t* w[3];   // per segment: weight rows,
@@ -558,6 +559,304 @@ void launch_gemm_planned(const GemmJob& j, const GemmPlan& plan, float* ws, hipS
     }
     if (a.nsplit > 1 || a.streamk)
         launch_kernel(gemm_reduce_kernel, dim3((ntot + 255) / 256, j.m), dim3(256), 0u, st, a);
+}
+
+// ---------------------------------------------------------------------------
+// The Q8_0-activation types (Q4_0, Q4_1, Q5_0, Q5_1, IQ4_NL) on the int8
+// matrix cores.  The reference's batched dot for them (matmul_quantized_batch,
+// c:2305-2318, with vec_dot_*_q8_0, c:1625-1720) quantizes each activation row
+// to Q8_0 and sums, block by block in order,
+//   sum += dw * dx * (float)isum  (+ mw * dx * (float)xsum for Q4_1, Q5_1)
+// with isum the exact integer dot of the block's weight codes and activation
+// quants.  Here q8_rows_kernel quantizes the rows once (int8 quants, the fp16
+// scale as float, the quant sum), a workgroup expands a 64 x 64 weight tile to
+// int8 codes in LDS (Q4_0 and Q5_0 subtract their offset 8 or 16 byte-wise,
+// IQ4_NL maps its nibbles through a byte permute of its table), and one
+// v_mfma_i32_16x16x32_i8 gives the exact isum of one block for 16 x 16
+// outputs.  Each output's lane then adds the block terms in block order with
+// the reference's expression, so no K split and no reordering of the terms.
+// ---------------------------------------------------------------------------
+namespace {
+
+__global__ void __launch_bounds__(256) q8_rows_kernel(const float* __restrict__ x, int ldx, int k, int rows,
+                                                      int8_t* __restrict__ xq, float* __restrict__ dx,
+                                                      float* __restrict__ sx) {
+    const int nb = k >> 5;
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t)rows * nb) return;
+    const int r = (int)(i / nb), b = (int)(i % nb);
+    const float4* src = reinterpret_cast<const float4*>(x + (size_t)r * ldx + 32 * b);
+    float v[32];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+        const float4 f = src[u];
+        v[4 * u] = f.x;
+        v[4 * u + 1] = f.y;
+        v[4 * u + 2] = f.z;
+        v[4 * u + 3] = f.w;
+    }
+    QBlock q;
+    quantize32(v, q);   // quantize_row_q8_0 (c:1508-1528)
+    uint32_t wq[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+        wq[u] = (uint32_t)(uint8_t)q.q[4 * u] | ((uint32_t)(uint8_t)q.q[4 * u + 1] << 8) |
+                ((uint32_t)(uint8_t)q.q[4 * u + 2] << 16) | ((uint32_t)(uint8_t)q.q[4 * u + 3] << 24);
+    uint4* dst = reinterpret_cast<uint4*>(xq + (size_t)r * k + 32 * b);
+    dst[0] = make_uint4(wq[0], wq[1], wq[2], wq[3]);
+    dst[1] = make_uint4(wq[4], wq[5], wq[6], wq[7]);
+    dx[i] = h2f_exact(q.dh);   // fp16_to_fp32(xq.d)
+    sx[i] = (float)q.sum;
+}
+
+// One thread's 16 weight codes of a step: row t / 4 of the tile, elements
+// e0 .. e0 + 15 (half of a 32-element block), fetched one step ahead.
+struct Q8aRegs {
+    uint4 x;            // 16 activation quants
+    uint4 q;            // the block's 16 nibble-pair bytes
+    uint32_t h0, h1;    // d (| m << 16), the 32 high bits (Q5_0, Q5_1)
+    float dxv, sxv;     // one activation block's scale and quant sum
+};
+
+template <int QT>
+__device__ __forceinline__ void fetch_q8a_w(Q8aRegs& r, const uint8_t* row, int e0) {
+    if constexpr (QT == L3P_Q4_0 || QT == L3P_IQ4_NL) {   // 18 bytes: d, qs[16]
+        const uint8_t* b = row + (size_t)(e0 >> 5) * 18;
+        r.h0 = *reinterpret_cast<const uint16_t*>(b);
+        __builtin_memcpy(&r.q, b + 2, 16);
+    } else if constexpr (QT == L3P_Q4_1) {   // 20 bytes: d, m, qs[16]
+        const uint8_t* b = row + (size_t)(e0 >> 5) * 20;
+        __builtin_memcpy(&r.h0, b, 4);
+        __builtin_memcpy(&r.q, b + 4, 16);
+    } else if constexpr (QT == L3P_Q5_0) {   // 22 bytes: d, qh[4], qs[16]
+        const uint8_t* b = row + (size_t)(e0 >> 5) * 22;
+        r.h0 = *reinterpret_cast<const uint16_t*>(b);
+        __builtin_memcpy(&r.h1, b + 2, 4);
+        __builtin_memcpy(&r.q, b + 6, 16);
+    } else {   // Q5_1, 24 bytes: d, m, qh[4], qs[16]
+        const uint8_t* b = row + (size_t)(e0 >> 5) * 24;
+        __builtin_memcpy(&r.h0, b, 4);
+        __builtin_memcpy(&r.h1, b + 4, 4);
+        __builtin_memcpy(&r.q, b + 8, 16);
+    }
+}
+
+// IQ4_NL's values (kvalues_iq4nl, c:920-934) of the four nibbles in the bytes
+// of nb: byte permutes over the table's two halves and a byte select on bit 3.
+__device__ __forceinline__ uint32_t iq4nl_bytes(uint32_t nb) {
+    const uint32_t sel = nb & 0x07070707u;
+    const uint32_t lo = __builtin_amdgcn_perm(0xF6EADDCFu, 0xBFAD9881u, sel);   // -127 -104 -83 -65 -49 -35 -22 -10
+    const uint32_t hi = __builtin_amdgcn_perm(0x71594535u, 0x26190D01u, sel);   // 1 13 25 38 53 69 89 113
+    const uint32_t m = ((nb >> 3) & 0x01010101u) * 0xffu;
+    return (hi & m) | (lo & ~m);
+}
+
+// byte-wise x - c for bytes x in 0..31 and c <= 16, as int8 (no borrow
+// crosses a byte: x | 0x80 - c stays >= 0x70)
+__device__ __forceinline__ uint32_t sub_bytes(uint32_t x, uint32_t c4) { return ((x | 0x80808080u) - c4) ^ 0x80808080u; }
+
+// the 16 int8 codes of elements e0 .. e0 + 15 (the weight values over d; the
+// codes vec_dot_*_q8_0 multiplies with the activation quants)
+template <int QT>
+__device__ __forceinline__ uint4 decode_q8a_w(const Q8aRegs& r, int e0) {
+    const int hi = (e0 >> 4) & 1;   // elements 16..31: the high nibbles
+    const uint32_t qw[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int w4 = 0; w4 < 4; ++w4) {
+        uint32_t nb = (qw[w4] >> (4 * hi)) & 0x0f0f0f0fu;
+        if constexpr (QT == L3P_Q5_0 || QT == L3P_Q5_1) {
+            // bits 16 hi + 4 w4 .. + 3 of qh to bit 4 of the four bytes
+            const uint32_t hb = (r.h1 >> (16 * hi + 4 * w4)) & 0xfu;
+            nb |= ((hb * 0x00204081u) & 0x01010101u) << 4;
+        }
+        if constexpr (QT == L3P_Q4_0) o[w4] = sub_bytes(nb, 0x08080808u);
+        else if constexpr (QT == L3P_Q5_0) o[w4] = sub_bytes(nb, 0x10101010u);
+        else if constexpr (QT == L3P_IQ4_NL) o[w4] = iq4nl_bytes(nb);
+        else o[w4] = nb;   // Q4_1, Q5_1: codes 0..15, 0..31
+    }
+    return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+constexpr int kQLD = 80;   // LDS row stride of the int8 tiles (bytes, 16-byte aligned rows)
+
+template <int QT>
+__global__ void __launch_bounds__(256) gemm_q8a_kernel(GemmArgs a, const int8_t* __restrict__ xq,
+                                                       const float* __restrict__ dxg, const float* __restrict__ sxg) {
+    constexpr bool kMin = QT == L3P_Q4_1 || QT == L3P_Q5_1;
+    __shared__ __align__(16) int8_t xs[kBM * kQLD];
+    __shared__ __align__(16) int8_t ws[64 * kQLD];
+    __shared__ __align__(16) float dxs[2][kBM];   // activation block scales [block of the step][row]
+    __shared__ __align__(16) float sxs[2][kBM];   // activation quant sums
+    __shared__ __align__(16) float dws[2][64];    // weight block scales [block][weight row]
+    __shared__ __align__(16) float mws[2][64];    // weight block minima
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const int wm = w >> 1, wn = w & 1;       // this wave's 32 x 32 block of the 64 x 64 tile
+    const int g = lane >> 4, i16 = lane & 15;
+    const TileRef tr = tile_ref<64>(a, blockIdx.x, blockIdx.y);
+    const int nb = a.k >> 5;
+    float acc[2][2][4];
+#pragma unroll
+    for (int im = 0; im < 2; ++im)
+#pragma unroll
+        for (int in = 0; in < 2; ++in)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[im][in][r] = 0.0f;
+    Q8aRegs R;
+    auto fetch = [&](int k0) {
+        const int m = tr.m0 + (t >> 2), kx = k0 + 16 * (t & 3);
+        R.x = make_uint4(0u, 0u, 0u, 0u);
+        if (m < a.m && kx < a.k) R.x = *reinterpret_cast<const uint4*>(xq + (size_t)m * a.k + kx);
+        R.dxv = 0.0f;
+        R.sxv = 0.0f;
+        if (t < 2 * kBM) {   // scale and quant sum of row t % 64, block t / 64 of the step
+            const int mm = tr.m0 + (t & 63), kb = (k0 >> 5) + (t >> 6);
+            if (mm < a.m && kb < nb) {
+                R.dxv = dxg[(size_t)mm * nb + kb];
+                if (kMin) R.sxv = sxg[(size_t)mm * nb + kb];
+            }
+        }
+        const int n = tr.n0 + (t >> 2);
+        R.q = make_uint4(0u, 0u, 0u, 0u);
+        R.h0 = R.h1 = 0u;
+        if (n < tr.N && kx < a.k) fetch_q8a_w<QT>(R, tr.W + (size_t)n * a.rb, kx);
+    };
+    fetch(0);
+    for (int k0 = 0; k0 < a.k; k0 += kBK) {
+        const int kx = k0 + 16 * (t & 3);
+        *reinterpret_cast<uint4*>(xs + (t >> 2) * kQLD + 16 * (t & 3)) = R.x;
+        *reinterpret_cast<uint4*>(ws + (t >> 2) * kQLD + 16 * (t & 3)) = decode_q8a_w<QT>(R, kx);
+        if (t < 2 * kBM) {
+            dxs[t >> 6][t & 63] = R.dxv;
+            if (kMin) sxs[t >> 6][t & 63] = R.sxv;
+        }
+        if ((t & 1) == 0) {   // the block's d (and m) of row t / 4, block (t / 2) % 2
+            dws[(t >> 1) & 1][t >> 2] = h2f_exact(R.h0 & 0xffffu);
+            if (kMin) mws[(t >> 1) & 1][t >> 2] = h2f_exact(R.h0 >> 16);
+        }
+        __syncthreads();
+        if (k0 + kBK < a.k) fetch(k0 + kBK);
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+            if (k0 + 32 * kb >= a.k) break;
+            long af[2], bf[2];
+#pragma unroll
+            for (int im = 0; im < 2; ++im)
+                af[im] = *reinterpret_cast<const long*>(xs + (32 * wm + 16 * im + i16) * kQLD + 32 * kb + 8 * g);
+#pragma unroll
+            for (int in = 0; in < 2; ++in)
+                bf[in] = *reinterpret_cast<const long*>(ws + (32 * wn + 16 * in + i16) * kQLD + 32 * kb + 8 * g);
+#pragma unroll
+            for (int in = 0; in < 2; ++in) {
+                const float dw = dws[kb][32 * wn + 16 * in + i16];
+                const float mw = kMin ? mws[kb][32 * wn + 16 * in + i16] : 0.0f;
+#pragma unroll
+                for (int im = 0; im < 2; ++im) {
+                    // D lane (g, i16): rows (activation rows) 4 g .. 4 g + 3 of column i16 (weight row)
+                    const int32x4 is = __builtin_amdgcn_mfma_i32_16x16x32_i8(af[im], bf[in], int32x4{0, 0, 0, 0}, 0, 0, 0);
+                    const float4 dx4 = *reinterpret_cast<const float4*>(&dxs[kb][32 * wm + 16 * im + 4 * g]);
+                    const float dxr[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
+                    float sxr[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+                    if (kMin) {
+                        const float4 s4 = *reinterpret_cast<const float4*>(&sxs[kb][32 * wm + 16 * im + 4 * g]);
+                        sxr[0] = s4.x;
+                        sxr[1] = s4.y;
+                        sxr[2] = s4.z;
+                        sxr[3] = s4.w;
+                    }
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        float term = dw * dxr[r] * (float)is[r];
+                        if (kMin) term = term + mw * dxr[r] * sxr[r];
+                        acc[im][in][r] += term;
+                    }
+                }
+            }
+        }
+        __syncthreads();
+    }
+    float* const Y = a.y[tr.sg];
+    const int ldy = a.ldy[tr.sg];
+#pragma unroll
+    for (int im = 0; im < 2; ++im)
+#pragma unroll
+        for (int in = 0; in < 2; ++in) {
+            const int n = tr.n0 + 32 * wn + 16 * in + i16;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int m = tr.m0 + 32 * wm + 16 * im + 4 * g + r;
+                if (m < a.m && n < tr.N) {
+                    float* p = Y + (size_t)m * ldy + n;
+                    *p = a.add ? *p + acc[im][in][r] : acc[im][in][r];
+                }
+            }
+        }
+}
+
+}  // namespace
+
+bool gemm_q8_activation(int type) {
+    return type == L3P_Q4_0 || type == L3P_Q4_1 || type == L3P_Q5_0 || type == L3P_Q5_1 || type == L3P_IQ4_NL;
+}
+
+size_t gemm_q8a_ws_floats(int rows, int k) {
+    // int8 quants (k bytes a row) and two floats per block, 256-byte aligned parts
+    const size_t q = ((size_t)rows * k + 255) / 256 * 64;
+    const size_t s = ((size_t)rows * (k / 32) + 63) / 64 * 64;
+    return q + 2 * s;
+}
+
+void launch_gemm_q8a(const GemmJob& j, float* ws, size_t ws_floats, hipStream_t st) {
+    L3P_REQUIRE(gemm_q8_activation(j.type), L3P_E_UNSUPPORTED, "gemm: type %d has no int8 path", j.type);
+    L3P_REQUIRE(j.k % 32 == 0 && j.ldx % 4 == 0 && ((uintptr_t)j.x & 15) == 0, L3P_E_INVALID,
+                "gemm: x rows must be 16-byte aligned");
+    L3P_REQUIRE(j.nseg >= 1 && j.nseg <= 3, L3P_E_INVALID, "gemm: %d segments", j.nseg);
+    if (j.m == 0) return;
+    // rows per launch: as many as the workspace holds the quantized rows of
+    const size_t per_row = gemm_q8a_ws_floats(1, j.k);
+    L3P_REQUIRE(ws && ws_floats >= gemm_q8a_ws_floats(1, j.k), L3P_E_INVALID, "gemm: workspace of %zu floats",
+                ws_floats);
+    int cr = (int)std::min<size_t>((size_t)j.m, ws_floats / per_row);
+    while (cr > 1 && gemm_q8a_ws_floats(cr, j.k) > ws_floats) --cr;
+    cr = std::min(cr, 65535 * kBM);
+    GemmArgs a{};
+    int tiles = 0;
+    for (int i = 0; i < j.nseg; ++i) {
+        if (j.seg[i].n == 0) continue;
+        a.w[a.nseg] = j.seg[i].w;
+        a.y[a.nseg] = j.seg[i].y;
+        a.ldy[a.nseg] = j.seg[i].ldy;
+        a.n[a.nseg] = j.seg[i].n;
+        a.tbeg[a.nseg] = tiles;
+        tiles += (j.seg[i].n + 63) / 64;
+        ++a.nseg;
+    }
+    if (a.nseg == 0) return;
+    a.tbeg[a.nseg] = tiles;
+    a.rb = type_row_bytes(j.type, j.k);
+    a.k = j.k;
+    a.add = j.add ? 1 : 0;
+    a.bn = 64;
+    for (int b0 = 0; b0 < j.m; b0 += cr) {
+        const int rows = std::min(cr, j.m - b0);
+        int8_t* xq = reinterpret_cast<int8_t*>(ws);
+        float* dx = ws + ((size_t)rows * j.k + 255) / 256 * 64;
+        float* sx = dx + ((size_t)rows * (j.k / 32) + 63) / 64 * 64;
+        const int64_t nblk = (int64_t)rows * (j.k / 32);
+        launch_kernel(q8_rows_kernel, dim3((unsigned)((nblk + 255) / 256)), dim3(256), 0u, st,
+                      j.x + (size_t)b0 * j.ldx, j.ldx, j.k, rows, xq, dx, sx);
+        GemmArgs c = a;
+        c.m = rows;
+        for (int i = 0; i < c.nseg; ++i) c.y[i] = a.y[i] + (size_t)b0 * a.ldy[i];
+        const dim3 grid(tiles, (rows + kBM - 1) / kBM);
+        switch (j.type) {
+        case L3P_Q4_0: launch_kernel(gemm_q8a_kernel<L3P_Q4_0>, grid, dim3(256), 0u, st, c, xq, dx, sx); break;
+        case L3P_Q4_1: launch_kernel(gemm_q8a_kernel<L3P_Q4_1>, grid, dim3(256), 0u, st, c, xq, dx, sx); break;
+        case L3P_Q5_0: launch_kernel(gemm_q8a_kernel<L3P_Q5_0>, grid, dim3(256), 0u, st, c, xq, dx, sx); break;
+        case L3P_Q5_1: launch_kernel(gemm_q8a_kernel<L3P_Q5_1>, grid, dim3(256), 0u, st, c, xq, dx, sx); break;
+        default: launch_kernel(gemm_q8a_kernel<L3P_IQ4_NL>, grid, dim3(256), 0u, st, c, xq, dx, sx); break;
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------

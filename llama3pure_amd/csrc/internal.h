@@ -181,6 +181,13 @@ struct GemmJob {
     bool add;
 };
 bool gemm_mfma_supported(int type);
+// the types whose batched dot takes Q8_0-quantized activation rows (Q4_0,
+// Q4_1, Q5_0, Q5_1, IQ4_NL): the int8 matrix-core path, exact block dots
+bool gemm_q8_activation(int type);
+// workspace floats the int8 path needs for `rows` activation rows of k columns
+size_t gemm_q8a_ws_floats(int rows, int k);
+// the job through workspace ws (the rows in as many launches as it needs)
+void launch_gemm_q8a(const GemmJob& j, float* ws, size_t ws_floats, hipStream_t s);
 void launch_gemm(const GemmJob& j, float* ws, size_t ws_floats, hipStream_t s);
 // K splits of a job and the fp32 partials they need, for a workspace of
 // ws_floats floats (0: no split)

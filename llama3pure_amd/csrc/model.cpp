@@ -750,16 +750,18 @@ struct RowsOut {
 };
 
 // y rows (=|+=) W . x rows for `rows` prompt tokens, for one to three
-// matrices over the same x rows.  Matrices of one MFMA type and width run as
-// one GEMM launch (label `what`); the Q8_0-activation types run the GEMV per
-// row, which quantizes each row to Q8_0 and takes the reference's integer
-// block dots (matmul_quantized_batch, c:2305-2318).
+// matrices over the same x rows.  Matrices of one type and width run as one
+// GEMM launch (label `what`): the fp32 matrix-core GEMM for the types the
+// reference dequantizes, the int8 one for the Q8_0-activation types (the
+// reference's exact integer block dots, matmul_quantized_batch, c:2305-2318).
+static bool gemm_capable(int type) { return gemm_mfma_supported(type) || gemm_q8_activation(type); }
+
 static void gemm_rows(l3p_ctx* c, std::initializer_list<RowsOut> outs, const float* x, int ldx, int rows, bool add,
                       const char* what) {
     hipStream_t s = c->stream;
     const RowsOut* o = outs.begin();
     const int n = (int)outs.size();
-    bool together = gemm_mfma_supported(o[0].W->type);
+    bool together = gemm_capable(o[0].W->type);
     for (int i = 1; i < n; ++i) together = together && o[i].W->type == o[0].W->type && o[i].W->cols == o[0].W->cols;
     if (together) {
         GemmJob j{};
@@ -779,12 +781,13 @@ static void gemm_rows(l3p_ctx* c, std::initializer_list<RowsOut> outs, const flo
         }
         ProfRange r(c->prof, s, gemm_label(n > 1 ? what : o[0].what, j.type, rows, ntot, j.k),
                     bytes + 4.0 * rows * (j.k + ntot));
-        launch_gemm(j, c->gemm_ws, c->gemm_ws_floats, s);
+        if (gemm_q8_activation(j.type)) launch_gemm_q8a(j, c->gemm_ws, c->gemm_ws_floats, s);
+        else launch_gemm(j, c->gemm_ws, c->gemm_ws_floats, s);
         return;
     }
     for (int i = 0; i < n; ++i) {
         const Mat& W = *o[i].W;
-        if (gemm_mfma_supported(W.type)) {
+        if (gemm_capable(W.type)) {
             gemm_rows(c, {o[i]}, x, ldx, rows, add, o[i].what);
             continue;
         }
@@ -1010,6 +1013,18 @@ static void sample_impl(l3p_ctx* c, const float* logits, int n, const l3p_sample
 // ---------------------------------------------------------------------------
 void run_gemm(l3p_ctx* c, int type, const uint8_t* w, int rows, int cols, const float* x, int batch, int in_stride,
               float* y, int out_stride) {
+    if (gemm_q8_activation(type)) {   // the reference's integer block dots on the int8 matrix cores
+        GemmJob j{};
+        j.type = type;
+        j.seg[0] = GemmSegment{w, rows, y, out_stride};
+        j.nseg = 1;
+        j.k = cols;
+        j.x = x;
+        j.m = batch;
+        j.ldx = in_stride;
+        launch_gemm_q8a(j, c->gemm_ws, c->gemm_ws_floats, c->stream);
+        return;
+    }
     if (gemm_mfma_supported(type)) {
         GemmJob j{};
         j.type = type;
@@ -1022,15 +1037,7 @@ void run_gemm(l3p_ctx* c, int type, const uint8_t* w, int rows, int cols, const 
         launch_gemm(j, c->gemm_ws, c->gemm_ws_floats, c->stream);
         return;
     }
-    // Q4_0: the reference quantizes every batch row to Q8_0 and takes integer
-    // block dots (c:2305-2318), which is what the GEMV computes per row
-    for (int b = 0; b < batch; ++b) {
-        GemvBatch gb{};
-        gb.seg[0] = GemvSegment{w, y + (size_t)b * out_stride, rows};
-        gb.nseg = 1;
-        gb.epilogue = EPI_STORE;
-        gemv_plain(c, type, gb, cols, x + (size_t)b * in_stride);
-    }
+    L3P_REQUIRE(false, L3P_E_UNSUPPORTED, "gemm: type %d", type);
 }
 
 void run_stream_read(l3p_ctx* c, const void* p, size_t bytes) {

@@ -241,23 +241,53 @@ def test_gemv_deterministic(ctx, torch_gpu):
 
 
 @pytest.mark.parametrize("qtype", Q8_ACT)
-def test_gemm_q8_activation_equals_gemv_rows(ctx, torch_gpu, qtype):
-    """Batches of the Q8_0-activation types run the GEMV per row (the
-    reference's integer Q8_0-activation dot, c:2305-2318): per batch element
-    exactly the GEMV result."""
-    rows, cols, batch = 1024, 2048, 7
-    w = dev(torch_gpu, synth.random_blocks(qtype, rows, cols, seed=5))
+@pytest.mark.parametrize("rows,cols,batch", [(1024, 2048, 7), (300, 4096, 130), (77, 96, 65)])
+def test_gemm_q8_activation_parity(ctx, torch_gpu, cpuref, qtype, rows, cols, batch):
+    """Batches of the Q8_0-activation types on the int8 matrix cores against
+    the float64 value of the reference's batched dot (matmul_quantized_batch,
+    c:2305-2318: every row quantized to Q8_0, vec_dot_*_q8_0 per block).  The
+    block dots are exact integers and each output adds its block terms in
+    block order with the reference's expression, so beyond the module's bound
+    gamma_(K+4) S the error stays within gamma_(blocks+4) S, S = sum of
+    |block terms| (a sum over per-element fp32 products would not).  The
+    oracle's own batched dot meets the same bounds.  96 columns give a K step
+    of one block; 65 and 130 rows leave ragged row tiles."""
+    w = synth.random_blocks(qtype, rows, cols, seed=5)
     xb = synth.random_x(cols, seed=6, batch=batch)
-    xd = dev(torch_gpu, xb)
     y = empty_f32(torch_gpu, batch * rows)
-    ctx.gemm(qtype, w, rows, cols, xd, batch, cols, y, rows)
+    ctx.gemm(qtype, dev(torch_gpu, w), rows, cols, dev(torch_gpu, xb), batch, cols, y, rows)
+    ctx.synchronize()
+    got = y.cpu().numpy().reshape(batch, rows).astype(np.float64)
+    terms = [q8_block_terms(cpuref, qtype, w, rows, cols, xb[b]) for b in range(batch)]
+    y64 = np.stack([t.sum(1) for t in terms])
+    S = np.stack([np.abs(t).sum(1) for t in terms])
+    ref = cpuref.matmul_batch(qtype, w, rows, cols, xb).astype(np.float64)
+    for name, tol in (("gamma_(K+4) S", gamma(cols + 4) * S), ("gamma_(blocks+4) S", gamma(cols // 32 + 4) * S)):
+        assert np.all(np.abs(ref - y64) <= tol), f"oracle outside {name}"
+        err = np.abs(got - y64)
+        assert np.all(err <= tol), f"{name}: max err/tol {np.max(err / np.maximum(tol, 1e-30)):.3g}"
+
+
+@pytest.mark.parametrize("qtype", Q8_ACT)
+def test_gemm_q8_activation_close_to_gemv(ctx, torch_gpu, cpuref, qtype):
+    """The batched and the single-row (GEMV) forms of these types agree
+    within twice the module's bound."""
+    rows, cols, batch = 1024, 2048, 5
+    w = synth.random_blocks(qtype, rows, cols, seed=15)
+    xb = synth.random_x(cols, seed=16, batch=batch)
+    wd, xd = dev(torch_gpu, w), dev(torch_gpu, xb)
+    y = empty_f32(torch_gpu, batch * rows)
+    ctx.gemm(qtype, wd, rows, cols, xd, batch, cols, y, rows)
     ys = []
     for b in range(batch):
         yb = empty_f32(torch_gpu, rows)
-        ctx.gemv(qtype, w, rows, cols, xd[b], yb)
+        ctx.gemv(qtype, wd, rows, cols, xd[b], yb)
         ys.append(yb)
     ctx.synchronize()
-    assert torch_gpu.equal(y.view(batch, rows), torch_gpu.stack(ys))
+    S = np.stack([np.abs(q8_block_terms(cpuref, qtype, w, rows, cols, xb[b])).sum(1) for b in range(batch)])
+    diff = np.abs(y.view(batch, rows).cpu().numpy().astype(np.float64) -
+                  torch_gpu.stack(ys).cpu().numpy().astype(np.float64))
+    assert np.all(diff <= 2 * gamma(cols + 4) * S)
 
 
 GEMM_TYPES = (l3p.F32, l3p.F16, l3p.BF16, l3p.Q8_0, l3p.Q2_K, l3p.Q3_K, l3p.Q4_K, l3p.Q5_K, l3p.Q6_K)

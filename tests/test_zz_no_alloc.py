@@ -26,7 +26,8 @@ def test_gemm_static_equals_gemm(torch_gpu, qt):
     with l3p.Context(0) as ctx:
         # rows x cols x batch: 64 output tiles of one 64-row tile whose K is
         # cut over 8 workgroups each (partials of 8 x 8 x 4096 floats), then a
-        # smaller call cut over 4; for Q4_0 the GEMV per batch row
+        # smaller call cut over 4; Q4_0 takes the int8 path with its quantized
+        # activation rows in the array
         for rows, cols, batch in ((4096, 4096, 8), (1024, 2048, 3)):
             w = torch.from_numpy(synth.random_blocks(qt, rows, cols, seed=rows + batch)).cuda()
             x = torch.from_numpy(synth.random_x(cols, seed=cols, batch=batch)).cuda()
@@ -49,7 +50,7 @@ def test_gemm_static_in_graph(torch_gpu, qt):
     a stream into a graph; every replay, with eager work and synchronizations
     between replays, equals l3p_gemm bit for bit.  4096 x 4096 x batch 8
     cuts K over 8 workgroups per tile (Q8_0), so the replays use the
-    file-scope partials; Q4_0 runs the GEMV per batch row."""
+    file-scope partials; Q4_0 keeps its quantized activation rows there."""
     torch = torch_gpu
     L = l3p.lib()
     rows, cols, batch = 4096, 4096, 8
@@ -105,3 +106,26 @@ def test_gemm_static_rejects_oversized_partials(torch_gpu):
                                  ctx.stream) == l3p.E_INVALID
         assert L.l3p_gemm_static(synth.Q8_0, w.data_ptr(), rows, 0, x.data_ptr(), 1, cols, y.data_ptr(), rows,
                                  ctx.stream) == l3p.E_INVALID
+
+
+def test_gemm_static_q8_activation_chunks(torch_gpu):
+    """Q4_0 rows whose quantized form exceeds the file-scope array go through
+    it in several launches (1000 rows of 14336 columns: 4480 floats a row
+    against 4 Mi floats); each output adds its blocks in order whatever the
+    rows per launch, so the result equals l3p_gemm's (one launch) bit for
+    bit."""
+    torch = torch_gpu
+    L = l3p.lib()
+    rows, cols, batch = 256, 14336, 1000
+    with l3p.Context(0) as ctx:
+        w = torch.from_numpy(synth.random_blocks(synth.Q4_0, rows, cols, seed=21)).cuda()
+        x = torch.from_numpy(synth.random_x(cols, seed=22, batch=batch)).cuda()
+        y_ref = torch.full((batch, rows), float("nan"), device="cuda")
+        y_st = torch.full((batch, rows), float("nan"), device="cuda")
+        torch.cuda.synchronize()
+        ctx.gemm(synth.Q4_0, w, rows, cols, x, batch, cols, y_ref, rows)
+        ctx.synchronize()
+        rc = _static(L, synth.Q4_0, w, rows, cols, x, batch, y_st, ctx.stream)
+        assert rc == l3p.OK, L.l3p_last_error(None).decode()
+        ctx.synchronize()
+        assert np.array_equal(y_ref.cpu().numpy().view(np.uint32), y_st.cpu().numpy().view(np.uint32))
