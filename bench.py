@@ -34,6 +34,12 @@ Printed as one JSON line:
                reference is not built.
 
 usage: python bench.py [--gpus 1] [--steps 128] [--warmup 8]
+
+Measurement-only modes (one JSON line per case, no decode): --gemv-shapes,
+--gemm-types (the batched product of every weight type at 4096 x 4096 x 1024
+rows), --prefill-types (a 1024-position prompt through four
+Llama-3-8B-shape layers for several weight mixes), --attn-sweep,
+--copy-ceiling, --calibrate-copy.
 """
 from __future__ import annotations
 
@@ -513,6 +519,110 @@ def cpu_baseline(img, seconds: float, start: int) -> dict | None:
     return out
 
 
+GEMM_TYPES = ("Q8_0", "Q4_K", "Q6_K", "Q5_K", "Q3_K", "Q2_K", "F16", "BF16", "F32",
+              "Q4_0", "Q4_1", "Q5_0", "Q5_1", "IQ4_NL")
+
+
+def gemm_types_only():
+    """Batched products (l3p_gemm) of every weight type at 4096 x 4096 and
+    1024 rows (Llama-3-8B's output projection over a 1024-position prompt
+    pass): random blocks (seed 1) in four copies used in turn, an N(0,1)
+    activation (seed 5); three warm calls, then 20 calls between two events on
+    the library's stream.  One JSON line per type.  The fp32-MFMA types are
+    quoted against the fp32 matrix peak; the Q8_0-activation types run on the
+    int8 matrix cores and are quoted against that peak as well."""
+    import torch
+
+    import llama3pure_amd as l3p
+    from llama3pure_amd import synth
+
+    ctx = l3p.Context(0)
+    st = torch.cuda.ExternalStream(ctx.stream)
+    rows = cols = 4096
+    m = 1024
+    x = torch.from_numpy(synth.random_x(cols, seed=5, batch=m)).cuda()
+    y = torch.empty(m * rows, dtype=torch.float32, device="cuda")
+    flops = 2.0 * rows * cols * m
+    for name in GEMM_TYPES:
+        qt = getattr(l3p, name)
+        w = synth.random_blocks(qt, rows, cols, seed=1)
+        wd = [torch.from_numpy(w).cuda() for _ in range(4)]
+        torch.cuda.synchronize()
+        for i in range(3):
+            ctx.gemm(qt, wd[i % 4], rows, cols, x, m, cols, y, rows)
+        ctx.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        n = 20
+        e0.record(st)
+        for i in range(n):
+            ctx.gemm(qt, wd[i % 4], rows, cols, x, m, cols, y, rows)
+        e1.record(st)
+        e1.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / n
+        int8 = name in ("Q4_0", "Q4_1", "Q5_0", "Q5_1", "IQ4_NL")
+        tf = flops / us / 1e6
+        line = {"type": name, "shape": f"{rows}x{cols} b{m}", "us": round(us, 1), "TFLOP/s": round(tf, 1),
+                "matrix_cores": "int8" if int8 else "fp32",
+                "frac_of_peak": round(tf / (5000.0 if int8 else 157.3), 4)}
+        print(json.dumps(line), flush=True)
+        del wd
+        torch.cuda.empty_cache()
+    ctx.close()
+
+
+def prefill_types_only(layers: int = 4):
+    """A 1024-position prompt (l3p_prefill) through a Llama-3-8B-shape model of
+    `layers` layers (dim 4096, FFN 14336, 32 / 8 heads, vocab 1024: the
+    projections at full size) for several weight mixes, random blocks;
+    the best of three prompts after a warm one, and its GEMM share from the
+    per-launch events of one more.  One JSON line per mix."""
+    import numpy as np
+    import torch
+
+    import llama3pure_amd as l3p
+    from llama3pure_amd import synth
+
+    def maker(seed):
+        state = [seed]
+
+        def make(qt, rows, cols, std, view):
+            state[0] += 1
+            view[:] = synth.random_blocks(qt, rows, cols, seed=state[0]).ravel()
+            return view
+
+        return make
+
+    mixes = [("Q8_0", l3p.Q8_0, None), ("Q4_0", l3p.Q4_0, None), ("Q5_0", l3p.Q5_0, None),
+             ("Q4_K", l3p.Q4_K, None), ("Q4_K, Q6_K attn_v and ffn_down", l3p.Q4_K,
+                                        {"attn_v": l3p.Q6_K, "ffn_down": l3p.Q6_K}),
+             ("Q6_K", l3p.Q6_K, None)]
+    for name, qt, mix in mixes:
+        ctx = l3p.Context(0)
+        img = synth.synthetic_model(arch="llama", dim=4096, hidden=14336, n_layers=layers, n_heads=32, n_kv=8,
+                                    vocab=1024, ctx=2048, qtype=qt, qtypes=mix, make_mat=maker(7))
+        mi = ctx.load_gguf(img)
+        prompt = np.random.default_rng(5).integers(0, mi.vocab_size, 1024).astype(np.int32)
+        ctx.prefill(prompt, 0)
+        ctx.synchronize()
+        ts = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            ctx.prefill(prompt, 0)
+            ctx.synchronize()
+            ts.append(time.perf_counter() - t0)
+        ctx.profile(True)
+        ctx.prefill(prompt, 0)
+        stats = ctx.profile_read()
+        ctx.profile(False)
+        ms = min(ts) * 1e3
+        gemm_ms = sum(v[1] for k, v in stats.items() if " gemm " in k)
+        print(json.dumps({"weights": name, "layers": layers, "positions": 1024, "ms": round(ms, 2),
+                          "ms_per_layer": round(ms / layers, 3), "gemm_ms": round(gemm_ms, 2)}), flush=True)
+        ctx.close()
+        del img
+        torch.cuda.empty_cache()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -536,6 +646,10 @@ def main():
     ap.add_argument("--attn-sweep", nargs="?", const="llama3-8b", choices=["llama3-8b", "gemma2b"],
                     help="only run both decode attentions at 65..3001 positions of the named attention shape "
                          "(for a kernel trace)")
+    ap.add_argument("--gemm-types", action="store_true",
+                    help="only the batched product of every weight type at 4096 x 4096 x 1024 rows")
+    ap.add_argument("--prefill-types", action="store_true",
+                    help="only a 1024-position prompt through 4 Llama-3-8B-shape layers for several weight mixes")
     ap.add_argument("--cpu-leg", help=argparse.SUPPRESS)
     ap.add_argument("--cpu-kind", default="omp", choices=["omp", "omp_v4", "o3", "port"], help=argparse.SUPPRESS)
     ap.add_argument("--cpu-start", type=int, default=0, help=argparse.SUPPRESS)
@@ -555,6 +669,12 @@ def main():
         return
     if a.gemv_shapes:
         gemv_shapes_only()
+        return
+    if a.gemm_types:
+        gemm_types_only()
+        return
+    if a.prefill_types:
+        prefill_types_only()
         return
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the decode path runs on a single MI355X and has no multi-GPU "
