@@ -241,7 +241,7 @@ def test_gemv_deterministic(ctx, torch_gpu):
 
 
 @pytest.mark.parametrize("qtype", Q8_ACT)
-@pytest.mark.parametrize("rows,cols,batch", [(1024, 2048, 7), (300, 4096, 130), (77, 96, 65)])
+@pytest.mark.parametrize("rows,cols,batch", [(1024, 2048, 7), (300, 4096, 130), (77, 96, 65), (1, 32, 1), (70, 160, 3)])
 def test_gemm_q8_activation_parity(ctx, torch_gpu, cpuref, qtype, rows, cols, batch):
     """Batches of the Q8_0-activation types on the int8 matrix cores against
     the reference's batched dot (matmul_quantized_batch, c:2305-2318: every
@@ -252,7 +252,8 @@ def test_gemm_q8_activation_parity(ctx, torch_gpu, cpuref, qtype, rows, cols, ba
     reference's arithmetic without contraction, as its -O3 build computes it)
     bit for bit; both also lie within gamma_(blocks+4) S of the float64
     value, S = sum of |block terms|.  96 columns give a K step of one block;
-    65 and 130 rows leave ragged row tiles."""
+    65 and 130 rows leave ragged row tiles; one row of one block, and 70 x
+    160 x 3, are the smallest cases."""
     w = synth.random_blocks(qtype, rows, cols, seed=5)
     xb = synth.random_x(cols, seed=6, batch=batch)
     y = empty_f32(torch_gpu, batch * rows)
