@@ -396,25 +396,46 @@ __global__ void __launch_bounds__(4 * BN) gemm_kernel(GemmArgs a) {
 }
 
 // Y (=|+=) the sum of the K splits' partials, in split order (stream-K: the
-// slots of the output's tile, in slot order): one thread per output,
-// blockIdx.y = batch row.
+// slots of the output's tile, in slot order): V consecutive outputs per
+// thread (V = 4: 16-byte loads and stores where every segment's width, row
+// stride and base allow them; each output's additions are the same either
+// way), blockIdx.y = batch row.
+template <int V>
 __global__ void __launch_bounds__(256) gemm_reduce_kernel(GemmArgs a) {
-    const int c = blockIdx.x * 256 + threadIdx.x, m = blockIdx.y;
+    const int c = (blockIdx.x * 256 + threadIdx.x) * V, m = blockIdx.y;
     if (c >= a.ntot) return;
     const int sg = (a.nseg > 1 && c >= a.noff[1]) ? ((a.nseg > 2 && c >= a.noff[2]) ? 2 : 1) : 0;
     int nslot = a.nsplit;
-    if (a.streamk) {
+    if (a.streamk) {   // the V outputs lie in one tile (V divides the tile width and the segment offsets)
         const int NT = a.tbeg[a.nseg], S = a.kst;
         const long W = (long)NT * ((a.m + kBM - 1) / kBM) * S;
         const long tt = (long)(m / kBM) * NT + a.tbeg[sg] + (c - a.noff[sg]) / a.bn;
         nslot = sk_owner((tt + 1) * S - 1, W, a.streamk) - sk_owner(tt * S, W, a.streamk) + 1;
     }
-    const float* p = a.part + (size_t)m * a.ntot + c;
     const size_t zs = (size_t)a.m * a.ntot;
-    float v = p[0];
-    for (int z = 1; z < nslot; ++z) v += p[z * zs];
     float* y = a.y[sg] + (size_t)m * a.ldy[sg] + (c - a.noff[sg]);
-    *y = a.add ? *y + v : v;
+    if constexpr (V == 4) {
+        const float4* p = reinterpret_cast<const float4*>(a.part + (size_t)m * a.ntot + c);
+        float4 v = p[0];
+        for (int z = 1; z < nslot; ++z) {
+            const float4 q = p[z * (zs / 4)];
+            v.x += q.x;
+            v.y += q.y;
+            v.z += q.z;
+            v.w += q.w;
+        }
+        float4* y4 = reinterpret_cast<float4*>(y);
+        if (a.add) {
+            const float4 o = *y4;
+            v = make_float4(o.x + v.x, o.y + v.y, o.z + v.z, o.w + v.w);
+        }
+        *y4 = v;
+    } else {
+        const float* p = a.part + (size_t)m * a.ntot + c;
+        float v = p[0];
+        for (int z = 1; z < nslot; ++z) v += p[z * zs];
+        *y = a.add ? *y + v : v;
+    }
 }
 
 template <int QT>
@@ -557,8 +578,13 @@ void launch_gemm_planned(const GemmJob& j, const GemmPlan& plan, float* ws, hipS
     case L3P_F32: launch_typed<L3P_F32>(a, plan.bn, st); break;
     default: launch_typed<L3P_BF16>(a, plan.bn, st); break;
     }
-    if (a.nsplit > 1 || a.streamk)
-        launch_kernel(gemm_reduce_kernel, dim3((ntot + 255) / 256, j.m), dim3(256), 0u, st, a);
+    if (a.nsplit > 1 || a.streamk) {
+        bool vec = ntot % 4 == 0;
+        for (int i = 0; i < a.nseg; ++i)
+            vec = vec && a.n[i] % 4 == 0 && a.ldy[i] % 4 == 0 && ((uintptr_t)a.y[i] & 15) == 0;
+        if (vec) launch_kernel(gemm_reduce_kernel<4>, dim3((ntot / 4 + 255) / 256, j.m), dim3(256), 0u, st, a);
+        else launch_kernel(gemm_reduce_kernel<1>, dim3((ntot + 255) / 256, j.m), dim3(256), 0u, st, a);
+    }
 }
 
 // ---------------------------------------------------------------------------
