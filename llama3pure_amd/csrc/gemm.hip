@@ -1,12 +1,14 @@
-// gemm.hip — the prefill GEMM on the fp32 matrix cores (gfx950):
+// gemm.hip — the prefill GEMMs on the matrix cores (gfx950):
 //   Y[m][n] (=|+=) sum_k W[n][k] * X[m][k]
 // for M prompt tokens, N output features and K inputs, with W in its GGUF
-// block layout.  It replaces matmul_quantized_batch (llama3pure-c-engine.c:
-// 2291-2331) for the types the reference dequantizes before its batched dot
-// (matmul_deq_batch_4row, c:2179-2273): every weight is expanded exactly to
-// fp32 (dequantize_row_*, c:611-934) and multiplied with the fp32
+// block layout.  They replace matmul_quantized_batch (llama3pure-c-engine.c:
+// 2291-2331).  For the types the reference dequantizes before its batched dot
+// (matmul_deq_batch_4row, c:2179-2273) the fp32 matrix cores multiply every
+// weight expanded exactly to fp32 (dequantize_row_*, c:611-934) with the fp32
 // activation, so the products are the reference's and only the fp32
-// summation order differs.
+// summation order differs.  For the types whose batched dot takes Q8_0
+// activations (Q4_0, Q4_1, Q5_0, Q5_1, IQ4_NL) the int8 matrix cores form
+// the exact block dots (the section at the end of this file).
 //
 // Tiling.  A workgroup owns a 64 x BN tile of Y (BN = 64, or 128 for passes
 // of at least 16 row tiles whose 128-wide tiles give every CU two workgroups

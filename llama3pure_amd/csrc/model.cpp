@@ -1009,7 +1009,8 @@ static void sample_impl(l3p_ctx* c, const float* logits, int n, const l3p_sample
 }
 
 // ---------------------------------------------------------------------------
-// batched matmul (matmul_quantized_batch): one GEMV per batch element
+// batched matmul (matmul_quantized_batch, c:2291-2331): the int8 matrix-core
+// GEMM for the Q8_0-activation types, the fp32 one for the others
 // ---------------------------------------------------------------------------
 void run_gemm(l3p_ctx* c, int type, const uint8_t* w, int rows, int cols, const float* x, int batch, int in_stride,
               float* y, int out_stride) {
