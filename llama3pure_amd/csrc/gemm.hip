@@ -8,7 +8,7 @@
 // activation, so the products are the reference's and only the fp32
 // summation order differs.  For the types whose batched dot takes Q8_0
 // activations (Q4_0, Q4_1, Q5_0, Q5_1, IQ4_NL) the int8 matrix cores form
-// the exact block dots (the section at the end of this file).
+// the exact block dots (the int8 section further down).
 //
 // Tiling.  A workgroup owns a 64 x BN tile of Y (BN = 64, or 128 for passes
 // of at least 16 row tiles whose 128-wide tiles give every CU two workgroups
