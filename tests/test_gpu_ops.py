@@ -272,6 +272,23 @@ def test_gemm_q8_activation_parity(ctx, torch_gpu, cpuref, qtype, rows, cols, ba
     assert diff.size == 0, f"{len(diff)} of {got.size} outputs differ from the oracle, first {tuple(diff[0])}"
 
 
+@pytest.mark.parametrize("rows,cols", [(14336, 4096), (4096, 14336)])
+def test_gemm_q4_0_c2_shapes_bit_exact(ctx, torch_gpu, cpuref, rows, cols):
+    """Q4_0 batches at the C2 shapes (Llama-3-8B's FFN up and down), 16
+    activation rows: the int8 matrix-core GEMM equals the oracle's batched dot
+    (matmul_quantized_batch, c:2305-2318) bit for bit."""
+    batch = 16
+    w = synth.random_blocks(l3p.Q4_0, rows, cols, seed=rows + 3)
+    xb = synth.random_x(cols, seed=cols + 4, batch=batch)
+    y = empty_f32(torch_gpu, batch * rows)
+    ctx.gemm(l3p.Q4_0, dev(torch_gpu, w), rows, cols, dev(torch_gpu, xb), batch, cols, y, rows)
+    ctx.synchronize()
+    got = y.cpu().numpy().reshape(batch, rows)
+    ref = cpuref.matmul_batch(l3p.Q4_0, w, rows, cols, xb)
+    diff = np.argwhere(got != ref)
+    assert diff.size == 0, f"{len(diff)} of {got.size} outputs differ from the oracle, first {tuple(diff[0])}"
+
+
 @pytest.mark.parametrize("qtype", Q8_ACT)
 def test_gemm_q8_activation_close_to_gemv(ctx, torch_gpu, cpuref, qtype):
     """The batched and the single-row (GEMV) forms of these types agree
