@@ -385,6 +385,29 @@ def test_gemm_mfma_parity(ctx, torch_gpu, cpuref, qtype, rows, cols, batch):
     assert np.all(np.isnan(got[:, rows:])), "wrote outside the output rows"
 
 
+@pytest.mark.parametrize("env", [{"L3P_GEMM_SK_BN": "128"}, {"L3P_GEMM_SK_WPC": "2"},
+                                 {"L3P_GEMM_SK_MIN": "16"}, {"L3P_GEMM_SK_BN": "128", "L3P_GEMM_SK_WPC": "2"}])
+def test_gemm_stream_k_overrides(ctx, torch_gpu, cpuref, env, monkeypatch):
+    """The stream-K plan overrides (128-wide tiles, workgroups per CU, the
+    shortest run) change only the schedule: a Gemma-2-2B-like output
+    projection (2304 x 2048, 130 rows: stream-K) stays within the fp32
+    summation bound under each of them."""
+    for k, v in env.items():
+        monkeypatch.setenv(k, v)
+    qtype, rows, cols, batch = l3p.Q8_0, 2304, 2048, 130
+    w = synth.random_blocks(qtype, rows, cols, seed=31)
+    xb = synth.random_x(cols, seed=32, batch=batch)
+    y = torch_gpu.full((batch * rows,), float("nan"), dtype=torch_gpu.float32, device="cuda")
+    ctx.gemm(qtype, dev(torch_gpu, w), rows, cols, dev(torch_gpu, xb), batch, cols, y, rows)
+    ctx.synchronize()
+    got = y.cpu().numpy().reshape(batch, rows)
+    W, A = _dequant_bound(cpuref, qtype, w, rows, cols)
+    x64 = xb.astype(np.float64)
+    err = np.abs(got - x64 @ W.T)
+    tol = gamma(cols + 4) * (np.abs(x64) @ A.T)
+    assert np.all(err <= tol), f"max err/tol {np.max(err / np.maximum(tol, 1e-30)):.3g}"
+
+
 def test_gemm_mfma_equals_gemv_within_bound(ctx, torch_gpu, cpuref):
     """The batched and the single-row forms agree within the same bound."""
     qtype, rows, cols, batch = l3p.Q8_0, 4096, 4096, 5
