@@ -1276,14 +1276,19 @@ __device__ __forceinline__ void pinj(f32x4 (&q)[J]) {
     for (int j = 0; j < J; ++j) asm volatile("" : "+v"(q[j]));
 }
 
-template <int J, int G, int NB, bool PAIR, bool POST>
-__global__ void __launch_bounds__(64) gemv_wide_kernel(GemvArgs a) {
+template <int J, int G, int NB, bool PAIR, bool POST, int S = 1>
+__global__ void __launch_bounds__(64 * S) gemv_wide_kernel(GemvArgs a) {
+    static_assert(S == 1 || (!PAIR && !POST), "sliced rows: plain rows only");
     constexpr int NOUT = PAIR ? G / 2 : G;
     constexpr int CI = wide_ci<J>();
     constexpr int BDW = CI * 256;   // dwords per ring buffer
     extern __shared__ __align__(16) uint32_t lds[];
-    float* xch = reinterpret_cast<float*>(lds + NB * BDW);   // [G] row totals of a group (pair epilogue)
-    const int lane = threadIdx.x;
+    // S > 1: wave s takes bytes [272 J s, 272 J (s + 1)) of every row (columns
+    // [256 J s, 256 J (s + 1))) through its own ring
+    const int sl = S > 1 ? (int)(threadIdx.x >> 6) : 0;
+    uint32_t* ring = lds + sl * NB * BDW;
+    float* xch = reinterpret_cast<float*>(lds + S * NB * BDW);   // [G] row totals (pair epilogue); S > 1: [2][S][G]
+    const int lane = threadIdx.x & 63;
     const uint32_t rb = 272u * J;
     Cursor cc;
     cc.w0 = a.w[0];
@@ -1297,19 +1302,19 @@ __global__ void __launch_bounds__(64) gemv_wide_kernel(GemvArgs a) {
     cc.gdim = gridDim.x;
     cc.rbeg = 0;
     cc.nmine = -1;
-    cc.rb = rb;
-    cc.coff = 0;
+    cc.rb = rb * S;
+    cc.coff = rb * sl;
     const WideDma dl = wide_dma<CI>(lane, rb);
     auto issue = [&](int k, int slot) {
         const uint8_t* src;
         chunk_src<G, PAIR>(cc, k, src);
-        wide_copy<CI>(lds + slot * BDW, src, dl);
+        wide_copy<CI>(ring + slot * BDW, src, dl);
     };
 
     // ---- the lane's activation columns, norm weights and residual-update
     // inputs, issued before the weight copies and waited for without them
     f32x4 xq[J], nq[J], yq[J], pq[J];
-    loadj_async<J>(xq, a.x + 4 * lane);
+    loadj_async<J>(xq, a.x + 256 * J * sl + 4 * lane);
     if (a.norm) loadj_async<J>(nq, a.norm + 4 * lane);
     if (POST) {
         loadj_async<J>(yq, a.post_y + 4 * lane);
@@ -1396,7 +1401,7 @@ __global__ void __launch_bounds__(64) gemv_wide_kernel(GemvArgs a) {
             wait_chunk<NB - 1, CI>(nk - 1 - k);
             const uint8_t* src;
             const bool real = chunk_src<G, PAIR>(cc, k, src);
-            const uint32_t* buf = lds + (k % NB) * BDW;
+            const uint32_t* buf = ring + (k % NB) * BDW;
             const uint16_t* hw = reinterpret_cast<const uint16_t*>(buf);
             float dv = 0.0f;
 #pragma unroll
@@ -1413,10 +1418,21 @@ __global__ void __launch_bounds__(64) gemv_wide_kernel(GemvArgs a) {
             acc[i] = real ? dv : 0.0f;
             wait_lgkm();   // this row's LDS reads are done before its buffer is refilled
         }
-        const float tot = xreduce<G>(acc, lane) * rscale;
+        float tot = xreduce<G>(acc, lane) * rscale;
         const int ri = rowof<G>(lane);
         const bool lead = (lane & ((64 / G) - 1)) == 0;
         const int grp = (int)blockIdx.x + gl * (int)gridDim.x;
+        if constexpr (S > 1) {
+            // the slices' row totals through LDS (two halves, so one barrier
+            // per group suffices), added in slice order by the first wave
+            float* red = xch + (gl & 1) * S * G;
+            if (lead) red[sl * G + ri] = tot;
+            lds_sync();
+            if (sl != 0) continue;
+            tot = red[ri];
+#pragma unroll
+            for (int q = 1; q < S; ++q) tot += red[q * G + ri];
+        }
         if (PAIR) {
             if (lead) xch[ri] = tot;
             if (lane < NOUT) {
@@ -1635,6 +1651,24 @@ int launch_wide(GemvArgs a, bool pair, hipStream_t st) {
     return launch_wide_g<10>(a, pair, G, wpc, nb, st);
 }
 
+// Rows of S x 2304 columns: a workgroup of S waves takes one row at a time,
+// each wave a 2304-column slice through its own 4-deep ring (the whole-row
+// kernel's lane layout), and the first wave adds the slices' totals.  Rows
+// are dealt evenly over as many workgroups as fit at once (Gemma-2-2B's 2304
+// x 9216 down projection: 768 workgroups of three rows, three per CU).
+template <int S>
+int launch_sliced(GemvArgs a, hipStream_t st) {
+    constexpr int J = 9, G = 1, NB = 4;
+    auto kern = gemv_wide_kernel<J, G, NB, false, false, S>;
+    const size_t lds = (size_t)S * NB * wide_ci<J>() * 1024 + (size_t)2 * S * G * 4;
+    a.ngroups = a.rows_total;
+    const int cap = std::max(1, occupancy(kern, 64 * S, lds)) * cus();
+    const int k = (a.ngroups + cap - 1) / cap;
+    const int grid = (a.ngroups + k - 1) / k;
+    launch_kernel(kern, dim3(grid), dim3(64 * S), (uint32_t)lds, st, a);
+    return 0;
+}
+
 template <int QT>
 int launch_type(GemvArgs a, bool pair, int G, bool standalone, hipStream_t st) {
     const int units = pair ? a.rows[0] : a.rows_total;
@@ -1754,9 +1788,14 @@ int launch_gemv(int type, const GemvBatch& b, int cols, const float* x, const fl
     a.ss_loads = (b.n_ss + 255) / 256;
     a.n_ss = b.n_ss;
     L3P_REQUIRE(!b.ss || (b.n_ss > 0 && b.n_ss <= kMaxSsParts), L3P_E_INVALID, "gemv: %d sums of squares", b.n_ss);
-    // Q8_0 rows of 2304 or 2560 columns stream whole rows per wave
+    // Q8_0 rows of 2304 or 2560 columns stream whole rows per wave; rows of
+    // 4 x 2304 columns (Gemma-2-2B's down projection) four 2304-column slices
+    // per workgroup
     if (type == L3P_Q8_0 && wide_cols(cols) && !b.xw && !b.ss && env_int("L3P_GEMV_WIDE", 1))
         return launch_wide(a, b.pair != 0, st);
+    if (type == L3P_Q8_0 && cols == 4 * 2304 && !b.pair && !b.post_y && !norm && !b.xw && !b.ss &&
+        env_int("L3P_GEMV_SLICED", 1))
+        return launch_sliced<4>(a, st);
     // Rows per group G: the largest of 16, 8, 4 that still gives about six
     // waves per CU (groups x column chunks); ring depth 3.  (Measured on
     // MI355X at the Llama-3-8B shapes.)

@@ -214,6 +214,21 @@ def test_gemv_wide_rows_ragged(ctx, torch_gpu, cpuref, monkeypatch, rows, cols):
         assert not np.array_equal(got, old), "both runs took the same kernel"
 
 
+@pytest.mark.parametrize("rows", [1, 3, 5, 769, 2304, 4097])
+def test_gemv_sliced_rows(ctx, torch_gpu, cpuref, monkeypatch, rows):
+    """Q8_0 rows of 9216 columns (Gemma-2-2B's down projection): four waves a
+    workgroup, each streaming a 2304-column slice of every row, the slices'
+    totals added in order; rows dealt over the workgroups, ragged counts
+    included, against the oracle's bound, and the chunk-column kernel
+    (L3P_GEMV_SLICED=0) on the same inputs within the same bound."""
+    cols = 9216
+    got = _check_gemv(ctx, torch_gpu, cpuref, l3p.Q8_0, rows, cols, seed=rows + 11, sample_rows=min(rows, 768))
+    monkeypatch.setenv("L3P_GEMV_SLICED", "0")
+    old = _check_gemv(ctx, torch_gpu, cpuref, l3p.Q8_0, rows, cols, seed=rows + 11, sample_rows=min(rows, 768))
+    if rows >= 2304:   # different summation orders: some row totals differ in their last bits
+        assert not np.array_equal(got, old), "both runs took the same kernel"
+
+
 def test_gemv_zero_rows_and_errors(ctx, torch_gpu):
     x = empty_f32(torch_gpu, 512)
     y = empty_f32(torch_gpu, 8)
