@@ -1793,9 +1793,12 @@ int launch_gemv(int type, const GemvBatch& b, int cols, const float* x, const fl
     // per workgroup
     if (type == L3P_Q8_0 && wide_cols(cols) && !b.xw && !b.ss && env_int("L3P_GEMV_WIDE", 1))
         return launch_wide(a, b.pair != 0, st);
-    if (type == L3P_Q8_0 && cols == 4 * 2304 && !b.pair && !b.post_y && !norm && !b.xw && !b.ss &&
-        env_int("L3P_GEMV_SLICED", 1))
+    if (type == L3P_Q8_0 && (cols == 2 * 2304 || cols == 3 * 2304 || cols == 4 * 2304) && !b.pair && !b.post_y &&
+        !norm && !b.xw && !b.ss && env_int("L3P_GEMV_SLICED", 1)) {
+        if (cols == 2 * 2304) return launch_sliced<2>(a, st);
+        if (cols == 3 * 2304) return launch_sliced<3>(a, st);
         return launch_sliced<4>(a, st);
+    }
     // Rows per group G: the largest of 16, 8, 4 that still gives about six
     // waves per CU (groups x column chunks); ring depth 3.  (Measured on
     // MI355X at the Llama-3-8B shapes.)

@@ -214,17 +214,18 @@ def test_gemv_wide_rows_ragged(ctx, torch_gpu, cpuref, monkeypatch, rows, cols):
         assert not np.array_equal(got, old), "both runs took the same kernel"
 
 
+@pytest.mark.parametrize("cols", [4608, 6912, 9216])
 @pytest.mark.parametrize("rows", [1, 3, 5, 769, 2304, 4097])
-def test_gemv_sliced_rows(ctx, torch_gpu, cpuref, monkeypatch, rows):
-    """Q8_0 rows of 9216 columns (Gemma-2-2B's down projection): four waves a
-    workgroup, each streaming a 2304-column slice of every row, the slices'
-    totals added in order; rows dealt over the workgroups, ragged counts
-    included, against the oracle's bound, and the chunk-column kernel
-    (L3P_GEMV_SLICED=0) on the same inputs within the same bound."""
-    cols = 9216
-    got = _check_gemv(ctx, torch_gpu, cpuref, l3p.Q8_0, rows, cols, seed=rows + 11, sample_rows=min(rows, 768))
+def test_gemv_sliced_rows(ctx, torch_gpu, cpuref, monkeypatch, rows, cols):
+    """Q8_0 rows of 2, 3 and 4 x 2304 columns (Gemma-2-2B's down projection
+    has 9216): that many waves a workgroup, each streaming a 2304-column slice
+    of every row, the slices' totals added in order; rows dealt over the
+    workgroups, ragged counts included, against the oracle's bound, and the
+    chunk-column kernel (L3P_GEMV_SLICED=0) on the same inputs within the
+    same bound."""
+    got = _check_gemv(ctx, torch_gpu, cpuref, l3p.Q8_0, rows, cols, seed=rows + cols, sample_rows=min(rows, 768))
     monkeypatch.setenv("L3P_GEMV_SLICED", "0")
-    old = _check_gemv(ctx, torch_gpu, cpuref, l3p.Q8_0, rows, cols, seed=rows + 11, sample_rows=min(rows, 768))
+    old = _check_gemv(ctx, torch_gpu, cpuref, l3p.Q8_0, rows, cols, seed=rows + cols, sample_rows=min(rows, 768))
     if rows >= 2304:   # different summation orders: some row totals differ in their last bits
         assert not np.array_equal(got, old), "both runs took the same kernel"
 
